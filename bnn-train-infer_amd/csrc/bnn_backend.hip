@@ -1,0 +1,850 @@
+// Host side of the HIP backend: the eleven BNN_* entry points of the BNN
+// accelerator API v2 (reference bnn-accelerator/bnn-accelerator.h:171-207),
+// plus the BNNX_* extensions of include/bnn-accelerator-hip.h.
+//
+// Argument validation follows the reference soft backend's order and status
+// codes exactly (bnn-accelerator/soft-bnn-accelerator.c:310-603), because the
+// reference's contract test pins both.  Input-value validation (-128, NaN/Inf)
+// happens on the GPU: the prep kernel raises a per-device flag with the job's
+// sequence number, every later kernel of the job checks it before writing, and
+// the host learns the outcome from a pinned status word after the one
+// synchronisation of the call.  So an illegal input leaves the output untouched.
+#include <fenv.h>
+#include <float.h>
+#include <hip/hip_runtime.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "bnn-accelerator-hip.h"
+#include "bnn-accelerator.h"
+#include "bnn_internal.h"
+
+using namespace bnnhip;
+
+#define EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+constexpr size_t kPinnedCap = size_t(8) << 20;       // largest transfer staged through pinned memory
+constexpr size_t kScratchRowsCap = 4096;              // rows per launch chunk
+constexpr size_t kScratchBytesCap = size_t(256) << 20;
+
+bool mul_size(size_t a, size_t b, size_t* out) {
+    if (a != 0 && b > SIZE_MAX / a)
+        return false;
+    *out = a * b;
+    return true;
+}
+
+bool span_fits(size_t capacity, size_t offset, size_t bytes) {
+    return offset <= capacity && bytes <= capacity - offset;
+}
+
+// (soft-bnn-accelerator.c:65-77) last logical row inside the buffer, overflow-free.
+bool rows_fit(size_t capacity, size_t offset, size_t stride, size_t row_bytes, uint32_t rows) {
+    if (rows == 0 || row_bytes == 0 || stride < row_bytes || offset > capacity)
+        return false;
+    size_t room = capacity - offset;
+    if (row_bytes > room)
+        return false;
+    return (uintmax_t)(rows - 1u) <= (uintmax_t)((room - row_bytes) / stride);
+}
+
+BNN_Status hip_status(hipError_t e) {
+    if (e == hipSuccess)
+        return BNN_OK;
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+        return BNN_ENOMEM;
+    return BNN_EIO;
+}
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+BNN_Status ensure_scratch(BNN_Device d, size_t bytes) {
+    if (bytes <= d->scratch_bytes)
+        return BNN_OK;
+    if (d->scratch) {
+        (void)hipFree(d->scratch);
+        d->scratch = nullptr;
+        d->scratch_bytes = 0;
+    }
+    size_t want = round_up(bytes, size_t(1) << 20);
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return BNN_ENOMEM;
+    }
+    d->scratch = static_cast<unsigned char*>(p);
+    d->scratch_bytes = want;
+    return BNN_OK;
+}
+
+BNN_Status ensure_pinned(BNN_Device d, size_t bytes) {
+    if (bytes <= d->pinned_bytes)
+        return BNN_OK;
+    if (d->pinned) {
+        (void)hipHostFree(d->pinned);
+        d->pinned = nullptr;
+        d->pinned_bytes = 0;
+    }
+    size_t want = round_up(bytes, size_t(1) << 16);
+    void* p = nullptr;
+    hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return BNN_ENOMEM;
+    }
+    d->pinned = static_cast<unsigned char*>(p);
+    d->pinned_bytes = want;
+    return BNN_OK;
+}
+
+// Adds the elapsed time of every recorded event pair; the stream must be idle.
+hipError_t resolve_timing(BNN_Device d) {
+    hipError_t result = hipSuccess;
+    for (int i = 0; i < d->ev_used; ++i) {
+        float ms = 0.0f;
+        hipError_t e = hipEventElapsedTime(&ms, d->ev_begin[i], d->ev_end[i]);
+        if (e != hipSuccess) {
+            result = e;
+            continue;
+        }
+        d->kernel_ms[d->ev_kind[i]] += ms;
+        d->kernel_launches[d->ev_kind[i]] += 1;
+    }
+    d->ev_used = 0;
+    return result;
+}
+
+// Launch helper: when timing is on, brackets `launch` with an event pair on the
+// device stream (no extra synchronisation unless the slots run out).
+template <typename F>
+hipError_t timed(BNN_Device d, int kind, F&& launch) {
+    if (!d->timing)
+        return launch();
+    if (d->ev_used == bnn_accel_device::kTimingSlots) {
+        hipError_t e = hipStreamSynchronize(d->stream);
+        if (e == hipSuccess)
+            e = resolve_timing(d);
+        if (e != hipSuccess)
+            return e;
+    }
+    const int slot = d->ev_used;
+    hipError_t e = hipEventRecord(d->ev_begin[slot], d->stream);
+    if (e == hipSuccess)
+        e = launch();
+    if (e == hipSuccess)
+        e = hipEventRecord(d->ev_end[slot], d->stream);
+    if (e == hipSuccess) {
+        d->ev_kind[slot] = kind;
+        d->ev_used = slot + 1;
+    }
+    return e;
+}
+
+BNN_Status op_types(BNN_Operation op, BNN_Type* in, BNN_Type* out) {
+    switch (op) {
+    case BNN_OP_GEMV:
+    case BNN_OP_GEMM:
+        *in = BNN_TYPE_I8;
+        *out = BNN_TYPE_F32;
+        return BNN_OK;
+    case BNN_OP_DOT_GROUPS:
+        *in = BNN_TYPE_I8;
+        *out = BNN_TYPE_I16;
+        return BNN_OK;
+    case BNN_OP_GEMV_F32:
+    case BNN_OP_GEMM_F32:
+        *in = BNN_TYPE_F32;
+        *out = BNN_TYPE_F32;
+        return BNN_OK;
+    default:
+        return BNN_ENOTSUP;
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Devices (soft-bnn-accelerator.c:310-356)
+// ---------------------------------------------------------------------------
+
+EXPORT BNN_Status BNN_DeviceOpen(uint32_t device_index, BNN_Device* out_device) {
+    if (out_device == nullptr)
+        return BNN_EINVAL;
+    *out_device = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        (void)hipGetLastError();
+        return BNN_ENOTSUP;
+    }
+    if (device_index >= (uint32_t)count)
+        return BNN_ENOTSUP;
+    float one = 1.0f;
+    uint32_t one_bits;
+    memcpy(&one_bits, &one, sizeof one_bits);
+    if (one_bits != 0x3f800000u)
+        return BNN_ENOTSUP;
+
+    BNN_Device d = static_cast<BNN_Device>(calloc(1, sizeof(bnn_accel_device)));
+    if (d == nullptr)
+        return BNN_ENOMEM;
+    d->ordinal = (int)device_index;
+    hipError_t e = hipSetDevice(d->ordinal);
+    if (e == hipSuccess)
+        e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
+    if (e == hipSuccess)
+        e = hipMalloc(reinterpret_cast<void**>(&d->flag_dev), 256);
+    if (e == hipSuccess)
+        e = hipHostMalloc(reinterpret_cast<void**>(&d->status_host), 256, hipHostMallocCoherent);
+    for (int i = 0; e == hipSuccess && i < bnn_accel_device::kTimingSlots; ++i) {
+        e = hipEventCreate(&d->ev_begin[i]);
+        if (e == hipSuccess)
+            e = hipEventCreate(&d->ev_end[i]);
+    }
+    if (e == hipSuccess) {
+        *d->status_host = 0;
+        const uint64_t zero = 0;
+        e = hipMemcpyAsync(d->flag_dev, &zero, sizeof zero, hipMemcpyHostToDevice, d->stream);
+        if (e == hipSuccess)
+            e = hipStreamSynchronize(d->stream);
+    }
+    if (e != hipSuccess) {
+        BNN_Status st = hip_status(e);
+        (void)hipGetLastError();
+        for (int i = 0; i < bnn_accel_device::kTimingSlots; ++i) {
+            if (d->ev_end[i])
+                (void)hipEventDestroy(d->ev_end[i]);
+            if (d->ev_begin[i])
+                (void)hipEventDestroy(d->ev_begin[i]);
+        }
+        if (d->status_host)
+            (void)hipHostFree(d->status_host);
+        if (d->flag_dev)
+            (void)hipFree(d->flag_dev);
+        if (d->stream)
+            (void)hipStreamDestroy(d->stream);
+        free(d);
+        return st == BNN_ENOMEM ? BNN_ENOMEM : BNN_EIO;
+    }
+    *out_device = d;
+    return BNN_OK;
+}
+
+EXPORT BNN_Status BNN_DeviceClose(BNN_Device device) {
+    if (device == nullptr)
+        return BNN_EINVAL;
+    if (device->live_matrices != 0 || device->live_buffers != 0)
+        return BNN_EBUSY;
+    (void)hipSetDevice(device->ordinal);
+    (void)hipStreamSynchronize(device->stream);
+    if (device->scratch)
+        (void)hipFree(device->scratch);
+    if (device->pinned)
+        (void)hipHostFree(device->pinned);
+    if (device->table_host)
+        (void)hipHostFree(device->table_host);
+    if (device->table_dev)
+        (void)hipFree(device->table_dev);
+    for (int i = 0; i < bnn_accel_device::kTimingSlots; ++i) {
+        (void)hipEventDestroy(device->ev_begin[i]);
+        (void)hipEventDestroy(device->ev_end[i]);
+    }
+    (void)hipHostFree(device->status_host);
+    (void)hipFree(device->flag_dev);
+    (void)hipStreamDestroy(device->stream);
+    free(device);
+    return BNN_OK;
+}
+
+EXPORT BNN_Status BNN_DeviceGetCaps(BNN_Device device, BNN_Caps* out_caps) {
+    if (device == nullptr || out_caps == nullptr)
+        return BNN_EINVAL;
+    memset(out_caps, 0, sizeof *out_caps);
+    out_caps->api_version = BNN_API_VERSION;
+    out_caps->max_in_features = kMaxFeatures;
+    out_caps->max_out_features = kMaxFeatures;
+    out_caps->max_rows = UINT32_MAX;
+    out_caps->group_size = kGroup;
+    out_caps->supported_ops =
+        BNN_CAP_GEMV | BNN_CAP_GEMM | BNN_CAP_DOT_GROUPS | BNN_CAP_GEMV_F32 | BNN_CAP_GEMM_F32;
+    return BNN_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Matrices (soft-bnn-accelerator.c:358-440): validate, repack to the tile
+// layout of bnn_internal.h on the host, upload once, keep resident.
+// ---------------------------------------------------------------------------
+
+EXPORT BNN_Status BNN_MatrixCreate(BNN_Device device, const BNN_MatrixDesc* desc, BNN_Matrix* out_matrix) {
+    if (out_matrix == nullptr)
+        return BNN_EINVAL;
+    *out_matrix = nullptr;
+    if (device == nullptr || desc == nullptr)
+        return BNN_EINVAL;
+    if (desc->in_features == 0 || desc->out_features == 0 || desc->group_size == 0 || desc->group_size > 256u ||
+        desc->group_size % 8u != 0)
+        return BNN_EINVAL;
+    if (desc->in_features > kMaxFeatures || desc->out_features > kMaxFeatures || desc->group_size != kGroup)
+        return BNN_ENOTSUP;
+    if (desc->in_features % kGroup != 0)
+        return BNN_EINVAL;
+    size_t bits_bytes, scale_count, scale_bytes;
+    if (!mul_size(desc->out_features, desc->in_features / 8u, &bits_bytes) ||
+        !mul_size(desc->out_features, desc->in_features / kGroup, &scale_count) ||
+        !mul_size(scale_count, sizeof(uint16_t), &scale_bytes))
+        return BNN_ERANGE;
+    if (desc->weight_bits == nullptr || desc->scale_fp16 == nullptr || desc->weight_bytes != bits_bytes ||
+        desc->scale_count != scale_count)
+        return BNN_EINVAL;
+    for (size_t i = 0; i < scale_count; ++i)
+        if ((desc->scale_fp16[i] & 0x7c00u) == 0x7c00u)
+            return BNN_EINVAL;
+    if (device->live_matrices == SIZE_MAX)
+        return BNN_ERANGE;
+
+    const uint32_t k = desc->in_features, n = desc->out_features, groups = k / kGroup;
+    const uint32_t tiles = (n + kTile - 1) / kTile;
+    const size_t wbits_bytes = (size_t)tiles * groups * kTile * 16u;
+    const size_t wscale_bytes = (size_t)tiles * kTile * groups * 2u;
+    const size_t total = wbits_bytes + round_up(wscale_bytes, 256);
+
+    BNN_Matrix m = static_cast<BNN_Matrix>(calloc(1, sizeof(bnn_accel_matrix)));
+    if (m == nullptr)
+        return BNN_ENOMEM;
+    unsigned char* host = static_cast<unsigned char*>(malloc(total));
+    if (host == nullptr) {
+        free(m);
+        return BNN_ENOMEM;
+    }
+    // repack: wbits[t][g][lane] <- row n = 64t + lane, bytes 16g..16g+15
+    const size_t row_bytes = k / 8u;
+    uint8_t* hb = host;
+    for (uint32_t t = 0; t < tiles; ++t)
+        for (uint32_t g = 0; g < groups; ++g)
+            for (uint32_t l = 0; l < kTile; ++l) {
+                const uint32_t nn = t * kTile + l;
+                uint8_t* dst = hb + (((size_t)t * groups + g) * kTile + l) * 16u;
+                if (nn < n)
+                    memcpy(dst, desc->weight_bits + (size_t)nn * row_bytes + (size_t)g * 16u, 16);
+                else
+                    memset(dst, 0, 16);
+            }
+    // wscale[t][g][lane] <- scale of (n = 64t + lane, g)
+    uint16_t* hs = reinterpret_cast<uint16_t*>(host + wbits_bytes);
+    for (uint32_t t = 0; t < tiles; ++t)
+        for (uint32_t g = 0; g < groups; ++g)
+            for (uint32_t l = 0; l < kTile; ++l) {
+                const uint32_t nn = t * kTile + l;
+                hs[((size_t)t * groups + g) * kTile + l] = nn < n ? desc->scale_fp16[(size_t)nn * groups + g] : 0;
+            }
+
+    hipError_t e = hipSetDevice(device->ordinal);
+    void* dev = nullptr;
+    if (e == hipSuccess)
+        e = hipMalloc(&dev, total);
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(dev, host, total, hipMemcpyHostToDevice, device->stream);
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(device->stream);
+    free(host);
+    if (e != hipSuccess) {
+        BNN_Status st = hip_status(e);
+        (void)hipGetLastError();
+        if (dev)
+            (void)hipFree(dev);
+        free(m);
+        return st;
+    }
+    m->device = device;
+    m->k = k;
+    m->n = n;
+    m->groups = groups;
+    m->tiles = tiles;
+    m->wbits = static_cast<uint4*>(dev);
+    m->wscale = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(dev) + wbits_bytes);
+    device->live_matrices++;
+    *out_matrix = m;
+    return BNN_OK;
+}
+
+EXPORT void BNN_MatrixDestroy(BNN_Matrix matrix) {
+    if (matrix == nullptr)
+        return;
+    (void)hipSetDevice(matrix->device->ordinal);
+    (void)hipStreamSynchronize(matrix->device->stream);
+    (void)hipFree(matrix->wbits);
+    matrix->device->live_matrices--;
+    free(matrix);
+}
+
+// ---------------------------------------------------------------------------
+// Buffers (soft-bnn-accelerator.c:442-511): device memory, synchronous copies.
+// ---------------------------------------------------------------------------
+
+EXPORT BNN_Status BNN_BufferAlloc(BNN_Device device, size_t bytes, BNN_Buffer* out_buffer) {
+    if (out_buffer == nullptr)
+        return BNN_EINVAL;
+    *out_buffer = nullptr;
+    if (device == nullptr || bytes == 0)
+        return BNN_EINVAL;
+    if (device->live_buffers == SIZE_MAX)
+        return BNN_ERANGE;
+    BNN_Buffer b = static_cast<BNN_Buffer>(calloc(1, sizeof(bnn_accel_buffer)));
+    if (b == nullptr)
+        return BNN_ENOMEM;
+    void* p = nullptr;
+    hipError_t e = hipSetDevice(device->ordinal);
+    if (e == hipSuccess)
+        e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        free(b);
+        return BNN_ENOMEM;
+    }
+    b->device = device;
+    b->size = bytes;
+    b->dev = static_cast<unsigned char*>(p);
+    device->live_buffers++;
+    *out_buffer = b;
+    return BNN_OK;
+}
+
+EXPORT void BNN_BufferFree(BNN_Buffer buffer) {
+    if (buffer == nullptr)
+        return;
+    (void)hipSetDevice(buffer->device->ordinal);
+    (void)hipStreamSynchronize(buffer->device->stream);
+    (void)hipFree(buffer->dev);
+    buffer->device->live_buffers--;
+    free(buffer);
+}
+
+EXPORT BNN_Status BNN_BufferWrite(BNN_Buffer buffer, size_t offset, const void* src, size_t bytes) {
+    if (buffer == nullptr || (bytes != 0 && src == nullptr))
+        return BNN_EINVAL;
+    if (!span_fits(buffer->size, offset, bytes))
+        return BNN_ERANGE;
+    if (bytes == 0)
+        return BNN_OK;
+    BNN_Device d = buffer->device;
+    hipError_t e = hipSetDevice(d->ordinal);
+    if (e != hipSuccess)
+        return BNN_EIO;
+    if (bytes <= kPinnedCap && ensure_pinned(d, bytes) == BNN_OK) {
+        memcpy(d->pinned, src, bytes);
+        e = hipMemcpyAsync(buffer->dev + offset, d->pinned, bytes, hipMemcpyHostToDevice, d->stream);
+    } else {
+        e = hipMemcpyAsync(buffer->dev + offset, src, bytes, hipMemcpyHostToDevice, d->stream);
+    }
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(d->stream);
+    return e == hipSuccess ? BNN_OK : BNN_EIO;
+}
+
+EXPORT BNN_Status BNN_BufferRead(BNN_Buffer buffer, size_t offset, void* dst, size_t bytes) {
+    if (buffer == nullptr || (bytes != 0 && dst == nullptr))
+        return BNN_EINVAL;
+    if (!span_fits(buffer->size, offset, bytes))
+        return BNN_ERANGE;
+    if (bytes == 0)
+        return BNN_OK;
+    BNN_Device d = buffer->device;
+    hipError_t e = hipSetDevice(d->ordinal);
+    if (e != hipSuccess)
+        return BNN_EIO;
+    if (bytes <= kPinnedCap && ensure_pinned(d, bytes) == BNN_OK) {
+        e = hipMemcpyAsync(d->pinned, buffer->dev + offset, bytes, hipMemcpyDeviceToHost, d->stream);
+        if (e == hipSuccess)
+            e = hipStreamSynchronize(d->stream);
+        if (e == hipSuccess)
+            memcpy(dst, d->pinned, bytes);
+    } else {
+        e = hipMemcpyAsync(dst, buffer->dev + offset, bytes, hipMemcpyDeviceToHost, d->stream);
+        if (e == hipSuccess)
+            e = hipStreamSynchronize(d->stream);
+    }
+    return e == hipSuccess ? BNN_OK : BNN_EIO;
+}
+
+// ---------------------------------------------------------------------------
+// Execute (soft-bnn-accelerator.c:513-603)
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// Everything Execute derives from a job before touching the device.
+struct JobPlan {
+    BNN_Matrix m;
+    bool f32_in, dot_out;
+    size_t in_row, out_row, in_stride, out_stride;
+    const unsigned char* in_base;
+    unsigned char* out_base;
+    bool in_aligned, out_aligned;
+    DotMode mode;
+};
+
+// Argument checks in the reference's order with its status codes
+// (soft-bnn-accelerator.c:527-573).
+BNN_Status plan_job(BNN_Device device, const BNN_Job* job, JobPlan* p) {
+    if (device == nullptr || job == nullptr || job->matrix == nullptr || job->input.buffer == nullptr ||
+        job->output.buffer == nullptr || job->rows == 0)
+        return BNN_EINVAL;
+    BNN_Type in_type, out_type;
+    BNN_Status st = op_types(job->operation, &in_type, &out_type);
+    if (st != BNN_OK)
+        return st;
+    if ((job->operation == BNN_OP_GEMV || job->operation == BNN_OP_GEMV_F32) && job->rows != 1)
+        return BNN_EINVAL;
+    if (job->input.type != in_type || job->output.type != out_type)
+        return BNN_EINVAL;
+    const BNN_Matrix m = job->matrix;
+    if (m->device != device || job->input.buffer->device != device || job->output.buffer->device != device ||
+        job->input.buffer == job->output.buffer)
+        return BNN_EINVAL;
+    p->m = m;
+    p->f32_in = in_type == BNN_TYPE_F32;
+    p->dot_out = job->operation == BNN_OP_DOT_GROUPS;
+    size_t out_count;
+    if (!mul_size(m->k, p->f32_in ? 4u : 1u, &p->in_row))
+        return BNN_ERANGE;
+    if (p->dot_out) {
+        if (!mul_size(m->n, m->groups, &out_count) || !mul_size(out_count, 2u, &p->out_row))
+            return BNN_ERANGE;
+    } else if (!mul_size(m->n, 4u, &p->out_row)) {
+        return BNN_ERANGE;
+    }
+    p->in_stride = job->input.row_stride ? job->input.row_stride : p->in_row;
+    p->out_stride = job->output.row_stride ? job->output.row_stride : p->out_row;
+    if (p->in_stride < p->in_row || p->out_stride < p->out_row)
+        return BNN_EINVAL;
+    if (!rows_fit(job->input.buffer->size, job->input.offset, p->in_stride, p->in_row, job->rows) ||
+        !rows_fit(job->output.buffer->size, job->output.offset, p->out_stride, p->out_row, job->rows))
+        return BNN_ERANGE;
+    if (!p->dot_out && fegetround() != FE_TONEAREST)
+        return BNN_ENOTSUP;
+    p->in_base = job->input.buffer->dev + job->input.offset;
+    p->out_base = job->output.buffer->dev + job->output.offset;
+    p->in_aligned = !p->f32_in || (((uintptr_t)p->in_base | p->in_stride) & 3u) == 0;
+    const size_t out_align = p->dot_out ? 2u : 4u;
+    p->out_aligned = (((uintptr_t)p->out_base | p->out_stride) & (out_align - 1u)) == 0;
+    p->mode = p->dot_out ? MODE_DOT_I16 : (p->f32_in ? MODE_SUM_SCALED : MODE_SUM);
+    return BNN_OK;
+}
+
+size_t row_scratch_bytes(const JobPlan& p, size_t rows, size_t* planes, size_t* sums, size_t* rscale) {
+    *planes = round_up(rows * p.m->groups * kPlaneWords * 4u, 256);
+    *sums = round_up(rows * p.m->groups * 4u, 256);
+    *rscale = round_up(rows * 4u, 256);
+    return *planes + *sums + *rscale;
+}
+
+PrepJob make_prep(const JobPlan& p, const unsigned char* in, uint32_t rows, unsigned char* scratch) {
+    size_t planes, sums, rscale;
+    row_scratch_bytes(p, rows, &planes, &sums, &rscale);
+    PrepJob j = {};
+    j.in = in;
+    j.in_stride = p.in_stride;
+    j.planes = reinterpret_cast<uint32_t*>(scratch);
+    j.sums = reinterpret_cast<int32_t*>(scratch + planes);
+    j.rscale = reinterpret_cast<float*>(scratch + planes + sums);
+    j.q = nullptr;
+    j.k = p.m->k;
+    j.rows = rows;
+    j.f32 = p.f32_in;
+    j.aligned = p.in_aligned;
+    return j;
+}
+
+DotJob make_dot(const JobPlan& p, const PrepJob& pj, unsigned char* out, size_t out_stride) {
+    DotJob j = {};
+    j.wbits = p.m->wbits;
+    j.wscale = p.m->wscale;
+    j.planes = pj.planes;
+    j.sums = pj.sums;
+    j.rscale = pj.rscale;
+    j.out = out;
+    j.out_stride = out_stride;
+    j.n = p.m->n;
+    j.groups = p.m->groups;
+    j.tiles = p.m->tiles;
+    j.rows = pj.rows;
+    j.mode = p.mode;
+    return j;
+}
+
+BNN_Status finish(BNN_Device device, hipError_t e, uint64_t seq) {
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(device->stream);
+    if (e == hipSuccess && device->ev_used)
+        e = resolve_timing(device);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return BNN_EIO;
+    }
+    if (__atomic_load_n(device->status_host, __ATOMIC_ACQUIRE) == seq)
+        return BNN_ERANGE;
+    return BNN_OK;
+}
+
+}  // namespace
+
+EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
+    JobPlan p;
+    BNN_Status st = plan_job(device, job, &p);
+    if (st != BNN_OK)
+        return st;
+
+    // rows per launch chunk, bounded by the scratch cap
+    const uint32_t rows = job->rows;
+    size_t a, b, c;
+    const size_t per_row = row_scratch_bytes(p, 1, &a, &b, &c) + (p.out_aligned ? 0u : p.out_row);
+    size_t chunk = rows < kScratchRowsCap ? rows : kScratchRowsCap;
+    while (chunk > 1 && chunk * per_row + 4096 > kScratchBytesCap)
+        chunk /= 2;
+    const size_t rows_bytes = row_scratch_bytes(p, chunk, &a, &b, &c);
+    const size_t staging_bytes = p.out_aligned ? 0 : round_up(chunk * p.out_row, 256);
+
+    if (hipSetDevice(device->ordinal) != hipSuccess)
+        return BNN_EIO;
+    st = ensure_scratch(device, rows_bytes + staging_bytes);
+    if (st != BNN_OK)
+        return st;
+    unsigned char* staging = device->scratch + rows_bytes;
+
+    const uint64_t seq = ++device->seq;
+    hipError_t e = hipSuccess;
+    if (chunk < rows) {
+        // every row is checked before any chunk writes output
+        const PrepJob all = make_prep(p, p.in_base, rows, device->scratch);
+        e = timed(device, KK_PREP, [&] {
+            return launch_prep(device->stream, all, true, seq, device->flag_dev, device->status_host);
+        });
+    }
+    for (size_t r0 = 0; e == hipSuccess && r0 < rows; r0 += chunk) {
+        const uint32_t rc = (uint32_t)((rows - r0) < chunk ? (rows - r0) : chunk);
+        const PrepJob pj = make_prep(p, p.in_base + r0 * p.in_stride, rc, device->scratch);
+        e = timed(device, KK_PREP, [&] {
+            return launch_prep(device->stream, pj, false, seq, device->flag_dev, device->status_host);
+        });
+        if (e != hipSuccess)
+            break;
+        const DotJob dj = p.out_aligned ? make_dot(p, pj, p.out_base + r0 * p.out_stride, p.out_stride)
+                                        : make_dot(p, pj, staging, p.out_row);
+        e = timed(device, KK_DOT, [&] { return launch_dot(device->stream, dj, seq, device->flag_dev); });
+        if (e == hipSuccess && !p.out_aligned)
+            e = timed(device, KK_SCATTER, [&] {
+                return launch_scatter(device->stream, staging, p.out_row, p.out_base + r0 * p.out_stride,
+                                      p.out_stride, p.out_row, rc, seq, device->flag_dev);
+            });
+    }
+    return finish(device, e, seq);
+}
+
+// ---------------------------------------------------------------------------
+// Batch extension (include/bnn-accelerator-hip.h; no reference counterpart)
+// ---------------------------------------------------------------------------
+
+EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint32_t count) {
+    if (device == nullptr || jobs == nullptr || count == 0)
+        return BNN_EINVAL;
+    JobPlan* plans = static_cast<JobPlan*>(malloc(sizeof(JobPlan) * count));
+    if (plans == nullptr)
+        return BNN_ENOMEM;
+    struct Extent {
+        const void* buffer;
+        size_t begin, end;
+    };
+    Extent* outs = static_cast<Extent*>(malloc(sizeof(Extent) * count));
+    BNN_Status st = outs ? BNN_OK : BNN_ENOMEM;
+    uint64_t prep_blocks = 0, dot_blocks = 0;
+    size_t scratch_bytes = 0;
+    for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
+        st = plan_job(device, &jobs[i], &plans[i]);
+        if (st != BNN_OK)
+            break;
+        const JobPlan& p = plans[i];
+        if (!p.in_aligned || !p.out_aligned || jobs[i].rows > kScratchRowsCap) {
+            st = BNN_ENOTSUP;
+            break;
+        }
+        size_t a, b, c;
+        scratch_bytes += row_scratch_bytes(p, jobs[i].rows, &a, &b, &c);
+        prep_blocks += jobs[i].rows;
+        dot_blocks += (uint64_t)jobs[i].rows * p.m->tiles;
+        outs[i].buffer = jobs[i].output.buffer;
+        outs[i].begin = jobs[i].output.offset;
+        outs[i].end = jobs[i].output.offset + (size_t)(jobs[i].rows - 1) * p.out_stride + p.out_row;
+    }
+    // jobs run concurrently: no output may alias any input buffer or another output
+    for (uint32_t i = 0; st == BNN_OK && i < count; ++i)
+        for (uint32_t j = 0; st == BNN_OK && j < count; ++j) {
+            if (jobs[i].output.buffer == jobs[j].input.buffer)
+                st = BNN_EINVAL;
+            else if (i < j && outs[i].buffer == outs[j].buffer && outs[i].begin < outs[j].end &&
+                     outs[j].begin < outs[i].end)
+                st = BNN_EINVAL;
+        }
+    if (st == BNN_OK && (prep_blocks > 0x7fffffffu || dot_blocks > 0x7fffffffu))
+        st = BNN_ENOTSUP;
+    if (st != BNN_OK) {
+        free(plans);
+        free(outs);
+        return st;
+    }
+    free(outs);
+
+    // tables: PrepJob[count] | DotJob[count] | prep block->job | dot block->job
+    const size_t prep_tab = round_up(sizeof(PrepJob) * count, 256);
+    const size_t dot_tab = round_up(sizeof(DotJob) * count, 256);
+    const size_t prep_map = round_up(4u * prep_blocks, 256);
+    const size_t dot_map = round_up(4u * dot_blocks, 256);
+    const size_t tables = prep_tab + dot_tab + prep_map + dot_map;
+    hipError_t e = hipSetDevice(device->ordinal);
+    if (e != hipSuccess) {
+        free(plans);
+        return BNN_EIO;
+    }
+    st = ensure_scratch(device, scratch_bytes);
+    if (st == BNN_OK && tables > device->table_dev_bytes) {
+        if (device->table_dev)
+            (void)hipFree(device->table_dev);
+        device->table_dev = nullptr;
+        device->table_dev_bytes = 0;
+        void* p = nullptr;
+        if (hipMalloc(&p, tables) != hipSuccess) {
+            (void)hipGetLastError();
+            st = BNN_ENOMEM;
+        } else {
+            device->table_dev = static_cast<unsigned char*>(p);
+            device->table_dev_bytes = tables;
+        }
+    }
+    if (st == BNN_OK && tables > device->table_host_bytes) {
+        if (device->table_host)
+            (void)hipHostFree(device->table_host);
+        device->table_host = nullptr;
+        device->table_host_bytes = 0;
+        void* p = nullptr;
+        if (hipHostMalloc(&p, tables, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            st = BNN_ENOMEM;
+        } else {
+            device->table_host = static_cast<unsigned char*>(p);
+            device->table_host_bytes = tables;
+        }
+    }
+    if (st != BNN_OK) {
+        free(plans);
+        return st;
+    }
+    PrepJob* hp = reinterpret_cast<PrepJob*>(device->table_host);
+    DotJob* hd = reinterpret_cast<DotJob*>(device->table_host + prep_tab);
+    uint32_t* hpm = reinterpret_cast<uint32_t*>(device->table_host + prep_tab + dot_tab);
+    uint32_t* hdm = reinterpret_cast<uint32_t*>(device->table_host + prep_tab + dot_tab + prep_map);
+    size_t soff = 0;
+    uint32_t pb = 0, db = 0;
+    for (uint32_t i = 0; i < count; ++i) {
+        const JobPlan& p = plans[i];
+        const uint32_t rows = jobs[i].rows;
+        size_t a, b, c;
+        hp[i] = make_prep(p, p.in_base, rows, device->scratch + soff);
+        hp[i].first_block = pb;
+        soff += row_scratch_bytes(p, rows, &a, &b, &c);
+        hd[i] = make_dot(p, hp[i], p.out_base, p.out_stride);
+        hd[i].first_block = db;
+        for (uint32_t r = 0; r < rows; ++r)
+            hpm[pb++] = i;
+        for (uint32_t r = 0; r < rows * p.m->tiles; ++r)
+            hdm[db++] = i;
+    }
+    free(plans);
+
+    const PrepJob* dp = reinterpret_cast<const PrepJob*>(device->table_dev);
+    const DotJob* dd = reinterpret_cast<const DotJob*>(device->table_dev + prep_tab);
+    const uint32_t* dpm = reinterpret_cast<const uint32_t*>(device->table_dev + prep_tab + dot_tab);
+    const uint32_t* ddm = reinterpret_cast<const uint32_t*>(device->table_dev + prep_tab + dot_tab + prep_map);
+    const uint64_t seq = ++device->seq;
+    e = hipMemcpyAsync(device->table_dev, device->table_host, tables, hipMemcpyHostToDevice, device->stream);
+    if (e == hipSuccess)
+        e = timed(device, KK_PREP, [&] {
+            return launch_prep_batch(device->stream, dp, dpm, pb, seq, device->flag_dev, device->status_host);
+        });
+    if (e == hipSuccess)
+        e = timed(device, KK_DOT, [&] { return launch_dot_batch(device->stream, dd, ddm, db, seq, device->flag_dev); });
+    return finish(device, e, seq);
+}
+
+EXPORT const char* BNN_StatusString(BNN_Status status) {
+    switch (status) {
+    case BNN_OK:
+        return "success";
+    case BNN_EINVAL:
+        return "invalid argument";
+    case BNN_ENOMEM:
+        return "out of memory";
+    case BNN_ENOTSUP:
+        return "unsupported operation or configuration";
+    case BNN_ERANGE:
+        return "buffer or input range error";
+    case BNN_EBUSY:
+        return "device still owns resources";
+    case BNN_EIO:
+        return "device I/O error";
+    case BNN_ETIMEOUT:
+        return "device timeout";
+    default:
+        return "unknown status";
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Extensions (include/bnn-accelerator-hip.h); no reference counterpart.
+// ---------------------------------------------------------------------------
+
+EXPORT BNN_Status BNNX_DeviceStream(BNN_Device device, void** out_stream) {
+    if (device == nullptr || out_stream == nullptr)
+        return BNN_EINVAL;
+    *out_stream = device->stream;
+    return BNN_OK;
+}
+
+EXPORT BNN_Status BNNX_KernelTiming(BNN_Device device, int enable) {
+    if (device == nullptr)
+        return BNN_EINVAL;
+    device->timing = enable != 0;
+    device->ev_used = 0;
+    for (int i = 0; i < KK_COUNT; ++i) {
+        device->kernel_ms[i] = 0.0;
+        device->kernel_launches[i] = 0;
+    }
+    return BNN_OK;
+}
+
+EXPORT BNN_Status BNNX_KernelTimingRead(BNN_Device device, uint32_t kind, double* total_ms, uint64_t* launches) {
+    if (device == nullptr || kind >= (uint32_t)KK_COUNT)
+        return BNN_EINVAL;
+    if (total_ms)
+        *total_ms = device->kernel_ms[kind];
+    if (launches)
+        *launches = device->kernel_launches[kind];
+    return BNN_OK;
+}
+
+EXPORT BNN_Status BNNX_DeviceName(BNN_Device device, char* name, size_t name_bytes, char* arch, size_t arch_bytes) {
+    if (device == nullptr)
+        return BNN_EINVAL;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device->ordinal) != hipSuccess)
+        return BNN_EIO;
+    if (name && name_bytes) {
+        strncpy(name, prop.name, name_bytes - 1);
+        name[name_bytes - 1] = 0;
+    }
+    if (arch && arch_bytes) {
+        strncpy(arch, prop.gcnArchName, arch_bytes - 1);
+        arch[arch_bytes - 1] = 0;
+    }
+    return BNN_OK;
+}

@@ -1,0 +1,132 @@
+// Internal definitions shared by the HIP backend's host code and kernels.
+//
+// Device layout of a matrix (written once by BNN_MatrixCreate):
+//   tiles = ceil(N / 64); one tile = 64 output features, one per wave lane.
+//   wbits [tiles][groups][64] x 16 bytes : the 128 sign bits of (n = 64t + lane, group g),
+//                                          byte/bit order as the caller's row (bit k&7 of byte k>>3);
+//                                          a wave reading one (t, g) touches 1 KiB contiguously.
+//   wscale[tiles][groups][64] fp16 bits  : scale of (n, g); 128 contiguous bytes per (t, g).
+//   Features n >= N in the last tile are zero-filled and never stored.
+//
+// Quantised activation rows (written by the prep kernel into device scratch):
+//   planes[row][g][8][4] u32 : bit-plane j, word i, bit b = bit j of Q[g*128 + 32i + b]
+//                              (two's complement byte), i.e. 128 bytes per (row, group)
+//   sums  [row][g]  i32      : sum of Q over the group
+//   rscale[row]     f32      : row scale s (F32 operations)
+//   q     [row][K]  i8       : the quantised row itself (matrix-core path)
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "bnn-accelerator.h"
+
+namespace bnnhip {
+
+constexpr uint32_t kGroup = 128;       // weights per scale group (the only size offered)
+constexpr uint32_t kMaxFeatures = 8192;
+constexpr uint32_t kMaxGroups = kMaxFeatures / kGroup;
+constexpr uint32_t kTile = 64;         // output features per tile
+constexpr uint32_t kPlaneWords = 32;   // 8 planes x 4 words per (row, group)
+constexpr uint32_t kDotWaves = 4;      // waves per dot workgroup (they split the groups)
+
+enum KernelKind { KK_PREP = 0, KK_DOT = 1, KK_SCATTER = 2, KK_COUNT = 3 };
+
+// Output interpretation of the group-dot kernel.
+enum DotMode : int {
+    MODE_DOT_I16 = 0,   // store D as int16 [n][g]
+    MODE_SUM = 1,       // store Z = sum_g scale*D
+    MODE_SUM_SCALED = 2 // store Z * s
+};
+
+// One activation block for the prep kernel.  In a batch, block b of the prep
+// grid serves row (b - first_block) of the job found through the block table.
+struct PrepJob {
+    const unsigned char* in;  // logical row 0
+    uint64_t in_stride;       // bytes
+    uint32_t* planes;         // [rows][groups][32]
+    int32_t* sums;            // [rows][groups]
+    float* rscale;            // [rows]
+    int8_t* q;                // [rows][k] or null
+    uint32_t k;
+    uint32_t rows;
+    int32_t f32;              // F32 input (else I8)
+    int32_t aligned;          // F32 rows 4-byte aligned
+    uint32_t first_block;
+    uint32_t pad_;
+};
+
+// One group-dot job.  Block b serves (row, tile) = divmod(b - first_block, tiles).
+struct DotJob {
+    const uint4* wbits;
+    const uint16_t* wscale;
+    const uint32_t* planes;
+    const int32_t* sums;
+    const float* rscale;
+    unsigned char* out;       // logical row 0 (4-byte aligned for F32, 2 for I16)
+    uint64_t out_stride;
+    uint32_t n;
+    uint32_t groups;
+    uint32_t tiles;
+    uint32_t rows;
+    int32_t mode;
+    uint32_t first_block;
+};
+
+// Host-side launchers (bnn_kernels.hip).  All are asynchronous on `stream`.
+// Single job: descriptor passed by value.  `validate_only` runs only the
+// legality pass of prep (over all rows of a job processed in several chunks).
+hipError_t launch_prep(hipStream_t stream, const PrepJob& job, bool validate_only, uint64_t seq,
+                       uint64_t* flag, uint64_t* host_status);
+hipError_t launch_dot(hipStream_t stream, const DotJob& job, uint64_t seq, const uint64_t* flag);
+// Batch: device-resident job tables and block -> job maps (uint32 per block).
+hipError_t launch_prep_batch(hipStream_t stream, const PrepJob* jobs, const uint32_t* block_job,
+                             uint32_t blocks, uint64_t seq, uint64_t* flag, uint64_t* host_status);
+hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32_t* block_job,
+                            uint32_t blocks, uint64_t seq, const uint64_t* flag);
+hipError_t launch_scatter(hipStream_t stream, const unsigned char* src, size_t src_stride,
+                          unsigned char* dst, size_t dst_stride, size_t row_bytes, uint32_t rows,
+                          uint64_t seq, const uint64_t* flag);
+
+}  // namespace bnnhip
+
+struct bnn_accel_device {
+    int ordinal;
+    hipStream_t stream;
+    size_t live_matrices;
+    size_t live_buffers;
+    uint64_t seq;              // job sequence number, never 0 for a launched job
+    uint64_t* flag_dev;        // device word: seq of the last job that met an illegal input
+    uint64_t* status_host;     // pinned host word, same meaning, written by the kernels
+    unsigned char* scratch;    // grow-only device scratch
+    size_t scratch_bytes;
+    unsigned char* pinned;     // grow-only pinned host staging for transfers
+    size_t pinned_bytes;
+    unsigned char* table_host; // grow-only pinned staging for batch job tables
+    size_t table_host_bytes;
+    unsigned char* table_dev;  // grow-only device copy of the batch job tables
+    size_t table_dev_bytes;
+    // optional kernel timing (extension API): event pairs recorded around
+    // launches, resolved after the call's synchronisation
+    int timing;
+    static constexpr int kTimingSlots = 64;
+    hipEvent_t ev_begin[kTimingSlots], ev_end[kTimingSlots];
+    int ev_kind[kTimingSlots];
+    int ev_used;
+    double kernel_ms[bnnhip::KK_COUNT];
+    uint64_t kernel_launches[bnnhip::KK_COUNT];
+};
+
+struct bnn_accel_matrix {
+    BNN_Device device;
+    uint32_t k, n, groups, tiles;
+    uint4* wbits;
+    uint16_t* wscale;
+};
+
+struct bnn_accel_buffer {
+    BNN_Device device;
+    size_t size;
+    unsigned char* dev;
+};

@@ -1,0 +1,192 @@
+"""GPU parity of the HIP backend against the reference's fixtures and the CPU oracle.
+
+Every comparison is bit-exact (integer, I16 and F32 outputs alike): the kernels
+keep the reference's sequential per-group FP32 accumulation, so no tolerance is
+needed or allowed.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import json
+import subprocess
+
+import numpy as np
+import pytest
+
+from bnn_cases import CASES, case_inputs, fast_oracle, first_mismatch, input_sha, run_chunks, sha
+from conftest import GOLDEN, REF_DIR
+from test_oracle import _quant_rows, _rtl, sum_order_case
+
+pytestmark = pytest.mark.gpu
+FIXTURES = json.loads((GOLDEN / "soft_fixtures.json").read_text())
+
+
+def test_reference_contract_suite_on_hip(tmp_path):
+    """The reference's own API test (tests/accelerator/test_bnn_accelerator.c), unchanged,
+    linked against libbnn_hip.so: 453 jobs byte-compared with its independent scalar
+    oracle, every error path, view layout, ownership, busy and isolation rule."""
+    exe = REF_DIR / "test_ref_vs_hip"
+    assert exe.exists(), "oracle/_ref/test_ref_vs_hip missing (built by __graft_entry__.build())"
+    dump = tmp_path / "dump.bin"
+    print(f"running {exe}", flush=True)
+    r = subprocess.run([str(exe), str(dump)], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    assert "453 successful jobs" in r.stdout
+    want = json.loads((GOLDEN / "ref_suite.json").read_text())
+    data = dump.read_bytes()
+    assert len(data) == want["bytes"]
+    assert hashlib.sha256(data).hexdigest() == want["sha256"]
+
+
+def test_rtl_golden_case(pkg, hipdev):
+    case, got = _rtl(pkg, hipdev)
+    for name, out in got.items():
+        assert np.array_equal(out.view(np.uint32), case[name]), (name, first_mismatch(out.view(np.uint32), case[name]))
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_benchmark_shapes_match_soft_fixtures(pkg, hipdev, oracle_fast, case):
+    name, op, k, n, rows, seed = case
+    print(f"case {name}", flush=True)
+    rec = FIXTURES[name]
+    chunks, x = case_inputs(pkg, op, k, n, rows, seed)
+    assert input_sha(chunks, x) == rec["input_sha256"], "synthetic generator drifted"
+    out = run_chunks(pkg, hipdev, op, chunks, x)
+    if sha(out) != rec["output_sha256"]:
+        want = np.concatenate([fast_oracle(pkg, oracle_fast, op, b, s, x) for b, s in chunks], axis=1)
+        pytest.fail(f"{name}: {first_mismatch(out, want)}")
+    small = np.load(GOLDEN / "soft_small.npz")
+    if name in small.files:
+        assert np.array_equal(out.view(np.uint8), small[name].view(np.uint8))
+
+
+def test_every_finite_fp16_scale_converts_exactly(pkg, hipdev):
+    """GEMV with D = 1 returns F32(scale) (test_bnn_accelerator.c:473-491), for all 63488
+    finite binary16 patterns; -0 sums to +0."""
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    h = h[(h & 0x7C00) != 0x7C00]
+    x = np.zeros((1, 128), np.int8)
+    x[0, 0] = 1
+    got = []
+    for off in range(0, h.size, 8192):
+        hs = h[off:off + 8192]
+        bits = np.zeros((hs.size, 16), np.uint8)
+        bits[:, 0] = 1  # weight 0 is +1, the rest -1 but multiplied by zero activations
+        m = hipdev.matrix(bits, hs.reshape(-1, 1))
+        got.append(hipdev.run(pkg.Op.GEMV, m, x)[0])
+        m.destroy()
+    got = np.concatenate(got)
+    want = h.view(np.float16).astype(np.float32) + np.float32(0.0)  # -0 -> +0 like 0 + (-0)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), first_mismatch(got, want)
+
+
+def test_fp32_accumulation_order_and_no_fma(pkg, hipdev):
+    bits, scales, q, want = sum_order_case()
+    m = hipdev.matrix(bits, scales)
+    z = hipdev.run(pkg.Op.GEMM, m, q)
+    m.destroy()
+    assert z[0, 0] == want[0]
+    assert z[1, 1] == want[1]
+
+
+@pytest.mark.parametrize("i", range(10))
+def test_quantiser_edge_rows(pkg, hipdev, oracle, i):
+    x = _quant_rows()[i]
+    k = -(-x.size // 128) * 128
+    xr = np.zeros((1, k), np.float32)
+    xr[0, :x.size] = x
+    bits, scales = pkg.synth.matrix(70, k, seed=i)
+    got = run_chunks(pkg, hipdev, "GEMV_F32", [(bits, scales)], xr)
+    with pkg.Device(oracle, 0) as dev:
+        want = run_chunks(pkg, dev, "GEMV_F32", [(bits, scales)], xr)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), first_mismatch(got, want)
+
+
+@pytest.mark.parametrize("op", ["DOT_GROUPS", "GEMM", "GEMM_F32"])
+def test_row_chunking_and_late_illegal_row(pkg, hipdev, oracle_fast, op):
+    """More rows than one launch chunk: all rows are validated before any chunk writes."""
+    rows, k, n = 5000, 256, 67
+    bits, scales = pkg.synth.matrix(n, k, seed=21)
+    f32 = op.endswith("F32")
+    x = pkg.synth.normal_f32(rows, k, seed=21) if f32 else pkg.synth.int8_uniform(rows, k, seed=21)
+    got = run_chunks(pkg, hipdev, op, [(bits, scales)], x)
+    want = fast_oracle(pkg, oracle_fast, op, bits, scales, x)
+    assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), first_mismatch(got, want)
+
+    # illegal value in the last row: ERANGE and the output buffer untouched
+    bad = x.copy()
+    bad[-1, 200] = np.nan if f32 else -128
+    m = hipdev.matrix(bits, scales)
+    in_t, out_t = pkg.api.OP_TYPES[pkg.Op[op]]
+    bi, bo = hipdev.buffer(bad.nbytes), hipdev.buffer(got.nbytes)
+    sentinel = np.full(got.nbytes, 0x5A, np.uint8)
+    bi.write(bad)
+    bo.write(sentinel)
+    job = pkg.Job(int(pkg.Op[op]), m.handle.value, bi.view(in_t), bo.view(out_t), rows)
+    assert hipdev.execute(job) == pkg.Status.ERANGE
+    assert np.array_equal(bo.read(), sentinel)
+    # recovery on the same buffers
+    bi.write(x)
+    assert hipdev.execute(job) == pkg.Status.OK
+    assert np.array_equal(bo.read().view(got.dtype).reshape(got.shape).view(np.uint8), got.view(np.uint8))
+    bi.free()
+    bo.free()
+    m.destroy()
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_odd_views_random(pkg, hipdev, oracle, seed):
+    """Unaligned offsets and strides on both sides, padding never written."""
+    rng = np.random.default_rng(seed)
+    for op in ("DOT_GROUPS", "GEMM", "GEMM_F32", "GEMV", "GEMV_F32"):
+        k = int(rng.integers(1, 9)) * 128
+        n = int(rng.integers(1, 200))
+        rows = 1 if op.startswith("GEMV") else int(rng.integers(1, 6))
+        bits, scales = pkg.synth.matrix(n, k, seed=seed * 10 + 1)
+        in_t, out_t = pkg.api.OP_TYPES[pkg.Op[op]]
+        esz = 4 if in_t == pkg.Type.F32 else 1
+        in_row = k * esz
+        out_row = n * (k // 128) * 2 if op == "DOT_GROUPS" else n * 4
+        in_off, out_off = int(rng.integers(0, 9)), int(rng.integers(0, 9))
+        in_stride = in_row + int(rng.integers(0, 13))
+        out_stride = out_row + int(rng.integers(0, 13))
+        in_bytes = in_off + rows * in_stride + 5
+        out_bytes = out_off + rows * out_stride + 7
+        x = pkg.synth.normal_f32(rows, k, seed=seed) if esz == 4 else pkg.synth.int8_uniform(rows, k, seed=seed)
+        raw = np.full(in_bytes, 0xFF if esz == 4 else 0x80, np.uint8)  # NaN / -128 padding is legal
+        for r in range(rows):
+            raw[in_off + r * in_stride: in_off + r * in_stride + in_row] = x[r].view(np.uint8)
+        results = []
+        with pkg.Device(oracle, 0) as odev:
+            for dev in (hipdev, odev):
+                m = dev.matrix(bits, scales)
+                bi, bo = dev.buffer(in_bytes), dev.buffer(out_bytes)
+                bi.write(raw)
+                bo.write(np.full(out_bytes, 0xA5, np.uint8))
+                job = pkg.Job(int(pkg.Op[op]), m.handle.value, bi.view(in_t, in_off, in_stride),
+                              bo.view(out_t, out_off, out_stride), rows)
+                assert dev.execute(job) == pkg.Status.OK
+                results.append(bo.read())
+                assert np.array_equal(bi.read(), raw)  # input untouched
+                bi.free()
+                bo.free()
+                m.destroy()
+        assert np.array_equal(results[0], results[1]), (op, k, n, rows, in_off, in_stride, out_off, out_stride)
+
+
+def test_two_devices_are_isolated(pkg, hip):
+    a, b = pkg.Device(hip, 0), pkg.Device(hip, 0)
+    bits, scales = pkg.synth.matrix(10, 256, seed=3)
+    ma, mb = a.matrix(bits, scales), b.matrix(bits, scales)
+    bi = a.buffer(256)
+    bo = b.buffer(40)
+    job = pkg.Job(int(pkg.Op.GEMV), ma.handle.value, bi.view(pkg.Type.I8), bo.view(pkg.Type.F32), 1)
+    assert a.execute(job) == pkg.Status.EINVAL  # output buffer of another device
+    assert a.api.BNN_DeviceClose(a.handle) == pkg.Status.EBUSY
+    bi.free()
+    bo.free()
+    ma.destroy()
+    mb.destroy()
+    a.close()
+    b.close()
