@@ -60,6 +60,24 @@ def traffic_from_profiles():
     return None
 
 
+def copy_calibration(mib: int = 256) -> None:
+    """One device-to-device hipMemcpy of known size through the HIP runtime (no product
+    code): rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over this run gives the factors that
+    turn those counters into bytes."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    n = mib << 20
+    assert hip.hipMalloc(ctypes.byref(a), ctypes.c_size_t(n)) == 0
+    assert hip.hipMalloc(ctypes.byref(b), ctypes.c_size_t(n)) == 0
+    assert hip.hipMemset(a, 1, ctypes.c_size_t(n)) == 0
+    assert hip.hipMemcpy(b, a, ctypes.c_size_t(n), 3) == 0  # hipMemcpyDeviceToDevice
+    assert hip.hipDeviceSynchronize() == 0
+    hip.hipFree(a)
+    hip.hipFree(b)
+    print(f"copy calibration: {mib} MiB device-to-device", flush=True)
+
+
 def cpu_baseline(pkg, seconds: float = 12.0):
     """Bounded single-core sample of the same jobs on the host (checker-side code)."""
     ref = ROOT / "oracle" / "_ref" / "libbnn_soft_ref.so"
@@ -102,10 +120,15 @@ def cpu_baseline(pkg, seconds: float = 12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run one 256 MiB device-to-device copy (counter calibration)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print("bench.py: this build runs on exactly one GPU (the BNN_* path has no multi-GPU form here; "
               "see DESIGN.md for how it would shard).", file=sys.stderr)

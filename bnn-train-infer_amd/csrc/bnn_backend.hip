@@ -15,6 +15,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "bnn-accelerator-hip.h"
 #include "bnn-accelerator.h"
 #include "bnn_internal.h"
@@ -77,6 +79,7 @@ BNN_Status ensure_scratch(BNN_Device d, size_t bytes) {
     }
     d->scratch = static_cast<unsigned char*>(p);
     d->scratch_bytes = want;
+    d->generation++;
     return BNN_OK;
 }
 
@@ -192,6 +195,10 @@ EXPORT BNN_Status BNN_DeviceOpen(uint32_t device_index, BNN_Device* out_device) 
         return BNN_ENOMEM;
     d->ordinal = (int)device_index;
     hipError_t e = hipSetDevice(d->ordinal);
+    int cus = 0;
+    if (e == hipSuccess)
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, d->ordinal);
+    d->cu_count = cus > 0 ? (uint32_t)cus : 256u;
     if (e == hipSuccess)
         e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
     if (e == hipSuccess)
@@ -247,6 +254,7 @@ EXPORT BNN_Status BNN_DeviceClose(BNN_Device device) {
         (void)hipHostFree(device->table_host);
     if (device->table_dev)
         (void)hipFree(device->table_dev);
+    free(device->batch_jobs);
     for (int i = 0; i < bnn_accel_device::kTimingSlots; ++i) {
         (void)hipEventDestroy(device->ev_begin[i]);
         (void)hipEventDestroy(device->ev_end[i]);
@@ -365,6 +373,7 @@ EXPORT BNN_Status BNN_MatrixCreate(BNN_Device device, const BNN_MatrixDesc* desc
     m->wbits = static_cast<uint4*>(dev);
     m->wscale = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(dev) + wbits_bytes);
     device->live_matrices++;
+    device->generation++;
     *out_matrix = m;
     return BNN_OK;
 }
@@ -376,6 +385,7 @@ EXPORT void BNN_MatrixDestroy(BNN_Matrix matrix) {
     (void)hipStreamSynchronize(matrix->device->stream);
     (void)hipFree(matrix->wbits);
     matrix->device->live_matrices--;
+    matrix->device->generation++;
     free(matrix);
 }
 
@@ -407,6 +417,7 @@ EXPORT BNN_Status BNN_BufferAlloc(BNN_Device device, size_t bytes, BNN_Buffer* o
     b->size = bytes;
     b->dev = static_cast<unsigned char*>(p);
     device->live_buffers++;
+    device->generation++;
     *out_buffer = b;
     return BNN_OK;
 }
@@ -418,6 +429,7 @@ EXPORT void BNN_BufferFree(BNN_Buffer buffer) {
     (void)hipStreamSynchronize(buffer->device->stream);
     (void)hipFree(buffer->dev);
     buffer->device->live_buffers--;
+    buffer->device->generation++;
     free(buffer);
 }
 
@@ -632,7 +644,8 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
             break;
         const DotJob dj = p.out_aligned ? make_dot(p, pj, p.out_base + r0 * p.out_stride, p.out_stride)
                                         : make_dot(p, pj, staging, p.out_row);
-        e = timed(device, KK_DOT, [&] { return launch_dot(device->stream, dj, seq, device->flag_dev); });
+        e = timed(device, KK_DOT,
+                  [&] { return launch_dot(device->stream, dj, device->cu_count, seq, device->flag_dev); });
         if (e == hipSuccess && !p.out_aligned)
             e = timed(device, KK_SCATTER, [&] {
                 return launch_scatter(device->stream, staging, p.out_row, p.out_base + r0 * p.out_stride,
@@ -646,20 +659,67 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
 // Batch extension (include/bnn-accelerator-hip.h; no reference counterpart)
 // ---------------------------------------------------------------------------
 
+namespace {
+
+struct Extent {
+    const void* buffer;
+    size_t begin, end;
+};
+
+bool extent_less(const Extent& a, const Extent& b) {
+    return a.buffer != b.buffer ? (uintptr_t)a.buffer < (uintptr_t)b.buffer : a.begin < b.begin;
+}
+
+// Grow-only pinned + device memory for the batch job tables.
+BNN_Status ensure_tables(BNN_Device d, size_t bytes) {
+    if (bytes > d->table_dev_bytes) {
+        if (d->table_dev)
+            (void)hipFree(d->table_dev);
+        d->table_dev = nullptr;
+        d->table_dev_bytes = 0;
+        void* p = nullptr;
+        if (hipMalloc(&p, bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            return BNN_ENOMEM;
+        }
+        d->table_dev = static_cast<unsigned char*>(p);
+        d->table_dev_bytes = bytes;
+        d->generation++;
+    }
+    if (bytes > d->table_host_bytes) {
+        if (d->table_host)
+            (void)hipHostFree(d->table_host);
+        d->table_host = nullptr;
+        d->table_host_bytes = 0;
+        void* p = nullptr;
+        if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            return BNN_ENOMEM;
+        }
+        d->table_host = static_cast<unsigned char*>(p);
+        d->table_host_bytes = bytes;
+    }
+    return BNN_OK;
+}
+
+}  // namespace
+
 EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint32_t count) {
     if (device == nullptr || jobs == nullptr || count == 0)
         return BNN_EINVAL;
+    // An identical job array of the same resource generation reuses the tables
+    // already on the device; every job is still checked as BNN_Execute checks it.
+    const bool cached = device->batch_jobs != nullptr && device->batch_count == count &&
+                        device->batch_generation == device->generation &&
+                        memcmp(device->batch_jobs, jobs, sizeof(BNN_Job) * count) == 0;
     JobPlan* plans = static_cast<JobPlan*>(malloc(sizeof(JobPlan) * count));
-    if (plans == nullptr)
-        return BNN_ENOMEM;
-    struct Extent {
-        const void* buffer;
-        size_t begin, end;
-    };
-    Extent* outs = static_cast<Extent*>(malloc(sizeof(Extent) * count));
-    BNN_Status st = outs ? BNN_OK : BNN_ENOMEM;
-    uint64_t prep_blocks = 0, dot_blocks = 0;
+    Extent* outs = cached ? nullptr : static_cast<Extent*>(malloc(sizeof(Extent) * count));
+    const void** ins = cached ? nullptr : static_cast<const void**>(malloc(sizeof(void*) * count));
+    BNN_Status st = plans && (cached || (outs && ins)) ? BNN_OK : BNN_ENOMEM;
+    uint64_t prep_blocks = 0, dot_items = 0;
     size_t scratch_bytes = 0;
+    uint32_t max_groups = 0;
+    bool uniform = true;
     for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
         st = plan_job(device, &jobs[i], &plans[i]);
         if (st != BNN_OK)
@@ -669,110 +729,135 @@ EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint
             st = BNN_ENOTSUP;
             break;
         }
+        if (cached)
+            continue;
         size_t a, b, c;
         scratch_bytes += row_scratch_bytes(p, jobs[i].rows, &a, &b, &c);
         prep_blocks += jobs[i].rows;
-        dot_blocks += (uint64_t)jobs[i].rows * p.m->tiles;
+        const uint64_t items = (uint64_t)jobs[i].rows * p.m->tiles;
+        uniform = uniform && items == (uint64_t)jobs[0].rows * plans[0].m->tiles;
+        dot_items += items;
+        max_groups = p.m->groups > max_groups ? p.m->groups : max_groups;
         outs[i].buffer = jobs[i].output.buffer;
         outs[i].begin = jobs[i].output.offset;
         outs[i].end = jobs[i].output.offset + (size_t)(jobs[i].rows - 1) * p.out_stride + p.out_row;
+        ins[i] = jobs[i].input.buffer;
     }
-    // jobs run concurrently: no output may alias any input buffer or another output
-    for (uint32_t i = 0; st == BNN_OK && i < count; ++i)
-        for (uint32_t j = 0; st == BNN_OK && j < count; ++j) {
-            if (jobs[i].output.buffer == jobs[j].input.buffer)
+    // the jobs run concurrently: no output buffer may be an input buffer, and
+    // outputs sharing a buffer may not overlap
+    if (st == BNN_OK && !cached) {
+        std::sort(ins, ins + count);
+        std::sort(outs, outs + count, extent_less);
+        for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
+            if (std::binary_search(ins, ins + count, outs[i].buffer))
                 st = BNN_EINVAL;
-            else if (i < j && outs[i].buffer == outs[j].buffer && outs[i].begin < outs[j].end &&
-                     outs[j].begin < outs[i].end)
+            else if (i > 0 && outs[i].buffer == outs[i - 1].buffer && outs[i].begin < outs[i - 1].end)
                 st = BNN_EINVAL;
         }
-    if (st == BNN_OK && (prep_blocks > 0x7fffffffu || dot_blocks > 0x7fffffffu))
-        st = BNN_ENOTSUP;
-    if (st != BNN_OK) {
-        free(plans);
-        free(outs);
-        return st;
+        if (st == BNN_OK && (prep_blocks > 0x7fffffffu || dot_items > 0x7fffffffu))
+            st = BNN_ENOTSUP;
     }
     free(outs);
-
-    // tables: PrepJob[count] | DotJob[count] | prep block->job | dot block->job
-    const size_t prep_tab = round_up(sizeof(PrepJob) * count, 256);
-    const size_t dot_tab = round_up(sizeof(DotJob) * count, 256);
-    const size_t prep_map = round_up(4u * prep_blocks, 256);
-    const size_t dot_map = round_up(4u * dot_blocks, 256);
-    const size_t tables = prep_tab + dot_tab + prep_map + dot_map;
-    hipError_t e = hipSetDevice(device->ordinal);
-    if (e != hipSuccess) {
+    free(ins);
+    if (st != BNN_OK) {
+        free(plans);
+        return st;
+    }
+    if (hipSetDevice(device->ordinal) != hipSuccess) {
         free(plans);
         return BNN_EIO;
     }
-    st = ensure_scratch(device, scratch_bytes);
-    if (st == BNN_OK && tables > device->table_dev_bytes) {
-        if (device->table_dev)
-            (void)hipFree(device->table_dev);
-        device->table_dev = nullptr;
-        device->table_dev_bytes = 0;
-        void* p = nullptr;
-        if (hipMalloc(&p, tables) != hipSuccess) {
-            (void)hipGetLastError();
-            st = BNN_ENOMEM;
-        } else {
-            device->table_dev = static_cast<unsigned char*>(p);
-            device->table_dev_bytes = tables;
+
+    if (!cached) {
+        // tables: PrepJob[count] | DotJob[count] | prep block->job | dot item->job (non-uniform only)
+        const size_t prep_tab = round_up(sizeof(PrepJob) * count, 256);
+        const size_t dot_tab = round_up(sizeof(DotJob) * count, 256);
+        const size_t prep_map = round_up(4u * prep_blocks, 256);
+        const size_t dot_map = uniform ? 0 : round_up(4u * dot_items, 256);
+        const size_t tables = prep_tab + dot_tab + prep_map + dot_map;
+        st = ensure_scratch(device, scratch_bytes);
+        if (st == BNN_OK)
+            st = ensure_tables(device, tables);
+        if (st == BNN_OK && count > device->batch_cap) {
+            BNN_Job* copy = static_cast<BNN_Job*>(realloc(device->batch_jobs, sizeof(BNN_Job) * count));
+            if (copy == nullptr) {
+                st = BNN_ENOMEM;
+            } else {
+                device->batch_jobs = copy;
+                device->batch_cap = count;
+            }
         }
-    }
-    if (st == BNN_OK && tables > device->table_host_bytes) {
-        if (device->table_host)
-            (void)hipHostFree(device->table_host);
-        device->table_host = nullptr;
-        device->table_host_bytes = 0;
-        void* p = nullptr;
-        if (hipHostMalloc(&p, tables, hipHostMallocDefault) != hipSuccess) {
-            (void)hipGetLastError();
-            st = BNN_ENOMEM;
-        } else {
-            device->table_host = static_cast<unsigned char*>(p);
-            device->table_host_bytes = tables;
+        if (st != BNN_OK) {
+            device->batch_count = 0;
+            free(plans);
+            return st;
         }
-    }
-    if (st != BNN_OK) {
-        free(plans);
-        return st;
-    }
-    PrepJob* hp = reinterpret_cast<PrepJob*>(device->table_host);
-    DotJob* hd = reinterpret_cast<DotJob*>(device->table_host + prep_tab);
-    uint32_t* hpm = reinterpret_cast<uint32_t*>(device->table_host + prep_tab + dot_tab);
-    uint32_t* hdm = reinterpret_cast<uint32_t*>(device->table_host + prep_tab + dot_tab + prep_map);
-    size_t soff = 0;
-    uint32_t pb = 0, db = 0;
-    for (uint32_t i = 0; i < count; ++i) {
-        const JobPlan& p = plans[i];
-        const uint32_t rows = jobs[i].rows;
-        size_t a, b, c;
-        hp[i] = make_prep(p, p.in_base, rows, device->scratch + soff);
-        hp[i].first_block = pb;
-        soff += row_scratch_bytes(p, rows, &a, &b, &c);
-        hd[i] = make_dot(p, hp[i], p.out_base, p.out_stride);
-        hd[i].first_block = db;
-        for (uint32_t r = 0; r < rows; ++r)
-            hpm[pb++] = i;
-        for (uint32_t r = 0; r < rows * p.m->tiles; ++r)
-            hdm[db++] = i;
+        PrepJob* hp = reinterpret_cast<PrepJob*>(device->table_host);
+        DotJob* hd = reinterpret_cast<DotJob*>(device->table_host + prep_tab);
+        uint32_t* hpm = reinterpret_cast<uint32_t*>(device->table_host + prep_tab + dot_tab);
+        uint32_t* hdm = reinterpret_cast<uint32_t*>(device->table_host + prep_tab + dot_tab + prep_map);
+        size_t soff = 0;
+        uint32_t pb = 0, di = 0;
+        for (uint32_t i = 0; i < count; ++i) {
+            const JobPlan& p = plans[i];
+            const uint32_t rows = jobs[i].rows;
+            size_t a, b, c;
+            hp[i] = make_prep(p, p.in_base, rows, device->scratch + soff);
+            hp[i].first_block = pb;
+            soff += row_scratch_bytes(p, rows, &a, &b, &c);
+            hd[i] = make_dot(p, hp[i], p.out_base, p.out_stride);
+            hd[i].first_block = di;
+            for (uint32_t r = 0; r < rows; ++r)
+                hpm[pb++] = i;
+            const uint32_t items = rows * p.m->tiles;
+            if (!uniform)
+                for (uint32_t r = 0; r < items; ++r)
+                    hdm[di + r] = i;
+            di += items;
+        }
+        hipError_t e =
+            hipMemcpyAsync(device->table_dev, device->table_host, tables, hipMemcpyHostToDevice, device->stream);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            device->batch_count = 0;
+            free(plans);
+            return BNN_EIO;
+        }
+        memcpy(device->batch_jobs, jobs, sizeof(BNN_Job) * count);
+        device->batch_count = count;
+        device->batch_generation = device->generation;
+        device->batch_prep_blocks = pb;
+        device->batch_items = di;
+        device->batch_uniform_items = uniform ? jobs[0].rows * plans[0].m->tiles : 0u;
+        device->batch_max_groups = max_groups;
+        device->batch_prep_tab = prep_tab;
+        device->batch_dot_tab = dot_tab;
+        device->batch_prep_map = prep_map;
+        device->batch_tables = tables;
     }
     free(plans);
 
     const PrepJob* dp = reinterpret_cast<const PrepJob*>(device->table_dev);
-    const DotJob* dd = reinterpret_cast<const DotJob*>(device->table_dev + prep_tab);
-    const uint32_t* dpm = reinterpret_cast<const uint32_t*>(device->table_dev + prep_tab + dot_tab);
-    const uint32_t* ddm = reinterpret_cast<const uint32_t*>(device->table_dev + prep_tab + dot_tab + prep_map);
+    const DotJob* dd = reinterpret_cast<const DotJob*>(device->table_dev + device->batch_prep_tab);
+    const uint32_t* dpm =
+        reinterpret_cast<const uint32_t*>(device->table_dev + device->batch_prep_tab + device->batch_dot_tab);
+    const uint32_t* ddm =
+        device->batch_uniform_items
+            ? nullptr
+            : reinterpret_cast<const uint32_t*>(device->table_dev + device->batch_prep_tab + device->batch_dot_tab +
+                                                device->batch_prep_map);
     const uint64_t seq = ++device->seq;
-    e = hipMemcpyAsync(device->table_dev, device->table_host, tables, hipMemcpyHostToDevice, device->stream);
+    hipError_t e = timed(device, KK_PREP, [&] {
+        return launch_prep_batch(device->stream, dp, dpm, device->batch_prep_blocks, seq, device->flag_dev,
+                                 device->status_host);
+    });
     if (e == hipSuccess)
-        e = timed(device, KK_PREP, [&] {
-            return launch_prep_batch(device->stream, dp, dpm, pb, seq, device->flag_dev, device->status_host);
+        e = timed(device, KK_DOT, [&] {
+            return launch_dot_batch(device->stream, dd, ddm, device->batch_items, device->batch_uniform_items,
+                                    device->batch_max_groups, device->cu_count, seq, device->flag_dev);
         });
-    if (e == hipSuccess)
-        e = timed(device, KK_DOT, [&] { return launch_dot_batch(device->stream, dd, ddm, db, seq, device->flag_dev); });
+    if (e != hipSuccess)
+        device->batch_count = 0;
     return finish(device, e, seq);
 }
 

@@ -30,6 +30,15 @@ constexpr uint32_t kMaxGroups = kMaxFeatures / kGroup;
 constexpr uint32_t kTile = 64;         // output features per tile
 constexpr uint32_t kPlaneWords = 32;   // 8 planes x 4 words per (row, group)
 constexpr uint32_t kDotWaves = 4;      // waves per dot workgroup (they split the groups)
+// Persistent dot workgroups per CU (tuning constants; overridable at build time).
+#ifndef BNN_DOT_WGS_PER_CU_SMALL
+#define BNN_DOT_WGS_PER_CU_SMALL 7  // K <= 2048: 71 VGPRs -> 7 waves per SIMD
+#endif
+#ifndef BNN_DOT_WGS_PER_CU_LARGE
+#define BNN_DOT_WGS_PER_CU_LARGE 2  // K > 2048
+#endif
+constexpr uint32_t kDotWgsPerCuSmall = BNN_DOT_WGS_PER_CU_SMALL;
+constexpr uint32_t kDotWgsPerCuLarge = BNN_DOT_WGS_PER_CU_LARGE;
 
 enum KernelKind { KK_PREP = 0, KK_DOT = 1, KK_SCATTER = 2, KK_COUNT = 3 };
 
@@ -57,7 +66,8 @@ struct PrepJob {
     uint32_t pad_;
 };
 
-// One group-dot job.  Block b serves (row, tile) = divmod(b - first_block, tiles).
+// One group-dot job.  Work item i of the job is (row, tile) = divmod(i, tiles);
+// in a table-mapped batch the job's items start at first_block.
 struct DotJob {
     const uint4* wbits;
     const uint16_t* wscale;
@@ -79,12 +89,16 @@ struct DotJob {
 // legality pass of prep (over all rows of a job processed in several chunks).
 hipError_t launch_prep(hipStream_t stream, const PrepJob& job, bool validate_only, uint64_t seq,
                        uint64_t* flag, uint64_t* host_status);
-hipError_t launch_dot(hipStream_t stream, const DotJob& job, uint64_t seq, const uint64_t* flag);
-// Batch: device-resident job tables and block -> job maps (uint32 per block).
+hipError_t launch_dot(hipStream_t stream, const DotJob& job, uint32_t cu_count, uint64_t seq,
+                      const uint64_t* flag);
+// Batch: device-resident job tables.  Prep: one block per row, block -> job map.
+// Dot: items = sum of rows*tiles; job of an item = item / uniform_items when every
+// job has that many items, else item_job[item].
 hipError_t launch_prep_batch(hipStream_t stream, const PrepJob* jobs, const uint32_t* block_job,
                              uint32_t blocks, uint64_t seq, uint64_t* flag, uint64_t* host_status);
-hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32_t* block_job,
-                            uint32_t blocks, uint64_t seq, const uint64_t* flag);
+hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32_t* item_job, uint32_t items,
+                            uint32_t uniform_items, uint32_t max_groups, uint32_t cu_count, uint64_t seq,
+                            const uint64_t* flag);
 hipError_t launch_scatter(hipStream_t stream, const unsigned char* src, size_t src_stride,
                           unsigned char* dst, size_t dst_stride, size_t row_bytes, uint32_t rows,
                           uint64_t seq, const uint64_t* flag);
@@ -93,6 +107,7 @@ hipError_t launch_scatter(hipStream_t stream, const unsigned char* src, size_t s
 
 struct bnn_accel_device {
     int ordinal;
+    uint32_t cu_count;
     hipStream_t stream;
     size_t live_matrices;
     size_t live_buffers;
@@ -107,6 +122,16 @@ struct bnn_accel_device {
     size_t table_host_bytes;
     unsigned char* table_dev;  // grow-only device copy of the batch job tables
     size_t table_dev_bytes;
+    // Resource generation: bumped by every matrix/buffer create or destroy and by
+    // every scratch reallocation, i.e. whenever a device pointer could change.
+    uint64_t generation;
+    // The last batch whose tables sit in table_dev (reused for an identical batch
+    // of the same generation).
+    BNN_Job* batch_jobs;
+    uint32_t batch_count, batch_cap;
+    uint64_t batch_generation;
+    uint32_t batch_prep_blocks, batch_items, batch_uniform_items, batch_max_groups;
+    size_t batch_prep_tab, batch_dot_tab, batch_prep_map, batch_tables;
     // optional kernel timing (extension API): event pairs recorded around
     // launches, resolved after the call's synchronisation
     int timing;

@@ -30,9 +30,22 @@ namespace bnnhip {
 namespace {
 
 constexpr int kLdsPitch = 65;                     // words per group row of the D/term exchange
-constexpr int kMaxGroupsPerWave = kMaxGroups / kDotWaves;
 
 __device__ __forceinline__ float f32_min_subnormal() { return __int_as_float(1); }
+
+// Pointers taken from job descriptors are generic; loading through these
+// global-address-space views makes the compiler emit global_load, not flat_load.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 gload(const uint4* p) {
+    const u32x4 v = *(const __attribute__((address_space(1))) u32x4*)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint32_t gload(const uint16_t* p) {
+    return *(const __attribute__((address_space(1))) uint16_t*)p;
+}
+__device__ __forceinline__ int gload(const int32_t* p) {
+    return *(const __attribute__((address_space(1))) int32_t*)p;
+}
 
 __device__ __forceinline__ float load_f32(const unsigned char* row, uint32_t k, bool aligned) {
     if (aligned)
@@ -42,18 +55,12 @@ __device__ __forceinline__ float load_f32(const unsigned char* row, uint32_t k, 
     return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-        v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
+extern "C" __device__ uint32_t __ockl_wfred_max_u32(uint32_t);
 
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-        v += __shfl_xor(v, off);
-    return v;
+// Max over the wave of non-negative finite floats: their bit patterns order
+// like the values, so the DPP-based unsigned wave reduction applies.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    return __uint_as_float(__ockl_wfred_max_u32(__float_as_uint(v)));
 }
 
 // Q = clamp(round-half-away(F32(x / s)), -127, 127)  (soft-bnn-accelerator.c:197-208)
@@ -74,26 +81,39 @@ __device__ __forceinline__ void raise_flag(uint64_t seq, uint64_t* flag, uint64_
 // prep: one workgroup (256 threads) per activation row.  Checks the logical row
 // (-128 for I8, NaN/Inf for F32: soft-bnn-accelerator.c:278-308), derives the
 // row scale, quantises, and writes bit planes, group sums and (optionally) Q.
+// Thread t owns elements k = t + 256 i; all its loads are issued before any use.
 // ---------------------------------------------------------------------------
+constexpr int kPrepPerThread = kMaxFeatures / 256;  // 32
+
 __device__ void prep_row(const PrepJob& j, uint32_t m, bool validate_only, uint64_t seq, uint64_t* flag,
                          uint64_t* host_status) {
     __shared__ float red_max[4];
-    __shared__ int red_sum[4];
+    __shared__ int red_sum[kPrepPerThread][4];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t k_total = j.k, groups = k_total / kGroup;
+    const uint32_t iters = (k_total + 255u) / 256u;
     const bool f32 = j.f32 != 0, aligned = j.aligned != 0;
     const unsigned char* row = j.in + (size_t)m * j.in_stride;
 
-    // pass 1: legality and absmax over the whole logical row
+    // pass 1: load the whole logical row (registers), legality and absmax
+    int raw[kPrepPerThread];  // float bits (F32) or the sign-extended byte (I8)
+#pragma unroll
+    for (int i = 0; i < kPrepPerThread; ++i) {
+        const uint32_t k = tid + 256u * i;
+        raw[i] = 0;
+        if ((uint32_t)i < iters && k < k_total)
+            raw[i] = f32 ? __float_as_int(load_f32(row, k, aligned)) : (int)(int8_t)row[k];
+    }
     float amax = 0.0f;
     int bad = 0;
-    for (uint32_t k = tid; k < k_total; k += 256u) {
+#pragma unroll
+    for (int i = 0; i < kPrepPerThread; ++i) {
         if (f32) {
-            float v = load_f32(row, k, aligned);
+            const float v = __int_as_float(raw[i]);
             bad |= !__builtin_isfinite(v);
             amax = fmaxf(amax, fabsf(v));
         } else {
-            bad |= ((int8_t)row[k] == -128);
+            bad |= (raw[i] == -128);
         }
     }
     if (__syncthreads_or(bad)) {
@@ -106,7 +126,7 @@ __device__ void prep_row(const PrepJob& j, uint32_t m, bool validate_only, uint6
 
     float s = 1.0f;
     if (f32) {
-        amax = wave_max(amax);
+        amax = wave_max_nonneg(amax);
         if (lane == 0)
             red_max[wave] = amax;
         __syncthreads();
@@ -118,38 +138,40 @@ __device__ void prep_row(const PrepJob& j, uint32_t m, bool validate_only, uint6
         }
     }
 
-    // pass 2: quantise; each wave owns 64 consecutive k = one half group
+    // pass 2: quantise; in iteration i wave w owns the 64 consecutive k of half (w & 1)
+    // of group 2i + (w >> 1)
     uint32_t* planes = j.planes + (size_t)m * groups * kPlaneWords;
-    for (uint32_t base = 0; base < k_total; base += 256u) {
-        const uint32_t k = base + tid;
-        const bool wave_live = base + wave * 64u < k_total;  // K % 128 == 0: whole waves
-        if (wave_live) {
-            const int q = f32 ? quantize(load_f32(row, k, aligned), s) : (int)(int8_t)row[k];
+#pragma unroll
+    for (int i = 0; i < kPrepPerThread; ++i) {
+        const uint32_t base = 256u * i;
+        if ((uint32_t)i < iters && base + wave * 64u < k_total) {  // K % 128 == 0: whole waves
+            const int q = f32 ? quantize(__int_as_float(raw[i]), s) : raw[i];
             if (j.q)
-                j.q[(size_t)m * k_total + k] = (int8_t)q;
+                j.q[(size_t)m * k_total + base + tid] = (int8_t)q;
+            // bit planes of these 64 values; the wave's sum follows from the same
+            // masks: sum q = sum_{b<7} 2^b popc(M_b) - 2^7 popc(M_7)  (scalar ops)
             uint32_t word = 0;
+            int part = 0;
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
                 const unsigned long long mask = __ballot((q >> b) & 1);
+                const int cnt = __popcll(mask);
+                part += b == 7 ? -(cnt << 7) : (cnt << b);
                 if (lane == 2u * b)
                     word = (uint32_t)mask;
                 if (lane == 2u * b + 1u)
                     word = (uint32_t)(mask >> 32);
             }
-            const uint32_t g = (base >> 7) + (wave >> 1), half = wave & 1u;
+            const uint32_t g = 2u * i + (wave >> 1), half = wave & 1u;
             if (lane < 16u)
                 planes[g * kPlaneWords + (lane >> 1) * 4u + half * 2u + (lane & 1u)] = word;
-            const int part = wave_sum(q);
             if (lane == 0)
-                red_sum[wave] = part;
+                red_sum[i][wave] = part;
         }
-        __syncthreads();
-        if (tid == 0)
-            j.sums[(size_t)m * groups + (base >> 7)] = red_sum[0] + red_sum[1];
-        if (tid == 128 && base + 128u < k_total)
-            j.sums[(size_t)m * groups + (base >> 7) + 1u] = red_sum[2] + red_sum[3];
-        __syncthreads();
     }
+    __syncthreads();
+    if (tid < groups)
+        j.sums[(size_t)m * groups + tid] = red_sum[tid >> 1][(tid & 1u) * 2u] + red_sum[tid >> 1][(tid & 1u) * 2u + 1u];
     if (tid == 0)
         j.rscale[m] = s;
 }
@@ -166,107 +188,217 @@ __global__ __launch_bounds__(256) void k_prep(PrepJob single, const PrepJob* __r
     }
 }
 
-// Positive-bit sum of one group: weights w (128 bits), activation planes p[32].
-__device__ __forceinline__ int group_pos(uint4 w, const uint32_t* p) {
-    int pos = 0;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-        const int c = __popc(w.x & p[4 * b + 0]) + __popc(w.y & p[4 * b + 1]) + __popc(w.z & p[4 * b + 2]) +
-                      __popc(w.w & p[4 * b + 3]);
-        pos += (b == 7) ? -(c << 7) : (c << b);
-    }
-    return pos;
+// D of one group from its weights w (128 bits) and activation planes p[32]:
+//   D = 2*pos - sum = sum_{b<7} 2^(b+1) c_b - 2^8 c_7 - sum,  c_b = popc(w & P_b)
+// Each c_b is one accumulating BCNT chain, so a group costs 32 AND + 32 BCNT +
+// 8 shift-adds.
+// popc(x) + acc in one VALU op.  Written as asm because the compiler otherwise
+// re-associates the chain into ADD3 trees (11 instead of 9 ops per plane).
+__device__ __forceinline__ uint32_t bcnt_acc(uint32_t x, uint32_t acc) {
+    uint32_t r;
+    asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));
+    return r;
+}
+
+// (c << SHIFT) + acc in one VALU op, kept fused for the same reason.
+template <int SHIFT>
+__device__ __forceinline__ uint32_t lshl_add(uint32_t c, uint32_t acc) {
+    uint32_t r;
+    asm("v_lshl_add_u32 %0, %1, %2, %3" : "=v"(r) : "v"(c), "i"(SHIFT), "v"(acc));
+    return r;
+}
+
+template <int B>
+__device__ __forceinline__ uint32_t plane_count(uint4 w, const uint32_t* p) {
+    uint32_t c = (uint32_t)__builtin_popcount(w.x & p[4 * B + 0]);
+    c = bcnt_acc(w.y & p[4 * B + 1], c);
+    c = bcnt_acc(w.z & p[4 * B + 2], c);
+    return bcnt_acc(w.w & p[4 * B + 3], c);
+}
+
+__device__ __forceinline__ int group_dot(uint4 w, const uint32_t* p, int neg_sum) {
+    uint32_t d = (uint32_t)neg_sum;  // two's complement arithmetic, exact result in [-16256, 16256]
+    d = lshl_add<1>(plane_count<0>(w, p), d);
+    d = lshl_add<2>(plane_count<1>(w, p), d);
+    d = lshl_add<3>(plane_count<2>(w, p), d);
+    d = lshl_add<4>(plane_count<3>(w, p), d);
+    d = lshl_add<5>(plane_count<4>(w, p), d);
+    d = lshl_add<6>(plane_count<5>(w, p), d);
+    d = lshl_add<7>(plane_count<6>(w, p), d);
+    d -= plane_count<7>(w, p) << 8;  // the sign plane weighs -2^7, doubled
+    return (int)d;
 }
 
 // ---------------------------------------------------------------------------
-// dot: one workgroup of 4 waves per (row, tile of 64 features).  Wave w owns a
-// contiguous run of groups, issues all its weight and scale loads first, then
-// computes D (and the rounded product) per group; lane = feature.  The row's
-// bit planes are staged once in LDS.  Wave 0 then adds the products in group
-// order (F32 modes) or the workgroup stores D as int16 (DOT_GROUPS).
+// dot: persistent workgroups of 4 waves; one work item = (job, row, tile of 64
+// features).  Wave w owns a contiguous run of the groups; lane = feature.  While
+// item i is computed, the loads of item i + gridDim.x (job descriptor, weights,
+// scales, the row's bit planes and group sums) are already in flight in a
+// second register set.  D and the rounded products go through double-buffered
+// LDS so that wave 0 can add the products in group order (F32 modes) or the
+// workgroup can store D as int16 (DOT_GROUPS).
+// MAXG bounds the groups per matrix (16 for K <= 2048, else 64).
 // ---------------------------------------------------------------------------
-__device__ void dot_tile(const DotJob& j, uint32_t local) {
-    __shared__ uint4 lds_planes[kMaxGroups * kPlaneWords / 4];
-    __shared__ int lds_sums[kMaxGroups];
-    __shared__ int lds_x[kMaxGroups * kLdsPitch];  // D (int) or product (float bits)
+enum ItemMap : int { MAP_SINGLE = 0, MAP_UNIFORM = 1, MAP_TABLE = 2 };
+
+template <int MAXG>
+struct DotRegs {
+    static constexpr int kGpw = MAXG / (int)kDotWaves;
+    static constexpr int kPlaneChunks = (MAXG * 8 + 255) / 256;  // uint4 of planes per thread
+    uint4 w[kGpw];
+    uint32_t sc[kGpw];
+    uint4 pl[kPlaneChunks];
+    int sum;
+};
+
+struct DotItem {
+    DotJob j;
+    uint32_t row, t;
+};
+
+template <int MAP>
+__device__ __forceinline__ void locate(uint32_t item, const DotJob& single, const DotJob* __restrict__ jobs,
+                                       const uint32_t* __restrict__ item_job, uint32_t uniform_items, DotItem& it) {
+    uint32_t local;
+    if (MAP == MAP_SINGLE) {
+        it.j = single;
+        local = item;
+    } else if (MAP == MAP_UNIFORM) {
+        const uint32_t ji = item / uniform_items;
+        it.j = jobs[ji];
+        local = item - ji * uniform_items;
+    } else {
+        it.j = jobs[item_job[item]];
+        local = item - it.j.first_block;
+    }
+    it.row = local / it.j.tiles;
+    it.t = local - it.row * it.j.tiles;
+}
+
+template <int MAXG>
+__device__ __forceinline__ void issue(const DotItem& it, uint32_t wave, uint32_t lane, uint32_t tid,
+                                      DotRegs<MAXG>& r) {
+    const uint32_t groups = it.j.groups;
+    const uint32_t gpw = (groups + kDotWaves - 1u) / kDotWaves;
+    const uint32_t g0 = wave * gpw;
+    const uint32_t gcount = g0 < groups ? min(groups - g0, gpw) : 0u;
+    const size_t first = ((size_t)it.t * groups + g0) * kTile + lane;
+    const uint4* wb = it.j.wbits + first;
+    const uint16_t* ws = it.j.wscale + first;
+    const bool sum_mode = it.j.mode != MODE_DOT_I16;
+#pragma unroll
+    for (int i = 0; i < DotRegs<MAXG>::kGpw; ++i) {
+        if ((uint32_t)i < gcount) {
+            r.w[i] = gload(wb + i * kTile);
+            r.sc[i] = sum_mode ? gload(ws + i * kTile) : 0u;
+        }
+    }
+    const uint4* pl = reinterpret_cast<const uint4*>(it.j.planes + (size_t)it.row * groups * kPlaneWords);
+#pragma unroll
+    for (int c = 0; c < DotRegs<MAXG>::kPlaneChunks; ++c) {
+        const uint32_t idx = tid + 256u * c;
+        if (idx < groups * (kPlaneWords / 4u))
+            r.pl[c] = gload(pl + idx);
+    }
+    if (tid < groups)
+        r.sum = gload(it.j.sums + (size_t)it.row * groups + tid);
+}
+
+template <int MAXG, int MAP>
+__global__ __launch_bounds__(64 * kDotWaves) void k_dot(DotJob single, const DotJob* __restrict__ jobs,
+                                                        const uint32_t* __restrict__ item_job, uint32_t items,
+                                                        uint32_t uniform_items, uint64_t seq,
+                                                        const uint64_t* __restrict__ flag) {
+    __shared__ uint4 lds_planes[2][MAXG * kPlaneWords / 4];
+    __shared__ int lds_negsum[2][MAXG];
+    __shared__ int lds_x[2][MAXG * kLdsPitch];  // D (int) or rounded product (float bits)
+    if (*flag == seq)
+        return;  // an illegal input row in this job (batch): write nothing
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t groups = j.groups;
-    const uint32_t row = local / j.tiles, t = local - row * j.tiles;
-    const uint32_t gpw = (groups + kDotWaves - 1u) / kDotWaves;
-    const uint32_t g0 = wave * gpw;
-    const uint32_t gcount = g0 < groups ? (groups - g0 < gpw ? groups - g0 : gpw) : 0u;
-    const bool sum_mode = j.mode != MODE_DOT_I16;
-
-    // 1. issue this wave's weight and scale loads (up to 16 groups)
-    uint4 w[kMaxGroupsPerWave];
-    uint16_t sc[kMaxGroupsPerWave];
-    const size_t tile_base = (size_t)t * groups;
+    uint32_t item = blockIdx.x;
+    if (item >= items)
+        return;
+    DotItem cur, nxt;
+    DotRegs<MAXG> rc, rn;
+    locate<MAP>(item, single, jobs, item_job, uniform_items, cur);
+    issue<MAXG>(cur, wave, lane, tid, rc);
+    int buf = 0;
+    for (;;) {
+        const uint32_t groups = cur.j.groups;
+        // stage this item's planes and group sums
 #pragma unroll
-    for (uint32_t i = 0; i < (uint32_t)kMaxGroupsPerWave; ++i) {
-        if (i < gcount) {
-            w[i] = j.wbits[(tile_base + g0 + i) * kTile + lane];
-            sc[i] = sum_mode ? j.wscale[(tile_base + g0 + i) * kTile + lane] : (uint16_t)0;
+        for (int c = 0; c < DotRegs<MAXG>::kPlaneChunks; ++c) {
+            const uint32_t idx = tid + 256u * c;
+            if (idx < groups * (kPlaneWords / 4u))
+                lds_planes[buf][idx] = rc.pl[c];
         }
-    }
-    // 2. stage the row's planes and group sums in LDS (coalesced, shared by all waves)
-    const uint4* src = reinterpret_cast<const uint4*>(j.planes + (size_t)row * groups * kPlaneWords);
-    for (uint32_t i = tid; i < groups * (kPlaneWords / 4u); i += 64u * kDotWaves)
-        lds_planes[i] = src[i];
-    if (tid < groups)
-        lds_sums[tid] = j.sums[(size_t)row * groups + tid];
-    __syncthreads();
+        if (tid < groups)
+            lds_negsum[buf][tid] = -rc.sum;
+        // prefetch the next item
+        const uint32_t next = item + gridDim.x;
+        const bool more = next < items;
+        if (more) {
+            locate<MAP>(next, single, jobs, item_job, uniform_items, nxt);
+            issue<MAXG>(nxt, wave, lane, tid, rn);
+        }
+        __syncthreads();
 
-    // 3. group dots (+ rounded products)
-    const uint32_t* lp = reinterpret_cast<const uint32_t*>(lds_planes);
+        // group dots and rounded products
+        const uint32_t gpw = (groups + kDotWaves - 1u) / kDotWaves;
+        const uint32_t g0 = wave * gpw;
+        const uint32_t gcount = g0 < groups ? min(groups - g0, gpw) : 0u;
+        const bool sum_mode = cur.j.mode != MODE_DOT_I16;
+        const uint32_t* lp = reinterpret_cast<const uint32_t*>(lds_planes[buf]);
 #pragma unroll
-    for (uint32_t i = 0; i < (uint32_t)kMaxGroupsPerWave; ++i) {
-        if (i < gcount) {
-            const uint32_t g = g0 + i;
-            const int d = 2 * group_pos(w[i], lp + g * kPlaneWords) - lds_sums[g];
-            if (sum_mode) {
-                const float prod = __half2float(__ushort_as_half(sc[i])) * (float)d;
-                lds_x[g * kLdsPitch + lane] = __float_as_int(prod);
-            } else {
-                lds_x[g * kLdsPitch + lane] = d;
+        for (int i = 0; i < DotRegs<MAXG>::kGpw; ++i) {
+            if ((uint32_t)i < gcount) {
+                const uint32_t g = g0 + i;
+                const int d = group_dot(rc.w[i], lp + g * kPlaneWords, lds_negsum[buf][g]);
+                if (sum_mode) {
+                    const float prod = __half2float(__ushort_as_half((uint16_t)rc.sc[i])) * (float)d;
+                    lds_x[buf][g * kLdsPitch + lane] = __float_as_int(prod);
+                } else {
+                    lds_x[buf][g * kLdsPitch + lane] = d;
+                }
             }
         }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // 4. in-order sums or int16 stores
-    const uint32_t n0 = t * kTile;
-    const uint32_t live = j.n - n0 < kTile ? j.n - n0 : kTile;
-    unsigned char* orow = j.out + (size_t)row * j.out_stride;
-    if (!sum_mode) {
-        int16_t* o = reinterpret_cast<int16_t*>(orow) + (size_t)n0 * groups;
-        for (uint32_t idx = tid; idx < live * groups; idx += 64u * kDotWaves) {
-            const uint32_t nl = idx / groups, g = idx - nl * groups;
-            o[idx] = (int16_t)lds_x[g * kLdsPitch + nl];
+        // in-order sums or int16 stores
+        const uint32_t n0 = cur.t * kTile;
+        const uint32_t live = min(cur.j.n - n0, kTile);
+        unsigned char* orow = cur.j.out + (size_t)cur.row * cur.j.out_stride;
+        if (!sum_mode) {
+            int16_t* o = reinterpret_cast<int16_t*>(orow) + (size_t)n0 * groups;
+            for (uint32_t idx = tid; idx < live * groups; idx += 64u * kDotWaves) {
+                const uint32_t nl = idx / groups, g = idx - nl * groups;
+                o[idx] = (int16_t)lds_x[buf][g * kLdsPitch + nl];
+            }
+        } else if (wave == 0 && lane < live) {
+            float acc = 0.0f;
+            for (uint32_t g = 0; g < groups; ++g)
+                acc = acc + __int_as_float(lds_x[buf][g * kLdsPitch + lane]);
+            if (cur.j.mode == MODE_SUM_SCALED)
+                acc = acc * cur.j.rscale[cur.row];
+            reinterpret_cast<float*>(orow)[n0 + lane] = acc;
         }
-    } else if (wave == 0 && lane < live) {
-        float acc = 0.0f;
-        for (uint32_t g = 0; g < groups; ++g)
-            acc = acc + __int_as_float(lds_x[g * kLdsPitch + lane]);
-        if (j.mode == MODE_SUM_SCALED)
-            acc = acc * j.rscale[row];
-        reinterpret_cast<float*>(orow)[n0 + lane] = acc;
+        if (!more)
+            break;
+        item = next;
+        cur = nxt;
+        rc = rn;
+        buf ^= 1;
     }
 }
 
-template <bool BATCH>
-__global__ __launch_bounds__(64 * kDotWaves) void k_dot(DotJob single, const DotJob* __restrict__ jobs,
-                                                        const uint32_t* __restrict__ block_job, uint64_t seq,
-                                                        const uint64_t* __restrict__ flag) {
-    if (*flag == seq)
-        return;  // some row of this job (batch) is illegal: write nothing
-    if (BATCH) {
-        const DotJob j = jobs[block_job[blockIdx.x]];
-        dot_tile(j, blockIdx.x - j.first_block);
-    } else {
-        dot_tile(single, blockIdx.x);
-    }
+template <int MAXG, int MAP>
+hipError_t launch_dot_t(hipStream_t stream, const DotJob& single, const DotJob* jobs, const uint32_t* item_job,
+                        uint32_t items, uint32_t uniform_items, uint32_t grid, uint64_t seq, const uint64_t* flag) {
+    hipLaunchKernelGGL((k_dot<MAXG, MAP>), dim3(grid), dim3(64 * kDotWaves), 0, stream, single, jobs, item_job,
+                       items, uniform_items, seq, flag);
+    return hipGetLastError();
 }
 
 // Copies tight staged rows into an arbitrarily aligned / strided view,
@@ -292,12 +424,6 @@ hipError_t launch_prep(hipStream_t stream, const PrepJob& job, bool validate_onl
     return hipGetLastError();
 }
 
-hipError_t launch_dot(hipStream_t stream, const DotJob& job, uint64_t seq, const uint64_t* flag) {
-    hipLaunchKernelGGL(k_dot<false>, dim3(job.tiles * job.rows), dim3(64 * kDotWaves), 0, stream, job, nullptr,
-                       nullptr, seq, flag);
-    return hipGetLastError();
-}
-
 hipError_t launch_prep_batch(hipStream_t stream, const PrepJob* jobs, const uint32_t* block_job, uint32_t blocks,
                              uint64_t seq, uint64_t* flag, uint64_t* host_status) {
     PrepJob none = {};
@@ -306,12 +432,33 @@ hipError_t launch_prep_batch(hipStream_t stream, const PrepJob* jobs, const uint
     return hipGetLastError();
 }
 
-hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32_t* block_job, uint32_t blocks,
-                            uint64_t seq, const uint64_t* flag) {
+static uint32_t dot_grid(uint32_t items, uint32_t max_groups, uint32_t cu_count) {
+    const uint32_t per_cu = max_groups <= 16u ? kDotWgsPerCuSmall : kDotWgsPerCuLarge;
+    const uint32_t cap = (cu_count ? cu_count : 256u) * per_cu;
+    return items < cap ? items : cap;
+}
+
+hipError_t launch_dot(hipStream_t stream, const DotJob& job, uint32_t cu_count, uint64_t seq,
+                      const uint64_t* flag) {
+    const uint32_t items = job.tiles * job.rows;
+    const uint32_t grid = dot_grid(items, job.groups, cu_count);
+    if (job.groups <= 16u)
+        return launch_dot_t<16, MAP_SINGLE>(stream, job, nullptr, nullptr, items, 0, grid, seq, flag);
+    return launch_dot_t<64, MAP_SINGLE>(stream, job, nullptr, nullptr, items, 0, grid, seq, flag);
+}
+
+hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32_t* item_job, uint32_t items,
+                            uint32_t uniform_items, uint32_t max_groups, uint32_t cu_count, uint64_t seq,
+                            const uint64_t* flag) {
     DotJob none = {};
-    hipLaunchKernelGGL(k_dot<true>, dim3(blocks), dim3(64 * kDotWaves), 0, stream, none, jobs, block_job, seq,
-                       flag);
-    return hipGetLastError();
+    const uint32_t grid = dot_grid(items, max_groups, cu_count);
+    if (max_groups <= 16u)
+        return uniform_items
+                   ? launch_dot_t<16, MAP_UNIFORM>(stream, none, jobs, item_job, items, uniform_items, grid, seq, flag)
+                   : launch_dot_t<16, MAP_TABLE>(stream, none, jobs, item_job, items, 0, grid, seq, flag);
+    return uniform_items
+               ? launch_dot_t<64, MAP_UNIFORM>(stream, none, jobs, item_job, items, uniform_items, grid, seq, flag)
+               : launch_dot_t<64, MAP_TABLE>(stream, none, jobs, item_job, items, 0, grid, seq, flag);
 }
 
 hipError_t launch_scatter(hipStream_t stream, const unsigned char* src, size_t src_stride, unsigned char* dst,

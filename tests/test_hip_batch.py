@@ -1,0 +1,144 @@
+"""BNNX_ExecuteBatch (HIP-backend extension): same results as BNN_Execute per job,
+all-or-nothing input checks, concurrency rules, and table-cache invalidation."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from bnn_cases import first_mismatch
+
+pytestmark = pytest.mark.gpu
+
+
+def _mk_batch(pkg, dev, specs, seed=0):
+    """specs: [(op, K, N, rows)] -> matrices, one input and one output buffer, jobs."""
+    mats, xs, in_off, out_off, layouts = [], [], [], [], []
+    ioff = ooff = 0
+    for i, (op, k, n, rows) in enumerate(specs):
+        mats.append(dev.matrix(*pkg.synth.matrix(n, k, seed=seed * 100 + i)))
+        f32 = op.endswith("F32")
+        x = pkg.synth.normal_f32(rows, k, seed=seed + i) if f32 else pkg.synth.int8_uniform(rows, k, seed=seed + i)
+        xs.append(x)
+        in_off.append(ioff)
+        ioff += -(-x.nbytes // 64) * 64
+        shape, dtype = ((rows, n, k // 128), np.int16) if op == "DOT_GROUPS" else ((rows, n), np.float32)
+        layouts.append((shape, dtype))
+        out_off.append(ooff)
+        ooff += -(-int(np.prod(shape)) * np.dtype(dtype).itemsize // 64) * 64
+    ioff += 64  # slack so that views can be shifted inside the buffers
+    ooff += 64
+    bi, bo = dev.buffer(ioff), dev.buffer(ooff)
+    raw = np.zeros(ioff, np.uint8)
+    for x, o in zip(xs, in_off):
+        raw[o:o + x.nbytes] = x.view(np.uint8).reshape(-1)
+    bi.write(raw)
+    jobs = (pkg.Job * len(specs))()
+    for i, (op, k, n, rows) in enumerate(specs):
+        in_t, out_t = pkg.api.OP_TYPES[pkg.Op[op]]
+        jobs[i] = pkg.Job(int(pkg.Op[op]), mats[i].handle.value, bi.view(in_t, in_off[i]), bo.view(out_t, out_off[i]),
+                          rows)
+    return mats, xs, bi, bo, jobs, out_off, layouts
+
+
+def _outputs(bo, out_off, layouts):
+    raw = bo.read()
+    res = []
+    for o, (shape, dtype) in zip(out_off, layouts):
+        nb = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        res.append(raw[o:o + nb].view(dtype).reshape(shape))
+    return res
+
+
+def _free(mats, bi, bo):
+    bi.free()
+    bo.free()
+    for m in mats:
+        m.destroy()
+
+
+@pytest.mark.parametrize("specs", [
+    [("GEMV_F32", 2048, 6144, 1)] * 12,                                   # uniform
+    [("GEMV_F32", 2048, 2048, 1), ("GEMV", 6144, 2048, 1), ("DOT_GROUPS", 384, 70, 3),
+     ("GEMM_F32", 8192, 129, 5), ("GEMM", 128, 1, 2), ("GEMV_F32", 2048, 8192, 1)],  # mixed
+], ids=["uniform", "mixed"])
+def test_batch_equals_single_jobs(pkg, hipdev, specs):
+    mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs)
+    assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, len(specs)) == pkg.Status.OK
+    got = _outputs(bo, out_off, layouts)
+    for i, (op, k, n, rows) in enumerate(specs):
+        want = hipdev.run(pkg.Op[op], mats[i], xs[i])
+        assert np.array_equal(got[i].view(np.uint8), want.view(np.uint8)), (i, op, first_mismatch(got[i], want))
+    # a second, cached call on new input data
+    xs2 = [(-x if x.dtype == np.float32 else np.negative(x)) for x in xs]
+    raw = bi.read()
+    for x, o in zip(xs2, [j.input.offset for j in jobs]):
+        raw[o:o + x.nbytes] = x.view(np.uint8).reshape(-1)
+    bi.write(raw)
+    assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, len(specs)) == pkg.Status.OK
+    got = _outputs(bo, out_off, layouts)
+    for i, (op, k, n, rows) in enumerate(specs):
+        want = hipdev.run(pkg.Op[op], mats[i], xs2[i])
+        assert np.array_equal(got[i].view(np.uint8), want.view(np.uint8)), (i, op)
+    _free(mats, bi, bo)
+
+
+def test_batch_cache_follows_resource_changes(pkg, hipdev):
+    specs = [("GEMV_F32", 256, 100, 1)] * 3
+    mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs, seed=5)
+    assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, 3) == pkg.Status.OK
+    # replace matrix 1 by a different one; the job array may even hold the same handle value
+    mats[1].destroy()
+    mats[1] = hipdev.matrix(*pkg.synth.matrix(100, 256, seed=999))
+    jobs[1].matrix = mats[1].handle.value
+    assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, 3) == pkg.Status.OK
+    got = _outputs(bo, out_off, layouts)
+    want = hipdev.run(pkg.Op.GEMV_F32, mats[1], xs[1])
+    assert np.array_equal(got[1].view(np.uint32), want.view(np.uint32))
+    _free(mats, bi, bo)
+
+
+def test_batch_illegal_input_writes_nothing(pkg, hipdev):
+    specs = [("GEMV_F32", 512, 64, 1), ("DOT_GROUPS", 256, 10, 2), ("GEMM", 128, 7, 3)]
+    mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs, seed=2)
+    raw = bi.read()
+    raw[jobs[2].input.offset + 2 * 128 + 5] = 0x80  # -128 in the last row of the last job
+    bi.write(raw)
+    sentinel = np.full(bo.nbytes, 0x5A, np.uint8)
+    bo.write(sentinel)
+    assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, 3) == pkg.Status.ERANGE
+    assert np.array_equal(bo.read(), sentinel)
+    raw[jobs[2].input.offset + 2 * 128 + 5] = 0x01
+    bi.write(raw)
+    assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, 3) == pkg.Status.OK
+    _free(mats, bi, bo)
+
+
+def test_batch_rejections(pkg, hipdev):
+    specs = [("GEMV_F32", 256, 16, 1), ("GEMV_F32", 256, 16, 1)]
+    mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs, seed=3)
+    api = hipdev.api
+    assert api.BNNX_ExecuteBatch(hipdev.handle, jobs, 0) == pkg.Status.EINVAL
+    assert api.BNNX_ExecuteBatch(None, jobs, 2) == pkg.Status.EINVAL
+    bad = (pkg.Job * 2)(*jobs)
+    bad[1].output.offset = jobs[0].output.offset + 4  # overlapping outputs
+    assert api.BNNX_ExecuteBatch(hipdev.handle, bad, 2) == pkg.Status.EINVAL
+    own_in = hipdev.buffer(bi.nbytes)
+    own_in.write(bi.read())
+    bad = (pkg.Job * 2)(*jobs)
+    bad[1].input.buffer = own_in.handle.value
+    bad[1].output.buffer = jobs[0].input.buffer  # job 1 would write what job 0 reads
+    bad[1].output.offset = 0
+    assert api.BNNX_ExecuteBatch(hipdev.handle, bad, 2) == pkg.Status.EINVAL
+    bad[1].output.buffer = jobs[1].output.buffer  # same views, own input: accepted
+    bad[1].output.offset = jobs[1].output.offset
+    assert api.BNNX_ExecuteBatch(hipdev.handle, bad, 2) == pkg.Status.OK
+    own_in.free()
+    bad = (pkg.Job * 2)(*jobs)
+    bad[1].output.offset += 2  # unaligned F32 output: single jobs only
+    assert api.BNNX_ExecuteBatch(hipdev.handle, bad, 2) == pkg.Status.ENOTSUP
+    bad = (pkg.Job * 2)(*jobs)
+    bad[0].rows = 2  # the first failing job's own status (GEMV with rows != 1)
+    bad[1].operation = 99
+    assert api.BNNX_ExecuteBatch(hipdev.handle, bad, 2) == pkg.Status.EINVAL
+    assert api.BNNX_ExecuteBatch(hipdev.handle, jobs, 2) == pkg.Status.OK
+    _free(mats, bi, bo)
