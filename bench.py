@@ -241,7 +241,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic_from_profiles(),
-            "kernel": "k_dot<true> (batched group-dot)",
+            "kernel": "k_dot_wave (batched group-dot, one wave per 64-feature tile)",
             "kernel_avg_us": round(dot_avg_s * 1e6, 2),
             "prep_kernel_avg_us": round(prep_ms / max(prep_n, 1) * 1e3, 2),
         },

@@ -384,6 +384,8 @@ EXPORT void BNN_MatrixDestroy(BNN_Matrix matrix) {
     (void)hipSetDevice(matrix->device->ordinal);
     (void)hipStreamSynchronize(matrix->device->stream);
     (void)hipFree(matrix->wbits);
+    if (matrix->wbytes)
+        (void)hipFree(matrix->wbytes);
     matrix->device->live_matrices--;
     matrix->device->generation++;
     free(matrix);
@@ -545,14 +547,20 @@ BNN_Status plan_job(BNN_Device device, const BNN_Job* job, JobPlan* p) {
     return BNN_OK;
 }
 
-size_t row_scratch_bytes(const JobPlan& p, size_t rows, size_t* planes, size_t* sums, size_t* rscale) {
+// Scratch per block of rows: planes | sums | rscale | (matrix-core jobs) Q rows.
+size_t row_scratch_bytes(const JobPlan& p, size_t rows, size_t* planes, size_t* sums, size_t* rscale,
+                         size_t* q = nullptr, bool with_q = false) {
     *planes = round_up(rows * p.m->groups * kPlaneWords * 4u, 256);
     *sums = round_up(rows * p.m->groups * 4u, 256);
     *rscale = round_up(rows * 4u, 256);
-    return *planes + *sums + *rscale;
+    const size_t qb = with_q ? round_up(rows * p.m->k, 256) : 0;
+    if (q)
+        *q = qb;
+    return *planes + *sums + *rscale + qb;
 }
 
-PrepJob make_prep(const JobPlan& p, const unsigned char* in, uint32_t rows, unsigned char* scratch) {
+PrepJob make_prep(const JobPlan& p, const unsigned char* in, uint32_t rows, unsigned char* scratch,
+                  bool with_q = false) {
     size_t planes, sums, rscale;
     row_scratch_bytes(p, rows, &planes, &sums, &rscale);
     PrepJob j = {};
@@ -561,7 +569,11 @@ PrepJob make_prep(const JobPlan& p, const unsigned char* in, uint32_t rows, unsi
     j.planes = reinterpret_cast<uint32_t*>(scratch);
     j.sums = reinterpret_cast<int32_t*>(scratch + planes);
     j.rscale = reinterpret_cast<float*>(scratch + planes + sums);
-    j.q = nullptr;
+    j.q = with_q ? reinterpret_cast<int8_t*>(scratch + planes + sums + rscale) : nullptr;
+    if (with_q) {  // the matrix-core path reads Q rows only
+        j.planes = nullptr;
+        j.sums = nullptr;
+    }
     j.k = p.m->k;
     j.rows = rows;
     j.f32 = p.f32_in;
@@ -579,6 +591,23 @@ DotJob make_dot(const JobPlan& p, const PrepJob& pj, unsigned char* out, size_t 
     j.out = out;
     j.out_stride = out_stride;
     j.n = p.m->n;
+    j.groups = p.m->groups;
+    j.tiles = p.m->tiles;
+    j.rows = pj.rows;
+    j.mode = p.mode;
+    return j;
+}
+
+GemmJob make_gemm(const JobPlan& p, const PrepJob& pj, unsigned char* out, size_t out_stride) {
+    GemmJob j = {};
+    j.wbytes = p.m->wbytes;
+    j.wscale = p.m->wscale;
+    j.q = pj.q;
+    j.rscale = pj.rscale;
+    j.out = out;
+    j.out_stride = out_stride;
+    j.n = p.m->n;
+    j.k = p.m->k;
     j.groups = p.m->groups;
     j.tiles = p.m->tiles;
     j.rows = pj.rows;
@@ -610,12 +639,13 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
 
     // rows per launch chunk, bounded by the scratch cap
     const uint32_t rows = job->rows;
+    const bool mfma = rows >= kMfmaMinRows;
     size_t a, b, c;
-    const size_t per_row = row_scratch_bytes(p, 1, &a, &b, &c) + (p.out_aligned ? 0u : p.out_row);
+    const size_t per_row = row_scratch_bytes(p, 1, &a, &b, &c, nullptr, mfma) + (p.out_aligned ? 0u : p.out_row);
     size_t chunk = rows < kScratchRowsCap ? rows : kScratchRowsCap;
     while (chunk > 1 && chunk * per_row + 4096 > kScratchBytesCap)
         chunk /= 2;
-    const size_t rows_bytes = row_scratch_bytes(p, chunk, &a, &b, &c);
+    const size_t rows_bytes = row_scratch_bytes(p, chunk, &a, &b, &c, nullptr, mfma);
     const size_t staging_bytes = p.out_aligned ? 0 : round_up(chunk * p.out_row, 256);
 
     if (hipSetDevice(device->ordinal) != hipSuccess)
@@ -625,9 +655,21 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
         return st;
     unsigned char* staging = device->scratch + rows_bytes;
 
-    const uint64_t seq = ++device->seq;
     hipError_t e = hipSuccess;
-    if (chunk < rows) {
+    if (mfma && p.m->wbytes == nullptr) {
+        // first multi-row job on this matrix: create its +1/-1 byte copy
+        const uint32_t n_pad = (p.m->n + kGemmRowPad - 1u) / kGemmRowPad * kGemmRowPad;
+        void* w = nullptr;
+        if (hipMalloc(&w, (size_t)n_pad * p.m->k) != hipSuccess) {
+            (void)hipGetLastError();
+            return BNN_ENOMEM;
+        }
+        p.m->wbytes = static_cast<int8_t*>(w);
+        p.m->n_pad = n_pad;
+        e = launch_expand(device->stream, p.m->wbits, p.m->tiles, p.m->groups, n_pad, p.m->wbytes);
+    }
+    const uint64_t seq = ++device->seq;
+    if (e == hipSuccess && chunk < rows) {
         // every row is checked before any chunk writes output
         const PrepJob all = make_prep(p, p.in_base, rows, device->scratch);
         e = timed(device, KK_PREP, [&] {
@@ -636,16 +678,23 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
     }
     for (size_t r0 = 0; e == hipSuccess && r0 < rows; r0 += chunk) {
         const uint32_t rc = (uint32_t)((rows - r0) < chunk ? (rows - r0) : chunk);
-        const PrepJob pj = make_prep(p, p.in_base + r0 * p.in_stride, rc, device->scratch);
+        const PrepJob pj = make_prep(p, p.in_base + r0 * p.in_stride, rc, device->scratch, mfma);
         e = timed(device, KK_PREP, [&] {
             return launch_prep(device->stream, pj, false, seq, device->flag_dev, device->status_host);
         });
         if (e != hipSuccess)
             break;
-        const DotJob dj = p.out_aligned ? make_dot(p, pj, p.out_base + r0 * p.out_stride, p.out_stride)
-                                        : make_dot(p, pj, staging, p.out_row);
-        e = timed(device, KK_DOT,
-                  [&] { return launch_dot(device->stream, dj, device->cu_count, seq, device->flag_dev); });
+        unsigned char* dst = p.out_aligned ? p.out_base + r0 * p.out_stride : staging;
+        const size_t dst_stride = p.out_aligned ? p.out_stride : p.out_row;
+        if (mfma) {
+            const GemmJob gj = make_gemm(p, pj, dst, dst_stride);
+            e = timed(device, KK_GEMM,
+                      [&] { return launch_gemm(device->stream, gj, device->cu_count, seq, device->flag_dev); });
+        } else {
+            const DotJob dj = make_dot(p, pj, dst, dst_stride);
+            e = timed(device, KK_DOT,
+                      [&] { return launch_dot(device->stream, dj, device->cu_count, seq, device->flag_dev); });
+        }
         if (e == hipSuccess && !p.out_aligned)
             e = timed(device, KK_SCATTER, [&] {
                 return launch_scatter(device->stream, staging, p.out_row, p.out_base + r0 * p.out_stride,
@@ -704,19 +753,38 @@ BNN_Status ensure_tables(BNN_Device d, size_t bytes) {
 
 }  // namespace
 
+static BNN_Status run_cached_batch(BNN_Device device);
+
 EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint32_t count) {
     if (device == nullptr || jobs == nullptr || count == 0)
         return BNN_EINVAL;
     // An identical job array of the same resource generation reuses the tables
-    // already on the device; every job is still checked as BNN_Execute checks it.
+    // already on the device.  Its per-job checks depend only on the job bytes
+    // (identical), on matrix/buffer objects (immutable while the generation is
+    // unchanged) and on the host rounding mode, so only the latter is re-checked.
     const bool cached = device->batch_jobs != nullptr && device->batch_count == count &&
                         device->batch_generation == device->generation &&
                         memcmp(device->batch_jobs, jobs, sizeof(BNN_Job) * count) == 0;
+    if (cached) {
+        if (device->batch_needs_nearest && fegetround() != FE_TONEAREST) {
+            // same outcome as the full checks: the first job that is not DOT_GROUPS fails
+            for (uint32_t i = 0; i < count; ++i) {
+                JobPlan p;
+                const BNN_Status st = plan_job(device, &jobs[i], &p);
+                if (st != BNN_OK)
+                    return st;
+            }
+        }
+        if (hipSetDevice(device->ordinal) != hipSuccess)
+            return BNN_EIO;
+        return run_cached_batch(device);
+    }
     JobPlan* plans = static_cast<JobPlan*>(malloc(sizeof(JobPlan) * count));
-    Extent* outs = cached ? nullptr : static_cast<Extent*>(malloc(sizeof(Extent) * count));
-    const void** ins = cached ? nullptr : static_cast<const void**>(malloc(sizeof(void*) * count));
-    BNN_Status st = plans && (cached || (outs && ins)) ? BNN_OK : BNN_ENOMEM;
-    uint64_t prep_blocks = 0, dot_items = 0;
+    Extent* outs = static_cast<Extent*>(malloc(sizeof(Extent) * count));
+    const void** ins = static_cast<const void**>(malloc(sizeof(void*) * count));
+    BNN_Status st = plans && outs && ins ? BNN_OK : BNN_ENOMEM;
+    bool needs_nearest = false;
+    uint64_t prep_blocks = 0, dot_items_total = 0;
     size_t scratch_bytes = 0;
     uint32_t max_groups = 0;
     bool uniform = true;
@@ -729,14 +797,10 @@ EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint
             st = BNN_ENOTSUP;
             break;
         }
-        if (cached)
-            continue;
+        needs_nearest = needs_nearest || !p.dot_out;
         size_t a, b, c;
         scratch_bytes += row_scratch_bytes(p, jobs[i].rows, &a, &b, &c);
         prep_blocks += jobs[i].rows;
-        const uint64_t items = (uint64_t)jobs[i].rows * p.m->tiles;
-        uniform = uniform && items == (uint64_t)jobs[0].rows * plans[0].m->tiles;
-        dot_items += items;
         max_groups = p.m->groups > max_groups ? p.m->groups : max_groups;
         outs[i].buffer = jobs[i].output.buffer;
         outs[i].begin = jobs[i].output.offset;
@@ -745,7 +809,13 @@ EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint
     }
     // the jobs run concurrently: no output buffer may be an input buffer, and
     // outputs sharing a buffer may not overlap
-    if (st == BNN_OK && !cached) {
+    // work items per job depend on the batch's largest group count
+    for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
+        const uint64_t items = dot_items(plans[i].m->tiles, jobs[i].rows, max_groups);
+        uniform = uniform && items == dot_items(plans[0].m->tiles, jobs[0].rows, max_groups);
+        dot_items_total += items;
+    }
+    if (st == BNN_OK) {
         std::sort(ins, ins + count);
         std::sort(outs, outs + count, extent_less);
         for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
@@ -754,7 +824,7 @@ EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint
             else if (i > 0 && outs[i].buffer == outs[i - 1].buffer && outs[i].begin < outs[i - 1].end)
                 st = BNN_EINVAL;
         }
-        if (st == BNN_OK && (prep_blocks > 0x7fffffffu || dot_items > 0x7fffffffu))
+        if (st == BNN_OK && (prep_blocks > 0x7fffffffu || dot_items_total > 0x7fffffffu))
             st = BNN_ENOTSUP;
     }
     free(outs);
@@ -768,12 +838,12 @@ EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint
         return BNN_EIO;
     }
 
-    if (!cached) {
+    {
         // tables: PrepJob[count] | DotJob[count] | prep block->job | dot item->job (non-uniform only)
         const size_t prep_tab = round_up(sizeof(PrepJob) * count, 256);
         const size_t dot_tab = round_up(sizeof(DotJob) * count, 256);
         const size_t prep_map = round_up(4u * prep_blocks, 256);
-        const size_t dot_map = uniform ? 0 : round_up(4u * dot_items, 256);
+        const size_t dot_map = uniform ? 0 : round_up(4u * dot_items_total, 256);
         const size_t tables = prep_tab + dot_tab + prep_map + dot_map;
         st = ensure_scratch(device, scratch_bytes);
         if (st == BNN_OK)
@@ -809,7 +879,7 @@ EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint
             hd[i].first_block = di;
             for (uint32_t r = 0; r < rows; ++r)
                 hpm[pb++] = i;
-            const uint32_t items = rows * p.m->tiles;
+            const uint32_t items = dot_items(p.m->tiles, rows, max_groups);
             if (!uniform)
                 for (uint32_t r = 0; r < items; ++r)
                     hdm[di + r] = i;
@@ -828,14 +898,20 @@ EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint
         device->batch_generation = device->generation;
         device->batch_prep_blocks = pb;
         device->batch_items = di;
-        device->batch_uniform_items = uniform ? jobs[0].rows * plans[0].m->tiles : 0u;
+        device->batch_uniform_items = uniform ? dot_items(plans[0].m->tiles, jobs[0].rows, max_groups) : 0u;
         device->batch_max_groups = max_groups;
         device->batch_prep_tab = prep_tab;
         device->batch_dot_tab = dot_tab;
         device->batch_prep_map = prep_map;
         device->batch_tables = tables;
+        device->batch_needs_nearest = needs_nearest;
     }
     free(plans);
+    return run_cached_batch(device);
+}
+
+// Launches the batch whose tables are on the device (the last one built).
+static BNN_Status run_cached_batch(BNN_Device device) {
 
     const PrepJob* dp = reinterpret_cast<const PrepJob*>(device->table_dev);
     const DotJob* dd = reinterpret_cast<const DotJob*>(device->table_dev + device->batch_prep_tab);

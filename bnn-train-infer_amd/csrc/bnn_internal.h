@@ -40,7 +40,7 @@ constexpr uint32_t kDotWaves = 4;      // waves per dot workgroup (they split th
 constexpr uint32_t kDotWgsPerCuSmall = BNN_DOT_WGS_PER_CU_SMALL;
 constexpr uint32_t kDotWgsPerCuLarge = BNN_DOT_WGS_PER_CU_LARGE;
 
-enum KernelKind { KK_PREP = 0, KK_DOT = 1, KK_SCATTER = 2, KK_COUNT = 3 };
+enum KernelKind { KK_PREP = 0, KK_DOT = 1, KK_SCATTER = 2, KK_GEMM = 3, KK_COUNT = 4 };
 
 // Output interpretation of the group-dot kernel.
 enum DotMode : int {
@@ -84,6 +84,26 @@ struct DotJob {
     uint32_t first_block;
 };
 
+// One multi-row job on the matrix cores (rows >= kMfmaMinRows).
+struct GemmJob {
+    const int8_t* wbytes;     // [n_pad][k] +1/-1
+    const uint16_t* wscale;   // matrix layout [tiles][groups][64]
+    const int8_t* q;          // [rows][k] quantised rows
+    const float* rscale;      // [rows]
+    unsigned char* out;       // logical row 0 (4-byte aligned for F32, 2 for I16)
+    uint64_t out_stride;
+    uint32_t n, k, groups, tiles;  // tiles of 64 features, as in the matrix layout
+    uint32_t rows;
+    int32_t mode;
+};
+constexpr uint32_t kGemmRowPad = 128;  // n_pad granularity = largest workgroup tile
+
+// Rows from which a job runs on the matrix cores instead of the bit-plane kernel.
+#ifndef BNN_MFMA_MIN_ROWS
+#define BNN_MFMA_MIN_ROWS 8
+#endif
+constexpr uint32_t kMfmaMinRows = BNN_MFMA_MIN_ROWS;
+
 // Host-side launchers (bnn_kernels.hip).  All are asynchronous on `stream`.
 // Single job: descriptor passed by value.  `validate_only` runs only the
 // legality pass of prep (over all rows of a job processed in several chunks).
@@ -91,6 +111,9 @@ hipError_t launch_prep(hipStream_t stream, const PrepJob& job, bool validate_onl
                        uint64_t* flag, uint64_t* host_status);
 hipError_t launch_dot(hipStream_t stream, const DotJob& job, uint32_t cu_count, uint64_t seq,
                       const uint64_t* flag);
+// Work items of the dot kernel for a job (rows x groups of tiles); in a batch the
+// tiles per item follow the batch's largest group count.
+uint32_t dot_items(uint32_t tiles, uint32_t rows, uint32_t max_groups);
 // Batch: device-resident job tables.  Prep: one block per row, block -> job map.
 // Dot: items = sum of rows*tiles; job of an item = item / uniform_items when every
 // job has that many items, else item_job[item].
@@ -99,6 +122,11 @@ hipError_t launch_prep_batch(hipStream_t stream, const PrepJob* jobs, const uint
 hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32_t* item_job, uint32_t items,
                             uint32_t uniform_items, uint32_t max_groups, uint32_t cu_count, uint64_t seq,
                             const uint64_t* flag);
+hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count, uint64_t seq,
+                       const uint64_t* flag);
+// wbytes[n_pad][k] <- sign bits of the matrix layout (once per matrix).
+hipError_t launch_expand(hipStream_t stream, const uint4* wbits, uint32_t tiles, uint32_t groups,
+                         uint32_t n_pad, int8_t* wbytes);
 hipError_t launch_scatter(hipStream_t stream, const unsigned char* src, size_t src_stride,
                           unsigned char* dst, size_t dst_stride, size_t row_bytes, uint32_t rows,
                           uint64_t seq, const uint64_t* flag);
@@ -132,6 +160,7 @@ struct bnn_accel_device {
     uint64_t batch_generation;
     uint32_t batch_prep_blocks, batch_items, batch_uniform_items, batch_max_groups;
     size_t batch_prep_tab, batch_dot_tab, batch_prep_map, batch_tables;
+    bool batch_needs_nearest;  // some job of the cached batch is an FP32 operation
     // optional kernel timing (extension API): event pairs recorded around
     // launches, resolved after the call's synchronisation
     int timing;
@@ -148,6 +177,11 @@ struct bnn_accel_matrix {
     uint32_t k, n, groups, tiles;
     uint4* wbits;
     uint16_t* wscale;
+    // Matrix-core copy of the weights, created on the first multi-row job:
+    // wbytes[n_pad][k] int8 of +1/-1 (n_pad = N rounded up to 128; padding rows
+    // are -1 and never stored).  8 bits per weight, freed with the matrix.
+    int8_t* wbytes;
+    uint32_t n_pad;
 };
 
 struct bnn_accel_buffer {

@@ -46,6 +46,15 @@ __device__ __forceinline__ uint32_t gload(const uint16_t* p) {
 __device__ __forceinline__ int gload(const int32_t* p) {
     return *(const __attribute__((address_space(1))) int32_t*)p;
 }
+__device__ __forceinline__ float gload(const float* p) {
+    return *(const __attribute__((address_space(1))) float*)p;
+}
+// Global (not flat) stores: a flat store is counted by both the vector-memory and
+// the LDS counters, which makes every later LDS wait also wait for the store.
+__device__ __forceinline__ void gstore(float* p, float v) { *(__attribute__((address_space(1))) float*)p = v; }
+__device__ __forceinline__ void gstore(int16_t* p, int16_t v) {
+    *(__attribute__((address_space(1))) int16_t*)p = v;
+}
 
 __device__ __forceinline__ float load_f32(const unsigned char* row, uint32_t k, bool aligned) {
     if (aligned)
@@ -85,14 +94,15 @@ __device__ __forceinline__ void raise_flag(uint64_t seq, uint64_t* flag, uint64_
 // ---------------------------------------------------------------------------
 constexpr int kPrepPerThread = kMaxFeatures / 256;  // 32
 
-__device__ void prep_row(const PrepJob& j, uint32_t m, bool validate_only, uint64_t seq, uint64_t* flag,
-                         uint64_t* host_status) {
+template <bool F32, bool ALIGNED>
+__device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uint64_t seq, uint64_t* flag,
+                           uint64_t* host_status) {
     __shared__ float red_max[4];
     __shared__ int red_sum[kPrepPerThread][4];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t k_total = j.k, groups = k_total / kGroup;
     const uint32_t iters = (k_total + 255u) / 256u;
-    const bool f32 = j.f32 != 0, aligned = j.aligned != 0;
+    constexpr bool f32 = F32, aligned = ALIGNED;
     const unsigned char* row = j.in + (size_t)m * j.in_stride;
 
     // pass 1: load the whole logical row (registers), legality and absmax
@@ -140,7 +150,7 @@ __device__ void prep_row(const PrepJob& j, uint32_t m, bool validate_only, uint6
 
     // pass 2: quantise; in iteration i wave w owns the 64 consecutive k of half (w & 1)
     // of group 2i + (w >> 1)
-    uint32_t* planes = j.planes + (size_t)m * groups * kPlaneWords;
+    uint32_t* planes = j.planes ? j.planes + (size_t)m * groups * kPlaneWords : nullptr;
 #pragma unroll
     for (int i = 0; i < kPrepPerThread; ++i) {
         const uint32_t base = 256u * i;
@@ -163,17 +173,27 @@ __device__ void prep_row(const PrepJob& j, uint32_t m, bool validate_only, uint6
                     word = (uint32_t)(mask >> 32);
             }
             const uint32_t g = 2u * i + (wave >> 1), half = wave & 1u;
-            if (lane < 16u)
+            if (planes && lane < 16u)
                 planes[g * kPlaneWords + (lane >> 1) * 4u + half * 2u + (lane & 1u)] = word;
             if (lane == 0)
                 red_sum[i][wave] = part;
         }
     }
     __syncthreads();
-    if (tid < groups)
+    if (j.sums && tid < groups)
         j.sums[(size_t)m * groups + tid] = red_sum[tid >> 1][(tid & 1u) * 2u] + red_sum[tid >> 1][(tid & 1u) * 2u + 1u];
     if (tid == 0)
         j.rscale[m] = s;
+}
+
+__device__ __forceinline__ void prep_row(const PrepJob& j, uint32_t m, bool validate_only, uint64_t seq,
+                                         uint64_t* flag, uint64_t* host_status) {
+    if (j.f32 && j.aligned)
+        prep_row_t<true, true>(j, m, validate_only, seq, flag, host_status);
+    else if (j.f32)
+        prep_row_t<true, false>(j, m, validate_only, seq, flag, host_status);
+    else
+        prep_row_t<false, true>(j, m, validate_only, seq, flag, host_status);
 }
 
 template <bool BATCH>
@@ -229,73 +249,131 @@ __device__ __forceinline__ int group_dot(uint4 w, const uint32_t* p, int neg_sum
     return (int)d;
 }
 
+// The same with the planes read as one 16-byte word each (P_b = p[b]).
+template <int B>
+__device__ __forceinline__ uint32_t plane_count_v(uint4 w, const uint4* p) {
+    const uint4 pb = p[B];
+    uint32_t c = (uint32_t)__builtin_popcount(w.x & pb.x);
+    c = bcnt_acc(w.y & pb.y, c);
+    c = bcnt_acc(w.z & pb.z, c);
+    return bcnt_acc(w.w & pb.w, c);
+}
+
+__device__ __forceinline__ int group_dot_v(uint4 w, const uint4* p, int neg_sum) {
+    uint32_t d = (uint32_t)neg_sum;
+    d = lshl_add<1>(plane_count_v<0>(w, p), d);
+    d = lshl_add<2>(plane_count_v<1>(w, p), d);
+    d = lshl_add<3>(plane_count_v<2>(w, p), d);
+    d = lshl_add<4>(plane_count_v<3>(w, p), d);
+    d = lshl_add<5>(plane_count_v<4>(w, p), d);
+    d = lshl_add<6>(plane_count_v<5>(w, p), d);
+    d = lshl_add<7>(plane_count_v<6>(w, p), d);
+    d -= plane_count_v<7>(w, p) << 8;
+    return (int)d;
+}
+
+
 // ---------------------------------------------------------------------------
-// dot: persistent workgroups of 4 waves; one work item = (job, row, tile of 64
-// features).  Wave w owns a contiguous run of the groups; lane = feature.  While
-// item i is computed, the loads of item i + gridDim.x (job descriptor, weights,
-// scales, the row's bit planes and group sums) are already in flight in a
-// second register set.  D and the rounded products go through double-buffered
-// LDS so that wave 0 can add the products in group order (F32 modes) or the
-// workgroup can store D as int16 (DOT_GROUPS).
+// dot: persistent workgroups of 4 waves; one work item = (job, row, TPI tiles of
+// 64 features), items assigned round-robin (all workgroups stream through a
+// common window of memory, which suits HBM better than one stream per workgroup).  Wave w owns a contiguous run of the groups; lane = feature (one
+// per tile of the item, sharing each group's activation planes).  With PREFETCH,
+// the loads of item i + gridDim.x (job descriptor, weights, scales, the row's bit
+// planes and group sums) are in flight in a second register set while item i is
+// computed.  D and the rounded products go through double-buffered LDS so that
+// one wave per tile adds the products in group order (F32 modes), or the
+// workgroup stores D as int16 (DOT_GROUPS).
 // MAXG bounds the groups per matrix (16 for K <= 2048, else 64).
 // ---------------------------------------------------------------------------
 enum ItemMap : int { MAP_SINGLE = 0, MAP_UNIFORM = 1, MAP_TABLE = 2 };
 
-template <int MAXG>
+#ifndef BNN_DOT_TPI_SMALL
+#define BNN_DOT_TPI_SMALL 1
+#endif
+#ifndef BNN_DOT_PREFETCH
+#define BNN_DOT_PREFETCH 1
+#endif
+#ifndef BNN_DOT_WAVE_ITEMS
+#define BNN_DOT_WAVE_ITEMS 1  // batches with K <= 2048 use one wave per item
+#endif
+#ifndef BNN_DOT_WAVE_WG_WAVES
+#define BNN_DOT_WAVE_WG_WAVES 8  // items (waves) per workgroup; one item per wave, no persistent loop
+#endif
+#ifndef BNN_DOT_WAVE_XCDS
+#define BNN_DOT_WAVE_XCDS 0  // > 1: keep consecutive workgroups on one XCD
+#endif
+#ifndef BNN_DOT_WAVE_OCC
+#define BNN_DOT_WAVE_OCC 4  // waves per SIMD the register budget is fitted to
+#endif
+
+template <int MAXG, int TPI>
 struct DotRegs {
     static constexpr int kGpw = MAXG / (int)kDotWaves;
     static constexpr int kPlaneChunks = (MAXG * 8 + 255) / 256;  // uint4 of planes per thread
-    uint4 w[kGpw];
-    uint32_t sc[kGpw];
+    uint4 w[TPI][kGpw];
+    uint32_t sc[TPI][kGpw];
     uint4 pl[kPlaneChunks];
     int sum;
 };
 
 struct DotItem {
     DotJob j;
-    uint32_t row, t;
+    uint32_t row, t0;  // first tile of the item
 };
 
-template <int MAP>
+template <int MAP, int TPI>
 __device__ __forceinline__ void locate(uint32_t item, const DotJob& single, const DotJob* __restrict__ jobs,
-                                       const uint32_t* __restrict__ item_job, uint32_t uniform_items, DotItem& it) {
+                                       const uint32_t* __restrict__ item_job, uint32_t uniform_items, DotItem& it,
+                                       uint32_t& job_index) {
     uint32_t local;
     if (MAP == MAP_SINGLE) {
         it.j = single;
         local = item;
     } else if (MAP == MAP_UNIFORM) {
         const uint32_t ji = item / uniform_items;
-        it.j = jobs[ji];
+        if (ji != job_index) {  // consecutive items mostly share the job: keep its descriptor
+            it.j = jobs[ji];
+            job_index = ji;
+        }
         local = item - ji * uniform_items;
     } else {
-        it.j = jobs[item_job[item]];
+        const uint32_t ji = item_job[item];
+        if (ji != job_index) {
+            it.j = jobs[ji];
+            job_index = ji;
+        }
         local = item - it.j.first_block;
     }
-    it.row = local / it.j.tiles;
-    it.t = local - it.row * it.j.tiles;
+    const uint32_t per_row = (it.j.tiles + TPI - 1u) / TPI;
+    it.row = local / per_row;
+    it.t0 = (local - it.row * per_row) * TPI;
 }
 
-template <int MAXG>
+template <int MAXG, int TPI>
 __device__ __forceinline__ void issue(const DotItem& it, uint32_t wave, uint32_t lane, uint32_t tid,
-                                      DotRegs<MAXG>& r) {
+                                      DotRegs<MAXG, TPI>& r) {
     const uint32_t groups = it.j.groups;
     const uint32_t gpw = (groups + kDotWaves - 1u) / kDotWaves;
     const uint32_t g0 = wave * gpw;
     const uint32_t gcount = g0 < groups ? min(groups - g0, gpw) : 0u;
-    const size_t first = ((size_t)it.t * groups + g0) * kTile + lane;
-    const uint4* wb = it.j.wbits + first;
-    const uint16_t* ws = it.j.wscale + first;
     const bool sum_mode = it.j.mode != MODE_DOT_I16;
 #pragma unroll
-    for (int i = 0; i < DotRegs<MAXG>::kGpw; ++i) {
-        if ((uint32_t)i < gcount) {
-            r.w[i] = gload(wb + i * kTile);
-            r.sc[i] = sum_mode ? gload(ws + i * kTile) : 0u;
+    for (int tt = 0; tt < TPI; ++tt) {
+        const uint32_t t = it.t0 + tt;
+        const size_t first = ((size_t)t * groups + g0) * kTile + lane;
+        const uint4* wb = it.j.wbits + first;
+        const uint16_t* ws = it.j.wscale + first;
+#pragma unroll
+        for (int i = 0; i < DotRegs<MAXG, TPI>::kGpw; ++i) {
+            if ((uint32_t)i < gcount && t < it.j.tiles) {
+                r.w[tt][i] = gload(wb + i * kTile);
+                r.sc[tt][i] = sum_mode ? gload(ws + i * kTile) : 0u;
+            }
         }
     }
     const uint4* pl = reinterpret_cast<const uint4*>(it.j.planes + (size_t)it.row * groups * kPlaneWords);
 #pragma unroll
-    for (int c = 0; c < DotRegs<MAXG>::kPlaneChunks; ++c) {
+    for (int c = 0; c < DotRegs<MAXG, TPI>::kPlaneChunks; ++c) {
         const uint32_t idx = tid + 256u * c;
         if (idx < groups * (kPlaneWords / 4u))
             r.pl[c] = gload(pl + idx);
@@ -304,14 +382,14 @@ __device__ __forceinline__ void issue(const DotItem& it, uint32_t wave, uint32_t
         r.sum = gload(it.j.sums + (size_t)it.row * groups + tid);
 }
 
-template <int MAXG, int MAP>
+template <int MAXG, int MAP, int TPI, bool PREFETCH>
 __global__ __launch_bounds__(64 * kDotWaves) void k_dot(DotJob single, const DotJob* __restrict__ jobs,
                                                         const uint32_t* __restrict__ item_job, uint32_t items,
                                                         uint32_t uniform_items, uint64_t seq,
                                                         const uint64_t* __restrict__ flag) {
     __shared__ uint4 lds_planes[2][MAXG * kPlaneWords / 4];
     __shared__ int lds_negsum[2][MAXG];
-    __shared__ int lds_x[2][MAXG * kLdsPitch];  // D (int) or rounded product (float bits)
+    __shared__ int lds_x[2][TPI * MAXG * kLdsPitch];  // D (int) or rounded product (float bits)
     if (*flag == seq)
         return;  // an illegal input row in this job (batch): write nothing
 
@@ -321,83 +399,196 @@ __global__ __launch_bounds__(64 * kDotWaves) void k_dot(DotJob single, const Dot
     if (item >= items)
         return;
     DotItem cur, nxt;
-    DotRegs<MAXG> rc, rn;
-    locate<MAP>(item, single, jobs, item_job, uniform_items, cur);
-    issue<MAXG>(cur, wave, lane, tid, rc);
+    DotRegs<MAXG, TPI> rc, rn;
+    uint32_t cur_job = 0xffffffffu, nxt_job = 0xffffffffu;
+    locate<MAP, TPI>(item, single, jobs, item_job, uniform_items, cur, cur_job);
+    issue<MAXG, TPI>(cur, wave, lane, tid, rc);
+    nxt = cur;
+    nxt_job = cur_job;
     int buf = 0;
     for (;;) {
         const uint32_t groups = cur.j.groups;
         // stage this item's planes and group sums
 #pragma unroll
-        for (int c = 0; c < DotRegs<MAXG>::kPlaneChunks; ++c) {
+        for (int c = 0; c < DotRegs<MAXG, TPI>::kPlaneChunks; ++c) {
             const uint32_t idx = tid + 256u * c;
             if (idx < groups * (kPlaneWords / 4u))
                 lds_planes[buf][idx] = rc.pl[c];
         }
         if (tid < groups)
             lds_negsum[buf][tid] = -rc.sum;
-        // prefetch the next item
         const uint32_t next = item + gridDim.x;
         const bool more = next < items;
-        if (more) {
-            locate<MAP>(next, single, jobs, item_job, uniform_items, nxt);
-            issue<MAXG>(nxt, wave, lane, tid, rn);
+        if (PREFETCH && more) {
+            locate<MAP, TPI>(next, single, jobs, item_job, uniform_items, nxt, nxt_job);
+            issue<MAXG, TPI>(nxt, wave, lane, tid, rn);
         }
         __syncthreads();
 
-        // group dots and rounded products
+        // group dots and rounded products; the planes of a group serve all TPI tiles
         const uint32_t gpw = (groups + kDotWaves - 1u) / kDotWaves;
         const uint32_t g0 = wave * gpw;
         const uint32_t gcount = g0 < groups ? min(groups - g0, gpw) : 0u;
         const bool sum_mode = cur.j.mode != MODE_DOT_I16;
         const uint32_t* lp = reinterpret_cast<const uint32_t*>(lds_planes[buf]);
 #pragma unroll
-        for (int i = 0; i < DotRegs<MAXG>::kGpw; ++i) {
+        for (int i = 0; i < DotRegs<MAXG, TPI>::kGpw; ++i) {
             if ((uint32_t)i < gcount) {
                 const uint32_t g = g0 + i;
-                const int d = group_dot(rc.w[i], lp + g * kPlaneWords, lds_negsum[buf][g]);
-                if (sum_mode) {
-                    const float prod = __half2float(__ushort_as_half((uint16_t)rc.sc[i])) * (float)d;
-                    lds_x[buf][g * kLdsPitch + lane] = __float_as_int(prod);
-                } else {
-                    lds_x[buf][g * kLdsPitch + lane] = d;
+                const int neg = lds_negsum[buf][g];
+#pragma unroll
+                for (int tt = 0; tt < TPI; ++tt) {
+                    if (cur.t0 + tt < cur.j.tiles) {
+                        const int d = group_dot(rc.w[tt][i], lp + g * kPlaneWords, neg);
+                        int* x = &lds_x[buf][(tt * MAXG + g) * kLdsPitch + lane];
+                        if (sum_mode)
+                            *x = __float_as_int(__half2float(__ushort_as_half((uint16_t)rc.sc[tt][i])) * (float)d);
+                        else
+                            *x = d;
+                    }
                 }
             }
         }
         __syncthreads();
 
-        // in-order sums or int16 stores
-        const uint32_t n0 = cur.t * kTile;
-        const uint32_t live = min(cur.j.n - n0, kTile);
+        // in-order sums (one wave per tile) or int16 stores
         unsigned char* orow = cur.j.out + (size_t)cur.row * cur.j.out_stride;
         if (!sum_mode) {
-            int16_t* o = reinterpret_cast<int16_t*>(orow) + (size_t)n0 * groups;
-            for (uint32_t idx = tid; idx < live * groups; idx += 64u * kDotWaves) {
-                const uint32_t nl = idx / groups, g = idx - nl * groups;
-                o[idx] = (int16_t)lds_x[buf][g * kLdsPitch + nl];
+#pragma unroll
+            for (int tt = 0; tt < TPI; ++tt) {
+                const uint32_t t = cur.t0 + tt;
+                if (t >= cur.j.tiles)
+                    break;
+                const uint32_t n0 = t * kTile;
+                const uint32_t live = min(cur.j.n - n0, kTile);
+                int16_t* o = reinterpret_cast<int16_t*>(orow) + (size_t)n0 * groups;
+                for (uint32_t idx = tid; idx < live * groups; idx += 64u * kDotWaves) {
+                    const uint32_t nl = idx / groups, g = idx - nl * groups;
+                    o[idx] = (int16_t)lds_x[buf][(tt * MAXG + g) * kLdsPitch + nl];
+                }
             }
-        } else if (wave == 0 && lane < live) {
-            float acc = 0.0f;
-            for (uint32_t g = 0; g < groups; ++g)
-                acc = acc + __int_as_float(lds_x[buf][g * kLdsPitch + lane]);
-            if (cur.j.mode == MODE_SUM_SCALED)
-                acc = acc * cur.j.rscale[cur.row];
-            reinterpret_cast<float*>(orow)[n0 + lane] = acc;
+        } else if (wave < (uint32_t)TPI && cur.t0 + wave < cur.j.tiles) {
+            const uint32_t n0 = (cur.t0 + wave) * kTile;
+            if (lane < min(cur.j.n - n0, kTile)) {
+                const int* x = &lds_x[buf][wave * MAXG * kLdsPitch + lane];
+                float acc = 0.0f;
+                for (uint32_t g = 0; g < groups; ++g)
+                    acc = acc + __int_as_float(x[g * kLdsPitch]);
+                if (cur.j.mode == MODE_SUM_SCALED)
+                    acc = acc * cur.j.rscale[cur.row];
+                reinterpret_cast<float*>(orow)[n0 + lane] = acc;
+            }
         }
         if (!more)
             break;
         item = next;
-        cur = nxt;
-        rc = rn;
+        if (PREFETCH) {
+            cur = nxt;
+            rc = rn;
+        } else {
+            locate<MAP, TPI>(item, single, jobs, item_job, uniform_items, cur, cur_job);
+            issue<MAXG, TPI>(cur, wave, lane, tid, rc);
+        }
         buf ^= 1;
     }
 }
 
-template <int MAXG, int MAP>
+// ---------------------------------------------------------------------------
+// dot, one wave per item (batches with K <= 2048): the wave loads all groups of its
+// 64-feature tile (16 KB of sign bits + 2 KB of scales in flight per wave), stages
+// the row's planes in its own LDS slice, and every lane adds its products in group
+// order in a register -- no workgroup barriers, no product exchange.  There is no
+// persistent loop: one wave per item and the hardware dispatcher balancing short
+// workgroups measured faster than any fixed item-to-wave assignment.
+// ---------------------------------------------------------------------------
+constexpr int kWaveMaxGroups = 16;
+static_assert(!BNN_DOT_WAVE_ITEMS || BNN_DOT_TPI_SMALL == 1, "wave items count one tile per item");
+
+// Workgroups are handed out round-robin over the XCDs; with kWaveXcds > 0 the
+// logical workgroup index is remapped so that consecutive items (the tiles of one
+// job, which share the row's planes) run on the same XCD and its L2.
+__device__ __forceinline__ uint32_t xcd_local_block(uint32_t b, uint32_t grid) {
+    if (BNN_DOT_WAVE_XCDS <= 1)
+        return b;
+    const uint32_t x = b % BNN_DOT_WAVE_XCDS, i = b / BNN_DOT_WAVE_XCDS;
+    const uint32_t q = grid / BNN_DOT_WAVE_XCDS, r = grid % BNN_DOT_WAVE_XCDS;
+    return (x < r ? x * (q + 1u) : r * (q + 1u) + (x - r) * q) + i;
+}
+
+template <int MAP>
+__global__ __launch_bounds__(64 * BNN_DOT_WAVE_WG_WAVES) __attribute__((amdgpu_waves_per_eu(BNN_DOT_WAVE_OCC)))
+void k_dot_wave(const DotJob* __restrict__ jobs, const uint32_t* __restrict__ item_job, uint32_t items,
+                uint32_t uniform_items, uint64_t seq, const uint64_t* __restrict__ flag) {
+    __shared__ uint4 lds_planes[BNN_DOT_WAVE_WG_WAVES][kWaveMaxGroups * kPlaneWords / 4];
+    if (*flag == seq)
+        return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t item = xcd_local_block(blockIdx.x, gridDim.x) * BNN_DOT_WAVE_WG_WAVES + wave;
+    if (item >= items)
+        return;
+    uint32_t job_index = 0xffffffffu;
+    DotItem it;
+    locate<MAP, 1>(item, DotJob{}, jobs, item_job, uniform_items, it, job_index);
+    const uint32_t groups = it.j.groups;
+    // Loads are unconditional (indexes clamped into the job's arrays) and issued
+    // in the order they are consumed: the in-order load counter then lets group g
+    // start as soon as its own weights have arrived.
+    const uint32_t plane_chunks = groups * (kPlaneWords / 4u);
+    const uint4* pl = reinterpret_cast<const uint4*>(it.j.planes + (size_t)it.row * groups * kPlaneWords);
+    const uint4 p0 = gload(pl + min(lane, plane_chunks - 1u));
+    const uint4 p1 = gload(pl + min(lane + 64u, plane_chunks - 1u));
+    const int sum = gload(it.j.sums + (size_t)it.row * groups + min(lane, groups - 1u));
+    const size_t first = (size_t)it.t0 * groups * kTile + lane;
+    uint4 w[kWaveMaxGroups];
+    uint32_t sc[kWaveMaxGroups];
+#pragma unroll
+    for (int g = 0; g < kWaveMaxGroups; ++g) {
+        const size_t at = first + (size_t)min((uint32_t)g, groups - 1u) * kTile;
+        w[g] = gload(it.j.wbits + at);
+        sc[g] = gload(it.j.wscale + at);
+    }
+    lds_planes[wave][lane] = p0;
+    lds_planes[wave][lane + 64u] = p1;
+    __builtin_amdgcn_wave_barrier();
+    const uint4* lp = lds_planes[wave];
+    const uint32_t n0 = it.t0 * kTile;
+    const bool live = n0 + lane < it.j.n;
+    unsigned char* orow = it.j.out + (size_t)it.row * it.j.out_stride;
+    if (it.j.mode != MODE_DOT_I16) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kWaveMaxGroups; ++g) {
+            if ((uint32_t)g < groups) {
+                const int d = group_dot_v(w[g], lp + g * (kPlaneWords / 4), -__shfl(sum, g));
+                acc = acc + __half2float(__ushort_as_half((uint16_t)sc[g])) * (float)d;
+            }
+        }
+        if (it.j.mode == MODE_SUM_SCALED)
+            acc = acc * gload(it.j.rscale + it.row);
+        if (live)
+            gstore(reinterpret_cast<float*>(orow) + n0 + lane, acc);
+    } else {
+        int dv[kWaveMaxGroups];
+#pragma unroll
+        for (int g = 0; g < kWaveMaxGroups; ++g) {
+            if ((uint32_t)g < groups)
+                dv[g] = group_dot_v(w[g], lp + g * (kPlaneWords / 4), -__shfl(sum, g));
+        }
+        int16_t* o = reinterpret_cast<int16_t*>(orow) + (size_t)(n0 + lane) * groups;
+#pragma unroll
+        for (int g = 0; g < kWaveMaxGroups; ++g) {
+            if ((uint32_t)g < groups && live)
+                gstore(o + g, (int16_t)dv[g]);
+        }
+    }
+}
+
+template <int MAXG, int MAP, int TPI>
 hipError_t launch_dot_t(hipStream_t stream, const DotJob& single, const DotJob* jobs, const uint32_t* item_job,
                         uint32_t items, uint32_t uniform_items, uint32_t grid, uint64_t seq, const uint64_t* flag) {
-    hipLaunchKernelGGL((k_dot<MAXG, MAP>), dim3(grid), dim3(64 * kDotWaves), 0, stream, single, jobs, item_job,
-                       items, uniform_items, seq, flag);
+    hipLaunchKernelGGL((k_dot<MAXG, MAP, TPI, BNN_DOT_PREFETCH != 0>), dim3(grid), dim3(64 * kDotWaves), 0, stream,
+                       single, jobs, item_job, items, uniform_items, seq, flag);
     return hipGetLastError();
 }
 
@@ -432,6 +623,13 @@ hipError_t launch_prep_batch(hipStream_t stream, const PrepJob* jobs, const uint
     return hipGetLastError();
 }
 
+uint32_t dot_tiles_per_item(uint32_t max_groups) { return max_groups <= 16u ? BNN_DOT_TPI_SMALL : 1u; }
+
+uint32_t dot_items(uint32_t tiles, uint32_t rows, uint32_t max_groups) {
+    const uint32_t tpi = dot_tiles_per_item(max_groups);
+    return rows * ((tiles + tpi - 1u) / tpi);
+}
+
 static uint32_t dot_grid(uint32_t items, uint32_t max_groups, uint32_t cu_count) {
     const uint32_t per_cu = max_groups <= 16u ? kDotWgsPerCuSmall : kDotWgsPerCuLarge;
     const uint32_t cap = (cu_count ? cu_count : 256u) * per_cu;
@@ -440,25 +638,38 @@ static uint32_t dot_grid(uint32_t items, uint32_t max_groups, uint32_t cu_count)
 
 hipError_t launch_dot(hipStream_t stream, const DotJob& job, uint32_t cu_count, uint64_t seq,
                       const uint64_t* flag) {
-    const uint32_t items = job.tiles * job.rows;
+    const uint32_t items = dot_items(job.tiles, job.rows, job.groups);
     const uint32_t grid = dot_grid(items, job.groups, cu_count);
     if (job.groups <= 16u)
-        return launch_dot_t<16, MAP_SINGLE>(stream, job, nullptr, nullptr, items, 0, grid, seq, flag);
-    return launch_dot_t<64, MAP_SINGLE>(stream, job, nullptr, nullptr, items, 0, grid, seq, flag);
+        return launch_dot_t<16, MAP_SINGLE, BNN_DOT_TPI_SMALL>(stream, job, nullptr, nullptr, items, 0, grid, seq,
+                                                               flag);
+    return launch_dot_t<64, MAP_SINGLE, 1>(stream, job, nullptr, nullptr, items, 0, grid, seq, flag);
 }
 
 hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32_t* item_job, uint32_t items,
                             uint32_t uniform_items, uint32_t max_groups, uint32_t cu_count, uint64_t seq,
                             const uint64_t* flag) {
     DotJob none = {};
+    if (BNN_DOT_WAVE_ITEMS && max_groups <= (uint32_t)kWaveMaxGroups) {
+        const uint32_t grid = (items + BNN_DOT_WAVE_WG_WAVES - 1u) / BNN_DOT_WAVE_WG_WAVES;
+        const dim3 block(64 * BNN_DOT_WAVE_WG_WAVES);
+        if (uniform_items)
+            hipLaunchKernelGGL(k_dot_wave<MAP_UNIFORM>, dim3(grid), block, 0, stream, jobs, item_job, items,
+                               uniform_items, seq, flag);
+        else
+            hipLaunchKernelGGL(k_dot_wave<MAP_TABLE>, dim3(grid), block, 0, stream, jobs, item_job, items, 0u, seq,
+                               flag);
+        return hipGetLastError();
+    }
     const uint32_t grid = dot_grid(items, max_groups, cu_count);
     if (max_groups <= 16u)
-        return uniform_items
-                   ? launch_dot_t<16, MAP_UNIFORM>(stream, none, jobs, item_job, items, uniform_items, grid, seq, flag)
-                   : launch_dot_t<16, MAP_TABLE>(stream, none, jobs, item_job, items, 0, grid, seq, flag);
+        return uniform_items ? launch_dot_t<16, MAP_UNIFORM, BNN_DOT_TPI_SMALL>(stream, none, jobs, item_job, items,
+                                                                               uniform_items, grid, seq, flag)
+                             : launch_dot_t<16, MAP_TABLE, BNN_DOT_TPI_SMALL>(stream, none, jobs, item_job, items, 0,
+                                                                             grid, seq, flag);
     return uniform_items
-               ? launch_dot_t<64, MAP_UNIFORM>(stream, none, jobs, item_job, items, uniform_items, grid, seq, flag)
-               : launch_dot_t<64, MAP_TABLE>(stream, none, jobs, item_job, items, 0, grid, seq, flag);
+               ? launch_dot_t<64, MAP_UNIFORM, 1>(stream, none, jobs, item_job, items, uniform_items, grid, seq, flag)
+               : launch_dot_t<64, MAP_TABLE, 1>(stream, none, jobs, item_job, items, 0, grid, seq, flag);
 }
 
 hipError_t launch_scatter(hipStream_t stream, const unsigned char* src, size_t src_stride, unsigned char* dst,

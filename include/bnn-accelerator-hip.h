@@ -18,7 +18,8 @@ extern "C" {
 enum {
     BNNX_KERNEL_PREP = 0,    /* row validation + quantisation + bit planes */
     BNNX_KERNEL_DOT = 1,     /* group dots + FP32 scale accumulation (the dominant kernel) */
-    BNNX_KERNEL_SCATTER = 2  /* copy into odd (unaligned) output views */
+    BNNX_KERNEL_SCATTER = 2, /* copy into odd (unaligned) output views */
+    BNNX_KERNEL_GEMM = 3     /* multi-row jobs on the matrix cores */
 };
 
 /* The hipStream_t (as void*) on which every transfer and kernel of the device runs. */

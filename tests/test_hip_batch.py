@@ -60,7 +60,9 @@ def _free(mats, bi, bo):
     [("GEMV_F32", 2048, 6144, 1)] * 12,                                   # uniform
     [("GEMV_F32", 2048, 2048, 1), ("GEMV", 6144, 2048, 1), ("DOT_GROUPS", 384, 70, 3),
      ("GEMM_F32", 8192, 129, 5), ("GEMM", 128, 1, 2), ("GEMV_F32", 2048, 8192, 1)],  # mixed
-], ids=["uniform", "mixed"])
+    [("GEMV_F32", 2048, 2048, 1), ("GEMV", 1024, 100, 1), ("DOT_GROUPS", 384, 70, 3),
+     ("GEMM_F32", 2048, 129, 5), ("GEMM", 128, 1, 2), ("DOT_GROUPS", 2048, 64, 2)],  # mixed, K <= 2048
+], ids=["uniform", "mixed", "mixed_small"])
 def test_batch_equals_single_jobs(pkg, hipdev, specs):
     mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs)
     assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, len(specs)) == pkg.Status.OK
