@@ -1,0 +1,149 @@
+/* Test infrastructure: a minimal driver of the BNN engine API (bnn-engine.h), linked
+ * either with the reference engine sources (bnn-sw-v2, compiled where they lie) or
+ * with this project's libbnn_engine.so, so that both engines can be run on the same
+ * GGUF file and their outputs compared bit for bit.  Not part of the product.
+ *
+ *   engine_run llm MODEL.gguf IDS_FILE STEPS CTX
+ *       prefill the prompt IDs, then STEPS greedy steps (no EOG stop); prints
+ *       "step <i> <argmax> <fnv64 of the logits bytes>" per decode call and a
+ *       "stats" line (BNNE_Stats fields)
+ *   engine_run classify MODEL.gguf INPUT_F32 SAMPLES BATCH
+ *       classifies SAMPLES rows of raw float32 input, BATCH per call; prints every
+ *       logit as 8 hex digits (its float32 bit pattern), one sample per line
+ */
+#include "bnn-engine.h"
+
+#include <inttypes.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static uint64_t fnv64(const void* data, size_t n) {
+    const unsigned char* p = data;
+    uint64_t h = 1469598103934665603ull;
+    for (size_t i = 0; i < n; i++) {
+        h ^= p[i];
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+static int fail(const char* what, BNNE_Status st) {
+    fprintf(stderr, "error: %s: %s (%s)\n", what, BNNE_StatusString(st), BNNE_LastError());
+    return 2;
+}
+
+static uint32_t argmax(const float* v, uint32_t n) {
+    uint32_t best = 0;
+    for (uint32_t i = 1; i < n; i++)
+        if (v[i] > v[best])
+            best = i;
+    return best;
+}
+
+static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint32_t ctx) {
+    BNNE_ModelInfo info;
+    BNNE_Status st = BNNE_ModelGetInfo(model, &info);
+    if (st != BNNE_OK)
+        return fail("BNNE_ModelGetInfo", st);
+    int32_t* ids = malloc((size_t)ctx * sizeof *ids);
+    float* logits = malloc((size_t)info.n_vocab * sizeof *logits);
+    FILE* f = fopen(ids_path, "r");
+    if (!ids || !logits || !f)
+        return 2;
+    uint32_t count = 0;
+    long v;
+    while (count < ctx && fscanf(f, "%ld", &v) == 1)
+        ids[count++] = (int32_t)v;
+    fclose(f);
+    BNNE_ContextParams params;
+    BNNE_ContextParamsInit(&params);
+    params.n_ctx = ctx;
+    BNNE_Context c = NULL;
+    st = BNNE_ContextCreate(model, &params, &c);
+    if (st != BNNE_OK)
+        return fail("BNNE_ContextCreate", st);
+    st = BNNE_Decode(c, ids, count, logits);
+    if (st != BNNE_OK)
+        return fail("BNNE_Decode(prefill)", st);
+    int32_t next = (int32_t)argmax(logits, info.n_vocab);
+    printf("step 0 %d %016" PRIx64 "\n", next, fnv64(logits, (size_t)info.n_vocab * 4));
+    for (uint32_t s = 1; s <= steps; s++) {
+        st = BNNE_Decode(c, &next, 1, logits);
+        if (st != BNNE_OK)
+            return fail("BNNE_Decode", st);
+        next = (int32_t)argmax(logits, info.n_vocab);
+        printf("step %u %d %016" PRIx64 "\n", s, next, fnv64(logits, (size_t)info.n_vocab * 4));
+        fflush(stdout);
+    }
+    BNNE_Stats stats;
+    BNNE_ContextGetStats(c, &stats);
+    printf("stats calls=%" PRIu64 " items=%" PRIu64 " total_ns=%" PRIu64 " transfer_ns=%" PRIu64
+           " execute_ns=%" PRIu64 " host_ns=%" PRIu64 " device_calls=%" PRIu64 "\n",
+           stats.calls, stats.items, stats.total_ns, stats.transfer_ns, stats.execute_ns, stats.host_ns,
+           stats.device_calls);
+    BNNE_ContextFree(c);
+    free(ids);
+    free(logits);
+    return 0;
+}
+
+static int run_classify(BNNE_Model model, const char* input_path, uint32_t samples, uint32_t batch) {
+    BNNE_ModelInfo info;
+    BNNE_Status st = BNNE_ModelGetInfo(model, &info);
+    if (st != BNNE_OK)
+        return fail("BNNE_ModelGetInfo", st);
+    float* x = malloc((size_t)samples * info.input_size * sizeof *x);
+    float* logits = malloc((size_t)batch * info.n_classes * sizeof *logits);
+    FILE* f = fopen(input_path, "rb");
+    if (!x || !logits || !f || fread(x, sizeof *x, (size_t)samples * info.input_size, f) !=
+                                   (size_t)samples * info.input_size)
+        return 2;
+    fclose(f);
+    BNNE_ContextParams params;
+    BNNE_ContextParamsInit(&params);
+    params.n_batch = batch;
+    BNNE_Context c = NULL;
+    st = BNNE_ContextCreate(model, &params, &c);
+    if (st != BNNE_OK)
+        return fail("BNNE_ContextCreate", st);
+    for (uint32_t s0 = 0; s0 < samples; s0 += batch) {
+        const uint32_t n = samples - s0 < batch ? samples - s0 : batch;
+        st = BNNE_Classify(c, x + (size_t)s0 * info.input_size, n, logits);
+        if (st != BNNE_OK)
+            return fail("BNNE_Classify", st);
+        for (uint32_t i = 0; i < n; i++) {
+            for (uint32_t k = 0; k < info.n_classes; k++) {
+                uint32_t bits;
+                memcpy(&bits, &logits[(size_t)i * info.n_classes + k], 4);
+                printf("%08x%c", bits, k + 1 == info.n_classes ? '\n' : ' ');
+            }
+        }
+    }
+    BNNE_ContextFree(c);
+    free(x);
+    free(logits);
+    return 0;
+}
+
+int main(int argc, char** argv) {
+    if (argc != 6 || (strcmp(argv[1], "llm") != 0 && strcmp(argv[1], "classify") != 0)) {
+        fprintf(stderr, "usage: %s llm MODEL IDS STEPS CTX | classify MODEL INPUT SAMPLES BATCH\n", argv[0]);
+        return 1;
+    }
+    BNN_Device dev = NULL;
+    BNN_Status ds = BNN_DeviceOpen(0, &dev);
+    if (ds != BNN_OK) {
+        fprintf(stderr, "error: BNN_DeviceOpen: %s\n", BNN_StatusString(ds));
+        return 2;
+    }
+    BNNE_Model model = NULL;
+    BNNE_Status st = BNNE_ModelLoad(dev, argv[2], &model);
+    if (st != BNNE_OK)
+        return fail("BNNE_ModelLoad", st);
+    const uint32_t a = (uint32_t)strtoul(argv[4], NULL, 10), b = (uint32_t)strtoul(argv[5], NULL, 10);
+    const int rc = strcmp(argv[1], "llm") == 0 ? run_llm(model, argv[3], a, b) : run_classify(model, argv[3], a, b);
+    BNNE_ModelFree(model);
+    BNN_DeviceClose(dev);
+    return rc;
+}

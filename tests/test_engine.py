@@ -1,0 +1,291 @@
+"""The model engine (lib/libbnn_engine.so): the caller of the accelerator API.
+
+CPU: the restated bnn-engine.h ABI, the exported symbols, the GGUF writer (format
+and determinism), format errors of the engine's GGUF reader, and the reference
+engine (soft backend) reproducing the committed fixtures from the same seeded models.
+GPU: this engine on the HIP backend (and the reference engine on the HIP backend)
+reproduces the reference engine + soft backend: every decode step's greedy token and
+the FNV-1a-64 hash of all logits bytes (bit-exact logits), every classifier logit.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import json
+import re
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, PKG_DIR, REF_DIR, ROOT
+
+ENGINE_RUN_OWN = ROOT / "oracle" / "lib" / "engine_run_own"
+ENGINE_RUN_SOFT = REF_DIR / "engine_run_soft"
+ENGINE_RUN_REFHIP = REF_DIR / "engine_run_refhip"
+TINY = json.loads((GOLDEN / "e2e_qwen3_tiny.json").read_text())
+MLP = json.loads((GOLDEN / "e2e_bnn_mlp.json").read_text())
+FULL_FIXTURE = GOLDEN / "e2e_qwen3_1p7b.json"
+
+
+def engine_declared() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "bnn-engine.h").read_text(), flags=re.S)
+    return set(re.findall(r"(BNNE_\w+)\s*\(", text))
+
+
+def parse_llm(text: str) -> list[list]:
+    return [[int(f[1]), int(f[2]), f[3]] for f in (ln.split() for ln in text.splitlines()) if f and f[0] == "step"]
+
+
+def write_tiny(pkg, tmp_path):
+    model, ids = tmp_path / "tiny.gguf", tmp_path / "ids.txt"
+    pkg.gguf.qwen3_random(model, **TINY["model"])
+    ids.write_text(" ".join(map(str, TINY["prompt"])) + "\n")
+    return model, ids
+
+
+def write_mlp(pkg, tmp_path):
+    model, inp = tmp_path / "mlp.gguf", tmp_path / "in.f32"
+    pkg.gguf.bnn_mlp_random(model, dims=tuple(MLP["dims"]), seed=MLP["seed"])
+    pkg.gguf.bnn_mlp_inputs(MLP["samples"]).tofile(inp)
+    return model, inp
+
+
+def check_mlp_output(text: str):
+    rows = [r.split() for r in text.splitlines()]
+    logits = np.array([[int(h, 16) for h in r] for r in rows], dtype=np.uint32)
+    assert [" ".join(r) for r in rows[:4]] == MLP["first_rows_hex"]
+    assert [int(i) for i in logits.view(np.float32).argmax(axis=1)] == MLP["argmax"]
+    assert hashlib.sha256(logits.tobytes()).hexdigest() == MLP["logits_sha256"]
+
+
+# ----------------------------------------------------------------------------- CPU
+
+
+def test_engine_header_abi_matches_reference():
+    probe = ROOT / "oracle" / "lib" / "engine_abi_probe_own"
+    own = subprocess.run([str(probe)], capture_output=True, text=True, check=True).stdout
+    assert own == (GOLDEN / "engine_abi_layout.txt").read_text()
+
+
+def test_engine_library_exports_exactly_the_header(pkg):
+    lib = pkg.engine.ENGINE_LIBRARY
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib)], capture_output=True, text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    assert exported == engine_declared()
+    needed = subprocess.run(["readelf", "-d", str(lib)], capture_output=True, text=True, check=True).stdout
+    assert "libbnn_hip.so" in needed and "oracle" not in needed
+    for src in (PKG_DIR / "engine").glob("*"):
+        assert "oracle" not in src.read_text().lower(), src
+
+
+def read_gguf(path):
+    """Independent minimal GGUF v3 parser (metadata scalars/strings, tensor table)."""
+    data = path.read_bytes()
+    pos = 0
+
+    def take(fmt):
+        nonlocal pos
+        v = struct.unpack_from(fmt, data, pos)
+        pos += struct.calcsize(fmt)
+        return v if len(v) > 1 else v[0]
+
+    def string():
+        n = take("<Q")
+        nonlocal pos
+        s = data[pos:pos + n]
+        pos += n
+        return s.decode("utf-8")
+
+    scalar = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<B", 10: "<Q", 11: "<q", 12: "<d"}
+
+    def value(t):
+        if t == 8:
+            return string()
+        if t == 9:
+            et, n = take("<I"), take("<Q")
+            return [value(et) for _ in range(n)]
+        return take(scalar[t])
+
+    assert data[:4] == b"GGUF"
+    pos = 4
+    version, n_tensors, n_kv = take("<I"), take("<Q"), take("<Q")
+    kv = {}
+    for _ in range(n_kv):
+        k = string()
+        kv[k] = value(take("<I"))
+    tensors = {}
+    for _ in range(n_tensors):
+        name = string()
+        rank = take("<I")
+        dims = [take("<Q") for _ in range(rank)]
+        ttype, off = take("<I"), take("<Q")
+        tensors[name] = (dims, ttype, off)
+    align = kv.get("general.alignment", 32)
+    base = (pos + align - 1) // align * align
+    return version, kv, tensors, base, data
+
+
+def test_gguf_writer_format(pkg, tmp_path):
+    path = tmp_path / "m.gguf"
+    pkg.gguf.qwen3_random(path, **TINY["model"])
+    version, kv, tensors, base, data = read_gguf(path)
+    m = TINY["model"]
+    assert version == 3 and kv["general.architecture"] == "qwen3"
+    assert kv["qwen3.block_count"] == m["layers"] and kv["qwen3.embedding_length"] == m["hidden"]
+    assert len(kv["tokenizer.ggml.tokens"]) == m["vocab"]
+    assert len(set(kv["tokenizer.ggml.tokens"][:256])) == 256
+    assert len(tensors) == 2 + 11 * m["layers"]
+    dims, ttype, off = tensors["blk.1.ffn_down.weight"]
+    assert dims == [m["ffn"], m["hidden"]] and ttype == 41 and off % 32 == 0
+    payload = data[base + off: base + off + m["hidden"] * (m["ffn"] // 128) * 18]
+    bits, scales = pkg.gguf.q1_0_split(payload, m["ffn"], m["hidden"])
+    assert pkg.gguf.q1_0_blocks(bits, scales) == payload
+    assert np.all(scales == np.float16(1 / np.sqrt(m["ffn"])).view(np.uint16))
+    # deterministic: the same seed writes the same bytes
+    path2 = tmp_path / "m2.gguf"
+    pkg.gguf.qwen3_random(path2, **TINY["model"])
+    assert path.read_bytes() == path2.read_bytes()
+
+
+def _engine_lib(pkg):
+    return pkg.engine.EngineLib()
+
+
+@pytest.mark.parametrize("case", ["missing", "magic", "version", "truncated", "no_tensors", "arch", "tensor_type"])
+def test_engine_format_errors_without_device(pkg, tmp_path, case):
+    """Malformed files fail inside the GGUF reader, before the device is used."""
+    eng = _engine_lib(pkg)
+    w = pkg.gguf.Writer()
+    w.string("general.architecture", "nosuch" if case == "arch" else "qwen3")
+    if case == "tensor_type":
+        w.tensors.append(("t", (4,), 2, b"\0" * 8))  # Q4_0 and others are not accepted
+    elif case != "no_tensors":
+        w.tensor("t", (4,), pkg.gguf.TYPE_F32, b"\0" * 16)
+    path = tmp_path / "bad.gguf"
+    w.write(path)
+    raw = bytearray(path.read_bytes())
+    if case == "magic":
+        raw[0:4] = b"GGUX"
+    elif case == "version":
+        raw[4:8] = struct.pack("<I", 2)
+    elif case == "truncated":
+        raw = raw[:40]
+    path.write_bytes(bytes(raw))
+    if case == "missing":
+        path = tmp_path / "absent.gguf"
+    fake_device = ctypes.c_void_p(1)  # never dereferenced on these paths
+    h = ctypes.c_void_p()
+    st = eng.BNNE_ModelLoad(fake_device, str(path).encode(), ctypes.byref(h))
+    want = {"missing": -5, "arch": -3, "tensor_type": -3}.get(case, -6)
+    assert st == want, (case, st, eng.BNNE_LastError())
+    assert not h.value
+    assert eng.BNNE_ModelLoad(None, str(path).encode(), ctypes.byref(h)) == -1
+
+
+def test_engine_status_strings(pkg):
+    eng = _engine_lib(pkg)
+    assert eng.BNNE_StatusString(0) == b"success"
+    assert eng.BNNE_StatusString(-6) == b"invalid or truncated model"
+    assert eng.BNNE_StatusString(5) == b"unknown status"
+
+
+@pytest.mark.skipif(not ENGINE_RUN_SOFT.exists(), reason="reference engine not built (no reference tree)")
+def test_reference_engine_reproduces_fixtures(pkg, tmp_path):
+    """The committed fixtures are what the reference engine + soft backend compute on
+    the models this package writes (pins the writer and the fixture together)."""
+    model, ids = write_tiny(pkg, tmp_path)
+    out = subprocess.run([str(ENGINE_RUN_SOFT), "llm", str(model), str(ids), str(TINY["steps_arg"]),
+                          str(TINY["ctx"])], capture_output=True, text=True, check=True).stdout
+    assert parse_llm(out) == TINY["steps"]
+    model, inp = write_mlp(pkg, tmp_path)
+    out = subprocess.run([str(ENGINE_RUN_SOFT), "classify", str(model), str(inp), str(MLP["samples"]),
+                          str(MLP["batch"])], capture_output=True, text=True, check=True).stdout
+    check_mlp_output(out)
+
+
+# ----------------------------------------------------------------------------- GPU
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("runner", ["own", "refhip"])
+def test_engine_qwen3_tiny_bit_exact(pkg, tmp_path, runner):
+    exe = ENGINE_RUN_OWN if runner == "own" else ENGINE_RUN_REFHIP
+    if runner == "refhip" and not exe.exists():
+        pytest.skip("reference engine on HIP not built")
+    model, ids = write_tiny(pkg, tmp_path)
+    print(f"engine qwen3 tiny via {exe.name}", flush=True)
+    out = subprocess.run([str(exe), "llm", str(model), str(ids), str(TINY["steps_arg"]), str(TINY["ctx"])],
+                         capture_output=True, text=True, timeout=120, check=True).stdout
+    assert parse_llm(out) == TINY["steps"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("runner", ["own", "refhip"])
+def test_engine_bnn_mlp_bit_exact(pkg, tmp_path, runner):
+    exe = ENGINE_RUN_OWN if runner == "own" else ENGINE_RUN_REFHIP
+    if runner == "refhip" and not exe.exists():
+        pytest.skip("reference engine on HIP not built")
+    model, inp = write_mlp(pkg, tmp_path)
+    print(f"engine bnn-mlp via {exe.name}", flush=True)
+    out = subprocess.run([str(exe), "classify", str(model), str(inp), str(MLP["samples"]), str(MLP["batch"])],
+                         capture_output=True, text=True, timeout=120, check=True).stdout
+    check_mlp_output(out)
+
+
+@pytest.mark.gpu
+def test_engine_api_behaviour(pkg, hip, tmp_path):
+    """Argument and range checks of the public API on a loaded model (engine.c:241-338)."""
+    model_path, _ = write_tiny(pkg, tmp_path)
+    eng = _engine_lib(pkg)
+    with pkg.Device(hip, 0) as dev:
+        m = pkg.engine.Model(eng, dev, model_path)
+        assert m.info.task == pkg.engine.TASK_LLM and m.info.n_vocab == TINY["model"]["vocab"]
+        assert m.info.n_ctx_train == TINY["model"]["context"] and m.info.eos_token == -1
+        with pytest.raises(pkg.engine.EngineError) as e:
+            pkg.engine.Context(m, n_ctx=TINY["model"]["context"] + 1)
+        assert e.value.status == -4
+        c = pkg.engine.Context(m, n_ctx=16, n_batch=4)
+        prompt = TINY["prompt"]
+        with pytest.raises(pkg.engine.EngineError) as e:
+            c.decode(prompt[:5])  # more than n_batch
+        assert e.value.status == -4
+        with pytest.raises(pkg.engine.EngineError) as e:
+            c.decode([TINY["model"]["vocab"]])  # outside the vocabulary
+        assert e.value.status == -4 and c.pos() == 0
+        with pytest.raises(pkg.engine.EngineError) as e:
+            c.classify(np.zeros((1, 4), np.float32))
+        assert e.value.status == -3
+        logits = None
+        for i in range(0, 8, 4):
+            logits = c.decode(prompt[i:i + 4])
+        assert c.pos() == 8 and int(np.argmax(logits)) == TINY["steps"][0][1]
+        s = c.stats()
+        assert s["calls"] == 2 and s["items"] == 8
+        assert s["device_calls"] == 8 * 2 * 7 + 2  # 7 linears per layer per token, lm_head once per call
+        assert s["total_ns"] >= s["transfer_ns"] + s["execute_ns"]
+        assert eng.BNNE_ContextTruncate(c.handle, 9) == -1
+        assert eng.BNNE_ContextTruncate(c.handle, 4) == 0 and c.pos() == 4
+        c.reset_stats()
+        assert c.stats()["calls"] == 0
+        tok = (ctypes.c_int32 * 4)()
+        n = ctypes.c_uint32()
+        assert eng.BNNE_Tokenize(m.handle, b"hi", 1, tok, 4, ctypes.byref(n)) == -3
+        c.free()
+        m.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not FULL_FIXTURE.exists(), reason="full-size fixture not generated")
+def test_engine_qwen3_1p7b_matches_reference(pkg, tmp_path):
+    """Benchmark configuration 5 at full Qwen3-1.7B shape: 32 prompt tokens, 128
+    greedy tokens; every step's token and logits hash equal the reference engine's."""
+    full = json.loads(FULL_FIXTURE.read_text())
+    model, ids = tmp_path / "q.gguf", tmp_path / "ids.txt"
+    pkg.gguf.qwen3_random(model)
+    ids.write_text(" ".join(map(str, full["prompt"])) + "\n")
+    print("engine qwen3 1.7B-shape decode, 32 + 128 tokens", flush=True)
+    out = subprocess.run([str(ENGINE_RUN_OWN), "llm", str(model), str(ids), str(full["steps_arg"]),
+                          str(full["ctx"])], capture_output=True, text=True, timeout=600, check=True).stdout
+    assert parse_llm(out) == full["steps"]
