@@ -157,6 +157,12 @@ class Api:
             "BNNX_KernelTimingRead": (S, [V, U32, P(ctypes.c_double), P(ctypes.c_uint64)]),
             "BNNX_DeviceName": (S, [V, ctypes.c_char_p, SZ, ctypes.c_char_p, SZ]),
             "BNNX_ExecuteBatch": (S, [V, P(Job), U32]),
+            "BNNX_BatchCreate": (S, [V, P(Job), U32, P(V)]),
+            "BNNX_BatchLaunch": (S, [V]),
+            "BNNX_BatchCheck": (S, [V]),
+            "BNNX_BatchDestroy": (None, [V]),
+            "BNNX_DeviceSynchronize": (S, [V]),
+            "BNNX_BufferDevicePointer": (S, [V, P(V)]),
         }
         self.extensions = set()
         for name, (res, args) in ext.items():

@@ -242,7 +242,7 @@ EXPORT BNN_Status BNN_DeviceOpen(uint32_t device_index, BNN_Device* out_device) 
 EXPORT BNN_Status BNN_DeviceClose(BNN_Device device) {
     if (device == nullptr)
         return BNN_EINVAL;
-    if (device->live_matrices != 0 || device->live_buffers != 0)
+    if (device->live_matrices != 0 || device->live_buffers != 0 || device->live_batches != 0)
         return BNN_EBUSY;
     (void)hipSetDevice(device->ordinal);
     (void)hipStreamSynchronize(device->stream);
@@ -388,6 +388,7 @@ EXPORT void BNN_MatrixDestroy(BNN_Matrix matrix) {
         (void)hipFree(matrix->wbytes);
     matrix->device->live_matrices--;
     matrix->device->generation++;
+    matrix->device->retired++;
     free(matrix);
 }
 
@@ -432,6 +433,7 @@ EXPORT void BNN_BufferFree(BNN_Buffer buffer) {
     (void)hipFree(buffer->dev);
     buffer->device->live_buffers--;
     buffer->device->generation++;
+    buffer->device->retired++;
     free(buffer);
 }
 
@@ -751,6 +753,125 @@ BNN_Status ensure_tables(BNN_Device d, size_t bytes) {
     return BNN_OK;
 }
 
+// All checks of a batch (per job as BNN_Execute, then the batch rules) and the
+// sizes of its scratch and job tables.
+struct BatchPlan {
+    JobPlan* plans = nullptr;
+    uint32_t count = 0;
+    bool needs_nearest = false, uniform = true;
+    uint64_t prep_blocks = 0, dot_items_total = 0;
+    size_t scratch_bytes = 0;
+    uint32_t max_groups = 0;
+    // tables: PrepJob[count] | DotJob[count] | prep block->job | dot item->job (non-uniform only)
+    size_t prep_tab = 0, dot_tab = 0, prep_map = 0, dot_map = 0, tables = 0;
+    ~BatchPlan() { free(plans); }
+};
+
+BNN_Status plan_batch(BNN_Device device, const BNN_Job* jobs, uint32_t count, BatchPlan* bp) {
+    bp->plans = static_cast<JobPlan*>(malloc(sizeof(JobPlan) * count));
+    bp->count = count;
+    Extent* outs = static_cast<Extent*>(malloc(sizeof(Extent) * count));
+    const void** ins = static_cast<const void**>(malloc(sizeof(void*) * count));
+    BNN_Status st = bp->plans && outs && ins ? BNN_OK : BNN_ENOMEM;
+    for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
+        st = plan_job(device, &jobs[i], &bp->plans[i]);
+        if (st != BNN_OK)
+            break;
+        const JobPlan& p = bp->plans[i];
+        if (!p.in_aligned || !p.out_aligned || jobs[i].rows > kScratchRowsCap) {
+            st = BNN_ENOTSUP;
+            break;
+        }
+        bp->needs_nearest = bp->needs_nearest || !p.dot_out;
+        size_t a, b, c;
+        bp->scratch_bytes += row_scratch_bytes(p, jobs[i].rows, &a, &b, &c);
+        bp->prep_blocks += jobs[i].rows;
+        bp->max_groups = p.m->groups > bp->max_groups ? p.m->groups : bp->max_groups;
+        outs[i].buffer = jobs[i].output.buffer;
+        outs[i].begin = jobs[i].output.offset;
+        outs[i].end = jobs[i].output.offset + (size_t)(jobs[i].rows - 1) * p.out_stride + p.out_row;
+        ins[i] = jobs[i].input.buffer;
+    }
+    // work items per job depend on the batch's largest group count
+    for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
+        const uint64_t items = dot_items(bp->plans[i].m->tiles, jobs[i].rows, bp->max_groups);
+        bp->uniform = bp->uniform && items == dot_items(bp->plans[0].m->tiles, jobs[0].rows, bp->max_groups);
+        bp->dot_items_total += items;
+    }
+    // the jobs run concurrently: no output buffer may be an input buffer, and
+    // outputs sharing a buffer may not overlap
+    if (st == BNN_OK) {
+        std::sort(ins, ins + count);
+        std::sort(outs, outs + count, extent_less);
+        for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
+            if (std::binary_search(ins, ins + count, outs[i].buffer))
+                st = BNN_EINVAL;
+            else if (i > 0 && outs[i].buffer == outs[i - 1].buffer && outs[i].begin < outs[i - 1].end)
+                st = BNN_EINVAL;
+        }
+        if (st == BNN_OK && (bp->prep_blocks > 0x7fffffffu || bp->dot_items_total > 0x7fffffffu))
+            st = BNN_ENOTSUP;
+    }
+    free(outs);
+    free(ins);
+    if (st == BNN_OK) {
+        bp->prep_tab = round_up(sizeof(PrepJob) * count, 256);
+        bp->dot_tab = round_up(sizeof(DotJob) * count, 256);
+        bp->prep_map = round_up(4u * bp->prep_blocks, 256);
+        bp->dot_map = bp->uniform ? 0 : round_up(4u * bp->dot_items_total, 256);
+        bp->tables = bp->prep_tab + bp->dot_tab + bp->prep_map + bp->dot_map;
+    }
+    return st;
+}
+
+// Writes the job tables of a planned batch into host memory, with the rows'
+// quantised forms placed consecutively from 'scratch' (a device address).
+void fill_batch_tables(const BatchPlan& bp, const BNN_Job* jobs, unsigned char* scratch, unsigned char* host) {
+    PrepJob* hp = reinterpret_cast<PrepJob*>(host);
+    DotJob* hd = reinterpret_cast<DotJob*>(host + bp.prep_tab);
+    uint32_t* hpm = reinterpret_cast<uint32_t*>(host + bp.prep_tab + bp.dot_tab);
+    uint32_t* hdm = reinterpret_cast<uint32_t*>(host + bp.prep_tab + bp.dot_tab + bp.prep_map);
+    size_t soff = 0;
+    uint32_t pb = 0, di = 0;
+    for (uint32_t i = 0; i < bp.count; ++i) {
+        const JobPlan& p = bp.plans[i];
+        const uint32_t rows = jobs[i].rows;
+        size_t a, b, c;
+        hp[i] = make_prep(p, p.in_base, rows, scratch + soff);
+        hp[i].first_block = pb;
+        soff += row_scratch_bytes(p, rows, &a, &b, &c);
+        hd[i] = make_dot(p, hp[i], p.out_base, p.out_stride);
+        hd[i].first_block = di;
+        for (uint32_t r = 0; r < rows; ++r)
+            hpm[pb++] = i;
+        const uint32_t items = dot_items(p.m->tiles, rows, bp.max_groups);
+        if (!bp.uniform)
+            for (uint32_t r = 0; r < items; ++r)
+                hdm[di + r] = i;
+        di += items;
+    }
+}
+
+// The two launches of a batch whose tables start at 'tables' on the device.
+hipError_t launch_batch(BNN_Device device, const unsigned char* tables, size_t prep_tab, size_t dot_tab,
+                        size_t prep_map, uint32_t prep_blocks, uint32_t items, uint32_t uniform_items,
+                        uint32_t max_groups, uint64_t seq) {
+    const PrepJob* dp = reinterpret_cast<const PrepJob*>(tables);
+    const DotJob* dd = reinterpret_cast<const DotJob*>(tables + prep_tab);
+    const uint32_t* dpm = reinterpret_cast<const uint32_t*>(tables + prep_tab + dot_tab);
+    const uint32_t* ddm =
+        uniform_items ? nullptr : reinterpret_cast<const uint32_t*>(tables + prep_tab + dot_tab + prep_map);
+    hipError_t e = timed(device, KK_PREP, [&] {
+        return launch_prep_batch(device->stream, dp, dpm, prep_blocks, seq, device->flag_dev, device->status_host);
+    });
+    if (e == hipSuccess)
+        e = timed(device, KK_DOT, [&] {
+            return launch_dot_batch(device->stream, dd, ddm, items, uniform_items, max_groups, device->cu_count, seq,
+                                    device->flag_dev);
+        });
+    return e;
+}
+
 }  // namespace
 
 static BNN_Status run_cached_batch(BNN_Device device);
@@ -779,162 +900,181 @@ EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint
             return BNN_EIO;
         return run_cached_batch(device);
     }
-    JobPlan* plans = static_cast<JobPlan*>(malloc(sizeof(JobPlan) * count));
-    Extent* outs = static_cast<Extent*>(malloc(sizeof(Extent) * count));
-    const void** ins = static_cast<const void**>(malloc(sizeof(void*) * count));
-    BNN_Status st = plans && outs && ins ? BNN_OK : BNN_ENOMEM;
-    bool needs_nearest = false;
-    uint64_t prep_blocks = 0, dot_items_total = 0;
-    size_t scratch_bytes = 0;
-    uint32_t max_groups = 0;
-    bool uniform = true;
-    for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
-        st = plan_job(device, &jobs[i], &plans[i]);
-        if (st != BNN_OK)
-            break;
-        const JobPlan& p = plans[i];
-        if (!p.in_aligned || !p.out_aligned || jobs[i].rows > kScratchRowsCap) {
-            st = BNN_ENOTSUP;
-            break;
+    BatchPlan bp;
+    BNN_Status st = plan_batch(device, jobs, count, &bp);
+    if (st != BNN_OK)
+        return st;
+    if (hipSetDevice(device->ordinal) != hipSuccess)
+        return BNN_EIO;
+    st = ensure_scratch(device, bp.scratch_bytes);
+    if (st == BNN_OK)
+        st = ensure_tables(device, bp.tables);
+    if (st == BNN_OK && count > device->batch_cap) {
+        BNN_Job* copy = static_cast<BNN_Job*>(realloc(device->batch_jobs, sizeof(BNN_Job) * count));
+        if (copy == nullptr) {
+            st = BNN_ENOMEM;
+        } else {
+            device->batch_jobs = copy;
+            device->batch_cap = count;
         }
-        needs_nearest = needs_nearest || !p.dot_out;
-        size_t a, b, c;
-        scratch_bytes += row_scratch_bytes(p, jobs[i].rows, &a, &b, &c);
-        prep_blocks += jobs[i].rows;
-        max_groups = p.m->groups > max_groups ? p.m->groups : max_groups;
-        outs[i].buffer = jobs[i].output.buffer;
-        outs[i].begin = jobs[i].output.offset;
-        outs[i].end = jobs[i].output.offset + (size_t)(jobs[i].rows - 1) * p.out_stride + p.out_row;
-        ins[i] = jobs[i].input.buffer;
     }
-    // the jobs run concurrently: no output buffer may be an input buffer, and
-    // outputs sharing a buffer may not overlap
-    // work items per job depend on the batch's largest group count
-    for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
-        const uint64_t items = dot_items(plans[i].m->tiles, jobs[i].rows, max_groups);
-        uniform = uniform && items == dot_items(plans[0].m->tiles, jobs[0].rows, max_groups);
-        dot_items_total += items;
-    }
-    if (st == BNN_OK) {
-        std::sort(ins, ins + count);
-        std::sort(outs, outs + count, extent_less);
-        for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
-            if (std::binary_search(ins, ins + count, outs[i].buffer))
-                st = BNN_EINVAL;
-            else if (i > 0 && outs[i].buffer == outs[i - 1].buffer && outs[i].begin < outs[i - 1].end)
-                st = BNN_EINVAL;
-        }
-        if (st == BNN_OK && (prep_blocks > 0x7fffffffu || dot_items_total > 0x7fffffffu))
-            st = BNN_ENOTSUP;
-    }
-    free(outs);
-    free(ins);
     if (st != BNN_OK) {
-        free(plans);
+        device->batch_count = 0;
         return st;
     }
-    if (hipSetDevice(device->ordinal) != hipSuccess) {
-        free(plans);
+    fill_batch_tables(bp, jobs, device->scratch, device->table_host);
+    if (hipMemcpyAsync(device->table_dev, device->table_host, bp.tables, hipMemcpyHostToDevice, device->stream) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        device->batch_count = 0;
         return BNN_EIO;
     }
-
-    {
-        // tables: PrepJob[count] | DotJob[count] | prep block->job | dot item->job (non-uniform only)
-        const size_t prep_tab = round_up(sizeof(PrepJob) * count, 256);
-        const size_t dot_tab = round_up(sizeof(DotJob) * count, 256);
-        const size_t prep_map = round_up(4u * prep_blocks, 256);
-        const size_t dot_map = uniform ? 0 : round_up(4u * dot_items_total, 256);
-        const size_t tables = prep_tab + dot_tab + prep_map + dot_map;
-        st = ensure_scratch(device, scratch_bytes);
-        if (st == BNN_OK)
-            st = ensure_tables(device, tables);
-        if (st == BNN_OK && count > device->batch_cap) {
-            BNN_Job* copy = static_cast<BNN_Job*>(realloc(device->batch_jobs, sizeof(BNN_Job) * count));
-            if (copy == nullptr) {
-                st = BNN_ENOMEM;
-            } else {
-                device->batch_jobs = copy;
-                device->batch_cap = count;
-            }
-        }
-        if (st != BNN_OK) {
-            device->batch_count = 0;
-            free(plans);
-            return st;
-        }
-        PrepJob* hp = reinterpret_cast<PrepJob*>(device->table_host);
-        DotJob* hd = reinterpret_cast<DotJob*>(device->table_host + prep_tab);
-        uint32_t* hpm = reinterpret_cast<uint32_t*>(device->table_host + prep_tab + dot_tab);
-        uint32_t* hdm = reinterpret_cast<uint32_t*>(device->table_host + prep_tab + dot_tab + prep_map);
-        size_t soff = 0;
-        uint32_t pb = 0, di = 0;
-        for (uint32_t i = 0; i < count; ++i) {
-            const JobPlan& p = plans[i];
-            const uint32_t rows = jobs[i].rows;
-            size_t a, b, c;
-            hp[i] = make_prep(p, p.in_base, rows, device->scratch + soff);
-            hp[i].first_block = pb;
-            soff += row_scratch_bytes(p, rows, &a, &b, &c);
-            hd[i] = make_dot(p, hp[i], p.out_base, p.out_stride);
-            hd[i].first_block = di;
-            for (uint32_t r = 0; r < rows; ++r)
-                hpm[pb++] = i;
-            const uint32_t items = dot_items(p.m->tiles, rows, max_groups);
-            if (!uniform)
-                for (uint32_t r = 0; r < items; ++r)
-                    hdm[di + r] = i;
-            di += items;
-        }
-        hipError_t e =
-            hipMemcpyAsync(device->table_dev, device->table_host, tables, hipMemcpyHostToDevice, device->stream);
-        if (e != hipSuccess) {
-            (void)hipGetLastError();
-            device->batch_count = 0;
-            free(plans);
-            return BNN_EIO;
-        }
-        memcpy(device->batch_jobs, jobs, sizeof(BNN_Job) * count);
-        device->batch_count = count;
-        device->batch_generation = device->generation;
-        device->batch_prep_blocks = pb;
-        device->batch_items = di;
-        device->batch_uniform_items = uniform ? dot_items(plans[0].m->tiles, jobs[0].rows, max_groups) : 0u;
-        device->batch_max_groups = max_groups;
-        device->batch_prep_tab = prep_tab;
-        device->batch_dot_tab = dot_tab;
-        device->batch_prep_map = prep_map;
-        device->batch_tables = tables;
-        device->batch_needs_nearest = needs_nearest;
-    }
-    free(plans);
+    memcpy(device->batch_jobs, jobs, sizeof(BNN_Job) * count);
+    device->batch_count = count;
+    device->batch_generation = device->generation;
+    device->batch_prep_blocks = (uint32_t)bp.prep_blocks;
+    device->batch_items = (uint32_t)bp.dot_items_total;
+    device->batch_uniform_items = bp.uniform ? dot_items(bp.plans[0].m->tiles, jobs[0].rows, bp.max_groups) : 0u;
+    device->batch_max_groups = bp.max_groups;
+    device->batch_prep_tab = bp.prep_tab;
+    device->batch_dot_tab = bp.dot_tab;
+    device->batch_prep_map = bp.prep_map;
+    device->batch_tables = bp.tables;
+    device->batch_needs_nearest = bp.needs_nearest;
     return run_cached_batch(device);
 }
 
 // Launches the batch whose tables are on the device (the last one built).
 static BNN_Status run_cached_batch(BNN_Device device) {
-
-    const PrepJob* dp = reinterpret_cast<const PrepJob*>(device->table_dev);
-    const DotJob* dd = reinterpret_cast<const DotJob*>(device->table_dev + device->batch_prep_tab);
-    const uint32_t* dpm =
-        reinterpret_cast<const uint32_t*>(device->table_dev + device->batch_prep_tab + device->batch_dot_tab);
-    const uint32_t* ddm =
-        device->batch_uniform_items
-            ? nullptr
-            : reinterpret_cast<const uint32_t*>(device->table_dev + device->batch_prep_tab + device->batch_dot_tab +
-                                                device->batch_prep_map);
     const uint64_t seq = ++device->seq;
-    hipError_t e = timed(device, KK_PREP, [&] {
-        return launch_prep_batch(device->stream, dp, dpm, device->batch_prep_blocks, seq, device->flag_dev,
-                                 device->status_host);
-    });
-    if (e == hipSuccess)
-        e = timed(device, KK_DOT, [&] {
-            return launch_dot_batch(device->stream, dd, ddm, device->batch_items, device->batch_uniform_items,
-                                    device->batch_max_groups, device->cu_count, seq, device->flag_dev);
-        });
+    const hipError_t e = launch_batch(device, device->table_dev, device->batch_prep_tab, device->batch_dot_tab,
+                                      device->batch_prep_map, device->batch_prep_blocks, device->batch_items,
+                                      device->batch_uniform_items, device->batch_max_groups, seq);
     if (e != hipSuccess)
         device->batch_count = 0;
     return finish(device, e, seq);
+}
+
+// ---------------------------------------------------------------------------
+// Prepared batches (asynchronous launches) and device pointers of buffers
+// ---------------------------------------------------------------------------
+
+EXPORT BNN_Status BNNX_BatchCreate(BNN_Device device, const BNN_Job* jobs, uint32_t count, BNNX_Batch* out_batch) {
+    if (out_batch == nullptr)
+        return BNN_EINVAL;
+    *out_batch = nullptr;
+    if (device == nullptr || jobs == nullptr || count == 0)
+        return BNN_EINVAL;
+    BatchPlan bp;
+    BNN_Status st = plan_batch(device, jobs, count, &bp);
+    if (st != BNN_OK)
+        return st;
+    if (hipSetDevice(device->ordinal) != hipSuccess)
+        return BNN_EIO;
+    BNNX_Batch b = static_cast<BNNX_Batch>(calloc(1, sizeof(bnnx_batch)));
+    unsigned char* host = static_cast<unsigned char*>(malloc(bp.tables));
+    if (b == nullptr || host == nullptr) {
+        free(b);
+        free(host);
+        return BNN_ENOMEM;
+    }
+    const size_t scratch_at = round_up(bp.tables, 256);
+    void* mem = nullptr;
+    if (hipMalloc(&mem, scratch_at + bp.scratch_bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        free(b);
+        free(host);
+        return BNN_ENOMEM;
+    }
+    b->mem = static_cast<unsigned char*>(mem);
+    fill_batch_tables(bp, jobs, b->mem + scratch_at, host);
+    hipError_t e = hipMemcpy(b->mem, host, bp.tables, hipMemcpyHostToDevice);
+    free(host);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(b->mem);
+        free(b);
+        return BNN_EIO;
+    }
+    b->device = device;
+    b->retired = device->retired;
+    b->prep_blocks = (uint32_t)bp.prep_blocks;
+    b->items = (uint32_t)bp.dot_items_total;
+    b->uniform_items = bp.uniform ? dot_items(bp.plans[0].m->tiles, jobs[0].rows, bp.max_groups) : 0u;
+    b->max_groups = bp.max_groups;
+    b->prep_tab = bp.prep_tab;
+    b->dot_tab = bp.dot_tab;
+    b->prep_map = bp.prep_map;
+    b->needs_nearest = bp.needs_nearest;
+    device->live_batches++;
+    *out_batch = b;
+    return BNN_OK;
+}
+
+EXPORT BNN_Status BNNX_BatchCheck(BNNX_Batch batch) {
+    if (batch == nullptr || batch->retired != batch->device->retired)  // a matrix or buffer it uses may be gone
+        return BNN_EINVAL;
+    if (batch->needs_nearest && fegetround() != FE_TONEAREST)
+        return BNN_ENOTSUP;
+    return BNN_OK;
+}
+
+EXPORT BNN_Status BNNX_BatchLaunch(BNNX_Batch batch) {
+    const BNN_Status st = BNNX_BatchCheck(batch);
+    if (st != BNN_OK)
+        return st;
+    BNN_Device device = batch->device;
+    if (hipSetDevice(device->ordinal) != hipSuccess)
+        return BNN_EIO;
+    const uint64_t seq = ++device->seq;
+    if (device->async_first_seq == 0)
+        device->async_first_seq = seq;
+    const hipError_t e = launch_batch(device, batch->mem, batch->prep_tab, batch->dot_tab, batch->prep_map,
+                                      batch->prep_blocks, batch->items, batch->uniform_items, batch->max_groups, seq);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return BNN_EIO;
+    }
+    return BNN_OK;
+}
+
+EXPORT void BNNX_BatchDestroy(BNNX_Batch batch) {
+    if (batch == nullptr)
+        return;
+    (void)hipSetDevice(batch->device->ordinal);
+    (void)hipStreamSynchronize(batch->device->stream);
+    (void)hipFree(batch->mem);
+    batch->device->live_batches--;
+    free(batch);
+}
+
+EXPORT BNN_Status BNNX_DeviceSynchronize(BNN_Device device) {
+    if (device == nullptr)
+        return BNN_EINVAL;
+    if (hipSetDevice(device->ordinal) != hipSuccess)
+        return BNN_EIO;
+    hipError_t e = hipStreamSynchronize(device->stream);
+    if (e == hipSuccess && device->ev_used)
+        e = resolve_timing(device);
+    const uint64_t first = device->async_first_seq;
+    device->async_first_seq = 0;
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return BNN_EIO;
+    }
+    if (first != 0 && __atomic_load_n(device->status_host, __ATOMIC_ACQUIRE) >= first)
+        return BNN_ERANGE;
+    return BNN_OK;
+}
+
+EXPORT BNN_Status BNNX_BufferDevicePointer(BNN_Buffer buffer, void** out_pointer) {
+    if (out_pointer == nullptr)
+        return BNN_EINVAL;
+    *out_pointer = nullptr;
+    if (buffer == nullptr)
+        return BNN_EINVAL;
+    *out_pointer = buffer->dev;
+    return BNN_OK;
 }
 
 EXPORT const char* BNN_StatusString(BNN_Status status) {

@@ -139,7 +139,10 @@ struct bnn_accel_device {
     hipStream_t stream;
     size_t live_matrices;
     size_t live_buffers;
+    size_t live_batches;       // prepared batches (extension API)
     uint64_t seq;              // job sequence number, never 0 for a launched job
+    uint64_t async_first_seq;  // first seq launched asynchronously since the last synchronise (0: none)
+    uint64_t retired;          // matrices and buffers destroyed so far
     uint64_t* flag_dev;        // device word: seq of the last job that met an illegal input
     uint64_t* status_host;     // pinned host word, same meaning, written by the kernels
     unsigned char* scratch;    // grow-only device scratch
@@ -182,6 +185,17 @@ struct bnn_accel_matrix {
     // are -1 and never stored).  8 bits per weight, freed with the matrix.
     int8_t* wbytes;
     uint32_t n_pad;
+};
+
+// A prepared batch: job tables and the rows' scratch in one device allocation,
+// built once; every launch is two kernel launches and nothing else.
+struct bnnx_batch {
+    BNN_Device device;
+    uint64_t retired;  // device->retired when built: valid while no matrix or buffer was destroyed since
+    unsigned char* mem;
+    uint32_t prep_blocks, items, uniform_items, max_groups;
+    size_t prep_tab, dot_tab, prep_map;
+    bool needs_nearest;
 };
 
 struct bnn_accel_buffer {

@@ -92,16 +92,24 @@ __device__ __forceinline__ void raise_flag(uint64_t seq, uint64_t* flag, uint64_
 // row scale, quantises, and writes bit planes, group sums and (optionally) Q.
 // Thread t owns elements k = t + 256 i; all its loads are issued before any use.
 // ---------------------------------------------------------------------------
-constexpr int kPrepPerThread = kMaxFeatures / 256;  // 32
+#ifndef BNN_PREP_THREADS
+#define BNN_PREP_THREADS 1024  // threads per row: more waves per row, shorter serial chains
+#endif
+constexpr int kPrepThreads = BNN_PREP_THREADS;
+constexpr int kPrepWaves = kPrepThreads / 64;
+constexpr int kPrepPerThread = kMaxFeatures / kPrepThreads;
+constexpr int kPrepGroupsPerIter = kPrepThreads / kGroup;
+static_assert(kPrepThreads % 128 == 0 && kMaxFeatures % kPrepThreads == 0, "whole groups per iteration");
+static_assert(kMaxFeatures / kGroup <= kPrepThreads, "one thread per group for the group sums");
 
 template <bool F32, bool ALIGNED>
 __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uint64_t seq, uint64_t* flag,
                            uint64_t* host_status) {
-    __shared__ float red_max[4];
-    __shared__ int red_sum[kPrepPerThread][4];
+    __shared__ float red_max[kPrepWaves];
+    __shared__ int red_sum[kPrepPerThread][kPrepWaves];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t k_total = j.k, groups = k_total / kGroup;
-    const uint32_t iters = (k_total + 255u) / 256u;
+    const uint32_t iters = (k_total + kPrepThreads - 1u) / kPrepThreads;
     constexpr bool f32 = F32, aligned = ALIGNED;
     const unsigned char* row = j.in + (size_t)m * j.in_stride;
 
@@ -109,7 +117,7 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
     int raw[kPrepPerThread];  // float bits (F32) or the sign-extended byte (I8)
 #pragma unroll
     for (int i = 0; i < kPrepPerThread; ++i) {
-        const uint32_t k = tid + 256u * i;
+        const uint32_t k = tid + (uint32_t)kPrepThreads * i;
         raw[i] = 0;
         if ((uint32_t)i < iters && k < k_total)
             raw[i] = f32 ? __float_as_int(load_f32(row, k, aligned)) : (int)(int8_t)row[k];
@@ -140,7 +148,10 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
         if (lane == 0)
             red_max[wave] = amax;
         __syncthreads();
-        amax = fmaxf(fmaxf(red_max[0], red_max[1]), fmaxf(red_max[2], red_max[3]));
+        amax = red_max[0];
+#pragma unroll
+        for (int w = 1; w < kPrepWaves; ++w)
+            amax = fmaxf(amax, red_max[w]);
         if (amax != 0.0f) {
             s = amax / 127.0f;
             if (s == 0.0f)
@@ -149,11 +160,11 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
     }
 
     // pass 2: quantise; in iteration i wave w owns the 64 consecutive k of half (w & 1)
-    // of group 2i + (w >> 1)
+    // of group kPrepGroupsPerIter*i + (w >> 1)
     uint32_t* planes = j.planes ? j.planes + (size_t)m * groups * kPlaneWords : nullptr;
 #pragma unroll
     for (int i = 0; i < kPrepPerThread; ++i) {
-        const uint32_t base = 256u * i;
+        const uint32_t base = (uint32_t)kPrepThreads * i;
         if ((uint32_t)i < iters && base + wave * 64u < k_total) {  // K % 128 == 0: whole waves
             const int q = f32 ? quantize(__int_as_float(raw[i]), s) : raw[i];
             if (j.q)
@@ -172,7 +183,7 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
                 if (lane == 2u * b + 1u)
                     word = (uint32_t)(mask >> 32);
             }
-            const uint32_t g = 2u * i + (wave >> 1), half = wave & 1u;
+            const uint32_t g = (uint32_t)kPrepGroupsPerIter * i + (wave >> 1), half = wave & 1u;
             if (planes && lane < 16u)
                 planes[g * kPlaneWords + (lane >> 1) * 4u + half * 2u + (lane & 1u)] = word;
             if (lane == 0)
@@ -181,7 +192,8 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
     }
     __syncthreads();
     if (j.sums && tid < groups)
-        j.sums[(size_t)m * groups + tid] = red_sum[tid >> 1][(tid & 1u) * 2u] + red_sum[tid >> 1][(tid & 1u) * 2u + 1u];
+        j.sums[(size_t)m * groups + tid] = red_sum[tid / kPrepGroupsPerIter][(tid % kPrepGroupsPerIter) * 2u] +
+                                           red_sum[tid / kPrepGroupsPerIter][(tid % kPrepGroupsPerIter) * 2u + 1u];
     if (tid == 0)
         j.rscale[m] = s;
 }
@@ -197,7 +209,7 @@ __device__ __forceinline__ void prep_row(const PrepJob& j, uint32_t m, bool vali
 }
 
 template <bool BATCH>
-__global__ __launch_bounds__(256) void k_prep(PrepJob single, const PrepJob* __restrict__ jobs,
+__global__ __launch_bounds__(kPrepThreads) void k_prep(PrepJob single, const PrepJob* __restrict__ jobs,
                                               const uint32_t* __restrict__ block_job, int validate_only,
                                               uint64_t seq, uint64_t* flag, uint64_t* host_status) {
     if (BATCH) {
@@ -276,8 +288,9 @@ __device__ __forceinline__ int group_dot_v(uint4 w, const uint4* p, int neg_sum)
 // ---------------------------------------------------------------------------
 // dot: persistent workgroups of 4 waves; one work item = (job, row, TPI tiles of
 // 64 features), items assigned round-robin (all workgroups stream through a
-// common window of memory, which suits HBM better than one stream per workgroup).  Wave w owns a contiguous run of the groups; lane = feature (one
-// per tile of the item, sharing each group's activation planes).  With PREFETCH,
+// common window of memory, which suits HBM better than one stream per workgroup).
+// Wave w owns a contiguous run of the groups; lane = feature (one per tile of the
+// item, sharing each group's activation planes).  With PREFETCH,
 // the loads of item i + gridDim.x (job descriptor, weights, scales, the row's bit
 // planes and group sums) are in flight in a second register set while item i is
 // computed.  D and the rounded products go through double-buffered LDS so that
@@ -298,6 +311,9 @@ enum ItemMap : int { MAP_SINGLE = 0, MAP_UNIFORM = 1, MAP_TABLE = 2 };
 #endif
 #ifndef BNN_DOT_WAVE_WG_WAVES
 #define BNN_DOT_WAVE_WG_WAVES 8  // items (waves) per workgroup; one item per wave, no persistent loop
+#endif
+#ifndef BNN_DOT_WAVE_MIN_ITEMS_PER_CU
+#define BNN_DOT_WAVE_MIN_ITEMS_PER_CU 4
 #endif
 #ifndef BNN_DOT_WAVE_XCDS
 #define BNN_DOT_WAVE_XCDS 0  // > 1: keep consecutive workgroups on one XCD
@@ -610,7 +626,7 @@ __global__ __launch_bounds__(256) void k_scatter(const unsigned char* __restrict
 
 hipError_t launch_prep(hipStream_t stream, const PrepJob& job, bool validate_only, uint64_t seq, uint64_t* flag,
                        uint64_t* host_status) {
-    hipLaunchKernelGGL(k_prep<false>, dim3(job.rows), dim3(256), 0, stream, job, nullptr, nullptr,
+    hipLaunchKernelGGL(k_prep<false>, dim3(job.rows), dim3(kPrepThreads), 0, stream, job, nullptr, nullptr,
                        (int)validate_only, seq, flag, host_status);
     return hipGetLastError();
 }
@@ -618,7 +634,7 @@ hipError_t launch_prep(hipStream_t stream, const PrepJob& job, bool validate_onl
 hipError_t launch_prep_batch(hipStream_t stream, const PrepJob* jobs, const uint32_t* block_job, uint32_t blocks,
                              uint64_t seq, uint64_t* flag, uint64_t* host_status) {
     PrepJob none = {};
-    hipLaunchKernelGGL(k_prep<true>, dim3(blocks), dim3(256), 0, stream, none, jobs, block_job, 0, seq, flag,
+    hipLaunchKernelGGL(k_prep<true>, dim3(blocks), dim3(kPrepThreads), 0, stream, none, jobs, block_job, 0, seq, flag,
                        host_status);
     return hipGetLastError();
 }
@@ -650,7 +666,11 @@ hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32
                             uint32_t uniform_items, uint32_t max_groups, uint32_t cu_count, uint64_t seq,
                             const uint64_t* flag) {
     DotJob none = {};
-    if (BNN_DOT_WAVE_ITEMS && max_groups <= (uint32_t)kWaveMaxGroups) {
+    // One wave per item streams best when the items fill the chip several times;
+    // a small batch is latency-bound, and the group-split kernel (4 waves per item)
+    // finishes each item sooner.
+    const bool many = (uint64_t)items >= (uint64_t)(cu_count ? cu_count : 256u) * BNN_DOT_WAVE_MIN_ITEMS_PER_CU;
+    if (BNN_DOT_WAVE_ITEMS && max_groups <= (uint32_t)kWaveMaxGroups && many) {
         const uint32_t grid = (items + BNN_DOT_WAVE_WG_WAVES - 1u) / BNN_DOT_WAVE_WG_WAVES;
         const dim3 block(64 * BNN_DOT_WAVE_WG_WAVES);
         if (uniform_items)

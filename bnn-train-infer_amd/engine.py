@@ -72,6 +72,8 @@ class EngineLib:
             "BNNE_ContextResetStats": (ctypes.c_int, [vp]),
             "BNNE_StatusString": (ctypes.c_char_p, [ctypes.c_int]),
             "BNNE_LastError": (ctypes.c_char_p, []),
+            "BNNEX_ContextSetResident": (ctypes.c_int, [vp, ctypes.c_int]),
+            "BNNEX_ContextIsResident": (ctypes.c_int, [vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -124,6 +126,13 @@ class Context:
         self.eng.check(self.eng.BNNE_Classify(self.handle, x.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), n,
                                               out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))), "BNNE_Classify")
         return out
+
+    def set_resident(self, enable: bool) -> None:
+        """Device path (default) or the host call pattern; only before the first token."""
+        self.eng.check(self.eng.BNNEX_ContextSetResident(self.handle, 1 if enable else 0), "BNNEX_ContextSetResident")
+
+    def resident(self) -> bool:
+        return bool(self.eng.BNNEX_ContextIsResident(self.handle))
 
     def pos(self) -> int:
         return int(self.eng.BNNE_ContextPos(self.handle))

@@ -376,3 +376,14 @@ BNNE_EXPORT const char* BNNE_StatusString(BNNE_Status s) {
 }
 
 BNNE_EXPORT const char* BNNE_LastError(void) { return g_error; }
+
+// ---- extensions (include/bnn-engine-hip.h) ----
+
+BNNE_EXPORT BNNE_Status BNNEX_ContextSetResident(BNNE_Context c, int enable) {
+    error_clear();
+    if (!c)
+        return BNNE_EINVAL;
+    return qwen3_set_resident(c, enable != 0);
+}
+
+BNNE_EXPORT int BNNEX_ContextIsResident(BNNE_Context c) { return c && qwen3_is_resident(c) ? 1 : 0; }

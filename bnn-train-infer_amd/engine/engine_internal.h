@@ -113,6 +113,8 @@ struct Arch {
 
 extern const Arch kArchQwen3;
 extern const Arch kArchBnnMlp;
+BNNE_Status qwen3_set_resident(bnne_context* c, bool enable);
+bool qwen3_is_resident(const bnne_context* c);
 const Arch* arch_find(const char* name);
 
 }  // namespace bnne

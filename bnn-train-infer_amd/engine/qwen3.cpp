@@ -11,6 +11,7 @@
 // lm_head (tied embeddings); per layer attn_norm, ffn_norm (C), attn_q_norm,
 // attn_k_norm (head_dim) in F32/F16, and Q1_0 attn_q/k/v/output, ffn_gate/up/down.
 #include "engine_internal.h"
+#include "resident.h"
 
 #include <cmath>
 #include <cstdio>
@@ -45,7 +46,8 @@ struct Model {
 struct State {
     uint32_t n_ctx;
     float *x, *norm, *q, *k, *v, *y, *o, *gate, *up, *scores, *probs;
-    float *k_cache, *v_cache, *rope_cos, *rope_sin;
+    float *k_cache, *v_cache, *rope_cos, *rope_sin;  // host KV cache: host step only
+    Resident* resident;  // device-resident step when non-null
 };
 
 float* alloc_f32(size_t count) {
@@ -242,6 +244,7 @@ void ctx_free(void* state) {
     State* s = static_cast<State*>(state);
     if (!s)
         return;
+    resident_free(s->resident);
     for (float* p : {s->x, s->norm, s->q, s->k, s->v, s->y, s->o, s->gate, s->up, s->scores, s->probs, s->k_cache,
                      s->v_cache, s->rope_cos, s->rope_sin})
         std::free(p);
@@ -268,6 +271,43 @@ void init_rope_tables(const Model* m, State* s) {
     }
 }
 
+BNNE_Status alloc_host_cache(const Model* m, State* s) {
+    const size_t cache = (size_t)m->L * s->n_ctx * m->kv_dim;
+    s->k_cache = alloc_f32(cache);
+    s->v_cache = alloc_f32(cache);
+    if (!s->k_cache || !s->v_cache) {
+        std::free(s->k_cache);
+        std::free(s->v_cache);
+        s->k_cache = s->v_cache = nullptr;
+        return error(BNNE_ENOMEM, "out of memory");
+    }
+    return BNNE_OK;
+}
+
+BNNE_Status make_resident(bnne_context* c, const Model* m, State* s) {
+    const float* attn[kMaxLayers];
+    const float* ffn[kMaxLayers];
+    const float* qn[kMaxLayers];
+    const float* kn[kMaxLayers];
+    const Linear* lin[7][kMaxLayers];
+    for (uint32_t l = 0; l < m->L; ++l) {
+        const Block& b = m->blocks[l];
+        attn[l] = b.attn_norm, ffn[l] = b.ffn_norm, qn[l] = b.q_norm, kn[l] = b.k_norm;
+        lin[0][l] = &b.wq, lin[1][l] = &b.wk, lin[2][l] = &b.wv, lin[3][l] = &b.wo;
+        lin[4][l] = &b.gate, lin[5][l] = &b.up, lin[6][l] = &b.down;
+    }
+    ResidentModel rm = {};
+    rm.C = m->C, rm.H = m->H, rm.Hk = m->Hk, rm.HD = m->HD, rm.FF = m->FF, rm.L = m->L, rm.V = m->V;
+    rm.kv_dim = m->kv_dim, rm.n_ctx = s->n_ctx, rm.eps = m->eps;
+    rm.attn_norm = attn, rm.ffn_norm = ffn, rm.q_norm = qn, rm.k_norm = kn, rm.final_norm = m->final_norm;
+    rm.emb_bits = m->emb_bits, rm.emb_scales = m->emb_scales, rm.rope_cos = s->rope_cos, rm.rope_sin = s->rope_sin;
+    rm.wq = lin[0], rm.wk = lin[1], rm.wv = lin[2], rm.wo = lin[3], rm.gate = lin[4], rm.up = lin[5];
+    rm.down = lin[6], rm.lm_head = &m->lm_head;
+    return resident_create(c, rm, &s->resident);
+}
+
+// Every context starts on the device-resident step; one whose shapes that step
+// does not support (resident_create: ENOTSUP) runs the host step.
 BNNE_Status ctx_init(bnne_context* c, void** out_state) {
     *out_state = nullptr;
     const Model* m = static_cast<const Model*>(c->model->impl);
@@ -275,7 +315,7 @@ BNNE_Status ctx_init(bnne_context* c, void** out_state) {
     if (!s)
         return error(BNNE_ENOMEM, "out of memory");
     s->n_ctx = c->params.n_ctx;
-    const size_t half = m->HD / 2, cache = (size_t)m->L * s->n_ctx * m->kv_dim;
+    const size_t half = m->HD / 2;
     s->x = alloc_f32(m->C);
     s->norm = alloc_f32(m->C);
     s->q = alloc_f32(m->C);
@@ -287,16 +327,23 @@ BNNE_Status ctx_init(bnne_context* c, void** out_state) {
     s->up = alloc_f32(m->FF);
     s->scores = alloc_f32(s->n_ctx);
     s->probs = alloc_f32(s->n_ctx);
-    s->k_cache = alloc_f32(cache);
-    s->v_cache = alloc_f32(cache);
     s->rope_cos = alloc_f32((size_t)s->n_ctx * half);
     s->rope_sin = alloc_f32((size_t)s->n_ctx * half);
     if (!s->x || !s->norm || !s->q || !s->y || !s->o || !s->k || !s->v || !s->gate || !s->up || !s->scores ||
-        !s->probs || !s->k_cache || !s->v_cache || !s->rope_cos || !s->rope_sin) {
+        !s->probs || !s->rope_cos || !s->rope_sin) {
         ctx_free(s);
         return error(BNNE_ENOMEM, "out of memory");
     }
     init_rope_tables(m, s);
+    BNNE_Status st = make_resident(c, m, s);
+    if (st == BNNE_ENOTSUP) {
+        error_clear();
+        st = alloc_host_cache(m, s);
+    }
+    if (st != BNNE_OK) {
+        ctx_free(s);
+        return st;
+    }
     *out_state = s;
     return BNNE_OK;
 }
@@ -433,6 +480,9 @@ BNNE_Status step(bnne_context* c, uint32_t token, uint32_t pos, float* logits) {
 }
 
 BNNE_Status decode(bnne_context* c, const int32_t* tokens, uint32_t n, float* logits) {
+    State* s = static_cast<State*>(c->state);
+    if (s->resident)
+        return resident_step(c, s->resident, tokens, n, c->pos, logits);
     for (uint32_t i = 0; i < n; ++i)
         TRY(step(c, (uint32_t)tokens[i], c->pos + i, i + 1 == n ? logits : nullptr));
     return BNNE_OK;
@@ -444,5 +494,35 @@ BNNE_Status truncate(bnne_context*, uint32_t) { return BNNE_OK; }
 }  // namespace
 
 const Arch kArchQwen3 = {"qwen3", BNNE_TASK_LLM, load, unload, ctx_init, ctx_free, nullptr, decode, truncate};
+
+BNNE_Status qwen3_set_resident(bnne_context* c, bool enable) {
+    if (c->model->arch != &kArchQwen3)
+        return error(BNNE_ENOTSUP, "only qwen3 contexts have a device-resident step");
+    State* s = static_cast<State*>(c->state);
+    if (enable == (s->resident != nullptr))
+        return BNNE_OK;
+    if (c->pos != 0)
+        return error(BNNE_EINVAL, "the decode path can only change before the first token");
+    const Model* m = static_cast<const Model*>(c->model->impl);
+    if (enable) {
+        const BNNE_Status st = make_resident(c, m, s);
+        if (st != BNNE_OK)
+            return st;
+        std::free(s->k_cache);
+        std::free(s->v_cache);
+        s->k_cache = s->v_cache = nullptr;
+        return BNNE_OK;
+    }
+    const BNNE_Status st = alloc_host_cache(m, s);
+    if (st != BNNE_OK)
+        return st;
+    resident_free(s->resident);
+    s->resident = nullptr;
+    return BNNE_OK;
+}
+
+bool qwen3_is_resident(const bnne_context* c) {
+    return c->model->arch == &kArchQwen3 && static_cast<const State*>(c->state)->resident != nullptr;
+}
 
 }  // namespace bnne

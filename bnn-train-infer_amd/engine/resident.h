@@ -1,0 +1,49 @@
+// Device-resident Qwen3 decode: the whole token step runs on the GPU, on the
+// accelerator device's stream.  Linear layers are prepared BNNX batches of the
+// HIP backend (q/k/v together, gate/up together, the lm_head chunks together);
+// RMSNorm, q/k norms, RoPE, the KV cache, attention, SiLU and the residual adds
+// are kernels of this engine that keep the host step's operation order (each
+// output's sums run sequentially in one lane, no FMA contraction, IEEE division
+// and square root, and an expf that returns what the host C library's expf
+// returns), so the logits are the ones the host step computes.
+#ifndef BNNE_RESIDENT_H
+#define BNNE_RESIDENT_H
+
+#include "engine_internal.h"
+
+namespace bnne {
+
+struct ResidentModel {  // host views of the model, used once to build the device state
+    uint32_t C, H, Hk, HD, FF, L, V, kv_dim, n_ctx;
+    float eps;
+    const float* const* attn_norm;  // [L][C]
+    const float* const* ffn_norm;   // [L][C]
+    const float* const* q_norm;     // [L][HD]
+    const float* const* k_norm;     // [L][HD]
+    const float* final_norm;        // [C]
+    const uint8_t* emb_bits;        // [V][C/8]
+    const uint16_t* emb_scales;     // [V][C/128]
+    const float* rope_cos;          // [n_ctx][HD/2]
+    const float* rope_sin;
+    const Linear* const* wq;  // [L] each
+    const Linear* const* wk;
+    const Linear* const* wv;
+    const Linear* const* wo;
+    const Linear* const* gate;
+    const Linear* const* up;
+    const Linear* const* down;
+    const Linear* lm_head;
+};
+
+struct Resident;
+
+BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, Resident** out);
+// One decode step of `token` at position `pos`; logits (host, V floats) only when
+// non-null.  Enqueues everything, waits once.
+BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, uint32_t n, uint32_t pos0,
+                          float* logits);
+void resident_free(Resident* r);
+
+}  // namespace bnne
+
+#endif

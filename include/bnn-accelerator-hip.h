@@ -50,6 +50,37 @@ BNN_Status BNNX_KernelTimingRead(BNN_Device device, uint32_t kind, double* total
  */
 BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint32_t count);
 
+/*
+ * Prepared batches: the checks and job tables of BNNX_ExecuteBatch done once, for
+ * callers that run the same set of jobs many times (a model's layers, token after
+ * token) and keep their activations on the device.
+ *
+ * BNNX_BatchCreate checks the jobs exactly as BNNX_ExecuteBatch does (same
+ * statuses) and builds the batch; the jobs' buffers and matrices must outlive it.
+ * BNNX_BatchLaunch enqueues the batch on the device's stream (BNNX_DeviceStream)
+ * and returns without waiting.  It fails with BNN_EINVAL once any matrix or buffer
+ * of the device has been destroyed after the batch was built (rebuild it), and
+ * with BNN_ENOTSUP when an FP32 job meets a host rounding mode other than
+ * FE_TONEAREST.  Input values are checked by the device: a job that meets an
+ * illegal input writes nothing, and the next BNNX_DeviceSynchronize reports it.
+ * BNNX_DeviceSynchronize waits for everything enqueued on the device's stream and
+ * returns BNN_ERANGE if any batch launched since the previous synchronisation met
+ * an illegal input (BNN_EIO on a device error).  A device with live batches cannot
+ * be closed (BNN_EBUSY).  Calls on one device must not overlap.
+ */
+typedef struct bnnx_batch* BNNX_Batch;
+BNN_Status BNNX_BatchCreate(BNN_Device device, const BNN_Job* jobs, uint32_t count, BNNX_Batch* out_batch);
+BNN_Status BNNX_BatchLaunch(BNNX_Batch batch);
+void BNNX_BatchDestroy(BNNX_Batch batch);
+/* What BNNX_BatchLaunch would return before enqueuing (BNN_OK, BNN_EINVAL for a
+ * stale batch, BNN_ENOTSUP for the rounding mode), without launching. */
+BNN_Status BNNX_BatchCheck(BNNX_Batch batch);
+BNN_Status BNNX_DeviceSynchronize(BNN_Device device);
+
+/* Device address of a buffer's memory, for kernels a caller runs on the device's
+ * stream between batch launches.  Valid until BNN_BufferFree. */
+BNN_Status BNNX_BufferDevicePointer(BNN_Buffer buffer, void** out_pointer);
+
 /* Name of the HIP device behind the handle (e.g. "AMD Instinct MI355X") and its
  * gfx architecture string; either pointer may be NULL. */
 BNN_Status BNNX_DeviceName(BNN_Device device, char* name, size_t name_bytes, char* arch, size_t arch_bytes);

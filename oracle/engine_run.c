@@ -10,8 +10,13 @@
  *   engine_run classify MODEL.gguf INPUT_F32 SAMPLES BATCH
  *       classifies SAMPLES rows of raw float32 input, BATCH per call; prints every
  *       logit as 8 hex digits (its float32 bit pattern), one sample per line
+ * Built against this project's engine (OWN_ENGINE), an optional last argument
+ * "host" runs the llm case on the host call pattern instead of the device path.
  */
 #include "bnn-engine.h"
+#ifdef OWN_ENGINE
+#include "bnn-engine-hip.h"
+#endif
 
 #include <inttypes.h>
 #include <stdio.h>
@@ -41,7 +46,7 @@ static uint32_t argmax(const float* v, uint32_t n) {
     return best;
 }
 
-static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint32_t ctx) {
+static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint32_t ctx, int host) {
     BNNE_ModelInfo info;
     BNNE_Status st = BNNE_ModelGetInfo(model, &info);
     if (st != BNNE_OK)
@@ -63,6 +68,13 @@ static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint3
     st = BNNE_ContextCreate(model, &params, &c);
     if (st != BNNE_OK)
         return fail("BNNE_ContextCreate", st);
+#ifdef OWN_ENGINE
+    if (host && (st = BNNEX_ContextSetResident(c, 0)) != BNNE_OK)
+        return fail("BNNEX_ContextSetResident", st);
+    printf("path %s\n", BNNEX_ContextIsResident(c) ? "device" : "host");
+#else
+    (void)host;
+#endif
     st = BNNE_Decode(c, ids, count, logits);
     if (st != BNNE_OK)
         return fail("BNNE_Decode(prefill)", st);
@@ -127,7 +139,8 @@ static int run_classify(BNNE_Model model, const char* input_path, uint32_t sampl
 }
 
 int main(int argc, char** argv) {
-    if (argc != 6 || (strcmp(argv[1], "llm") != 0 && strcmp(argv[1], "classify") != 0)) {
+    const int host = argc == 7 && strcmp(argv[6], "host") == 0;
+    if ((argc != 6 && !host) || (strcmp(argv[1], "llm") != 0 && strcmp(argv[1], "classify") != 0)) {
         fprintf(stderr, "usage: %s llm MODEL IDS STEPS CTX | classify MODEL INPUT SAMPLES BATCH\n", argv[0]);
         return 1;
     }
@@ -142,7 +155,7 @@ int main(int argc, char** argv) {
     if (st != BNNE_OK)
         return fail("BNNE_ModelLoad", st);
     const uint32_t a = (uint32_t)strtoul(argv[4], NULL, 10), b = (uint32_t)strtoul(argv[5], NULL, 10);
-    const int rc = strcmp(argv[1], "llm") == 0 ? run_llm(model, argv[3], a, b) : run_classify(model, argv[3], a, b);
+    const int rc = strcmp(argv[1], "llm") == 0 ? run_llm(model, argv[3], a, b, host) : run_classify(model, argv[3], a, b);
     BNNE_ModelFree(model);
     BNN_DeviceClose(dev);
     return rc;

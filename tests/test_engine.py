@@ -30,8 +30,15 @@ FULL_FIXTURE = GOLDEN / "e2e_qwen3_1p7b.json"
 
 
 def engine_declared() -> set[str]:
-    text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / "bnn-engine.h").read_text(), flags=re.S)
-    return set(re.findall(r"(BNNE_\w+)\s*\(", text))
+    names = set()
+    for h in ("bnn-engine.h", "bnn-engine-hip.h"):
+        text = re.sub(r"/\*.*?\*/", "", (ROOT / "include" / h).read_text(), flags=re.S)
+        names |= set(re.findall(r"(BNNEX?_\w+)\s*\(", text))
+    return names
+
+
+def parse_path(text: str) -> str:
+    return next((ln.split()[1] for ln in text.splitlines() if ln.startswith("path ")), "")
 
 
 def parse_llm(text: str) -> list[list]:
@@ -209,15 +216,18 @@ def test_reference_engine_reproduces_fixtures(pkg, tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("runner", ["own", "refhip"])
+@pytest.mark.parametrize("runner", ["own-device", "own-host", "refhip"])
 def test_engine_qwen3_tiny_bit_exact(pkg, tmp_path, runner):
-    exe = ENGINE_RUN_OWN if runner == "own" else ENGINE_RUN_REFHIP
+    exe = ENGINE_RUN_REFHIP if runner == "refhip" else ENGINE_RUN_OWN
     if runner == "refhip" and not exe.exists():
         pytest.skip("reference engine on HIP not built")
     model, ids = write_tiny(pkg, tmp_path)
-    print(f"engine qwen3 tiny via {exe.name}", flush=True)
-    out = subprocess.run([str(exe), "llm", str(model), str(ids), str(TINY["steps_arg"]), str(TINY["ctx"])],
-                         capture_output=True, text=True, timeout=120, check=True).stdout
+    print(f"engine qwen3 tiny via {exe.name} {runner}", flush=True)
+    args = [str(exe), "llm", str(model), str(ids), str(TINY["steps_arg"]), str(TINY["ctx"])]
+    out = subprocess.run(args + (["host"] if runner == "own-host" else []), capture_output=True, text=True,
+                         timeout=120, check=True).stdout
+    if runner != "refhip":
+        assert parse_path(out) == runner.split("-")[1]
     assert parse_llm(out) == TINY["steps"]
 
 
@@ -235,7 +245,8 @@ def test_engine_bnn_mlp_bit_exact(pkg, tmp_path, runner):
 
 
 @pytest.mark.gpu
-def test_engine_api_behaviour(pkg, hip, tmp_path):
+@pytest.mark.parametrize("resident", [True, False], ids=["device", "host"])
+def test_engine_api_behaviour(pkg, hip, tmp_path, resident):
     """Argument and range checks of the public API on a loaded model (engine.c:241-338)."""
     model_path, _ = write_tiny(pkg, tmp_path)
     eng = _engine_lib(pkg)
@@ -247,6 +258,9 @@ def test_engine_api_behaviour(pkg, hip, tmp_path):
             pkg.engine.Context(m, n_ctx=TINY["model"]["context"] + 1)
         assert e.value.status == -4
         c = pkg.engine.Context(m, n_ctx=16, n_batch=4)
+        assert c.resident()
+        c.set_resident(resident)
+        assert c.resident() == resident
         prompt = TINY["prompt"]
         with pytest.raises(pkg.engine.EngineError) as e:
             c.decode(prompt[:5])  # more than n_batch
@@ -261,6 +275,9 @@ def test_engine_api_behaviour(pkg, hip, tmp_path):
         for i in range(0, 8, 4):
             logits = c.decode(prompt[i:i + 4])
         assert c.pos() == 8 and int(np.argmax(logits)) == TINY["steps"][0][1]
+        with pytest.raises(pkg.engine.EngineError) as e:
+            c.set_resident(not resident)  # only before the first token
+        assert e.value.status == -1
         s = c.stats()
         assert s["calls"] == 2 and s["items"] == 8
         assert s["device_calls"] == 8 * 2 * 7 + 2  # 7 linears per layer per token, lm_head once per call
@@ -278,14 +295,17 @@ def test_engine_api_behaviour(pkg, hip, tmp_path):
 
 @pytest.mark.gpu
 @pytest.mark.skipif(not FULL_FIXTURE.exists(), reason="full-size fixture not generated")
-def test_engine_qwen3_1p7b_matches_reference(pkg, tmp_path):
+@pytest.mark.parametrize("path", ["device", "host"])
+def test_engine_qwen3_1p7b_matches_reference(pkg, tmp_path, path):
     """Benchmark configuration 5 at full Qwen3-1.7B shape: 32 prompt tokens, 128
     greedy tokens; every step's token and logits hash equal the reference engine's."""
     full = json.loads(FULL_FIXTURE.read_text())
     model, ids = tmp_path / "q.gguf", tmp_path / "ids.txt"
     pkg.gguf.qwen3_random(model)
     ids.write_text(" ".join(map(str, full["prompt"])) + "\n")
-    print("engine qwen3 1.7B-shape decode, 32 + 128 tokens", flush=True)
+    print(f"engine qwen3 1.7B-shape decode, 32 + 128 tokens, {path} path", flush=True)
     out = subprocess.run([str(ENGINE_RUN_OWN), "llm", str(model), str(ids), str(full["steps_arg"]),
-                          str(full["ctx"])], capture_output=True, text=True, timeout=600, check=True).stdout
+                          str(full["ctx"])] + (["host"] if path == "host" else []), capture_output=True, text=True,
+                         timeout=600, check=True).stdout
+    assert parse_path(out) == path
     assert parse_llm(out) == full["steps"]

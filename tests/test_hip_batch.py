@@ -144,3 +144,52 @@ def test_batch_rejections(pkg, hipdev):
     assert api.BNNX_ExecuteBatch(hipdev.handle, bad, 2) == pkg.Status.EINVAL
     assert api.BNNX_ExecuteBatch(hipdev.handle, jobs, 2) == pkg.Status.OK
     _free(mats, bi, bo)
+
+
+def test_prepared_batch_launches(pkg, hipdev):
+    """BNNX_BatchCreate/Launch/DeviceSynchronize: same results as single jobs, input
+    errors reported at the synchronisation, batches invalidated by destroys."""
+    api = hipdev.api
+    specs = [("GEMV_F32", 2048, 1024, 1), ("GEMV", 1024, 100, 1), ("DOT_GROUPS", 384, 70, 3), ("GEMM_F32", 256, 129, 5)]
+    mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs, seed=7)
+    import ctypes
+    # expected results first: single jobs allocate and free buffers, which makes
+    # prepared batches stale
+    want = [hipdev.run(pkg.Op[op], mats[i], xs[i]) for i, (op, k, n, rows) in enumerate(specs)]
+    b = ctypes.c_void_p()
+    assert api.BNNX_BatchCreate(hipdev.handle, jobs, len(specs), ctypes.byref(b)) == pkg.Status.OK
+    for rep in range(3):  # launched repeatedly without waiting in between
+        assert api.BNNX_BatchLaunch(b) == pkg.Status.OK
+    assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.OK
+    got = _outputs(bo, out_off, layouts)
+    for i, (op, k, n, rows) in enumerate(specs):
+        assert np.array_equal(got[i].view(np.uint8), want[i].view(np.uint8)), (i, op)
+    # an illegal F32 input: the device skips the batch, the synchronisation reports it
+    raw = bi.read()
+    raw[jobs[0].input.offset:jobs[0].input.offset + 4] = np.frombuffer(np.float32(np.nan).tobytes(), np.uint8)
+    bi.write(raw)
+    sentinel = np.full(bo.nbytes, 0x3C, np.uint8)
+    bo.write(sentinel)
+    assert api.BNNX_BatchLaunch(b) == pkg.Status.OK
+    assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.ERANGE
+    assert np.array_equal(bo.read(), sentinel)
+    assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.OK  # reported once
+    # device pointers of buffers are distinct and non-null
+    p1, p2 = ctypes.c_void_p(), ctypes.c_void_p()
+    assert api.BNNX_BufferDevicePointer(bi.handle, ctypes.byref(p1)) == pkg.Status.OK
+    assert api.BNNX_BufferDevicePointer(bo.handle, ctypes.byref(p2)) == pkg.Status.OK
+    assert p1.value and p2.value and p1.value != p2.value
+    assert api.BNNX_BufferDevicePointer(None, ctypes.byref(p1)) == pkg.Status.EINVAL
+    # any destroy invalidates prepared batches; a live batch keeps the device open
+    assert api.BNNX_BatchCheck(b) == pkg.Status.OK
+    extra = hipdev.buffer(64)
+    extra.free()
+    assert api.BNNX_BatchCheck(b) == pkg.Status.EINVAL
+    assert api.BNNX_BatchLaunch(b) == pkg.Status.EINVAL
+    api.BNNX_BatchDestroy(b)
+    bad = (pkg.Job * 2)(*jobs[:2])
+    bad[1].output.buffer = jobs[0].input.buffer
+    bad[1].output.offset = 0
+    assert api.BNNX_BatchCreate(hipdev.handle, bad, 2, ctypes.byref(b)) == pkg.Status.EINVAL
+    assert not b.value
+    _free(mats, bi, bo)
