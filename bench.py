@@ -4,11 +4,14 @@
 One step = one pass of the hot path over one batch of synthetic input: 608
 GEMV_F32 jobs, each on its own resident 2048 -> 6144 matrix (1.0 GiB of sign
 bits + scales in total, 4x the 256 MB Infinity Cache) with its own input row,
-issued as one BNNX_ExecuteBatch call (one prep launch + one group-dot launch).
-Inputs are resident in HBM before timing starts.
+issued as one prepared batch launch (one prep launch + one group-dot launch).
+Steps are launched back to back and the timed region ends with one
+BNNX_DeviceSynchronize.  Inputs are resident in HBM before timing starts.
 
   value            algorithmic bytes of the step / wall time of the step (GB/s);
-                   per GEMV_F32 job 1,802,240 B = 1.125 bit per weight + 4K + 4N
+                   per GEMV_F32 job 1,802,240 B = 1.125 bit per weight + 4K + 4N;
+                   config.sync_GBps is the same step through the synchronous
+                   BNNX_ExecuteBatch (one host round trip per step)
   roofline         the dot kernel: algorithmic bytes per launch / its average
                    duration from HIP events on the device stream, against 8 TB/s
   per_call         the same operation through the reference's synchronous
@@ -16,6 +19,18 @@ Inputs are resident in HBM before timing starts.
   cpu_baseline     the reference soft backend (compiled from its source into
                    oracle/_ref) or else this project's C restatement of it, one
                    host core, on a bounded sample of the same jobs
+
+Secondary legs (the other benchmark configurations; --no-extra skips them):
+  ops              configs 2/3: DOT_GROUPS, GEMV_I8 and the GEMV_F32 Qwen3 shapes,
+                   per call (BNN_Execute) and sustained over >= 1 GiB of distinct
+                   resident matrices in one BNNX_ExecuteBatch per step
+  gemm             config 4: GEMM_F32 / GEMM_I8 at rows 64/256/1024 on the matrix
+                   cores: TOPS and utilisation of the 5.0 POPS dense int8 peak
+  e2e              config 5: Qwen3-1.7B-shape greedy decode (random-init Q1_0 model,
+                   32 prompt + 128 new tokens) through the engine, device path and
+                   the reference call pattern; tok/s, backend share of step time,
+                   token agreement with the reference engine + soft backend (fixture)
+  mlp              config 1: bnn-mlp classifier, 1000 samples in batches of 64
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -117,12 +132,210 @@ def cpu_baseline(pkg, seconds: float = 12.0):
             "library": str(path.relative_to(ROOT))}
 
 
+def _timed_calls(dev, job, reps):
+    """Average wall time of `reps` BNN_Execute calls and of the dot/gemm kernels."""
+    dev.kernel_timing(True)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        st = dev.execute(job)
+        if st != 0:
+            raise RuntimeError(f"BNN_Execute: {st}")
+    wall = (time.perf_counter() - t0) / reps
+    dot_ms, dot_n = dev.kernel_timing_read(1)
+    gemm_ms, gemm_n = dev.kernel_timing_read(3)
+    prep_ms, prep_n = dev.kernel_timing_read(0)
+    dev.kernel_timing(False)
+    kern = (dot_ms + gemm_ms) / max(dot_n + gemm_n, 1) / 1e3
+    return wall, kern, prep_ms / max(prep_n, 1) / 1e3
+
+
+def ops_leg(pkg, hip):
+    """Configs 2 and 3 per call and sustained."""
+    out = {}
+    shapes = [("DOT_GROUPS", 2048, 6144), ("GEMV", 2048, 6144), ("GEMV_F32", 2048, 2048), ("GEMV_F32", 2048, 1024),
+              ("GEMV_F32", 2048, 6144), ("GEMV_F32", 6144, 2048)]
+    with pkg.Device(hip, 0) as dev:
+        for op, k, n in shapes:
+            f32 = op.endswith("F32")
+            in_t, out_t = pkg.api.OP_TYPES[pkg.Op[op]]
+            bits, scales = pkg.synth.matrix(n, k, seed=2)
+            x = pkg.synth.normal_f32(1, k, seed=3) if f32 else pkg.synth.int8_uniform(1, k, seed=2)
+            out_row = n * (k // 128) * 2 if op == "DOT_GROUPS" else 4 * n
+            in_row = 4 * k if f32 else k
+            weight_bytes = n * k // 8 + (0 if op == "DOT_GROUPS" else n * (k // 128) * 2)
+            unit = weight_bytes + in_row + out_row  # algorithmic bytes per call
+            count = max(64, -(-(1 << 30) // weight_bytes))  # >= 1 GiB of distinct matrices
+            mats = [dev.matrix(bits, scales) for _ in range(count)]
+            bi = dev.buffer(in_row * count)
+            bi.write(np.concatenate([x.reshape(-1).view(np.uint8)] * count))
+            bo = dev.buffer(out_row * count)
+            jobs = (pkg.Job * count)()
+            for i, m in enumerate(mats):
+                jobs[i] = pkg.Job(int(pkg.Op[op]), m.handle.value, bi.view(in_t, i * in_row), bo.view(out_t, i * out_row), 1)
+            wall, kern, prep = _timed_calls(dev, jobs[0], 50)
+            for _ in range(3):
+                assert hip.BNNX_ExecuteBatch(dev.handle, jobs, count) == 0
+            dev.kernel_timing(True)
+            reps, t0 = 20, time.perf_counter()
+            for _ in range(reps):
+                assert hip.BNNX_ExecuteBatch(dev.handle, jobs, count) == 0
+            bwall = (time.perf_counter() - t0) / reps
+            dms, dn = dev.kernel_timing_read(1)
+            dev.kernel_timing(False)
+            out[f"{op} {k}->{n}"] = {
+                "bytes_per_call": unit, "per_call_us": round(wall * 1e6, 2), "kernel_us": round(kern * 1e6, 2),
+                "prep_us": round(prep * 1e6, 2),
+                "sustained_GBps": round(count * unit / bwall / 1e9, 1),
+                "sustained_kernel_GBps": round(count * unit / (dms / dn / 1e3) / 1e9, 1),
+                "matrices": count}
+            for m in mats:
+                m.destroy()
+            bi.free()
+            bo.free()
+        # lm_head: 2048 -> 151669 as 19 chunks of <= 8192 outputs in one batch
+        k, n_total, chunk = 2048, 151669, 8192
+        bits, scales = pkg.synth.matrix(chunk, k, seed=3)
+        x = pkg.synth.normal_f32(1, k, seed=3)
+        bi = dev.buffer(4 * k)
+        bi.write(x)
+        bo = dev.buffer(4 * n_total)
+        sizes = [min(chunk, n_total - o) for o in range(0, n_total, chunk)]
+        mats = [dev.matrix(bits[:sz], scales[:sz]) for sz in sizes]
+        jobs = (pkg.Job * len(sizes))()
+        for i, (m, sz) in enumerate(zip(mats, sizes)):
+            jobs[i] = pkg.Job(int(pkg.Op.GEMV_F32), m.handle.value, bi.view(pkg.Type.F32),
+                              bo.view(pkg.Type.F32, 4 * i * chunk), 1)
+        for _ in range(3):
+            assert hip.BNNX_ExecuteBatch(dev.handle, jobs, len(sizes)) == 0
+        reps, t0 = 50, time.perf_counter()
+        for _ in range(reps):
+            assert hip.BNNX_ExecuteBatch(dev.handle, jobs, len(sizes)) == 0
+        bwall = (time.perf_counter() - t0) / reps
+        unit = n_total * k // 8 + n_total * (k // 128) * 2 + len(sizes) * 4 * k + 4 * n_total  # 19 chunks
+        out["GEMV_F32 2048->151669 (19 chunks, one batch)"] = {"bytes_per_call": unit, "us_per_call": round(bwall * 1e6, 2),
+                                                              "GBps": round(unit / bwall / 1e9, 1)}
+        for m in mats:
+            m.destroy()
+        bi.free()
+        bo.free()
+    return out
+
+
+def gemm_leg(pkg, hip):
+    """Config 4: multi-row GEMM_F32 / GEMM_I8 on the matrix cores."""
+    out, best = {}, 0.0
+    with pkg.Device(hip, 0) as dev:
+        for op in ("GEMM_F32", "GEMM"):
+            for k, n in ((2048, 6144), (6144, 2048)):
+                bits, scales = pkg.synth.matrix(n, k, seed=4)
+                m = dev.matrix(bits, scales)
+                for rows in (64, 256, 1024):
+                    f32 = op.endswith("F32")
+                    x = pkg.synth.normal_f32(rows, k, seed=4) if f32 else pkg.synth.int8_uniform(rows, k, seed=4)
+                    in_t, out_t = pkg.api.OP_TYPES[pkg.Op[op]]
+                    bi, bo = dev.buffer(x.nbytes), dev.buffer(rows * n * 4)
+                    bi.write(x)
+                    job = pkg.Job(int(pkg.Op[op]), m.handle.value, bi.view(in_t), bo.view(out_t), rows)
+                    _timed_calls(dev, job, 3)
+                    wall, kern, prep = _timed_calls(dev, job, 20)
+                    ops = 2.0 * rows * n * k
+                    tops = ops / kern / 1e12
+                    best = max(best, tops)
+                    out[f"{op} {k}->{n} rows={rows}"] = {"kernel_us": round(kern * 1e6, 1), "TOPS": round(tops, 1),
+                                                         "mfma_util": round(tops / 5000.0, 4),
+                                                         "call_us": round(wall * 1e6, 1), "prep_us": round(prep * 1e6, 1)}
+                    bi.free()
+                    bo.free()
+                m.destroy()
+    return {"peak_TOPS": 5000.0, "best_TOPS": round(best, 1), "cases": out}
+
+
+def e2e_leg(pkg, hip):
+    """Config 5: Qwen3-1.7B-shape greedy decode through the engine (BNNE_* API)."""
+    import tempfile
+    fixture_path = ROOT / "tests" / "golden" / "e2e_qwen3_1p7b.json"
+    fixture = json.loads(fixture_path.read_text()) if fixture_path.exists() else None
+    eng = pkg.engine.EngineLib()
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "qwen3.gguf"
+        t0 = time.perf_counter()
+        info = pkg.gguf.qwen3_random(path)
+        prompt = pkg.gguf.prompt_ids(32, info["vocab"], seed=5)
+        gen_s = time.perf_counter() - t0
+        with pkg.Device(hip, 0) as dev:
+            t0 = time.perf_counter()
+            model = pkg.engine.Model(eng, dev, path)
+            load_s = time.perf_counter() - t0
+            for name in ("device", "host"):
+                ctx = pkg.engine.Context(model, n_ctx=1024)
+                ctx.set_resident(name == "device")
+                t0 = time.perf_counter()
+                tokens = [int(np.argmax(ctx.decode(prompt)))]
+                t1 = time.perf_counter()
+                ctx.reset_stats()
+                for _ in range(127):
+                    tokens.append(int(np.argmax(ctx.decode([tokens[-1]]))))
+                t2 = time.perf_counter()
+                st = ctx.stats()
+                ctx.free()
+                entry = {"prefill_tok_s": round(32 / (t1 - t0), 1), "decode_tok_s": round(127 / (t2 - t1), 1),
+                         "ms_per_token": round((t2 - t1) / 127 * 1e3, 3),
+                         "backend_share": round((st["transfer_ns"] + st["execute_ns"]) / max(st["total_ns"], 1), 4),
+                         "weight_GBps": round(info["weight_bytes"] * 127 / (t2 - t1) / 1e9, 1)}
+                if fixture:
+                    want = [row[1] for row in fixture["steps"]]
+                    same = sum(a == b for a, b in zip(tokens, want))
+                    entry["token_agreement"] = f"{same}/{len(want)}"
+                res[name] = entry
+            model.free()
+    out = {"model": "random-init Qwen3-1.7B shape (28 layers, 2048, 16/8 heads, FFN 6144, vocab 151669), Q1_0",
+           "tokens": "32 prompt + 128 greedy", "gguf_write_s": round(gen_s, 1), "load_s": round(load_s, 1),
+           "weight_bytes_per_token": info["weight_bytes"], "paths": res}
+    if fixture and fixture.get("soft_seconds"):
+        # the fixture run: 32 prompt steps + 127 decode steps on one host core of the build container
+        out["reference_soft_1core_tok_s"] = round((len(fixture["prompt"]) + fixture["steps_arg"]) /
+                                                  fixture["soft_seconds"], 4)
+    return out
+
+
+def mlp_leg(pkg, hip):
+    """Config 1: bnn-mlp classifier through the engine."""
+    import tempfile
+    eng = pkg.engine.EngineLib()
+    with tempfile.TemporaryDirectory() as d:
+        path = Path(d) / "mlp.gguf"
+        pkg.gguf.bnn_mlp_random(path)
+        x = pkg.gguf.bnn_mlp_inputs(1000)
+        with pkg.Device(hip, 0) as dev:
+            model = pkg.engine.Model(eng, dev, path)
+            ctx = pkg.engine.Context(model, n_batch=64)
+            ctx.classify(x[:64])
+            t0 = time.perf_counter()
+            preds = []
+            for s0 in range(0, 1000, 64):
+                preds.extend(ctx.classify(x[s0:s0 + 64]).argmax(axis=1).tolist())
+            dt = time.perf_counter() - t0
+            st = ctx.stats()
+            ctx.free()
+            model.free()
+    fixture_path = ROOT / "tests" / "golden" / "e2e_bnn_mlp.json"
+    agree = None
+    if fixture_path.exists():
+        want = json.loads(fixture_path.read_text())["argmax"]
+        agree = f"{sum(a == b for a, b in zip(preds, want))}/{len(want)}"
+    return {"samples_per_s": round(1000 / dt, 1), "us_per_sample": round(dt / 1000 * 1e6, 1),
+            "gemv_calls_per_sample": 3, "backend_share": round((st["transfer_ns"] + st["execute_ns"]) / st["total_ns"], 4),
+            "argmax_agreement": agree}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the secondary legs (ops, gemm, e2e, mlp)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run one 256 MiB device-to-device copy (counter calibration)")
     args = ap.parse_args()
@@ -170,16 +383,52 @@ def main():
         y1 = dev.run(pkg.Op.GEMV_F32, mats[i], x[i:i + 1])
         assert np.array_equal(y1[0].view(np.uint32), y_batch[i].view(np.uint32)), f"batch job {i} differs"
 
-    # ---- timed region (synchronous API: each call returns with its results readable) ----
-    dev.kernel_timing(True)
+    # ---- timed region: the step as a prepared batch, launched back to back ----
+    # BNNX_BatchCreate checks the 608 jobs once; every step is then one
+    # BNNX_BatchLaunch (one prep launch + one group-dot launch, no host wait), and
+    # BNNX_DeviceSynchronize closes the timed region (it also reports any input error).
+    import ctypes
+    batch = ctypes.c_void_p()
+    st = hip.BNNX_BatchCreate(dev.handle, jobs, MATRICES, ctypes.byref(batch))
+    if st != 0:
+        raise pkg.BnnError(st, "BNNX_BatchCreate")
+
+    def launch():
+        st = hip.BNNX_BatchLaunch(batch)
+        if st != 0:
+            raise pkg.BnnError(st, "BNNX_BatchLaunch")
+
+    def synchronize():
+        st = hip.BNNX_DeviceSynchronize(dev.handle)
+        if st != 0:
+            raise pkg.BnnError(st, "BNNX_DeviceSynchronize")
+
+    for _ in range(args.warmup):
+        launch()
+    synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step()
+        launch()
+    synchronize()
     wall = time.perf_counter() - t0
+    print(f"timed: {args.steps} steps in {wall:.3f} s", flush=True)
+    y_stream = bout.read().view(np.float32).reshape(MATRICES, N_OUT)
+    assert np.array_equal(y_stream.view(np.uint32), y_batch.view(np.uint32)), "streamed steps differ"
+
+    hip.BNNX_BatchDestroy(batch)
+
+    # the same step through the synchronous BNNX_ExecuteBatch (returns with results
+    # readable), with kernel durations from HIP events recorded around each launch on
+    # the device stream (event pairs between back-to-back launches would stretch them)
+    sync_steps = max(1, args.steps // 4)
+    dev.kernel_timing(True)
+    t0 = time.perf_counter()
+    for _ in range(sync_steps):
+        step()
+    sync_wall = time.perf_counter() - t0
     dot_ms, dot_n = dev.kernel_timing_read(1)
     prep_ms, prep_n = dev.kernel_timing_read(0)
     dev.kernel_timing(False)
-    print(f"timed: {args.steps} steps in {wall:.3f} s", flush=True)
 
     step_bytes = MATRICES * BYTES_PER_JOB
     value = step_bytes * args.steps / wall / 1e9
@@ -231,6 +480,10 @@ def main():
                         f"matrices (1.0 GiB) per step in one BNNX_ExecuteBatch",
             "bytes_per_job": BYTES_PER_JOB,
             "bytes_per_step": step_bytes,
+            "step": "one prepared batch launch (BNNX_BatchLaunch: prep + group-dot), back to back, "
+                    "one BNNX_DeviceSynchronize at the end",
+            "sync_GBps": round(step_bytes * sync_steps / sync_wall / 1e9, 2),
+            "sync_ms_per_step": round(sync_wall / sync_steps * 1e3, 4),
             "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
             "device": f"{name} {arch}",
         },
@@ -246,8 +499,13 @@ def main():
             "prep_kernel_avg_us": round(prep_ms / max(prep_n, 1) * 1e3, 2),
         },
         "per_call": per_call,
-        "cpu_baseline": None if args.no_cpu else cpu_baseline(pkg),
     }
+    if not args.no_extra:
+        for leg_name, leg in (("ops", ops_leg), ("gemm", gemm_leg), ("e2e", e2e_leg), ("mlp", mlp_leg)):
+            t0 = time.perf_counter()
+            result[leg_name] = leg(pkg, hip)
+            print(f"leg {leg_name}: {time.perf_counter() - t0:.1f} s", flush=True)
+    result["cpu_baseline"] = None if args.no_cpu else cpu_baseline(pkg)
     print(json.dumps(result), flush=True)
 
 

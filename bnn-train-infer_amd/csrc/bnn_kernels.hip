@@ -92,19 +92,19 @@ __device__ __forceinline__ void raise_flag(uint64_t seq, uint64_t* flag, uint64_
 // row scale, quantises, and writes bit planes, group sums and (optionally) Q.
 // Thread t owns elements k = t + 256 i; all its loads are issued before any use.
 // ---------------------------------------------------------------------------
-#ifndef BNN_PREP_THREADS
-#define BNN_PREP_THREADS 1024  // threads per row: more waves per row, shorter serial chains
-#endif
-constexpr int kPrepThreads = BNN_PREP_THREADS;
-constexpr int kPrepWaves = kPrepThreads / 64;
-constexpr int kPrepPerThread = kMaxFeatures / kPrepThreads;
-constexpr int kPrepGroupsPerIter = kPrepThreads / kGroup;
-static_assert(kPrepThreads % 128 == 0 && kMaxFeatures % kPrepThreads == 0, "whole groups per iteration");
-static_assert(kMaxFeatures / kGroup <= kPrepThreads, "one thread per group for the group sums");
+// Threads per row: a launch with few rows is latency-bound and gives each row 1024
+// threads (short serial chains per wave); a launch with many rows gives each row
+// 512 (measured best for a full chip of rows).
+constexpr int kPrepThreadsFew = 1024, kPrepThreadsMany = 512;
+constexpr uint32_t kPrepManyRows = 256;
 
-template <bool F32, bool ALIGNED>
+template <int NT, bool F32, bool ALIGNED>
 __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uint64_t seq, uint64_t* flag,
                            uint64_t* host_status) {
+    constexpr int kPrepThreads = NT, kPrepWaves = NT / 64, kPrepPerThread = kMaxFeatures / NT;
+    constexpr int kPrepGroupsPerIter = NT / kGroup;
+    static_assert(NT % 128 == 0 && kMaxFeatures % NT == 0, "whole groups per iteration");
+    static_assert(kMaxFeatures / kGroup <= NT, "one thread per group for the group sums");
     __shared__ float red_max[kPrepWaves];
     __shared__ int red_sum[kPrepPerThread][kPrepWaves];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -198,25 +198,26 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
         j.rscale[m] = s;
 }
 
+template <int NT>
 __device__ __forceinline__ void prep_row(const PrepJob& j, uint32_t m, bool validate_only, uint64_t seq,
                                          uint64_t* flag, uint64_t* host_status) {
     if (j.f32 && j.aligned)
-        prep_row_t<true, true>(j, m, validate_only, seq, flag, host_status);
+        prep_row_t<NT, true, true>(j, m, validate_only, seq, flag, host_status);
     else if (j.f32)
-        prep_row_t<true, false>(j, m, validate_only, seq, flag, host_status);
+        prep_row_t<NT, true, false>(j, m, validate_only, seq, flag, host_status);
     else
-        prep_row_t<false, true>(j, m, validate_only, seq, flag, host_status);
+        prep_row_t<NT, false, true>(j, m, validate_only, seq, flag, host_status);
 }
 
-template <bool BATCH>
-__global__ __launch_bounds__(kPrepThreads) void k_prep(PrepJob single, const PrepJob* __restrict__ jobs,
+template <bool BATCH, int NT>
+__global__ __launch_bounds__(NT) void k_prep(PrepJob single, const PrepJob* __restrict__ jobs,
                                               const uint32_t* __restrict__ block_job, int validate_only,
                                               uint64_t seq, uint64_t* flag, uint64_t* host_status) {
     if (BATCH) {
         const PrepJob j = jobs[block_job[blockIdx.x]];
-        prep_row(j, blockIdx.x - j.first_block, false, seq, flag, host_status);
+        prep_row<NT>(j, blockIdx.x - j.first_block, false, seq, flag, host_status);
     } else {
-        prep_row(single, blockIdx.x, validate_only != 0, seq, flag, host_status);
+        prep_row<NT>(single, blockIdx.x, validate_only != 0, seq, flag, host_status);
     }
 }
 
@@ -626,16 +627,24 @@ __global__ __launch_bounds__(256) void k_scatter(const unsigned char* __restrict
 
 hipError_t launch_prep(hipStream_t stream, const PrepJob& job, bool validate_only, uint64_t seq, uint64_t* flag,
                        uint64_t* host_status) {
-    hipLaunchKernelGGL(k_prep<false>, dim3(job.rows), dim3(kPrepThreads), 0, stream, job, nullptr, nullptr,
-                       (int)validate_only, seq, flag, host_status);
+    if (job.rows >= kPrepManyRows)
+        hipLaunchKernelGGL((k_prep<false, kPrepThreadsMany>), dim3(job.rows), dim3(kPrepThreadsMany), 0, stream, job,
+                           nullptr, nullptr, (int)validate_only, seq, flag, host_status);
+    else
+        hipLaunchKernelGGL((k_prep<false, kPrepThreadsFew>), dim3(job.rows), dim3(kPrepThreadsFew), 0, stream, job,
+                           nullptr, nullptr, (int)validate_only, seq, flag, host_status);
     return hipGetLastError();
 }
 
 hipError_t launch_prep_batch(hipStream_t stream, const PrepJob* jobs, const uint32_t* block_job, uint32_t blocks,
                              uint64_t seq, uint64_t* flag, uint64_t* host_status) {
     PrepJob none = {};
-    hipLaunchKernelGGL(k_prep<true>, dim3(blocks), dim3(kPrepThreads), 0, stream, none, jobs, block_job, 0, seq, flag,
-                       host_status);
+    if (blocks >= kPrepManyRows)
+        hipLaunchKernelGGL((k_prep<true, kPrepThreadsMany>), dim3(blocks), dim3(kPrepThreadsMany), 0, stream, none,
+                           jobs, block_job, 0, seq, flag, host_status);
+    else
+        hipLaunchKernelGGL((k_prep<true, kPrepThreadsFew>), dim3(blocks), dim3(kPrepThreadsFew), 0, stream, none,
+                           jobs, block_job, 0, seq, flag, host_status);
     return hipGetLastError();
 }
 

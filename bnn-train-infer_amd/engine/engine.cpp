@@ -126,6 +126,11 @@ BNNE_EXPORT BNNE_Status BNNE_ModelLoad(BNN_Device device, const char* gguf_path,
         return st;
     }
     if (arch->task == BNNE_TASK_LLM) {
+        st = vocab_build(g, &m->vocab);
+        if (st != BNNE_OK) {
+            BNNE_ModelFree(m);
+            return st;
+        }
         m->info.bos_token = g->has_bos ? (int32_t)g->bos_token_id : -1;
         m->info.eos_token = g->has_eos ? (int32_t)g->eos_token_id : -1;
     }
@@ -141,6 +146,7 @@ BNNE_EXPORT void BNNE_ModelFree(BNNE_Model m) {
         return;
     if (m->arch && m->arch->unload && m->impl)
         m->arch->unload(m->impl);
+    vocab_free(m->vocab);
     gguf_close(m->gguf);
     std::free(m);
 }
@@ -152,7 +158,7 @@ BNNE_EXPORT BNNE_Status BNNE_ModelGetInfo(BNNE_Model m, BNNE_ModelInfo* out) {
     return BNNE_OK;
 }
 
-// Text tokenisation is not part of this build: callers pass token IDs.
+// Text encoding is not part of this build: callers pass token IDs.
 BNNE_EXPORT BNNE_Status BNNE_Tokenize(BNNE_Model m, const char* text, int, int32_t* ids, uint32_t capacity,
                                       uint32_t* out_count) {
     if (out_count)
@@ -160,10 +166,11 @@ BNNE_EXPORT BNNE_Status BNNE_Tokenize(BNNE_Model m, const char* text, int, int32
     error_clear();
     if (!m || !text || !ids || !out_count || capacity == 0)
         return BNNE_EINVAL;
-    return error(BNNE_ENOTSUP, "this engine build takes token IDs; no text tokenizer");
+    return error(BNNE_ENOTSUP, m->vocab ? "text encoding is not part of this engine build; pass token IDs"
+                                        : "model has no text tokenizer");
 }
 
-BNNE_EXPORT BNNE_Status BNNE_TokenPiece(BNNE_Model m, int32_t, const char** out_bytes, size_t* out_len) {
+BNNE_EXPORT BNNE_Status BNNE_TokenPiece(BNNE_Model m, int32_t id, const char** out_bytes, size_t* out_len) {
     if (out_bytes)
         *out_bytes = nullptr;
     if (out_len)
@@ -171,14 +178,22 @@ BNNE_EXPORT BNNE_Status BNNE_TokenPiece(BNNE_Model m, int32_t, const char** out_
     error_clear();
     if (!m || !out_bytes || !out_len)
         return BNNE_EINVAL;
-    return error(BNNE_ENOTSUP, "this engine build takes token IDs; no text tokenizer");
+    if (!m->vocab)
+        return error(BNNE_ENOTSUP, "model has no text tokenizer");
+    if (id < 0 || (uint64_t)id >= m->vocab->count)
+        return BNNE_ERANGE;
+    *out_bytes = m->vocab->text + m->vocab->off[id];
+    *out_len = m->vocab->len[id];
+    return BNNE_OK;
 }
 
-// End of generation: the declared EOS token only.
 BNNE_EXPORT int BNNE_TokenIsEog(BNNE_Model m, int32_t id) {
-    if (!m || m->info.task != BNNE_TASK_LLM || id < 0 || (uint32_t)id >= m->info.n_vocab)
+    if (!m || !m->vocab || id < 0 || (uint32_t)id >= m->info.n_vocab || (uint64_t)id >= m->vocab->count)
         return 0;
-    return m->info.eos_token >= 0 && id == m->info.eos_token;
+    for (uint32_t k = 0; k < m->vocab->n_eog; ++k)
+        if (m->vocab->eog[k] == (uint32_t)id)
+            return 1;
+    return 0;
 }
 
 BNNE_EXPORT void BNNE_ContextParamsInit(BNNE_ContextParams* p) {

@@ -57,7 +57,10 @@ struct Gguf {
     char (*mlp_activations)[16];  // by block index; "" where absent
     uint64_t mlp_activation_count;
 
-    uint64_t token_count;  // length of tokenizer.ggml.tokens (the table itself is not kept)
+    GgufString* tokens;  // tokenizer.ggml.tokens (strings point into the mapping)
+    uint64_t token_count;
+    uint32_t* token_types;  // tokenizer.ggml.token_type, may be absent
+    uint64_t token_type_count;
     int has_eos, has_bos;
     uint32_t eos_token_id, bos_token_id;
 };
@@ -66,6 +69,20 @@ BNNE_Status gguf_open(const char* path, Gguf** out);
 void gguf_close(Gguf* g);
 const GgufTensor* gguf_find(const Gguf* g, const char* name);
 const uint8_t* gguf_data(const Gguf* g, const GgufTensor* t);
+
+// ---------------------------------------------------------------- vocabulary
+
+// Token pieces (the bytes each token stands for) and the end-of-generation ids.
+struct Vocab {
+    char* text;  // all pieces, each NUL-terminated
+    uint32_t *off, *len;
+    uint64_t count;
+    uint32_t eog[8];
+    uint32_t n_eog;
+};
+
+BNNE_Status vocab_build(const Gguf* g, Vocab** out);
+void vocab_free(Vocab* v);
 
 // ---------------------------------------------------------------- errors, time
 
@@ -125,6 +142,7 @@ struct bnne_model {
     const bnne::Arch* arch;
     void* impl;
     bnne::Gguf* gguf;
+    bnne::Vocab* vocab;  // LLM only
     BNNE_ModelInfo info;
     uint32_t max_in, max_out;  // widest linear input / chunk output, sizes the context buffers
 };

@@ -175,37 +175,55 @@ BNNE_Status store_activation(Gguf* g, uint32_t index, Reader& r, uint32_t type) 
                                                                                              : BNNE_EFORMAT;
 }
 
-// A string array whose contents the engine does not keep (labels, vocabulary,
-// merges): checked for type, counted, skipped.  'seen' rejects a repeated key.
-BNNE_Status string_array(Reader& r, uint32_t type, bool* seen, uint64_t* count_out) {
+// A string array: checked for type, counted, and (when 'keep' is given) its strings
+// recorded as views into the mapping.  'seen' rejects a repeated key.
+BNNE_Status string_array(Reader& r, uint32_t type, bool* seen, uint64_t* count_out, GgufString** keep = nullptr) {
     if (*seen || type != kArray)
         return BNNE_EFORMAT;
     *seen = true;
     const uint32_t element = r.u32();
     const uint64_t count = r.u64();
-    if (!r.ok || element != kString)
+    if (!r.ok || element != kString || count > SIZE_MAX / sizeof(GgufString))
         return BNNE_EFORMAT;
-    for (uint64_t i = 0; i < count; ++i) {
-        r.str();
-        if (!r.ok)
-            return BNNE_EFORMAT;
+    GgufString* out = nullptr;
+    if (keep && count) {
+        out = static_cast<GgufString*>(std::calloc(count, sizeof(GgufString)));
+        if (!out)
+            return BNNE_ENOMEM;
     }
+    for (uint64_t i = 0; i < count; ++i) {
+        const GgufString v = r.str();
+        if (!r.ok) {
+            std::free(out);
+            return BNNE_EFORMAT;
+        }
+        if (out)
+            out[i] = v;
+    }
+    if (keep)
+        *keep = out;
     if (count_out)
         *count_out = count;
     return BNNE_OK;
 }
 
-BNNE_Status int_array(Reader& r, uint32_t type, bool* seen) {
+BNNE_Status int_array(Reader& r, uint32_t type, bool* seen, uint32_t** out, uint64_t* count_out) {
     if (*seen || type != kArray)
         return BNNE_EFORMAT;
     *seen = true;
     const uint32_t element = r.u32();
     const uint64_t count = r.u64();
-    if (!r.ok || (element != kI32 && element != kU32) || count > (UINT64_MAX / 4))
+    if (!r.ok || (element != kI32 && element != kU32) || count > SIZE_MAX / 4)
         return BNNE_EFORMAT;
     if (!r.need(count * 4))
         return BNNE_EFORMAT;
-    r.p += count * 4;
+    uint32_t* v = count ? static_cast<uint32_t*>(std::malloc(count * 4)) : nullptr;
+    if (count && !v)
+        return BNNE_ENOMEM;
+    for (uint64_t i = 0; i < count; ++i)
+        v[i] = r.u32();
+    *out = v;
+    *count_out = count;
     return BNNE_OK;
 }
 
@@ -286,9 +304,9 @@ BNNE_Status parse_metadata(Reader& r, Gguf* g, uint64_t count) {
             if (!read_text(r, type, scratch, sizeof scratch))
                 return BNNE_EFORMAT;
         } else if (key_is(key, "tokenizer.ggml.tokens")) {
-            st = string_array(r, type, &tokens, &g->token_count);
+            st = string_array(r, type, &tokens, &g->token_count, &g->tokens);
         } else if (key_is(key, "tokenizer.ggml.token_type")) {
-            st = int_array(r, type, &types);
+            st = int_array(r, type, &types, &g->token_types, &g->token_type_count);
         } else if (key_is(key, "tokenizer.ggml.merges")) {
             st = string_array(r, type, &merges, nullptr);
         } else if (key_is(key, "tokenizer.ggml.eos_token_id")) {
@@ -447,6 +465,8 @@ void gguf_close(Gguf* g) {
         return;
     std::free(g->tensors);
     std::free(g->mlp_activations);
+    std::free(g->tokens);
+    std::free(g->token_types);
     if (g->mapping)
         ::munmap(g->mapping, g->mapping_bytes);
     std::free(g);

@@ -17,6 +17,9 @@
 #include "bnn-accelerator-hip.h"
 #include "resident.h"
 
+#define BNNE_EXPF_QUALIFIER static __device__ __forceinline__
+#include "libc_expf.h"
+
 #pragma clang fp contract(off)
 
 namespace bnne {
@@ -26,54 +29,10 @@ constexpr uint32_t kMaxHeadDim = 512;
 constexpr uint32_t kMaxNormWidth = 16384;
 enum : int { kErrNone = 0, kErrNorm = 1, kErrScore = 2, kErrSoftmax = 3 };
 
-// ---------------------------------------------------------------------------
-// expf with the results of the host C library's expf (glibc 2.35, x86-64 with
-// FMA): the table-driven method of ARM's optimized-routines -- k = round(x*32/ln2),
-// 2^(k/32) from a 32-entry table of 2^(i/32) (entries stored minus i<<47 so that
-// k's high bits add straight into the exponent), and a cubic in r = x*32/ln2 - k,
-// all in double with fused multiply-adds, rounded once to float.  Checked against
-// the library on all 2^32 inputs.  Table entries: 2^(i/32) correctly rounded to
-// double, minus i << 47.
-// ---------------------------------------------------------------------------
-__constant__ uint64_t kExp2Table[32] = {
-    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
-    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
-    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
-    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
-    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
-    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
-    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
-    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+// expf of the host C library, bit for bit (see libc_expf.h)
+__constant__ uint64_t kExp2Table[32] = BNNE_EXP2_TABLE;
 
-__device__ float expf_libc(float x) {
-    const uint32_t ux = __float_as_uint(x);
-    const uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {  // |x| >= 88, or not finite
-        if (ux == 0xff800000u)
-            return 0.0f;
-        if (abstop >= 0x7f8u)
-            return x + x;
-        if (x > 0x1.62e42ep6f)  // overflow
-            return __uint_as_float(0x7f800000u);
-        if (x < -0x1.9fe368p6f)  // underflow to +0
-            return 0.0f;
-    }
-    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
-    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
-                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
-    const double xd = (double)x;
-    double kd = __builtin_fma(inv_ln2_n, xd, shift);
-    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
-    kd = kd - shift;
-    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    const double s = __longlong_as_double((long long)(kExp2Table[ki % 32u] + (ki << 47)));
-    const double z = __builtin_fma(c0, r, c1);
-    const double r2 = r * r;
-    double y = __builtin_fma(c2, r, 1.0);
-    y = __builtin_fma(z, r2, y);
-    y = y * s;
-    return (float)y;
-}
+__device__ __forceinline__ float expf_libc(float x) { return bnne_expf_libc(x, kExp2Table); }
 
 // Sequential sums with latency hiding: the values of a chunk are loaded into
 // registers first (independent loads, issued back to back), then added one after

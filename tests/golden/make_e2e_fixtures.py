@@ -26,6 +26,7 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parents[2]
 GOLDEN = ROOT / "tests" / "golden"
 RUN = ROOT / "oracle" / "_ref" / "engine_run_soft"
+CLI = ROOT / "oracle" / "_ref" / "bnn-infer-v2-soft"  # the reference CLI with the soft backend
 
 TINY = dict(layers=2, hidden=256, heads=2, kv_heads=1, head_dim=128, ffn=512, vocab=1000, context=128, seed=11)
 TINY_PROMPT, TINY_STEPS, TINY_CTX = 8, 12, 64
@@ -61,7 +62,10 @@ def tiny(pkg):
         ids.write_text(" ".join(map(str, prompt)) + "\n")
         out = subprocess.run([str(RUN), "llm", str(model), str(ids), str(TINY_STEPS), str(TINY_CTX)], check=True,
                              capture_output=True, text=True).stdout
-    res = {"model": TINY, "prompt": prompt, "steps_arg": TINY_STEPS, "ctx": TINY_CTX, **parse_llm(out)}
+        cli = subprocess.run([str(CLI), "llm", str(model), "--ids", str(ids), "--steps", str(TINY_STEPS),
+                              "--ctx", str(TINY_CTX)], check=True, capture_output=True).stdout
+    res = {"model": TINY, "prompt": prompt, "steps_arg": TINY_STEPS, "ctx": TINY_CTX, **parse_llm(out),
+           "cli_steps": TINY_STEPS, "cli_stdout_hex": cli.hex()}
     (GOLDEN / "e2e_qwen3_tiny.json").write_text(json.dumps(res, indent=1) + "\n")
 
 

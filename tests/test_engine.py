@@ -232,6 +232,21 @@ def test_engine_qwen3_tiny_bit_exact(pkg, tmp_path, runner):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("cli", ["bnn-infer-v2-own", "bnn-infer-v2-hip"])
+def test_reference_cli_on_this_build(pkg, tmp_path, cli):
+    """The reference CLI (bnn-infer-v2.c, unchanged) linked against this engine
+    (-own) or the reference engine on this backend (-hip) prints the same token
+    pieces as the reference CLI with the soft backend."""
+    exe = REF_DIR / cli
+    if not exe.exists():
+        pytest.skip(f"{cli} not built")
+    model, ids = write_tiny(pkg, tmp_path)
+    out = subprocess.run([str(exe), "llm", str(model), "--ids", str(ids), "--steps", str(TINY["cli_steps"]),
+                          "--ctx", str(TINY["ctx"])], capture_output=True, timeout=120, check=True).stdout
+    assert out.hex() == TINY["cli_stdout_hex"]
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("runner", ["own", "refhip"])
 def test_engine_bnn_mlp_bit_exact(pkg, tmp_path, runner):
     exe = ENGINE_RUN_OWN if runner == "own" else ENGINE_RUN_REFHIP
@@ -289,6 +304,15 @@ def test_engine_api_behaviour(pkg, hip, tmp_path, resident):
         tok = (ctypes.c_int32 * 4)()
         n = ctypes.c_uint32()
         assert eng.BNNE_Tokenize(m.handle, b"hi", 1, tok, 4, ctypes.byref(n)) == -3
+        piece, plen = ctypes.c_char_p(), ctypes.c_size_t()
+        eng.lib.BNNE_TokenPiece.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_char_p),
+                                            ctypes.POINTER(ctypes.c_size_t)]
+        assert eng.lib.BNNE_TokenPiece(m.handle, 300, ctypes.byref(piece), ctypes.byref(plen)) == 0
+        assert piece.value == b"<t300>" and plen.value == 6
+        assert eng.lib.BNNE_TokenPiece(m.handle, 33, ctypes.byref(piece), ctypes.byref(plen)) == 0
+        assert piece.value == b"!"  # byte tokens stand for their byte
+        assert eng.lib.BNNE_TokenPiece(m.handle, TINY["model"]["vocab"], ctypes.byref(piece),
+                                       ctypes.byref(plen)) == -4
         c.free()
         m.free()
 
@@ -309,3 +333,12 @@ def test_engine_qwen3_1p7b_matches_reference(pkg, tmp_path, path):
                          timeout=600, check=True).stdout
     assert parse_path(out) == path
     assert parse_llm(out) == full["steps"]
+
+
+def test_device_expf_restatement_matches_host_libm():
+    """The device expf (engine/libc_expf.h, shared with the kernels) returns what the
+    host C library's expf returns: every 13th float bit pattern here (the full 2^32
+    sweep is the same program with stride 1)."""
+    exe = ROOT / "oracle" / "lib" / "libc_expf_check"
+    out = subprocess.run([str(exe), "13"], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0 and out.stdout.strip().endswith("mismatches 0"), out.stdout
