@@ -227,6 +227,381 @@ __global__ __launch_bounds__(256) void k_gemm(GemmJob j, uint32_t mtiles, uint64
     }
 }
 
+// ---------------------------------------------------------------------------
+// k_gemm_big: F32-accumulating jobs large enough to give every CU a 128 x 128 tile.
+// Workgroup tile 128 x 128 (4 waves, 2 x 2, 64 x 64 each = 4 x 4 MFMA subtiles).
+// Per group g (one iteration, one barrier):
+//   * the group's A (Q rows) and B (+-1 weight rows) blocks, 16 KB each, and each
+//     wave's 64 column scales (128 B) go straight from global memory into LDS
+//     (global_load_lds, 16 bytes per lane, no registers), double buffered: group
+//     g+1 is issued right after the barrier of iteration g;
+//   * every wave issues the same loads (8, plus 1 for the scales), so "my part of
+//     group g has landed" is vmcnt(0) before the barrier, and after it the whole
+//     group is in LDS;
+//   * the epilogue of group g-1 (RN(scale * D) added to the FP32 accumulators) is
+//     interleaved subtile by subtile with the first-half MFMAs of group g, which
+//     restart that subtile's integer accumulator: VALU and matrix pipes overlap
+//     without a second set of accumulator registers.
+// LDS layout of a block: 16-byte chunk c (0..7) of row r at r*128 + 16*(c ^ ((r >> 1) & 7)):
+// the 16 lanes reading one fragment (rows r0..r0+15, one chunk) hit 16 distinct
+// 16-byte bank groups.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kBigTile = 128;
+constexpr uint32_t kBlock = kBigTile * kGroup;  // bytes per operand per group
+
+__device__ __forceinline__ uint32_t swz128(uint32_t r, uint32_t c) { return r * 128u + 16u * (c ^ ((r >> 1) & 7u)); }
+
+// The bijective workgroup remap that keeps consecutive tiles (the M tiles of one
+// N tile, which share B) on one XCD and its L2.
+__device__ __forceinline__ uint32_t gemm_tile_of_block(uint32_t b, uint32_t grid) {
+    const uint32_t x = b % 8u, i = b / 8u, q = grid / 8u, r = grid % 8u;
+    return (x < r ? x * (q + 1u) : r * (q + 1u) + (x - r) * q) + i;
+}
+
+// 16 bytes per lane from global memory into LDS at lds_addr + 16 * lane (M0 holds the
+// wave's LDS base).  Issued as inline assembly so that the compiler's own wait
+// insertion does not add a wait for every LDS DMA before each later LDS read: the
+// kernel bounds the outstanding loads itself.  The s_nop covers the one wait state
+// between writing M0 and the LDS DMA reading it.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_big(
+    GemmJob j, uint32_t mtiles, uint64_t seq, const uint64_t* __restrict__ flag) {
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[2][2][kBlock];  // [buffer][A/B]
+    __shared__ __attribute__((aligned(16))) unsigned char lds_sc[2][4][128];   // [buffer][wave]
+    if (*flag == seq)
+        return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave >> 1, wn = wave & 1u;
+    const uint32_t tile = gemm_tile_of_block(blockIdx.x, gridDim.x);
+    const uint32_t mt = tile % mtiles, nt = tile / mtiles;
+    const uint32_t m0 = mt * kBigTile, n0 = nt * kBigTile;
+    const uint32_t groups = j.groups;
+
+    // this lane's chunks of a block: instruction i of wave w fills positions
+    // (4w + i) * 64 + lane, i.e. row r = (4w + i) * 8 + lane / 8, slot lane % 8
+    const uint8_t* a_src[4];
+    const uint8_t* b_src[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = (4u * wave + i) * 8u + (lane >> 3);
+        const uint32_t c = (lane & 7u) ^ ((r >> 1) & 7u);
+        const uint32_t m = min(m0 + r, j.rows - 1u);
+        a_src[i] = reinterpret_cast<const uint8_t*>(j.q) + (size_t)m * j.k + 16u * c;
+        b_src[i] = reinterpret_cast<const uint8_t*>(j.wbytes) + (size_t)(n0 + r) * j.k + 16u * c;
+    }
+    // scales of this wave's 64 columns: one 64-feature tile of the scale layout
+    // (clamped into the array for columns past the last tile; those are never stored)
+    const uint32_t stile = min((n0 + wn * 64u) >> 6, j.tiles - 1u);
+    const uint8_t* sc_src = reinterpret_cast<const uint8_t*>(j.wscale) + ((size_t)stile * groups) * 128u + 16u * (lane & 7u);
+    const uint32_t lds0 = lds_offset(lds);
+    const uint32_t lds_sc0 = lds_offset(lds_sc) + wave * 128u;
+    auto issue_group = [&](uint32_t g) {
+        const uint32_t koff = g * kGroup;
+        const uint32_t buf = lds0 + (g & 1u) * (2u * kBlock);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            dma16(a_src[i] + koff, buf + (4u * wave + i) * 1024u);
+            dma16(b_src[i] + koff, buf + kBlock + (4u * wave + i) * 1024u);
+        }
+        if (lane < 8u)
+            dma16(sc_src + (size_t)g * 128u, lds_sc0 + (g & 1u) * 512u);
+    };
+
+    float acc[4][4][4];
+    v4i d[4][4];
+    const v4i c_init = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            d[mi][ni] = c_init;  // with scale 0 the first epilogue adds +0
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mi][ni][r] = 0.0f;
+        }
+    float sc_prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    issue_group(0);
+
+    const uint32_t arow0 = wm * 64u + (lane & 15u), brow0 = wn * 64u + (lane & 15u);
+    const uint32_t chunk = lane >> 4;
+    for (uint32_t g = 0; g < groups; ++g) {
+        // only group g is outstanding; after the barrier every wave's part of it is
+        // in LDS, and every wave has finished reading the other buffer (group g-1:
+        // its MFMAs consumed those registers)
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (g + 1u < groups)
+            issue_group(g + 1u);
+        const unsigned char* blk = lds[g & 1u][0];
+        const uint16_t* scl = reinterpret_cast<const uint16_t*>(lds_sc[g & 1u][wave]);
+        float sc_cur[4];
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+            sc_cur[ni] = __half2float(__ushort_as_half(scl[16u * ni + (lane & 15u)]));
+        v4i a[4], b[4];
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+            a[mi] = *reinterpret_cast<const v4i*>(blk + swz128(arow0 + 16u * mi, chunk));
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+            b[ni] = *reinterpret_cast<const v4i*>(blk + kBlock + swz128(brow0 + 16u * ni, chunk));
+        // first half: epilogue of group g-1 on each subtile, then restart it
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            const float sc = sc_prev[ni];
+            const float cneg = sc * -kMagicValue;  // exact
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc, __int_as_float(d[mi][ni][r]), cneg);
+                d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], c_init, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+            a[mi] = *reinterpret_cast<const v4i*>(blk + swz128(arow0 + 16u * mi, 4u + chunk));
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+            b[ni] = *reinterpret_cast<const v4i*>(blk + kBlock + swz128(brow0 + 16u * ni, 4u + chunk));
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+                d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], d[mi][ni], 0, 0, 0);
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+            sc_prev[ni] = sc_cur[ni];
+        // issue order: the 12 LDS reads of the scales and first half, then per
+        // subtile its 8 epilogue VALU ops and its restarting MFMA (the matrix pipe
+        // runs while the next subtile's VALU ops issue), the second-half LDS reads
+        // spread among them, then the 16 second-half MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i >= 4 && i < 12)
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    }
+    // epilogue of the last group, then store Z (or Z * s)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+        const float sc = sc_prev[ni];
+        const float cneg = sc * -kMagicValue;
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc, __int_as_float(d[mi][ni][r]), cneg);
+    }
+    const uint32_t ncol0 = n0 + wn * 64u + (lane & 15u);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + wm * 64u + 16u * mi + 4u * (lane >> 4) + r;
+            if (m >= j.rows)
+                continue;
+            const float s = j.mode == MODE_SUM_SCALED ? j.rscale[m] : 1.0f;
+            float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const uint32_t n = ncol0 + 16u * ni;
+                if (n < j.n)
+                    orow[n] = j.mode == MODE_SUM_SCALED ? acc[mi][ni][r] * s : acc[mi][ni][r];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// k_gemm_ks: F32-accumulating jobs too small to give every CU a 128 x 128 tile.
+// Workgroup tile (16*TMS) x (16*TNS); the W waves split the K dimension instead of
+// the tile: wave w computes groups w, w+W, w+2W, ... for the whole tile, with its
+// operands loaded straight into registers DEPTH-1 rounds ahead.  Per round of W
+// groups each wave turns its integer results into the exact products
+// RN(scale * D) (the same magic-bias FMA as above) and writes them to LDS; then the
+// threads add the W products of their outputs to their FP32 accumulators in group
+// order -- the order of the sums is the reference's, only the integer work ran in
+// parallel.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ v4i gload_v4i(const void* p) {
+    return *(const __attribute__((address_space(1))) v4i*)p;
+}
+
+template <int TMS, int TNS>
+struct KsOps {
+    v4i a[TMS][2];
+    v4i b[TNS][2];
+    uint16_t s[TNS];
+};
+
+template <int TMS, int TNS, int W, int DEPTH>
+__global__ __launch_bounds__(64 * W) void k_gemm_ks(GemmJob j, uint32_t mtiles, uint64_t seq,
+                                                   const uint64_t* __restrict__ flag) {
+    constexpr uint32_t TM = 16u * TMS, TN = 16u * TNS, SUBS = TMS * TNS, NT = 64u * W;
+    constexpr uint32_t BLOCKS = SUBS * 64u;              // 16-byte blocks of products per wave
+    constexpr uint32_t PER_THREAD = (BLOCKS + NT - 1u) / NT;
+    static_assert(DEPTH >= 2, "at least one round in flight");
+    __shared__ __attribute__((aligned(16))) float prod[W][BLOCKS * 4u];  // [wave][subtile][lane][4]
+    if (*flag == seq)
+        return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t tile = gemm_tile_of_block(blockIdx.x, gridDim.x);
+    const uint32_t mt = tile % mtiles, nt = tile / mtiles;
+    const uint32_t m0 = mt * TM, n0 = nt * TN;
+    const uint32_t groups = j.groups;
+
+    // lane l supplies row (or column) l % 16 of a subtile and bytes 16*(l/16) .. +16 of
+    // each 64-byte half group; rows past the end are clamped (never stored), columns
+    // stay below n_pad (TN divides 128) and their scale tile is clamped into the array
+    const uint8_t* a_ptr[TMS];
+    const uint8_t* b_ptr[TNS];
+    const uint16_t* s_ptr[TNS];
+#pragma unroll
+    for (int mi = 0; mi < TMS; ++mi) {
+        const uint32_t m = min(m0 + 16u * mi + (lane & 15u), j.rows - 1u);
+        a_ptr[mi] = reinterpret_cast<const uint8_t*>(j.q) + (size_t)m * j.k + 16u * (lane >> 4);
+    }
+#pragma unroll
+    for (int ni = 0; ni < TNS; ++ni) {
+        const uint32_t n = n0 + 16u * ni + (lane & 15u);
+        b_ptr[ni] = reinterpret_cast<const uint8_t*>(j.wbytes) + (size_t)n * j.k + 16u * (lane >> 4);
+        const uint32_t st = min(n >> 6, j.tiles - 1u);
+        s_ptr[ni] = reinterpret_cast<const uint16_t*>(j.wscale) + (size_t)st * groups * kTile + (n & 63u);
+    }
+    // loads are unconditional (group clamped into range) so that every path has the
+    // same loads in flight and the wait for a round's operands leaves the later
+    // rounds' loads outstanding
+    auto load = [&](KsOps<TMS, TNS>& o, uint32_t round) {
+        const uint32_t g = min(W * round + wave, groups - 1u);
+#pragma unroll
+        for (int mi = 0; mi < TMS; ++mi)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                o.a[mi][h] = gload_v4i(a_ptr[mi] + (size_t)g * kGroup + 64u * h);
+#pragma unroll
+        for (int ni = 0; ni < TNS; ++ni)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                o.b[ni][h] = gload_v4i(b_ptr[ni] + (size_t)g * kGroup + 64u * h);
+#pragma unroll
+        for (int ni = 0; ni < TNS; ++ni)
+            o.s[ni] = s_ptr[ni][(size_t)g * kTile];
+    };
+
+    float acc[PER_THREAD][4];
+#pragma unroll
+    for (int i = 0; i < (int)PER_THREAD; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[i][r] = 0.0f;
+    const v4i c_init = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+
+    auto round = [&](const KsOps<TMS, TNS>& cur, KsOps<TMS, TNS>& nxt, uint32_t r) {
+        load(nxt, r + DEPTH - 1u);
+        const uint32_t g = W * r + wave;
+        float4 p[TMS][TNS];
+        if (g < groups) {
+#pragma unroll
+            for (int ni = 0; ni < TNS; ++ni) {
+                const float sc = __half2float(__ushort_as_half(cur.s[ni]));
+                const float cneg = sc * -kMagicValue;  // exact
+#pragma unroll
+                for (int mi = 0; mi < TMS; ++mi) {
+                    v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[mi][0], cur.b[ni][0], c_init, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[mi][1], cur.b[ni][1], d, 0, 0, 0);
+                    p[mi][ni].x = __builtin_fmaf(sc, __int_as_float(d[0]), cneg);
+                    p[mi][ni].y = __builtin_fmaf(sc, __int_as_float(d[1]), cneg);
+                    p[mi][ni].z = __builtin_fmaf(sc, __int_as_float(d[2]), cneg);
+                    p[mi][ni].w = __builtin_fmaf(sc, __int_as_float(d[3]), cneg);
+                }
+            }
+        }
+        // the previous round's reads of prod are done (their sums consumed them)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (g < groups) {
+#pragma unroll
+            for (int mi = 0; mi < TMS; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < TNS; ++ni)
+                    *reinterpret_cast<float4*>(&prod[wave][((mi * TNS + ni) * 64u + lane) * 4u]) = p[mi][ni];
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            if (W * r + w < groups) {
+#pragma unroll
+                for (int i = 0; i < (int)PER_THREAD; ++i) {
+                    const uint32_t blk = NT * i + tid;
+                    if (BLOCKS % NT == 0 || blk < BLOCKS) {
+                        const float4 v = *reinterpret_cast<const float4*>(&prod[w][blk * 4u]);
+                        acc[i][0] = acc[i][0] + v.x;
+                        acc[i][1] = acc[i][1] + v.y;
+                        acc[i][2] = acc[i][2] + v.z;
+                        acc[i][3] = acc[i][3] + v.w;
+                    }
+                }
+            }
+        }
+    };
+
+    KsOps<TMS, TNS> o[DEPTH];
+#pragma unroll
+    for (int d = 0; d + 1 < DEPTH; ++d)
+        load(o[d], d);
+    const uint32_t rounds = (groups + W - 1u) / W;
+    // the round count is padded to a multiple of DEPTH with rounds of no groups
+    for (uint32_t r = 0; r < rounds; r += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d)
+            round(o[d], o[(d + DEPTH - 1) % DEPTH], r + d);
+    }
+    // block NT*i + tid is subtile W*i + wave, lane `lane`
+#pragma unroll
+    for (int i = 0; i < (int)PER_THREAD; ++i) {
+        const uint32_t sub = W * i + wave;
+        if (sub >= SUBS)
+            continue;
+        const uint32_t mi = sub / TNS, ni = sub % TNS;
+        const uint32_t n = n0 + 16u * ni + (lane & 15u);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + 16u * mi + 4u * (lane >> 4) + r;
+            if (m >= j.rows || n >= j.n)
+                continue;
+            float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
+            orow[n] = j.mode == MODE_SUM_SCALED ? acc[i][r] * j.rscale[m] : acc[i][r];
+        }
+    }
+}
+
+template <int TMS, int TNS, int W, int DEPTH>
+hipError_t launch_ks(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
+    const uint32_t mtiles = (job.rows + 16u * TMS - 1u) / (16u * TMS);
+    const uint32_t ntiles = (job.n + 16u * TNS - 1u) / (16u * TNS);
+    hipLaunchKernelGGL((k_gemm_ks<TMS, TNS, W, DEPTH>), dim3(mtiles * ntiles), dim3(64 * W), 0, stream, job, mtiles,
+                       seq, flag);
+    return hipGetLastError();
+}
+
 template <int MS, int NS>
 hipError_t launch_t(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
     const uint32_t mtiles = (job.rows + 32u * MS - 1u) / (32u * MS);
@@ -256,12 +631,43 @@ hipError_t launch_expand(hipStream_t stream, const uint4* wbits, uint32_t tiles,
 #ifndef BNN_GEMM_TILE
 #define BNN_GEMM_TILE 0  // 0: choose by size; 44 / 24 / 22: force MS x NS
 #endif
+#ifndef BNN_GEMM_KS
+#define BNN_GEMM_KS 0  // tuning: TMS TNS W DEPTH (four digits) forces k_gemm_ks with that shape
+#endif
+#ifndef BNN_GEMM_BIG
+#define BNN_GEMM_BIG 1  // k_gemm_big for F32-accumulating jobs with a 128 x 128 tile per CU
+#endif
 hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count, uint64_t seq,
                        const uint64_t* flag) {
     const uint64_t cus = cu_count ? cu_count : 256u;
     auto blocks = [&](uint32_t tm, uint32_t tn) {
         return (uint64_t)((job.rows + tm - 1u) / tm) * ((job.n + tn - 1u) / tn);
     };
+    if (BNN_GEMM_BIG && job.mode != MODE_DOT_I16 && blocks(kBigTile, kBigTile) >= cus) {
+        const uint32_t mtiles = (job.rows + kBigTile - 1u) / kBigTile;
+        const uint32_t ntiles = (job.n + kBigTile - 1u) / kBigTile;
+        hipLaunchKernelGGL(k_gemm_big, dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq, flag);
+        return hipGetLastError();
+    }
+#if BNN_GEMM_KS
+    if (job.mode != MODE_DOT_I16) {
+        // tuning: BNN_GEMM_KS = TMS TNS W DEPTH as four digits
+        constexpr int v = BNN_GEMM_KS;
+        return launch_ks<v / 1000, (v / 100) % 10, (v / 10) % 10, v % 10>(stream, job, seq, flag);
+    }
+#else
+    // too few 64 x 64 tiles to occupy the CUs: split K across 8 waves per tile, with
+    // the largest tile that still yields about a workgroup per CU (measured on the
+    // 64/256-row 2048x6144 and 6144x2048 shapes)
+    if (BNN_GEMM_TILE == 0 && job.mode != MODE_DOT_I16 && blocks(64, 64) < cus) {
+        const uint64_t enough = cus * 3u / 4u;
+        if (blocks(64, 32) >= enough)
+            return launch_ks<4, 2, 8, 2>(stream, job, seq, flag);
+        if (blocks(32, 32) >= enough)
+            return launch_ks<2, 2, 8, 2>(stream, job, seq, flag);
+        return launch_ks<2, 1, 8, 3>(stream, job, seq, flag);
+    }
+#endif
     if (BNN_GEMM_TILE == 44 || (BNN_GEMM_TILE == 0 && blocks(128, 128) >= cus))
         return launch_t<4, 4>(stream, job, seq, flag);
     if (BNN_GEMM_TILE == 24 || (BNN_GEMM_TILE == 0 && blocks(64, 128) >= cus))

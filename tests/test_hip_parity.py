@@ -103,6 +103,25 @@ def test_quantiser_edge_rows(pkg, hipdev, oracle, i):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), first_mismatch(got, want)
 
 
+@pytest.mark.parametrize("op", ["GEMM", "GEMM_F32"])
+@pytest.mark.parametrize("rows,k,n", [
+    (1000, 384, 4100), (2049, 128, 2000), (1152, 640, 8128),  # 128 x 128 tiles, one wave per subtile block
+    (50, 640, 1000), (100, 3200, 3000), (120, 1152, 5000),    # K split over 8 waves: 32x16, 32x32, 64x32 tiles
+])
+def test_gemm_tilings_ragged_edges(pkg, hipdev, oracle_fast, op, rows, k, n):
+    """Shapes that select each multi-row tiling, with a partial last row tile, a last
+    column tile that ends inside a 64-feature scale tile or past it, odd and even
+    group counts, fewer groups than waves, and round counts that do not fill the
+    prefetch ring."""
+    print(f"case {op} rows={rows} k={k} n={n}", flush=True)
+    bits, scales = pkg.synth.matrix(n, k, seed=rows + n)
+    f32 = op.endswith("F32")
+    x = pkg.synth.normal_f32(rows, k, seed=k) if f32 else pkg.synth.int8_uniform(rows, k, seed=k)
+    got = run_chunks(pkg, hipdev, op, [(bits, scales)], x)
+    want = fast_oracle(pkg, oracle_fast, op, bits, scales, x)
+    assert np.array_equal(got.view(np.uint8), want.view(np.uint8)), first_mismatch(got, want)
+
+
 @pytest.mark.parametrize("op", ["DOT_GROUPS", "GEMM", "GEMM_F32"])
 def test_row_chunking_and_late_illegal_row(pkg, hipdev, oracle_fast, op):
     """More rows than one launch chunk: all rows are validated before any chunk writes."""
