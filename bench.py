@@ -27,12 +27,13 @@ Secondary legs (the other benchmark configurations; --no-extra skips them):
   gemm             config 4: GEMM_F32 / GEMM_I8 at rows 64/256/1024 on the matrix
                    cores: TOPS and utilisation of the 5.0 POPS dense int8 peak
   e2e              config 5: Qwen3-1.7B-shape greedy decode (random-init Q1_0 model,
-                   32 prompt + 128 new tokens) through the engine, device path and
-                   the reference call pattern; tok/s, backend share of step time,
+                   32 prompt + 128 new tokens) through the engine: the device path
+                   (fused batches), the device path with prepared batches, and the
+                   reference call pattern; tok/s, backend share of step time,
                    token agreement with the reference engine + soft backend (fixture)
   mlp              config 1: bnn-mlp classifier, 1000 samples in batches of 64
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--only LEG]
 """
 from __future__ import annotations
 
@@ -267,9 +268,10 @@ def e2e_leg(pkg, hip):
             t0 = time.perf_counter()
             model = pkg.engine.Model(eng, dev, path)
             load_s = time.perf_counter() - t0
-            for name in ("device", "host"):
+            for name, mode in (("device", 1), ("prepared", 2), ("host", 0)):
                 ctx = pkg.engine.Context(model, n_ctx=1024)
-                ctx.set_resident(name == "device")
+                ctx.set_resident(mode)
+                assert ctx.resident() == mode, f"{name} path not available"
                 t0 = time.perf_counter()
                 tokens = [int(np.argmax(ctx.decode(prompt)))]
                 t1 = time.perf_counter()
@@ -338,6 +340,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary legs (ops, gemm, e2e, mlp)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run one 256 MiB device-to-device copy (counter calibration)")
+    ap.add_argument("--only", choices=("ops", "gemm", "e2e", "mlp"),
+                    help="run one secondary leg alone and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
@@ -349,6 +353,10 @@ def main():
 
     pkg = load_pkg()
     hip = pkg.load_hip()
+    if args.only:
+        legs = {"ops": ops_leg, "gemm": gemm_leg, "e2e": e2e_leg, "mlp": mlp_leg}
+        print(json.dumps({args.only: legs[args.only](pkg, hip)}), flush=True)
+        return
     dev = pkg.Device(hip, 0)
     name, arch = dev.name()
     print(f"device: {name} {arch}", flush=True)

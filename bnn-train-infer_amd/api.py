@@ -113,6 +113,21 @@ class Job(ctypes.Structure):  # bnn-accelerator.h:155-161
     ]
 
 
+class PreOp(ctypes.Structure):  # include/bnn-accelerator-hip.h (BNNX_PreOp)
+    ROW, RMSNORM, SILU_MUL = 0, 1, 2
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("width", ctypes.c_uint32),
+        ("a", ctypes.c_void_p),
+        ("b", ctypes.c_void_p),
+        ("gain", ctypes.c_void_p),
+        ("a_out", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("err", ctypes.c_void_p),
+        ("err_code", ctypes.c_int32),
+    ]
+
+
 class BnnError(RuntimeError):
     def __init__(self, status: int, what: str = ""):
         self.status = Status(status) if status in Status._value2member_map_ else status
@@ -158,6 +173,7 @@ class Api:
             "BNNX_DeviceName": (S, [V, ctypes.c_char_p, SZ, ctypes.c_char_p, SZ]),
             "BNNX_ExecuteBatch": (S, [V, P(Job), U32]),
             "BNNX_BatchCreate": (S, [V, P(Job), U32, P(V)]),
+            "BNNX_BatchCreateFused": (S, [V, P(Job), U32, P(PreOp), P(V)]),
             "BNNX_BatchLaunch": (S, [V]),
             "BNNX_BatchCheck": (S, [V]),
             "BNNX_BatchDestroy": (None, [V]),
@@ -211,6 +227,12 @@ class Buffer:
 
     def view(self, type_: Type, offset: int = 0, row_stride: int = 0) -> BufferView:
         return BufferView(self.handle.value, int(type_), offset, row_stride)
+
+    def device_pointer(self) -> int:
+        """Device address of the buffer (HIP backend extension)."""
+        p = ctypes.c_void_p()
+        _check(self.device.api.BNNX_BufferDevicePointer(self.handle, ctypes.byref(p)), "BNNX_BufferDevicePointer")
+        return p.value
 
     def free(self) -> None:
         if self.handle:

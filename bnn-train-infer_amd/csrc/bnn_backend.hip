@@ -1011,6 +1011,148 @@ EXPORT BNN_Status BNNX_BatchCreate(BNN_Device device, const BNN_Job* jobs, uint3
     return BNN_OK;
 }
 
+namespace {
+struct Span {
+    uintptr_t begin, end;
+};
+bool spans_overlap(const Span& x, const Span& y) { return x.begin < y.end && y.begin < x.end; }
+Span span_of(const void* p, size_t bytes) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    return Span{a, p ? a + bytes : a};
+}
+}  // namespace
+
+EXPORT BNN_Status BNNX_BatchCreateFused(BNN_Device device, const BNN_Job* jobs, uint32_t count, const BNNX_PreOp* pre,
+                                        BNNX_Batch* out_batch) {
+    if (out_batch == nullptr)
+        return BNN_EINVAL;
+    *out_batch = nullptr;
+    if (device == nullptr || jobs == nullptr || count == 0 || pre == nullptr)
+        return BNN_EINVAL;
+    if (pre->kind != BNNX_PRE_ROW && pre->kind != BNNX_PRE_RMSNORM && pre->kind != BNNX_PRE_SILU_MUL)
+        return BNN_EINVAL;
+    const uint32_t width = pre->width;
+    if (width == 0 || width % kGroup != 0)
+        return BNN_EINVAL;
+    if ((pre->kind == BNNX_PRE_RMSNORM && (pre->a == nullptr || pre->gain == nullptr)) ||
+        (pre->kind == BNNX_PRE_SILU_MUL && (pre->a == nullptr || pre->b == nullptr)))
+        return BNN_EINVAL;
+    const size_t row_bytes = (size_t)width * 4u;
+    // everything the workgroups read while others write
+    Span reads[5];
+    uint32_t nreads = 0;
+    if (pre->kind != BNNX_PRE_ROW) {
+        reads[nreads++] = span_of(pre->a, row_bytes);
+        if (pre->b)
+            reads[nreads++] = span_of(pre->b, row_bytes);
+        if (pre->kind == BNNX_PRE_RMSNORM)
+            reads[nreads++] = span_of(pre->gain, row_bytes);
+    }
+    const float* a_out = pre->kind == BNNX_PRE_RMSNORM ? pre->a_out : nullptr;
+    if (a_out) {
+        const Span w = span_of(a_out, row_bytes);
+        for (uint32_t r = 0; r < nreads; ++r)
+            if (spans_overlap(w, reads[r]))
+                return BNN_EINVAL;
+    }
+    Span* outs = static_cast<Span*>(malloc(sizeof(Span) * (count + 1u)));
+    FusedJob* table = static_cast<FusedJob*>(malloc(sizeof(FusedJob) * count));
+    BNN_Status st = outs && table ? BNN_OK : BNN_ENOMEM;
+    uint32_t tiles = 0;
+    const unsigned char* row = nullptr;
+    for (uint32_t i = 0; st == BNN_OK && i < count; ++i) {
+        JobPlan p;
+        st = plan_job(device, &jobs[i], &p);
+        if (st != BNN_OK)
+            break;
+        if (jobs[i].operation != BNN_OP_GEMV_F32 || !p.out_aligned || p.m->k > kFusedMaxWidth) {
+            st = BNN_ENOTSUP;
+            break;
+        }
+        if (p.m->k != width) {
+            st = BNN_EINVAL;
+            break;
+        }
+        if (pre->kind == BNNX_PRE_ROW) {
+            if (!p.in_aligned) {
+                st = BNN_ENOTSUP;
+                break;
+            }
+            if (i == 0) {
+                row = p.in_base;
+                reads[nreads++] = span_of(row, row_bytes);
+            } else if (p.in_base != row) {
+                st = BNN_EINVAL;
+                break;
+            }
+        }
+        outs[i] = span_of(p.out_base, p.out_row);
+        table[i] = FusedJob{p.m->wbits, p.m->wscale, reinterpret_cast<float*>(p.out_base), p.m->n, p.m->tiles, tiles, 0};
+        tiles += p.m->tiles;
+    }
+    if (st == BNN_OK) {
+        if (a_out)
+            outs[count] = span_of(a_out, row_bytes);
+        const uint32_t nouts = count + (a_out ? 1u : 0u);
+        std::sort(outs, outs + nouts, [](const Span& x, const Span& y) { return x.begin < y.begin; });
+        for (uint32_t i = 0; st == BNN_OK && i < nouts; ++i) {
+            if (i > 0 && outs[i].begin < outs[i - 1].end)
+                st = BNN_EINVAL;
+            for (uint32_t r = 0; st == BNN_OK && r < nreads; ++r)
+                if (spans_overlap(outs[i], reads[r]))
+                    st = BNN_EINVAL;
+        }
+    }
+    free(outs);
+    if (st == BNN_OK && hipSetDevice(device->ordinal) != hipSuccess)
+        st = BNN_EIO;
+    BNNX_Batch b = nullptr;
+    if (st == BNN_OK) {
+        b = static_cast<BNNX_Batch>(calloc(1, sizeof(bnnx_batch)));
+        void* mem = nullptr;
+        if (b == nullptr || hipMalloc(&mem, sizeof(FusedJob) * count) != hipSuccess) {
+            (void)hipGetLastError();
+            st = BNN_ENOMEM;
+        } else if (hipMemcpy(mem, table, sizeof(FusedJob) * count, hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(mem);
+            st = BNN_EIO;
+        } else {
+            b->mem = static_cast<unsigned char*>(mem);
+        }
+    }
+    free(table);
+    if (st != BNN_OK) {
+        free(b);
+        return st;
+    }
+    b->device = device;
+    b->retired = device->retired;
+    b->needs_nearest = true;
+    b->fused = true;
+    b->fused_tiles = tiles;
+    // one workgroup per tile up to two per CU; beyond that workgroups loop over tiles
+    // (each produces the row once)
+    const uint32_t cus = device->cu_count ? device->cu_count : 256u;
+    b->fused_grid = tiles < 2u * cus ? tiles : 2u * cus;
+    FusedArgs& fa = b->fused_args;
+    fa.jobs = reinterpret_cast<const FusedJob*>(b->mem);
+    fa.njobs = count;
+    fa.kind = pre->kind;
+    fa.width = width;
+    fa.eps = pre->eps;
+    fa.a = pre->kind == BNNX_PRE_ROW ? nullptr : pre->a;
+    fa.b = pre->kind == BNNX_PRE_ROW ? nullptr : pre->b;
+    fa.gain = pre->kind == BNNX_PRE_RMSNORM ? pre->gain : nullptr;
+    fa.a_out = const_cast<float*>(a_out);
+    fa.row = reinterpret_cast<const float*>(row);
+    fa.err = pre->kind == BNNX_PRE_RMSNORM ? pre->err : nullptr;
+    fa.err_code = pre->err_code;
+    device->live_batches++;
+    *out_batch = b;
+    return BNN_OK;
+}
+
 EXPORT BNN_Status BNNX_BatchCheck(BNNX_Batch batch) {
     if (batch == nullptr || batch->retired != batch->device->retired)  // a matrix or buffer it uses may be gone
         return BNN_EINVAL;
@@ -1029,8 +1171,14 @@ EXPORT BNN_Status BNNX_BatchLaunch(BNNX_Batch batch) {
     const uint64_t seq = ++device->seq;
     if (device->async_first_seq == 0)
         device->async_first_seq = seq;
-    const hipError_t e = launch_batch(device, batch->mem, batch->prep_tab, batch->dot_tab, batch->prep_map,
-                                      batch->prep_blocks, batch->items, batch->uniform_items, batch->max_groups, seq);
+    const hipError_t e =
+        batch->fused ? timed(device, KK_DOT,
+                             [&] {
+                                 return launch_fused(device->stream, batch->fused_args, batch->fused_tiles,
+                                                     batch->fused_grid, seq, device->flag_dev, device->status_host);
+                             })
+                     : launch_batch(device, batch->mem, batch->prep_tab, batch->dot_tab, batch->prep_map,
+                                    batch->prep_blocks, batch->items, batch->uniform_items, batch->max_groups, seq);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return BNN_EIO;

@@ -258,14 +258,13 @@ __device__ __forceinline__ uint32_t gemm_tile_of_block(uint32_t b, uint32_t grid
     return (x < r ? x * (q + 1u) : r * (q + 1u) + (x - r) * q) + i;
 }
 
-// 16 bytes per lane from global memory into LDS at lds_addr + 16 * lane (M0 holds the
-// wave's LDS base).  Issued as inline assembly so that the compiler's own wait
+// 16 bytes per lane from global memory into LDS at lds_addr + 16 * lane (the wave's
+// LDS base goes in M0).  Issued as inline assembly so that the compiler's own wait
 // insertion does not add a wait for every LDS DMA before each later LDS read: the
 // kernel bounds the outstanding loads itself.  The s_nop covers the one wait state
 // between writing M0 and the LDS DMA reading it.
 __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr)
-                 : "memory", "m0");
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_addr) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {

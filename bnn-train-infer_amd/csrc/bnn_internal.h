@@ -104,6 +104,34 @@ constexpr uint32_t kGemmRowPad = 128;  // n_pad granularity = largest workgroup 
 #endif
 constexpr uint32_t kMfmaMinRows = BNN_MFMA_MIN_ROWS;
 
+// Fused batches (bnn_fused.hip): GEMV_F32 jobs sharing one input row produced on
+// the device by a pre-operation.  One entry per job; the job's tiles are the
+// workgroups first_tile .. first_tile + tiles - 1 of the launch.
+enum PreKind : int32_t { PRE_ROW = 0, PRE_RMSNORM = 1, PRE_SILU_MUL = 2 };
+constexpr uint32_t kFusedMaxWidth = 6144;  // K of a fused batch (LDS holds the whole row)
+
+struct FusedJob {
+    const uint4* wbits;
+    const uint16_t* wscale;
+    float* out;  // output row
+    uint32_t n, tiles, first_tile, pad_;
+};
+
+struct FusedArgs {
+    const FusedJob* jobs;  // device table
+    uint32_t njobs;
+    int32_t kind;          // PreKind
+    uint32_t width;        // K
+    float eps;
+    const float* a;        // RMSNORM: x; SILU_MUL: gate
+    const float* b;        // RMSNORM: residual (may be null); SILU_MUL: up
+    const float* gain;     // RMSNORM
+    float* a_out;          // RMSNORM: receives x + residual (may be null)
+    const float* row;      // ROW: the input row
+    int32_t* err;          // set to err_code when the RMSNORM check fails (may be null)
+    int32_t err_code;
+};
+
 // Host-side launchers (bnn_kernels.hip).  All are asynchronous on `stream`.
 // Single job: descriptor passed by value.  `validate_only` runs only the
 // legality pass of prep (over all rows of a job processed in several chunks).
@@ -124,6 +152,10 @@ hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32
                             const uint64_t* flag);
 hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count, uint64_t seq,
                        const uint64_t* flag);
+// One launch of a fused batch of `tiles` 64-feature tiles on `grid` workgroups
+// (bnn_fused.hip).
+hipError_t launch_fused(hipStream_t stream, const FusedArgs& args, uint32_t tiles, uint32_t grid, uint64_t seq,
+                        uint64_t* flag, uint64_t* host_status);
 // wbytes[n_pad][k] <- sign bits of the matrix layout (once per matrix).
 hipError_t launch_expand(hipStream_t stream, const uint4* wbits, uint32_t tiles, uint32_t groups,
                          uint32_t n_pad, int8_t* wbytes);
@@ -196,6 +228,10 @@ struct bnnx_batch {
     uint32_t prep_blocks, items, uniform_items, max_groups;
     size_t prep_tab, dot_tab, prep_map;
     bool needs_nearest;
+    // fused batch (BNNX_BatchCreateFused): one launch of `fused_tiles` workgroups
+    bool fused;
+    uint32_t fused_tiles, fused_grid;
+    bnnhip::FusedArgs fused_args;  // jobs points into mem
 };
 
 struct bnn_accel_buffer {

@@ -12,8 +12,9 @@
  * k << 47 restores it and scales by 2^(k div 32)).  The polynomial coefficients are
  * those of the published method (2^(r/32) in r, scaled by powers of 1/32).
  *
- * One source for the device (resident.hip) and for the test-side host check that
- * compares it with the C library on every float.
+ * One source for the device (the backend's fused SiLU pre-operation, the engine's
+ * kernels) and for the test-side host check that compares it with the C library on
+ * every float.
  * Plain C: define BNNE_EXPF_QUALIFIER for device compilation.
  */
 #ifndef BNNE_LIBC_EXPF_H

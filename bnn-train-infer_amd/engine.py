@@ -127,12 +127,15 @@ class Context:
                                               out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))), "BNNE_Classify")
         return out
 
-    def set_resident(self, enable: bool) -> None:
-        """Device path (default) or the host call pattern; only before the first token."""
-        self.eng.check(self.eng.BNNEX_ContextSetResident(self.handle, 1 if enable else 0), "BNNEX_ContextSetResident")
+    def set_resident(self, mode: int) -> None:
+        """Decode path, only before the first token: 1 device with fused batches (the
+        default), 2 device with prepared batches, 0 the host call pattern (True and
+        False mean 1 and 0)."""
+        self.eng.check(self.eng.BNNEX_ContextSetResident(self.handle, int(mode)), "BNNEX_ContextSetResident")
 
-    def resident(self) -> bool:
-        return bool(self.eng.BNNEX_ContextIsResident(self.handle))
+    def resident(self) -> int:
+        """The path in effect: 1 device (fused), 2 device (prepared batches), 0 host."""
+        return int(self.eng.BNNEX_ContextIsResident(self.handle))
 
     def pos(self) -> int:
         return int(self.eng.BNNE_ContextPos(self.handle))

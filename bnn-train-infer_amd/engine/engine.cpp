@@ -398,7 +398,7 @@ BNNE_EXPORT BNNE_Status BNNEX_ContextSetResident(BNNE_Context c, int enable) {
     error_clear();
     if (!c)
         return BNNE_EINVAL;
-    return qwen3_set_resident(c, enable != 0);
+    return qwen3_set_resident(c, enable);
 }
 
-BNNE_EXPORT int BNNEX_ContextIsResident(BNNE_Context c) { return c && qwen3_is_resident(c) ? 1 : 0; }
+BNNE_EXPORT int BNNEX_ContextIsResident(BNNE_Context c) { return c ? qwen3_resident_mode(c) : 0; }

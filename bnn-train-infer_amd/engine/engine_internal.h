@@ -130,8 +130,10 @@ struct Arch {
 
 extern const Arch kArchQwen3;
 extern const Arch kArchBnnMlp;
-BNNE_Status qwen3_set_resident(bnne_context* c, bool enable);
-bool qwen3_is_resident(const bnne_context* c);
+// Decode path of a qwen3 context: 0 host call pattern, 1 device with fused
+// batches (where the backend takes them), 2 device with prepared batches.
+BNNE_Status qwen3_set_resident(bnne_context* c, int mode);
+int qwen3_resident_mode(const bnne_context* c);
 const Arch* arch_find(const char* name);
 
 }  // namespace bnne

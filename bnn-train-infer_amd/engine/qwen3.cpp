@@ -284,7 +284,7 @@ BNNE_Status alloc_host_cache(const Model* m, State* s) {
     return BNNE_OK;
 }
 
-BNNE_Status make_resident(bnne_context* c, const Model* m, State* s) {
+BNNE_Status make_resident(bnne_context* c, const Model* m, State* s, bool fused) {
     const float* attn[kMaxLayers];
     const float* ffn[kMaxLayers];
     const float* qn[kMaxLayers];
@@ -303,7 +303,7 @@ BNNE_Status make_resident(bnne_context* c, const Model* m, State* s) {
     rm.emb_bits = m->emb_bits, rm.emb_scales = m->emb_scales, rm.rope_cos = s->rope_cos, rm.rope_sin = s->rope_sin;
     rm.wq = lin[0], rm.wk = lin[1], rm.wv = lin[2], rm.wo = lin[3], rm.gate = lin[4], rm.up = lin[5];
     rm.down = lin[6], rm.lm_head = &m->lm_head;
-    return resident_create(c, rm, &s->resident);
+    return resident_create(c, rm, fused, &s->resident);
 }
 
 // Every context starts on the device-resident step; one whose shapes that step
@@ -335,7 +335,7 @@ BNNE_Status ctx_init(bnne_context* c, void** out_state) {
         return error(BNNE_ENOMEM, "out of memory");
     }
     init_rope_tables(m, s);
-    BNNE_Status st = make_resident(c, m, s);
+    BNNE_Status st = make_resident(c, m, s, true);
     if (st == BNNE_ENOTSUP) {
         error_clear();
         st = alloc_host_cache(m, s);
@@ -495,19 +495,26 @@ BNNE_Status truncate(bnne_context*, uint32_t) { return BNNE_OK; }
 
 const Arch kArchQwen3 = {"qwen3", BNNE_TASK_LLM, load, unload, ctx_init, ctx_free, nullptr, decode, truncate};
 
-BNNE_Status qwen3_set_resident(bnne_context* c, bool enable) {
+BNNE_Status qwen3_set_resident(bnne_context* c, int mode) {
     if (c->model->arch != &kArchQwen3)
         return error(BNNE_ENOTSUP, "only qwen3 contexts have a device-resident step");
+    if (mode < 0 || mode > 2)
+        return error(BNNE_EINVAL, "unknown decode path %d", mode);
     State* s = static_cast<State*>(c->state);
-    if (enable == (s->resident != nullptr))
+    if (mode == qwen3_resident_mode(c))
         return BNNE_OK;
     if (c->pos != 0)
         return error(BNNE_EINVAL, "the decode path can only change before the first token");
     const Model* m = static_cast<const Model*>(c->model->impl);
-    if (enable) {
-        const BNNE_Status st = make_resident(c, m, s);
-        if (st != BNNE_OK)
+    if (mode != 0) {
+        Resident* old = s->resident;
+        s->resident = nullptr;
+        const BNNE_Status st = make_resident(c, m, s, mode == 1);
+        if (st != BNNE_OK) {
+            s->resident = old;
             return st;
+        }
+        resident_free(old);
         std::free(s->k_cache);
         std::free(s->v_cache);
         s->k_cache = s->v_cache = nullptr;
@@ -521,8 +528,11 @@ BNNE_Status qwen3_set_resident(bnne_context* c, bool enable) {
     return BNNE_OK;
 }
 
-bool qwen3_is_resident(const bnne_context* c) {
-    return c->model->arch == &kArchQwen3 && static_cast<const State*>(c->state)->resident != nullptr;
+int qwen3_resident_mode(const bnne_context* c) {
+    if (c->model->arch != &kArchQwen3)
+        return 0;
+    const Resident* r = static_cast<const State*>(c->state)->resident;
+    return r == nullptr ? 0 : resident_fused(r) ? 1 : 2;
 }
 
 }  // namespace bnne

@@ -1,8 +1,12 @@
 // Device-resident Qwen3 decode: the whole token step runs on the GPU, on the
-// accelerator device's stream.  Linear layers are prepared BNNX batches of the
-// HIP backend (q/k/v together, gate/up together, the lm_head chunks together);
-// RMSNorm, q/k norms, RoPE, the KV cache, attention, SiLU and the residual adds
-// are kernels of this engine that keep the host step's operation order (each
+// accelerator device's stream.  Linear layers are fused BNNX batches of the HIP
+// backend (q/k/v together, gate/up together, the lm_head chunks together), whose
+// single launch also produces the layer's input row: the RMSNorm with the
+// residual add, the attention output, or SiLU(gate)*up.  The q/k norms, RoPE, the
+// KV cache and attention are one kernel of this engine.  Where the backend does
+// not take fused batches (wider layers), prepared batches run beside this
+// engine's RMSNorm and SiLU kernels instead.  Every kernel keeps the host step's
+// operation order (each
 // output's sums run sequentially in one lane, no FMA contraction, IEEE division
 // and square root, and an expf that returns what the host C library's expf
 // returns), so the logits are the ones the host step computes.
@@ -37,7 +41,12 @@ struct ResidentModel {  // host views of the model, used once to build the devic
 
 struct Resident;
 
-BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, Resident** out);
+// fused: run the linear layers as fused batches where the backend takes them
+// (BNNX_BatchCreateFused), else as prepared batches with this engine's norm and
+// SiLU kernels.
+BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, bool fused, Resident** out);
+// Whether the step runs fused batches.
+bool resident_fused(const Resident* r);
 // One decode step of `token` at position `pos`; logits (host, V floats) only when
 // non-null.  Enqueues everything, waits once.
 BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, uint32_t n, uint32_t pos0,

@@ -18,7 +18,7 @@
 #include "resident.h"
 
 #define BNNE_EXPF_QUALIFIER static __device__ __forceinline__
-#include "libc_expf.h"
+#include "../csrc/libc_expf.h"
 
 #pragma clang fp contract(off)
 
@@ -215,11 +215,55 @@ __global__ __launch_bounds__(64) void k_head_norm_rope(float* __restrict__ q, fl
             v_row[(size_t)kh * HD + i] = v[(size_t)kh * HD + i];
 }
 
+// value[i] = sum over t = 0..pos in order of p[t] * V[t][i] for the head's i (one
+// per thread, HD <= 512 over two rounds).  V rows come through LDS in chunks of
+// kVChunk rows, loaded with coalesced 16-byte reads by the whole workgroup; row pos
+// is read from `v_last` when it is not null (the row not yet in the cache).
+constexpr uint32_t kVChunkFloats = 4096;  // 16 KB of V rows per chunk
+
+__device__ __forceinline__ void pv_accumulate(const float* __restrict__ sc, const float* __restrict__ vc,
+                                              const float* __restrict__ v_last, size_t head_off, uint32_t pos,
+                                              uint32_t kv_dim, uint32_t HD, float4* vs4, float* __restrict__ y) {
+    const uint32_t tid = threadIdx.x;
+    const float* vs = reinterpret_cast<const float*>(vs4);
+    const uint32_t rows = kVChunkFloats / HD, hd4 = HD / 4u;
+    float acc0 = 0.0f, acc1 = 0.0f;
+    for (uint32_t t0 = 0; t0 <= pos; t0 += rows) {
+        const uint32_t n = min(rows, pos + 1u - t0);
+        for (uint32_t idx = tid; idx < n * hd4; idx += 256u) {
+            const uint32_t r = idx / hd4, c = idx - r * hd4;
+            const uint32_t t = t0 + r;
+            const float* src = (t == pos && v_last) ? v_last + head_off : vc + (size_t)t * kv_dim + head_off;
+            vs4[idx] = reinterpret_cast<const float4*>(src)[c];
+        }
+        __syncthreads();
+        if (tid < HD) {
+            uint32_t r = 0;
+            for (; r + 8u <= n; r += 8u) {
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    acc0 = acc0 + sc[t0 + r + c] * vs[(r + c) * HD + tid];
+            }
+            for (; r < n; ++r)
+                acc0 = acc0 + sc[t0 + r] * vs[r * HD + tid];
+        }
+        if (tid + 256u < HD) {
+            for (uint32_t r = 0; r < n; ++r)
+                acc1 = acc1 + sc[t0 + r] * vs[r * HD + tid + 256u];
+        }
+        __syncthreads();
+    }
+    if (tid < HD)
+        y[tid] = acc0;
+    if (tid + 256u < HD)
+        y[tid + 256u] = acc1;
+}
+
 // Causal attention of one head against cache rows 0..pos (qwen3.c:441-478):
 // scores (each dot sequential over head_dim), max, exp, the sum in position order,
 // probabilities, and each output element's sum in position order.  Scores and
 // probabilities live in LDS up to kLdsPositions positions, in `scores` beyond.
-constexpr uint32_t kLdsPositions = 8192;
+constexpr uint32_t kLdsPositions = 8192;  // 32 KB of scores; beyond, `scores` in global memory
 
 __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, const float* __restrict__ kc,
                                                    const float* __restrict__ vc, uint32_t pos, uint32_t kv_dim,
@@ -230,6 +274,7 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
     __shared__ float red[256];
     __shared__ float sum_s;
     __shared__ float4 lds_sc4[kLdsPositions / 4];
+    __shared__ float4 vs4[kVChunkFloats / 4];
     float* lds_sc = reinterpret_cast<float*>(lds_sc4);
     const uint32_t h = blockIdx.x, tid = threadIdx.x;
     const size_t head_off = (size_t)(h / kv_mul) * HD;
@@ -288,25 +333,226 @@ __global__ __launch_bounds__(256) void k_attention(const float* __restrict__ q, 
         sc[t] = sc[t] / sum;
     __threadfence_block();
     __syncthreads();
-    // value[i] = sum_t p[t] * v[t][i]: lanes over i, positions in order, 8 rows of
-    // V loaded ahead of their adds
-    for (uint32_t i = tid; i < HD; i += 256u) {
-        const float* col = vc + head_off + i;
-        float acc = 0.0f;
-        uint32_t t = 0;
-        for (; t + 8u <= pos + 1u; t += 8u) {
-            float vv[8];
-#pragma unroll
-            for (int c = 0; c < 8; ++c)
-                vv[c] = col[(size_t)(t + c) * kv_dim];
-#pragma unroll
-            for (int c = 0; c < 8; ++c)
-                acc = acc + sc[t + c] * vv[c];
-        }
-        for (; t <= pos; ++t)
-            acc = acc + sc[t] * col[(size_t)t * kv_dim];
-        y[(size_t)h * HD + i] = acc;
+    pv_accumulate(sc, vc, nullptr, head_off, pos, kv_dim, HD, vs4, y + (size_t)h * HD);
+}
+
+// Error words of the fused step: the code of the earliest failure in the host
+// step's order wins.  Per layer l the codes are l * span + p, with p = 1 for the
+// attention RMSNorm, 2 for the q/k head norms, 3 + 2h / 4 + 2h for the score /
+// softmax checks of head h and 3 + 2H for the FFN RMSNorm (span = 4 + 2H); the
+// final RMSNorm is L * span + 1.  Codes only grow along the step, so "smallest
+// code" is "first failure"; the backend's fused batches store theirs only into a
+// clear word, which they can only meet after every earlier code of the step.
+__device__ void set_error_first(int* err, int code) {
+    int old = __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    while (old == kErrNone || old > code) {
+        const int prev = atomicCAS(err, old, code);
+        if (prev == old)
+            break;
+        old = prev;
     }
+}
+
+// One query head h per workgroup (qwen3.c:419-478 for that head): RMSNorm of the
+// head and of its kv head over head_dim (the two in-order sums run in two waves at
+// once), RoPE of both, the kv head's cache row at pos stored by its first query
+// head, then causal attention against rows 0..pos -- row pos taken from this
+// workgroup's own normalised k and from v, so no workgroup reads a row another is
+// writing.  Every global read the step needs is issued before the first sum: each
+// thread's key row for the scores (one position per thread, 256 per round) into
+// registers, and V rows 0..kAttnVRows-1 straight into LDS (global_load_lds, no
+// registers); longer contexts stream further V rows through the same LDS.  All
+// sums are sequential in index / position order, as in the host step.
+constexpr uint32_t kAttnThreads = 256;
+constexpr uint32_t kAttnHD = 128;                   // head_dim of the register-resident key rows
+constexpr uint32_t kAttnVRows = 192;                // V rows resident in LDS (96 KB)
+constexpr uint32_t kAttnLdsPositions = 4096;        // scores in LDS (16 KB); beyond, `scores`
+constexpr uint32_t kAttnV4 = kAttnVRows * kAttnHD / 4;
+
+// 16 bytes per lane from global memory into LDS at lds_addr + 16 * lane (lds_addr is
+// the wave's base, in M0).  Inline assembly: the kernel waits for these loads
+// itself (vmcnt(0) before the first read).  The s_nop covers the wait state between
+// writing M0 and the LDS DMA reading it.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_addr) : "memory");
+}
+
+// V rows t0 .. t0 + kAttnVRows - 1 (clamped to pos; row pos from v) into vs4: thread
+// tid moves 16-byte piece idx = tid + 256 j, i.e. row idx / 32, column piece idx % 32;
+// waves whose pieces all lie past row pos skip the load.
+__device__ __forceinline__ void attn_dma_v(float4* vs4, const float* __restrict__ vc, const float* __restrict__ v,
+                                           size_t head_off, uint32_t t0, uint32_t pos, uint32_t kv_dim) {
+    constexpr uint32_t hd4 = kAttnHD / 4;
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63u;
+    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
+    const uint32_t live = min(pos + 1u - t0, kAttnVRows) * hd4;  // pieces holding rows t0..pos
+    for (uint32_t j = 0; j < kAttnV4 / kAttnThreads; ++j) {
+        const uint32_t first = kAttnThreads * j + 64u * wave;  // the wave's first piece
+        if (first >= live)
+            break;
+        const uint32_t idx = first + lane, r = idx / hd4, c = idx % hd4;
+        const uint32_t t = min(t0 + r, pos);
+        const float* src = t == pos ? v + head_off : vc + (size_t)t * kv_dim + head_off;
+        dma16(src + 4u * c, base + first * 16u);
+    }
+}
+
+__global__ __launch_bounds__(kAttnThreads) void k_attention_fused(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, uint32_t kv_mul, float eps,
+    const float* __restrict__ q_gain, const float* __restrict__ k_gain, const float* __restrict__ cosv,
+    const float* __restrict__ sinv, float* __restrict__ kc, float* __restrict__ vc, uint32_t pos, uint32_t kv_dim,
+    float scale, float* __restrict__ scores, uint32_t n_ctx, float* __restrict__ y, int* err, int code_base) {
+    constexpr uint32_t HD = kAttnHD, hd4 = HD / 4;
+    __shared__ float4 vs4[kAttnV4];
+    __shared__ float4 lds_sc4[kAttnLdsPositions / 4];
+    __shared__ float4 qs4[HD / 4], ks4[HD / 4];
+    __shared__ float4 sq4[2][HD / 4];
+    __shared__ float red[kAttnThreads / 64];
+    __shared__ float rms_s[2];
+    __shared__ float sum_s;
+    float* qs = reinterpret_cast<float*>(qs4);
+    float* ks = reinterpret_cast<float*>(ks4);
+    float* lds_sc = reinterpret_cast<float*>(lds_sc4);
+    const float* vs = reinterpret_cast<const float*>(vs4);
+    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t kh = h / kv_mul;
+    const size_t head_off = (size_t)kh * HD;
+    float* sc = pos < kAttnLdsPositions ? lds_sc : scores + (size_t)h * n_ctx;
+
+    // reads: the head vectors, the first V rows (to LDS), this thread's key row
+    const float qv = tid < HD ? q[(size_t)h * HD + tid] : 0.0f;
+    const float kv = tid < HD ? k[head_off + tid] : 0.0f;
+    attn_dma_v(vs4, vc, v, head_off, 0, pos, kv_dim);
+    float4 key[hd4];
+    {
+        const float* row = kc + (size_t)min(tid, pos) * kv_dim + head_off;  // row pos itself is never used
+#pragma unroll
+        for (uint32_t c = 0; c < hd4; ++c)
+            key[c] = reinterpret_cast<const float4*>(row)[c];
+    }
+
+    // head norms: the q sum in wave 0, the k sum in wave 1, concurrently
+    float* sq_q = reinterpret_cast<float*>(sq4[0]);
+    float* sq_k = reinterpret_cast<float*>(sq4[1]);
+    if (tid < HD) {
+        qs[tid] = qv;
+        ks[tid] = kv;
+        sq_q[tid] = qv * qv;
+        sq_k[tid] = kv * kv;
+    }
+    __syncthreads();
+    if (tid == 0 || tid == 64) {
+        const float sum = sum_lds_in_order(tid == 0 ? sq_q : sq_k, HD);
+        rms_s[tid == 0 ? 0 : 1] = sqrtf(sum / (float)HD + eps);
+    }
+    __syncthreads();
+    const float rq = rms_s[0], rk = rms_s[1];
+    if (!isfinite(rq) || rq == 0.0f || !isfinite(rk) || rk == 0.0f) {
+        if (tid == 0)
+            set_error_first(err, code_base + 2);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no LDS DMA outlives the workgroup
+        return;
+    }
+    if (tid < HD) {
+        qs[tid] = qs[tid] / rq * q_gain[tid];
+        ks[tid] = ks[tid] / rk * k_gain[tid];
+    }
+    __syncthreads();
+    // RoPE of pairs (j, j + HD/2); thread j owns pair j of both vectors
+    constexpr uint32_t half = HD / 2u;
+    if (tid < half) {
+        const float c = cosv[tid], s = sinv[tid];
+        float a = qs[tid], b = qs[tid + half];
+        qs[tid] = a * c - b * s;
+        qs[tid + half] = a * s + b * c;
+        a = ks[tid], b = ks[tid + half];
+        ks[tid] = a * c - b * s;
+        ks[tid + half] = a * s + b * c;
+    }
+    __syncthreads();
+    if (h % kv_mul == 0 && tid < HD) {
+        kc[(size_t)pos * kv_dim + head_off + tid] = ks[tid];
+        vc[(size_t)pos * kv_dim + head_off + tid] = v[head_off + tid];
+    }
+
+    // scores: position t by thread t mod 256; the first round's key rows are in
+    // registers, later rounds load theirs; row pos from ks
+    float mx = -INFINITY;
+    for (uint32_t t = tid; t <= pos; t += kAttnThreads) {
+        if (t != tid) {
+            const float* row = kc + (size_t)min(t, pos) * kv_dim + head_off;
+#pragma unroll
+            for (uint32_t c = 0; c < hd4; ++c)
+                key[c] = reinterpret_cast<const float4*>(row)[c];
+        }
+        float dot = 0.0f;
+        if (t == pos) {
+            for (uint32_t i = 0; i < HD; ++i)
+                dot = dot + qs[i] * ks[i];
+        } else {
+#pragma unroll
+            for (uint32_t c = 0; c < hd4; ++c) {
+                const float4 qq = qs4[c];
+                dot = dot + qq.x * key[c].x;
+                dot = dot + qq.y * key[c].y;
+                dot = dot + qq.z * key[c].z;
+                dot = dot + qq.w * key[c].w;
+            }
+        }
+        const float score = dot * scale;
+        if (!isfinite(score))
+            set_error_first(err, code_base + 3 + 2 * (int)h);
+        sc[t] = score;
+        mx = score > mx ? score : mx;
+    }
+    // the maximum over the workgroup (order-free)
+    for (uint32_t o = 32; o > 0; o >>= 1)
+        mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0)
+        red[tid >> 6] = mx;
+    __syncthreads();
+    const float maximum = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (uint32_t t = tid; t <= pos; t += kAttnThreads)
+        sc[t] = expf_libc(sc[t] - maximum);
+    __threadfence_block();
+    __syncthreads();
+    if (tid == 0) {
+        const float sum = pos < kAttnLdsPositions ? sum_lds_in_order(sc, pos + 1u)
+                                                  : sum_in_order<32>(pos + 1u, [&](uint32_t t) { return sc[t]; });
+        if (!(sum > 0.0f) || !isfinite(sum))
+            set_error_first(err, code_base + 4 + 2 * (int)h);
+        sum_s = sum;
+    }
+    __syncthreads();
+    const float sum = sum_s;
+    for (uint32_t t = tid; t <= pos; t += kAttnThreads)
+        sc[t] = sc[t] / sum;
+    __threadfence_block();
+
+    // value[i] = sum over t in order of p[t] * V[t][i]; V rows in LDS, kAttnVRows at a time
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's V pieces have landed
+    float acc = 0.0f;
+    for (uint32_t t0 = 0; t0 <= pos; t0 += kAttnVRows) {
+        if (t0 > 0) {
+            __syncthreads();  // every thread is done with the previous rows
+            attn_dma_v(vs4, vc, v, head_off, t0, pos, kv_dim);
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        }
+        __syncthreads();
+        if (tid < HD) {
+            const uint32_t n = min(kAttnVRows, pos + 1u - t0);
+            uint32_t r = 0;
+            for (; r + 8u <= n; r += 8u) {
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    acc = acc + sc[t0 + r + c] * vs[(r + c) * HD + tid];
+            }
+            for (; r < n; ++r)
+                acc = acc + sc[t0 + r] * vs[r * HD + tid];
+        }
+    }
+    if (tid < HD)
+        y[(size_t)h * HD + tid] = acc;
 }
 
 // gate = gate / (1 + exp(-gate)) * up (qwen3.c:491-495).
@@ -331,10 +577,14 @@ struct Resident {
     BNN_Buffer b_norm, b_q, b_k, b_v, b_y, b_o, b_gate, b_up, b_logits;
     float *norm, *q, *k, *v, *y, *o, *gate, *up;
     // everything else: this engine's device memory
-    float *x, *kc, *vc, *scores, *gains, *rope_cos, *rope_sin;
+    float *x, *x2, *kc, *vc, *scores, *gains, *rope_cos, *rope_sin;
     uint8_t* emb_bits;
     uint16_t* emb_scales;
     int* err;
+    // fused: every linear layer is a fused batch (its input row produced and
+    // quantised inside its one launch), else prepared batches plus this engine's
+    // norm and SiLU kernels (models wider than a fused batch takes)
+    bool allow_fused, fused;
     BNNX_Batch *qkv, *attn_out, *gate_up, *down;
     BNNX_Batch lm_head;
     const Linear** lin;  // [7 * L + 1]: per layer q, k, v, o, gate, up, down; then lm_head
@@ -396,6 +646,27 @@ BNNE_Status make_batch(Resident* r, std::initializer_list<std::pair<const Linear
     return st;
 }
 
+BNNE_Status make_fused(Resident* r, std::initializer_list<std::pair<const Linear*, BNN_Buffer>> parts, BNN_Buffer in,
+                       const BNNX_PreOp& pre, BNNX_Batch* out, uint64_t* jobs_total, uint64_t* macs,
+                       BNN_Status* accel_status) {
+    uint32_t count = 0;
+    for (const auto& p : parts)
+        count += p.first->n_chunks;
+    BNN_Job* jobs = static_cast<BNN_Job*>(std::calloc(count, sizeof(BNN_Job)));
+    if (!jobs)
+        return error(BNNE_ENOMEM, "out of memory");
+    uint32_t n = 0;
+    for (const auto& p : parts)
+        add_jobs(p.first, in, p.second, jobs, &n, macs);
+    *accel_status = BNNX_BatchCreateFused(r->dev, jobs, n, &pre, out);
+    std::free(jobs);
+    *jobs_total += n;
+    return *accel_status == BNN_OK ? BNNE_OK : accel_error(*accel_status, "BNNX_BatchCreateFused");
+}
+
+// Error codes of the fused step (see set_error_first).
+int code_span(const Resident* r) { return 4 + 2 * (int)r->H; }
+
 }  // namespace
 
 namespace {
@@ -423,10 +694,99 @@ void destroy_batches(Resident* r) {
     r->lm_head = nullptr;
 }
 
-// The prepared batches of every layer and of the lm_head.  Rebuilt when the
-// backend reports them stale (some other matrix or buffer of the device was
-// destroyed since; this context's own objects are still alive).
+// Fused batches of every layer and of the lm_head:
+//   qkv:    RMSNorm(x [+ o]) with attn_norm, the sum stored to x2   -> q, k, v
+//   o:      the attention output row y                               -> o
+//   gate/up RMSNorm(x2 + o) with ffn_norm, the sum stored to x       -> gate, up
+//   down:   SiLU(gate) * up                                          -> o
+//   lm_head RMSNorm(x + o) with final_norm                           -> logits
+// so the residual stream alternates between x and x2 within a layer and is in x
+// (plus the down output in o) between layers.  *accel_status is the backend's
+// status of the first batch it refused.
+BNNE_Status build_fused(Resident* r, BNN_Status* accel_status) {
+    r->jobs_per_token = r->macs_per_token = r->lm_jobs = r->lm_macs = 0;
+    *accel_status = BNN_OK;
+    const uint32_t C = r->C;
+    const float* attn_norm = r->gains;
+    const float* ffn_norm = r->gains + (size_t)r->L * C;
+    const float* final_norm = r->gains + 2 * (size_t)r->L * C + 2 * (size_t)r->L * r->HD;
+    BNNE_Status st = BNNE_OK;
+    for (uint32_t l = 0; st == BNNE_OK && l < r->L; ++l) {
+        const Linear* const* p = r->lin + 7 * (size_t)l;
+        const int base = (int)l * code_span(r);
+        BNNX_PreOp pre{};
+        pre.kind = BNNX_PRE_RMSNORM;
+        pre.width = C;
+        pre.a = r->x;
+        pre.b = l ? r->o : nullptr;
+        pre.gain = attn_norm + (size_t)l * C;
+        pre.a_out = r->x2;
+        pre.eps = r->eps;
+        pre.err = r->err;
+        pre.err_code = base + 1;
+        st = make_fused(r, {{p[0], r->b_q}, {p[1], r->b_k}, {p[2], r->b_v}}, r->b_norm, pre, &r->qkv[l],
+                        &r->jobs_per_token, &r->macs_per_token, accel_status);
+        if (st == BNNE_OK) {
+            BNNX_PreOp row{};
+            row.kind = BNNX_PRE_ROW;
+            row.width = C;
+            st = make_fused(r, {{p[3], r->b_o}}, r->b_y, row, &r->attn_out[l], &r->jobs_per_token, &r->macs_per_token,
+                            accel_status);
+        }
+        if (st == BNNE_OK) {
+            pre.a = r->x2;
+            pre.b = r->o;
+            pre.gain = ffn_norm + (size_t)l * C;
+            pre.a_out = r->x;
+            pre.err_code = base + 3 + 2 * (int)r->H;
+            st = make_fused(r, {{p[4], r->b_gate}, {p[5], r->b_up}}, r->b_norm, pre, &r->gate_up[l], &r->jobs_per_token,
+                            &r->macs_per_token, accel_status);
+        }
+        if (st == BNNE_OK) {
+            BNNX_PreOp silu{};
+            silu.kind = BNNX_PRE_SILU_MUL;
+            silu.width = r->FF;
+            silu.a = r->gate;
+            silu.b = r->up;
+            st = make_fused(r, {{p[6], r->b_o}}, r->b_gate, silu, &r->down[l], &r->jobs_per_token, &r->macs_per_token,
+                            accel_status);
+        }
+    }
+    if (st == BNNE_OK) {
+        BNNX_PreOp pre{};
+        pre.kind = BNNX_PRE_RMSNORM;
+        pre.width = C;
+        pre.a = r->x;
+        pre.b = r->o;
+        pre.gain = final_norm;
+        pre.eps = r->eps;
+        pre.err = r->err;
+        pre.err_code = (int)r->L * code_span(r) + 1;
+        st = make_fused(r, {{r->lin[7 * (size_t)r->L], r->b_logits}}, r->b_norm, pre, &r->lm_head, &r->lm_jobs,
+                        &r->lm_macs, accel_status);
+    }
+    return st;
+}
+
+// The prepared batches of every layer and of the lm_head (fused where the backend
+// takes them).  Rebuilt when the backend reports them stale (some other matrix or
+// buffer of the device was destroyed since; this context's own objects are still
+// alive).
+BNNE_Status build_unfused(Resident* r);
 BNNE_Status build_batches(Resident* r) {
+    r->fused = false;
+    if (!r->allow_fused || r->HD != kAttnHD)  // the fused step's attention kernel is built for one head_dim
+        return build_unfused(r);
+    BNN_Status accel = BNN_OK;
+    BNNE_Status st = build_fused(r, &accel);
+    r->fused = st == BNNE_OK;
+    if (st == BNNE_OK || accel != BNN_ENOTSUP)
+        return st;
+    destroy_batches(r);
+    return build_unfused(r);
+}
+
+BNNE_Status build_unfused(Resident* r) {
     r->jobs_per_token = r->macs_per_token = r->lm_jobs = r->lm_macs = 0;
     BNNE_Status st = BNNE_OK;
     for (uint32_t l = 0; st == BNNE_OK && l < r->L; ++l) {
@@ -448,17 +808,20 @@ BNNE_Status build_batches(Resident* r) {
 
 }  // namespace
 
-BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, Resident** out) {
+bool resident_fused(const Resident* r) { return r->fused; }
+
+BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, bool fused, Resident** out) {
     *out = nullptr;
-    if (m.HD > kMaxHeadDim || m.C > kMaxNormWidth)
-        return error(BNNE_ENOTSUP, "device-resident decode supports head_dim <= %u and width <= %u", kMaxHeadDim,
-                     kMaxNormWidth);
+    if (m.HD > kMaxHeadDim || m.HD % 4u != 0 || m.C > kMaxNormWidth)
+        return error(BNNE_ENOTSUP, "device-resident decode supports head_dim <= %u (a multiple of 4) and width <= %u",
+                     kMaxHeadDim, kMaxNormWidth);
     Resident* r = static_cast<Resident*>(std::calloc(1, sizeof(Resident)));
     if (!r)
         return error(BNNE_ENOMEM, "out of memory");
     r->dev = c->model->device;
     r->C = m.C, r->H = m.H, r->Hk = m.Hk, r->HD = m.HD, r->FF = m.FF, r->L = m.L, r->V = m.V;
     r->kv_dim = m.kv_dim, r->n_ctx = m.n_ctx, r->eps = m.eps;
+    r->allow_fused = fused;
     BNNE_Status st = accel_error(BNNX_DeviceStream(r->dev, reinterpret_cast<void**>(&r->stream)), "BNNX_DeviceStream");
     hipError_t e = hipSuccess;
     if (st == BNNE_OK) {
@@ -490,6 +853,8 @@ BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, Resident** 
     const size_t cache = (size_t)m.L * m.n_ctx * m.kv_dim * sizeof(float);
     if (st == BNNE_OK)
         st = upload(&r->x, nullptr, (size_t)m.C * sizeof(float));
+    if (st == BNNE_OK)
+        st = upload(&r->x2, nullptr, (size_t)m.C * sizeof(float));
     if (st == BNNE_OK)
         st = upload(&r->kc, nullptr, cache);
     if (st == BNNE_OK)
@@ -569,7 +934,7 @@ void resident_free(Resident* r) {
     std::free(r->lin);
     for (BNN_Buffer b : {r->b_norm, r->b_q, r->b_k, r->b_v, r->b_y, r->b_o, r->b_gate, r->b_up, r->b_logits})
         BNN_BufferFree(b);
-    for (void* p : {(void*)r->x, (void*)r->kc, (void*)r->vc, (void*)r->scores, (void*)r->gains, (void*)r->rope_cos,
+    for (void* p : {(void*)r->x, (void*)r->x2, (void*)r->kc, (void*)r->vc, (void*)r->scores, (void*)r->gains, (void*)r->rope_cos,
                     (void*)r->rope_sin, (void*)r->emb_bits, (void*)r->emb_scales, (void*)r->err})
         if (p)
             (void)hipFree(p);
@@ -608,7 +973,26 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         if (st == BNNE_OK)
             st = accel_error(BNNX_BatchLaunch(b), "BNNX_BatchLaunch");
     };
-    for (uint32_t i = 0; i < n && st == BNNE_OK; ++i) {
+    for (uint32_t i = 0; i < n && st == BNNE_OK && r->fused; ++i) {
+        const uint32_t pos = pos0 + i;
+        hipLaunchKernelGGL(k_embed, dim3((C + 255u) / 256u), dim3(256), 0, r->stream, (uint32_t)tokens[i],
+                           r->emb_bits, r->emb_scales, C, r->x);
+        for (uint32_t l = 0; l < r->L && st == BNNE_OK; ++l) {
+            const size_t cache_layer = (size_t)l * r->n_ctx * r->kv_dim;
+            launch(r->qkv[l]);
+            hipLaunchKernelGGL(k_attention_fused, dim3(r->H), dim3(kAttnThreads), 0, r->stream, r->q, r->k, r->v,
+                               r->H / r->Hk, r->eps, q_norm + (size_t)l * HD, k_norm + (size_t)l * HD,
+                               r->rope_cos + (size_t)pos * half, r->rope_sin + (size_t)pos * half,
+                               r->kc + cache_layer, r->vc + cache_layer, pos, r->kv_dim, scale, r->scores, r->n_ctx,
+                               r->y, r->err, (int)l * code_span(r));
+            launch(r->attn_out[l]);
+            launch(r->gate_up[l]);
+            launch(r->down[l]);
+        }
+        if (logits && i + 1 == n)
+            launch(r->lm_head);
+    }
+    for (uint32_t i = 0; i < n && st == BNNE_OK && !r->fused; ++i) {
         const uint32_t pos = pos0 + i;
         hipLaunchKernelGGL(k_embed, dim3((C + 255u) / 256u), dim3(256), 0, r->stream, (uint32_t)tokens[i],
                            r->emb_bits, r->emb_scales, C, r->x);
@@ -652,11 +1036,16 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         e = hipMemset(r->err, 0, sizeof(int));
     if (e != hipSuccess)
         return hip_error(e, "error word");
-    if (err == kErrNorm)
+    int kind = err;
+    if (r->fused && err != kErrNone) {
+        const int p = err % code_span(r);  // 1: attention norm, 2: head norms, 3 + 2H: FFN norm
+        kind = p == 1 || p == 2 || p == code_span(r) - 1 ? kErrNorm : ((p - 3) % 2 == 0 ? kErrScore : kErrSoftmax);
+    }
+    if (kind == kErrNorm)
         return error(BNNE_ECOMPUTE, "Qwen3 RMSNorm produced a non-finite divisor");
-    if (err == kErrScore)
+    if (kind == kErrScore)
         return error(BNNE_ECOMPUTE, "Qwen3 attention score is not finite");
-    if (err == kErrSoftmax)
+    if (kind == kErrSoftmax)
         return error(BNNE_ECOMPUTE, "Qwen3 attention softmax failed");
     st = accel_error(sync, "BNN_Execute");
     if (st != BNNE_OK)

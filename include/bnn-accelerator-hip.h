@@ -77,6 +77,45 @@ void BNNX_BatchDestroy(BNNX_Batch batch);
 BNN_Status BNNX_BatchCheck(BNNX_Batch batch);
 BNN_Status BNNX_DeviceSynchronize(BNN_Device device);
 
+/*
+ * Fused batches: GEMV_F32 jobs (rows = 1) that all read one input row, where the
+ * row is produced on the device by a pre-operation and quantised inside the same
+ * single kernel launch that computes the dots -- no prep launch, no host work per
+ * launch.  For decode loops whose linear layers read normalised or gated
+ * device-resident vectors.  With x_i = a_i + b_i (just a_i when b is NULL):
+ *   BNNX_PRE_ROW      input = the jobs' input row (every job must name the same view)
+ *   BNNX_PRE_RMSNORM  rms = sqrtf((sum over i in index order of x_i * x_i) / width + eps),
+ *                     input_i = x_i / rms * gain_i; a_out (if not NULL) receives x
+ *   BNNX_PRE_SILU_MUL input_i = a_i / (1 + expf(-a_i)) * b_i  (expf of the host C library)
+ * every product, quotient and sum rounded to binary32 separately.  The produced row
+ * then goes through exactly what GEMV_F32 does with an input row (check,
+ * quantisation, dots, FP32 accumulation in group order): results are bit-identical
+ * to computing the row on the host and calling BNN_Execute.
+ * a, b, gain, a_out are device addresses on the batch's device (BNNX_BufferDevicePointer
+ * or memory allocated there) of `width` floats, valid whenever the batch runs; a_out
+ * may not overlap a or b, and no job output may overlap any of them (BNN_EINVAL).
+ * Every job must be GEMV_F32 with rows = 1, K = width <= 6144 and an aligned output
+ * view (else BNN_ENOTSUP or the BNN_Execute status).  A non-finite produced row is
+ * an illegal input (nothing written; BNNX_DeviceSynchronize reports BNN_ERANGE); when
+ * the RMSNORM divisor is not finite or zero, err_code is also stored to *err (if err
+ * is not NULL and *err is 0).  Launch, check, destroy and synchronise as any
+ * prepared batch.
+ */
+enum { BNNX_PRE_ROW = 0, BNNX_PRE_RMSNORM = 1, BNNX_PRE_SILU_MUL = 2 };
+typedef struct {
+    int32_t kind;      /* BNNX_PRE_* */
+    uint32_t width;    /* values in the row (the matrices' K) */
+    const float* a;    /* RMSNORM: x; SILU_MUL: gate */
+    const float* b;    /* RMSNORM: residual added to x first (NULL: none); SILU_MUL: up */
+    const float* gain; /* RMSNORM */
+    float* a_out;      /* RMSNORM: receives x (NULL: not stored) */
+    float eps;         /* RMSNORM */
+    int32_t* err;      /* RMSNORM: error word (NULL: none) */
+    int32_t err_code;
+} BNNX_PreOp;
+BNN_Status BNNX_BatchCreateFused(BNN_Device device, const BNN_Job* jobs, uint32_t count, const BNNX_PreOp* pre,
+                                 BNNX_Batch* out_batch);
+
 /* Device address of a buffer's memory, for kernels a caller runs on the device's
  * stream between batch launches.  Valid until BNN_BufferFree. */
 BNN_Status BNNX_BufferDevicePointer(BNN_Buffer buffer, void** out_pointer);

@@ -4,8 +4,11 @@
  *
  * A Qwen3 context runs each decode step on the device by default: activations,
  * the KV cache and every step of the model stay in HBM, the linear layers run as
- * prepared batches of the accelerator (BNNX_BatchCreate), and the host waits once
- * per BNNE_Decode call.  The other path is the reference's call pattern: host
+ * fused batches of the accelerator (BNNX_BatchCreateFused: each layer's input
+ * row -- RMSNorm with the residual add, attention output, SiLU(gate)*up -- is
+ * produced inside the layer's one launch) or, for layers wider than those take,
+ * prepared batches (BNNX_BatchCreate), and the host waits once per BNNE_Decode
+ * call.  The other path is the reference's call pattern: host
  * arithmetic, one synchronous BNN_Execute per linear layer chunk, the activations
  * copied across for every call.  Both compute the same logits bit for bit.
  * Statistics of the device path: execute_ns is the wait for the device,
@@ -20,12 +23,15 @@
 extern "C" {
 #endif
 
-/* Selects the device path (enable != 0) or the host call pattern for a qwen3
- * context.  Only before its first token (BNNE_EINVAL otherwise); BNNE_ENOTSUP for
- * other architectures or shapes the device path does not take. */
+/* Selects the decode path of a qwen3 context: 0 the host call pattern, 1 the
+ * device path with fused batches where the backend takes them (the default), 2
+ * the device path with prepared batches only.  Only before its first token
+ * (BNNE_EINVAL otherwise, and for other values); BNNE_ENOTSUP for other
+ * architectures or shapes the device path does not take. */
 BNNE_Status BNNEX_ContextSetResident(BNNE_Context ctx, int enable);
 
-/* 1 when the context runs the device path. */
+/* The path in effect: 0 host, 1 device with fused batches, 2 device with
+ * prepared batches. */
 int BNNEX_ContextIsResident(BNNE_Context ctx);
 
 #ifdef __cplusplus

@@ -11,7 +11,9 @@
  *       classifies SAMPLES rows of raw float32 input, BATCH per call; prints every
  *       logit as 8 hex digits (its float32 bit pattern), one sample per line
  * Built against this project's engine (OWN_ENGINE), an optional last argument
- * "host" runs the llm case on the host call pattern instead of the device path.
+ * selects the llm decode path: "host" (the host call pattern), "prepared" (the
+ * device path with prepared batches only) or "device" (the default: fused
+ * batches); the path in effect is printed as "path host|prepared|device".
  */
 #include "bnn-engine.h"
 #ifdef OWN_ENGINE
@@ -46,7 +48,7 @@ static uint32_t argmax(const float* v, uint32_t n) {
     return best;
 }
 
-static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint32_t ctx, int host) {
+static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint32_t ctx, int mode) {
     BNNE_ModelInfo info;
     BNNE_Status st = BNNE_ModelGetInfo(model, &info);
     if (st != BNNE_OK)
@@ -69,11 +71,12 @@ static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint3
     if (st != BNNE_OK)
         return fail("BNNE_ContextCreate", st);
 #ifdef OWN_ENGINE
-    if (host && (st = BNNEX_ContextSetResident(c, 0)) != BNNE_OK)
+    if ((st = BNNEX_ContextSetResident(c, mode)) != BNNE_OK)
         return fail("BNNEX_ContextSetResident", st);
-    printf("path %s\n", BNNEX_ContextIsResident(c) ? "device" : "host");
+    static const char* const kPath[] = {"host", "device", "prepared"};
+    printf("path %s\n", kPath[BNNEX_ContextIsResident(c)]);
 #else
-    (void)host;
+    (void)mode;
 #endif
     st = BNNE_Decode(c, ids, count, logits);
     if (st != BNNE_OK)
@@ -139,8 +142,11 @@ static int run_classify(BNNE_Model model, const char* input_path, uint32_t sampl
 }
 
 int main(int argc, char** argv) {
-    const int host = argc == 7 && strcmp(argv[6], "host") == 0;
-    if ((argc != 6 && !host) || (strcmp(argv[1], "llm") != 0 && strcmp(argv[1], "classify") != 0)) {
+    int mode = 1;  /* BNNEX_ContextSetResident: 0 host, 1 device (fused), 2 prepared batches */
+    if (argc == 7)
+        mode = strcmp(argv[6], "host") == 0 ? 0 : strcmp(argv[6], "prepared") == 0 ? 2
+                                            : strcmp(argv[6], "device") == 0 ? 1 : -1;
+    if ((argc != 6 && argc != 7) || mode < 0 || (strcmp(argv[1], "llm") != 0 && strcmp(argv[1], "classify") != 0)) {
         fprintf(stderr, "usage: %s llm MODEL IDS STEPS CTX | classify MODEL INPUT SAMPLES BATCH\n", argv[0]);
         return 1;
     }
@@ -155,7 +161,7 @@ int main(int argc, char** argv) {
     if (st != BNNE_OK)
         return fail("BNNE_ModelLoad", st);
     const uint32_t a = (uint32_t)strtoul(argv[4], NULL, 10), b = (uint32_t)strtoul(argv[5], NULL, 10);
-    const int rc = strcmp(argv[1], "llm") == 0 ? run_llm(model, argv[3], a, b, host) : run_classify(model, argv[3], a, b);
+    const int rc = strcmp(argv[1], "llm") == 0 ? run_llm(model, argv[3], a, b, mode) : run_classify(model, argv[3], a, b);
     BNNE_ModelFree(model);
     BNN_DeviceClose(dev);
     return rc;

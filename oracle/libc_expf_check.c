@@ -1,5 +1,5 @@
 /* Test infrastructure: compares the device expf restatement (one shared source,
- * bnn-train-infer_amd/engine/libc_expf.h) with the host C library's expf on every
+ * bnn-train-infer_amd/csrc/libc_expf.h) with the host C library's expf on every
  * STRIDE-th float bit pattern (STRIDE 1 = all 2^32).  Prints the mismatch count;
  * NaN results compare equal to NaN.  Not part of the product. */
 #include <math.h>
@@ -8,7 +8,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-#include "../bnn-train-infer_amd/engine/libc_expf.h"
+#include "../bnn-train-infer_amd/csrc/libc_expf.h"
 
 int main(int argc, char** argv) {
     const uint64_t stride = argc > 1 ? strtoull(argv[1], NULL, 10) : 1;

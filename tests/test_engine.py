@@ -216,7 +216,7 @@ def test_reference_engine_reproduces_fixtures(pkg, tmp_path):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("runner", ["own-device", "own-host", "refhip"])
+@pytest.mark.parametrize("runner", ["own-device", "own-prepared", "own-host", "refhip"])
 def test_engine_qwen3_tiny_bit_exact(pkg, tmp_path, runner):
     exe = ENGINE_RUN_REFHIP if runner == "refhip" else ENGINE_RUN_OWN
     if runner == "refhip" and not exe.exists():
@@ -224,8 +224,8 @@ def test_engine_qwen3_tiny_bit_exact(pkg, tmp_path, runner):
     model, ids = write_tiny(pkg, tmp_path)
     print(f"engine qwen3 tiny via {exe.name} {runner}", flush=True)
     args = [str(exe), "llm", str(model), str(ids), str(TINY["steps_arg"]), str(TINY["ctx"])]
-    out = subprocess.run(args + (["host"] if runner == "own-host" else []), capture_output=True, text=True,
-                         timeout=120, check=True).stdout
+    out = subprocess.run(args + ([runner.split("-")[1]] if runner != "refhip" else []), capture_output=True,
+                         text=True, timeout=120, check=True).stdout
     if runner != "refhip":
         assert parse_path(out) == runner.split("-")[1]
     assert parse_llm(out) == TINY["steps"]
@@ -260,7 +260,7 @@ def test_engine_bnn_mlp_bit_exact(pkg, tmp_path, runner):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("resident", [True, False], ids=["device", "host"])
+@pytest.mark.parametrize("resident", [1, 2, 0], ids=["device", "prepared", "host"])
 def test_engine_api_behaviour(pkg, hip, tmp_path, resident):
     """Argument and range checks of the public API on a loaded model (engine.c:241-338)."""
     model_path, _ = write_tiny(pkg, tmp_path)
@@ -273,9 +273,12 @@ def test_engine_api_behaviour(pkg, hip, tmp_path, resident):
             pkg.engine.Context(m, n_ctx=TINY["model"]["context"] + 1)
         assert e.value.status == -4
         c = pkg.engine.Context(m, n_ctx=16, n_batch=4)
-        assert c.resident()
+        assert c.resident() == 1  # fused batches by default
         c.set_resident(resident)
         assert c.resident() == resident
+        with pytest.raises(pkg.engine.EngineError) as e:
+            c.set_resident(3)
+        assert e.value.status == -1 and c.resident() == resident
         prompt = TINY["prompt"]
         with pytest.raises(pkg.engine.EngineError) as e:
             c.decode(prompt[:5])  # more than n_batch
@@ -291,7 +294,7 @@ def test_engine_api_behaviour(pkg, hip, tmp_path, resident):
             logits = c.decode(prompt[i:i + 4])
         assert c.pos() == 8 and int(np.argmax(logits)) == TINY["steps"][0][1]
         with pytest.raises(pkg.engine.EngineError) as e:
-            c.set_resident(not resident)  # only before the first token
+            c.set_resident(0 if resident else 1)  # only before the first token
         assert e.value.status == -1
         s = c.stats()
         assert s["calls"] == 2 and s["items"] == 8
@@ -319,7 +322,7 @@ def test_engine_api_behaviour(pkg, hip, tmp_path, resident):
 
 @pytest.mark.gpu
 @pytest.mark.skipif(not FULL_FIXTURE.exists(), reason="full-size fixture not generated")
-@pytest.mark.parametrize("path", ["device", "host"])
+@pytest.mark.parametrize("path", ["device", "prepared", "host"])
 def test_engine_qwen3_1p7b_matches_reference(pkg, tmp_path, path):
     """Benchmark configuration 5 at full Qwen3-1.7B shape: 32 prompt tokens, 128
     greedy tokens; every step's token and logits hash equal the reference engine's."""
@@ -329,14 +332,13 @@ def test_engine_qwen3_1p7b_matches_reference(pkg, tmp_path, path):
     ids.write_text(" ".join(map(str, full["prompt"])) + "\n")
     print(f"engine qwen3 1.7B-shape decode, 32 + 128 tokens, {path} path", flush=True)
     out = subprocess.run([str(ENGINE_RUN_OWN), "llm", str(model), str(ids), str(full["steps_arg"]),
-                          str(full["ctx"])] + (["host"] if path == "host" else []), capture_output=True, text=True,
-                         timeout=600, check=True).stdout
+                          str(full["ctx"]), path], capture_output=True, text=True, timeout=600, check=True).stdout
     assert parse_path(out) == path
     assert parse_llm(out) == full["steps"]
 
 
 def test_device_expf_restatement_matches_host_libm():
-    """The device expf (engine/libc_expf.h, shared with the kernels) returns what the
+    """The device expf (csrc/libc_expf.h, shared by the backend and engine kernels) returns what the
     host C library's expf returns: every 13th float bit pattern here (the full 2^32
     sweep is the same program with stride 1)."""
     exe = ROOT / "oracle" / "lib" / "libc_expf_check"
