@@ -166,6 +166,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     __shared__ uint4 planes[kFusedMaxGroups * kPlaneWords / 4];
     __shared__ int part[kFusedMaxGroups][2];
     __shared__ uint32_t amax_w[kFusedWaves];
+    __shared__ uint64_t exp_tab[32];
     __shared__ float rms_s;
     float* scratch = reinterpret_cast<float*>(scratch4);
 
@@ -229,9 +230,13 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
             uv[i] = fload(fa.b + min(tid + kFusedThreads * i, K - 1u));
+        // the expf table in LDS: its lookups are per-lane gathers
+        if (tid < 32u)
+            exp_tab[tid] = kFusedExp2Table[tid];
+        __syncthreads();
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
-            const float silu = xv[i] / (1.0f + bnne_expf_libc(-xv[i], kFusedExp2Table));
+            const float silu = xv[i] / (1.0f + bnne_expf_libc(-xv[i], exp_tab));
             xv[i] = silu * uv[i];
         }
     } else {

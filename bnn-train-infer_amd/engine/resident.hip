@@ -410,10 +410,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_fused(
     __shared__ float red[kAttnThreads / 64];
     __shared__ float rms_s[2];
     __shared__ float sum_s;
+    __shared__ uint64_t exp_tab[32];  // the expf table: its lookups are per-lane gathers
     float* qs = reinterpret_cast<float*>(qs4);
     float* ks = reinterpret_cast<float*>(ks4);
     float* lds_sc = reinterpret_cast<float*>(lds_sc4);
     const float* vs = reinterpret_cast<const float*>(vs4);
+    if (threadIdx.x < 32u)
+        exp_tab[threadIdx.x] = kExp2Table[threadIdx.x];
     const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u;
     const uint32_t kh = h / kv_mul;
     const size_t head_off = (size_t)kh * HD;
@@ -513,7 +516,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_fused(
     __syncthreads();
     const float maximum = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     for (uint32_t t = tid; t <= pos; t += kAttnThreads)
-        sc[t] = expf_libc(sc[t] - maximum);
+        sc[t] = bnne_expf_libc(sc[t] - maximum, exp_tab);
     __threadfence_block();
     __syncthreads();
     if (tid == 0) {
