@@ -127,6 +127,17 @@ __device__ __forceinline__ float sum_in_order_lds(const float* p, uint32_t n) {
     return sum;
 }
 
+// Workgroup barrier for data exchanged through LDS: waits for this wave's LDS
+// accesses only.  __syncthreads would also wait for every outstanding global load
+// and store of the wave (its release fence), i.e. for the weight prefetch and for
+// the acknowledgement of earlier output stores, none of which the other waves read.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ void fused_raise(uint64_t seq, uint64_t* flag, uint64_t* host_status) {
     __hip_atomic_store(flag, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(host_status, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -174,29 +185,38 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t K = fa.width, G = K / kGroup;
 
-    // 1. the first tile's weights load while the row is produced
+    // 1. the row operands load first and the first tile's weights after them (the
+    // load counter completes in order: the row is needed first), arriving while the
+    // row is produced; thread t owns k = t + 1024 i
     uint32_t tile = blockIdx.x, ji = 0;
     while (ji + 1u < fa.njobs && fa.jobs[ji + 1u].first_tile <= tile)
         ++ji;
     FusedJob job = fa.jobs[ji];
-    TileRegs<GPW> cur, nxt;
-    load_tile<GPW>(job, tile - job.first_tile, G, wave, lane, cur);
-
-    // 2. the input row; thread t owns k = t + 1024 i
-    float xv[EPT];
+    const float* src_a = fa.kind == PRE_ROW ? fa.row : fa.a;
+    float xv[EPT], bv[EPT], gv[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i)
+        xv[i] = fload(src_a + min(tid + kFusedThreads * i, K - 1u));
+    if (fa.b) {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i)
+            bv[i] = fload(fa.b + min(tid + kFusedThreads * i, K - 1u));
+    }
     if (fa.kind == PRE_RMSNORM) {
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
-            xv[i] = fload(fa.a + min(tid + kFusedThreads * i, K - 1u));
+            gv[i] = fload(fa.gain + min(tid + kFusedThreads * i, K - 1u));
+    }
+    TileRegs<GPW> cur, nxt;
+    load_tile<GPW>(job, tile - job.first_tile, G, wave, lane, cur);
+
+    // 2. the input row
+    if (fa.kind == PRE_RMSNORM) {
         if (fa.b) {
 #pragma unroll
             for (int i = 0; i < EPT; ++i)
-                xv[i] = xv[i] + fload(fa.b + min(tid + kFusedThreads * i, K - 1u));
+                xv[i] = xv[i] + bv[i];
         }
-        float gv[EPT];
-#pragma unroll
-        for (int i = 0; i < EPT; ++i)
-            gv[i] = fload(fa.gain + min(tid + kFusedThreads * i, K - 1u));
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
             const uint32_t k = tid + kFusedThreads * i;
@@ -206,10 +226,10 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
                     fstore(fa.a_out + k, xv[i]);
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (tid == 0)
             rms_s = sqrtf(sum_in_order_lds(scratch, K) / (float)K + fa.eps);
-        __syncthreads();
+        lds_barrier();
         const float rms = rms_s;
         if (!__builtin_isfinite(rms) || rms == 0.0f) {
             if (tid == 0) {
@@ -223,26 +243,15 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
         for (int i = 0; i < EPT; ++i)
             xv[i] = xv[i] / rms * gv[i];
     } else if (fa.kind == PRE_SILU_MUL) {
-#pragma unroll
-        for (int i = 0; i < EPT; ++i)
-            xv[i] = fload(fa.a + min(tid + kFusedThreads * i, K - 1u));
-        float uv[EPT];
-#pragma unroll
-        for (int i = 0; i < EPT; ++i)
-            uv[i] = fload(fa.b + min(tid + kFusedThreads * i, K - 1u));
         // the expf table in LDS: its lookups are per-lane gathers
         if (tid < 32u)
             exp_tab[tid] = kFusedExp2Table[tid];
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
             const float silu = xv[i] / (1.0f + bnne_expf_libc(-xv[i], exp_tab));
-            xv[i] = silu * uv[i];
+            xv[i] = silu * bv[i];
         }
-    } else {
-#pragma unroll
-        for (int i = 0; i < EPT; ++i)
-            xv[i] = fload(fa.row + min(tid + kFusedThreads * i, K - 1u));
     }
 
     // 3. the GEMV_F32 input check and the row scale, in one exchange: a wave with a
@@ -258,7 +267,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     abits = __ockl_wfred_max_u32(abits);
     if (lane == 0)
         amax_w[wave] = abits;
-    __syncthreads();
+    lds_barrier();
     abits = amax_w[0];
 #pragma unroll
     for (uint32_t w = 1; w < kFusedWaves; ++w)
@@ -294,7 +303,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
                 part[g][half] = sum;
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     // 5. per tile: group dots and the rounded products F32(scale) * D into one of two
     // product buffers, then wave 0 adds them in group order (one lane per feature)
@@ -319,7 +328,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
                 prod[g * 64u + lane] = __half2float(__ushort_as_half((uint16_t)cur.s[i])) * (float)d;
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (wave == 0) {
             const uint32_t n = (tile - job.first_tile) * kTile + lane;
             float acc = 0.0f;

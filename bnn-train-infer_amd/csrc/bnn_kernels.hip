@@ -319,6 +319,9 @@ enum ItemMap : int { MAP_SINGLE = 0, MAP_UNIFORM = 1, MAP_TABLE = 2 };
 #ifndef BNN_DOT_WAVE_XCDS
 #define BNN_DOT_WAVE_XCDS 0  // > 1: keep consecutive workgroups on one XCD
 #endif
+#ifndef BNN_DOT_WAVE_LONG
+#define BNN_DOT_WAVE_LONG 1  // batches with 16 < K/128 <= 64: one wave per item, groups in blocks
+#endif
 #ifndef BNN_DOT_WAVE_OCC
 #define BNN_DOT_WAVE_OCC 4  // waves per SIMD the register budget is fitted to
 #endif
@@ -601,6 +604,105 @@ void k_dot_wave(const DotJob* __restrict__ jobs, const uint32_t* __restrict__ it
     }
 }
 
+// ---------------------------------------------------------------------------
+// dot, one wave per item for 16 < K/128 <= 64: as k_dot_wave, with the groups in
+// NB blocks of 8 and two register sets -- block b+1's weights and scales load while
+// block b computes.  The block loop is unrolled (NB from the batch's largest group
+// count) and every load is unconditional (group index clamped), so each wait leaves
+// exactly the next block in flight.  Products are added in group order in one
+// register per lane; DOT_GROUPS stores each group's D.
+// ---------------------------------------------------------------------------
+constexpr int kLongBlock = 8;
+constexpr int kLongMaxGroups = 64;
+constexpr int kLongWaves = 4;
+
+template <int MAP, int NB>
+__global__ __launch_bounds__(64 * kLongWaves) __attribute__((amdgpu_waves_per_eu(4)))
+void k_dot_wave_long(const DotJob* __restrict__ jobs, const uint32_t* __restrict__ item_job, uint32_t items,
+                     uint32_t uniform_items, uint64_t seq, const uint64_t* __restrict__ flag) {
+    constexpr int kChunks = NB * kLongBlock * (int)kPlaneWords / 4 / 64;  // uint4 of planes per lane
+    __shared__ uint4 lds_planes[kLongWaves][NB * kLongBlock * kPlaneWords / 4];
+    if (*flag == seq)
+        return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t item = xcd_local_block(blockIdx.x, gridDim.x) * kLongWaves + wave;
+    if (item >= items)
+        return;
+    uint32_t job_index = 0xffffffffu;
+    DotItem it;
+    locate<MAP, 1>(item, DotJob{}, jobs, item_job, uniform_items, it, job_index);
+    const uint32_t groups = it.j.groups;
+    const uint32_t plane_chunks = groups * (kPlaneWords / 4u);
+    const uint4* pl = reinterpret_cast<const uint4*>(it.j.planes + (size_t)it.row * groups * kPlaneWords);
+    uint4 p[kChunks];
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+        p[c] = gload(pl + min(lane + 64u * c, plane_chunks - 1u));
+    const int sum = gload(it.j.sums + (size_t)it.row * groups + min(lane, groups - 1u));
+    const size_t first = (size_t)it.t0 * groups * kTile + lane;
+    uint4 w[2][kLongBlock];
+    uint32_t sc[2][kLongBlock];
+    auto load_block = [&](int buf, int blk) {
+#pragma unroll
+        for (int i = 0; i < kLongBlock; ++i) {
+            const size_t at = first + (size_t)min((uint32_t)(blk * kLongBlock + i), groups - 1u) * kTile;
+            w[buf][i] = gload(it.j.wbits + at);
+            sc[buf][i] = gload(it.j.wscale + at);
+        }
+    };
+    load_block(0, 0);
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+        lds_planes[wave][lane + 64u * c] = p[c];
+    __builtin_amdgcn_wave_barrier();
+    const uint4* lp = lds_planes[wave];
+    const uint32_t n0 = it.t0 * kTile;
+    const bool live = n0 + lane < it.j.n;
+    unsigned char* orow = it.j.out + (size_t)it.row * it.j.out_stride;
+    const bool sum_mode = it.j.mode != MODE_DOT_I16;
+    int16_t* od = reinterpret_cast<int16_t*>(orow) + (size_t)(n0 + lane) * groups;
+    float acc = 0.0f;
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+        if (blk + 1 < NB)
+            load_block((blk + 1) & 1, blk + 1);
+#pragma unroll
+        for (int i = 0; i < kLongBlock; ++i) {
+            const uint32_t g = blk * kLongBlock + i;
+            if (g < groups) {
+                const int d = group_dot_v(w[blk & 1][i], lp + g * (kPlaneWords / 4), -__shfl(sum, g));
+                if (sum_mode)
+                    acc = acc + __half2float(__ushort_as_half((uint16_t)sc[blk & 1][i])) * (float)d;
+                else if (live)
+                    gstore(od + g, (int16_t)d);
+            }
+        }
+    }
+    if (sum_mode) {
+        if (it.j.mode == MODE_SUM_SCALED)
+            acc = acc * gload(it.j.rscale + it.row);
+        if (live)
+            gstore(reinterpret_cast<float*>(orow) + n0 + lane, acc);
+    }
+}
+
+template <int MAP>
+hipError_t launch_dot_long(hipStream_t stream, const DotJob* jobs, const uint32_t* item_job, uint32_t items,
+                           uint32_t uniform_items, uint32_t max_groups, uint64_t seq, const uint64_t* flag) {
+    const uint32_t grid = (items + kLongWaves - 1u) / kLongWaves;
+    const dim3 block(64 * kLongWaves);
+    switch ((max_groups + kLongBlock - 1u) / kLongBlock) {
+    case 3: hipLaunchKernelGGL((k_dot_wave_long<MAP, 3>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 4: hipLaunchKernelGGL((k_dot_wave_long<MAP, 4>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 5: hipLaunchKernelGGL((k_dot_wave_long<MAP, 5>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 6: hipLaunchKernelGGL((k_dot_wave_long<MAP, 6>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 7: hipLaunchKernelGGL((k_dot_wave_long<MAP, 7>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    default: hipLaunchKernelGGL((k_dot_wave_long<MAP, 8>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    }
+    return hipGetLastError();
+}
+
 template <int MAXG, int MAP, int TPI>
 hipError_t launch_dot_t(hipStream_t stream, const DotJob& single, const DotJob* jobs, const uint32_t* item_job,
                         uint32_t items, uint32_t uniform_items, uint32_t grid, uint64_t seq, const uint64_t* flag) {
@@ -690,6 +792,12 @@ hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32
                                flag);
         return hipGetLastError();
     }
+#if BNN_DOT_WAVE_LONG
+    if (BNN_DOT_WAVE_ITEMS && max_groups <= (uint32_t)kLongMaxGroups && many)
+        return uniform_items ? launch_dot_long<MAP_UNIFORM>(stream, jobs, item_job, items, uniform_items, max_groups,
+                                                            seq, flag)
+                             : launch_dot_long<MAP_TABLE>(stream, jobs, item_job, items, 0u, max_groups, seq, flag);
+#endif
     const uint32_t grid = dot_grid(items, max_groups, cu_count);
     if (max_groups <= 16u)
         return uniform_items ? launch_dot_t<16, MAP_UNIFORM, BNN_DOT_TPI_SMALL>(stream, none, jobs, item_job, items,

@@ -92,6 +92,8 @@ __device__ __forceinline__ float sum_lds_in_order(const float* p, uint32_t n) {
 
 __device__ void set_error(int* err, int code) { atomicCAS(err, kErrNone, code); }
 
+extern "C" __device__ float __ockl_wfred_max_f32(float);
+
 // x[i] = +scale or -scale of the token's Q1_0 embedding row (qwen3.c:355-366).
 __global__ __launch_bounds__(256) void k_embed(uint32_t token, const uint8_t* __restrict__ bits,
                                                const uint16_t* __restrict__ scales, uint32_t C,
@@ -369,6 +371,17 @@ constexpr uint32_t kAttnVRows = 192;                // V rows resident in LDS (9
 constexpr uint32_t kAttnLdsPositions = 4096;        // scores in LDS (16 KB); beyond, `scores`
 constexpr uint32_t kAttnV4 = kAttnVRows * kAttnHD / 4;
 
+// Workgroup barrier for data exchanged through LDS: waits for this wave's LDS
+// accesses only.  __syncthreads would also wait for every outstanding global load
+// and store of the wave (its release fence): for the key rows and V rows issued at
+// the start, and for the KV-cache stores, none of which the other waves read.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // 16 bytes per lane from global memory into LDS at lds_addr + 16 * lane (lds_addr is
 // the wave's base, in M0).  Inline assembly: the kernel waits for these loads
 // itself (vmcnt(0) before the first read).  The s_nop covers the wait state between
@@ -385,7 +398,8 @@ __device__ __forceinline__ void attn_dma_v(float4* vs4, const float* __restrict_
     constexpr uint32_t hd4 = kAttnHD / 4;
     const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63u;
     const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
-    const uint32_t live = min(pos + 1u - t0, kAttnVRows) * hd4;  // pieces holding rows t0..pos
+    // pieces of rows t0 .. (pos rounded up to a multiple of 8); rows past pos are copies of row pos
+    const uint32_t live = min(((pos + 8u) & ~7u) - t0, kAttnVRows) * hd4;
     for (uint32_t j = 0; j < kAttnV4 / kAttnThreads; ++j) {
         const uint32_t first = kAttnThreads * j + 64u * wave;  // the wave's first piece
         if (first >= live)
@@ -421,18 +435,33 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_fused(
     const uint32_t kh = h / kv_mul;
     const size_t head_off = (size_t)kh * HD;
     float* sc = pos < kAttnLdsPositions ? lds_sc : scores + (size_t)h * n_ctx;
+    // a barrier after writes to sc: LDS-only unless the scores spill to global memory
+    auto sc_barrier = [&]() {
+        if (pos < kAttnLdsPositions) {
+            lds_barrier();
+        } else {
+            __threadfence_block();
+            __syncthreads();
+        }
+    };
 
-    // reads: the head vectors, the first V rows (to LDS), this thread's key row
-    const float qv = tid < HD ? q[(size_t)h * HD + tid] : 0.0f;
-    const float kv = tid < HD ? k[head_off + tid] : 0.0f;
-    attn_dma_v(vs4, vc, v, head_off, 0, pos, kv_dim);
+    // reads, in the order they are needed (the load counter completes in order, so
+    // a small load issued after the big ones would wait for them): the head
+    // vectors, gains, RoPE factors and v, then this thread's key row, then the first
+    // V rows straight into LDS
+    const uint32_t ti = min(tid, HD - 1u), tj = min(tid, HD / 2u - 1u);
+    const float qv = q[(size_t)h * HD + ti], kv = k[head_off + ti];
+    const float qg = q_gain[ti], kg = k_gain[ti];
+    const float rc = cosv[tj], rs = sinv[tj];
+    const float vv = v[head_off + ti];
     float4 key[hd4];
-    {
-        const float* row = kc + (size_t)min(tid, pos) * kv_dim + head_off;  // row pos itself is never used
+    if (tid < pos) {  // row pos comes from ks
+        const float* row = kc + (size_t)tid * kv_dim + head_off;
 #pragma unroll
         for (uint32_t c = 0; c < hd4; ++c)
             key[c] = reinterpret_cast<const float4*>(row)[c];
     }
+    attn_dma_v(vs4, vc, v, head_off, 0, pos, kv_dim);
 
     // head norms: the q sum in wave 0, the k sum in wave 1, concurrently
     float* sq_q = reinterpret_cast<float*>(sq4[0]);
@@ -443,12 +472,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_fused(
         sq_q[tid] = qv * qv;
         sq_k[tid] = kv * kv;
     }
-    __syncthreads();
+    lds_barrier();
     if (tid == 0 || tid == 64) {
         const float sum = sum_lds_in_order(tid == 0 ? sq_q : sq_k, HD);
         rms_s[tid == 0 ? 0 : 1] = sqrtf(sum / (float)HD + eps);
     }
-    __syncthreads();
+    lds_barrier();
     const float rq = rms_s[0], rk = rms_s[1];
     if (!isfinite(rq) || rq == 0.0f || !isfinite(rk) || rk == 0.0f) {
         if (tid == 0)
@@ -457,14 +486,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_fused(
         return;
     }
     if (tid < HD) {
-        qs[tid] = qs[tid] / rq * q_gain[tid];
-        ks[tid] = ks[tid] / rk * k_gain[tid];
+        qs[tid] = qs[tid] / rq * qg;
+        ks[tid] = ks[tid] / rk * kg;
     }
-    __syncthreads();
+    lds_barrier();
     // RoPE of pairs (j, j + HD/2); thread j owns pair j of both vectors
     constexpr uint32_t half = HD / 2u;
     if (tid < half) {
-        const float c = cosv[tid], s = sinv[tid];
+        const float c = rc, s = rs;
         float a = qs[tid], b = qs[tid + half];
         qs[tid] = a * c - b * s;
         qs[tid + half] = a * s + b * c;
@@ -472,18 +501,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_fused(
         ks[tid] = a * c - b * s;
         ks[tid + half] = a * s + b * c;
     }
-    __syncthreads();
+    lds_barrier();
     if (h % kv_mul == 0 && tid < HD) {
         kc[(size_t)pos * kv_dim + head_off + tid] = ks[tid];
-        vc[(size_t)pos * kv_dim + head_off + tid] = v[head_off + tid];
+        vc[(size_t)pos * kv_dim + head_off + tid] = vv;
     }
 
     // scores: position t by thread t mod 256; the first round's key rows are in
     // registers, later rounds load theirs; row pos from ks
     float mx = -INFINITY;
     for (uint32_t t = tid; t <= pos; t += kAttnThreads) {
-        if (t != tid) {
-            const float* row = kc + (size_t)min(t, pos) * kv_dim + head_off;
+        if (t != tid && t != pos) {
+            const float* row = kc + (size_t)t * kv_dim + head_off;
 #pragma unroll
             for (uint32_t c = 0; c < hd4; ++c)
                 key[c] = reinterpret_cast<const float4*>(row)[c];
@@ -508,50 +537,59 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention_fused(
         sc[t] = score;
         mx = score > mx ? score : mx;
     }
-    // the maximum over the workgroup (order-free)
-    for (uint32_t o = 32; o > 0; o >>= 1)
-        mx = fmaxf(mx, __shfl_xor(mx, o));
+    // the maximum over the workgroup (order-free; the scores are finite or flagged)
+    mx = __ockl_wfred_max_f32(mx);
     if (lane == 0)
         red[tid >> 6] = mx;
-    __syncthreads();
+    lds_barrier();
     const float maximum = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (uint32_t t = tid; t <= pos; t += kAttnThreads)
-        sc[t] = bnne_expf_libc(sc[t] - maximum, exp_tab);
-    __threadfence_block();
-    __syncthreads();
+    // exp, and +0 after pos up to a multiple of 64 positions: adding +0 to this sum of
+    // non-negative terms changes nothing, and the sums below then run whole steps
+    const uint32_t padded = pos < kAttnLdsPositions ? (pos + 64u) & ~63u : pos + 1u;
+    for (uint32_t t = tid; t < padded; t += kAttnThreads)
+        sc[t] = t <= pos ? bnne_expf_libc(sc[t] - maximum, exp_tab) : 0.0f;
+    sc_barrier();
     if (tid == 0) {
-        const float sum = pos < kAttnLdsPositions ? sum_lds_in_order(sc, pos + 1u)
+        const float sum = pos < kAttnLdsPositions ? sum_lds_in_order(sc, padded)
                                                   : sum_in_order<32>(pos + 1u, [&](uint32_t t) { return sc[t]; });
         if (!(sum > 0.0f) || !isfinite(sum))
             set_error_first(err, code_base + 4 + 2 * (int)h);
         sum_s = sum;
     }
-    __syncthreads();
+    lds_barrier();
     const float sum = sum_s;
     for (uint32_t t = tid; t <= pos; t += kAttnThreads)
         sc[t] = sc[t] / sum;
-    __threadfence_block();
 
-    // value[i] = sum over t in order of p[t] * V[t][i]; V rows in LDS, kAttnVRows at a time
+    // value[i] = sum over t in order of p[t] * V[t][i]; V rows in LDS, kAttnVRows at a
+    // time.  Steps of 8 rows: past pos the probabilities are +0 and the rows finite
+    // copies of row pos, so the extra products are ±0 and the (never -0) sum is unchanged
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's V pieces have landed
     float acc = 0.0f;
     for (uint32_t t0 = 0; t0 <= pos; t0 += kAttnVRows) {
         if (t0 > 0) {
-            __syncthreads();  // every thread is done with the previous rows
+            lds_barrier();  // every thread is done with the previous rows
             attn_dma_v(vs4, vc, v, head_off, t0, pos, kv_dim);
             __builtin_amdgcn_s_waitcnt(0x0F70);
         }
-        __syncthreads();
-        if (tid < HD) {
+        sc_barrier();  // the probabilities (first pass) and this thread's V pieces are visible
+        if (tid < HD && pos >= kAttnLdsPositions) {  // scores in global memory: exactly rows t0..pos
             const uint32_t n = min(kAttnVRows, pos + 1u - t0);
-            uint32_t r = 0;
-            for (; r + 8u <= n; r += 8u) {
+            for (uint32_t r = 0; r < n; ++r)
+                acc = acc + sc[t0 + r] * vs[r * HD + tid];
+        } else if (tid < HD) {
+            const uint32_t n = min(kAttnVRows, ((pos + 8u) & ~7u) - t0);
+            for (uint32_t r = 0; r < n; r += 8u) {
+                float p8[8], v8[8];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    p8[c] = sc[t0 + r + c];
+                    v8[c] = vs[(r + c) * HD + tid];
+                }
 #pragma unroll
                 for (int c = 0; c < 8; ++c)
-                    acc = acc + sc[t0 + r + c] * vs[(r + c) * HD + tid];
+                    acc = acc + p8[c] * v8[c];
             }
-            for (; r < n; ++r)
-                acc = acc + sc[t0 + r] * vs[r * HD + tid];
         }
     }
     if (tid < HD)

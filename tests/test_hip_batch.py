@@ -62,7 +62,10 @@ def _free(mats, bi, bo):
      ("GEMM_F32", 8192, 129, 5), ("GEMM", 128, 1, 2), ("GEMV_F32", 2048, 8192, 1)],  # mixed
     [("GEMV_F32", 2048, 2048, 1), ("GEMV", 1024, 100, 1), ("DOT_GROUPS", 384, 70, 3),
      ("GEMM_F32", 2048, 129, 5), ("GEMM", 128, 1, 2), ("DOT_GROUPS", 2048, 64, 2)],  # mixed, K <= 2048
-], ids=["uniform", "mixed", "mixed_small"])
+    [("GEMV_F32", 6144, 2048, 1)] * 32,                                   # long K: one wave per tile, 6 blocks
+    [("GEMV_F32", 6144, 2048, 1)] * 16 + [("GEMV", 2176, 4100, 1)] * 8 + [("DOT_GROUPS", 8192, 640, 1)] * 4
+    + [("GEMV_F32", 3072, 1000, 1)] * 8,                                  # long K, table-mapped: 17..64 groups
+], ids=["uniform", "mixed", "mixed_small", "long_k", "long_k_mixed"])
 def test_batch_equals_single_jobs(pkg, hipdev, specs):
     mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs)
     assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, len(specs)) == pkg.Status.OK
