@@ -11,7 +11,7 @@
 //      residual add of :497-498/:510-511 folded in, :491-495 for SiLU(gate)*up) --
 //      and checks it like the GEMV_F32 input check (soft-bnn-accelerator.c:278-308);
 //   3. quantises it exactly as the prep kernel does (absmax scale, round half away,
-//      bit planes and group sums);
+//      bit planes and group sums), each wave the groups of its own dots;
 //   4. per tile computes D per group (bit-plane dots), the rounded products
 //      F32(scale)*D, and adds them in group order (one lane per feature), times
 //      the row scale, with the next tile's weights already loading.
@@ -44,6 +44,7 @@ __device__ __forceinline__ float fload(const float* p) { return *(const __attrib
 __device__ __forceinline__ void fstore(float* p, float v) { *(__attribute__((address_space(1))) float*)p = v; }
 
 extern "C" __device__ uint32_t __ockl_wfred_max_u32(uint32_t);
+extern "C" __device__ double __ockl_wfred_add_f64(double);
 
 // popc(x) + acc and (c << SHIFT) + acc as single instructions (the compiler would
 // otherwise re-associate the chains)
@@ -80,6 +81,28 @@ __device__ __forceinline__ int f_group_dot(uint4 w, const uint4* p, int neg_sum)
     return (int)d;
 }
 
+// The same with the group's planes as wave-uniform values: bit b of mask m[h][b] is
+// bit b of element 64 h + lane (plane words 2h and 2h + 1)
+template <int B>
+__device__ __forceinline__ uint32_t f_plane_count_s(uint4 w, const uint64_t (&m)[2][8]) {
+    uint32_t c = (uint32_t)__builtin_popcount(w.x & (uint32_t)m[0][B]);
+    c = f_bcnt_acc(w.y & (uint32_t)(m[0][B] >> 32), c);
+    c = f_bcnt_acc(w.z & (uint32_t)m[1][B], c);
+    return f_bcnt_acc(w.w & (uint32_t)(m[1][B] >> 32), c);
+}
+__device__ __forceinline__ int f_group_dot_s(uint4 w, const uint64_t (&m)[2][8], int neg_sum) {
+    uint32_t d = (uint32_t)neg_sum;
+    d = f_lshl_add<1>(f_plane_count_s<0>(w, m), d);
+    d = f_lshl_add<2>(f_plane_count_s<1>(w, m), d);
+    d = f_lshl_add<3>(f_plane_count_s<2>(w, m), d);
+    d = f_lshl_add<4>(f_plane_count_s<3>(w, m), d);
+    d = f_lshl_add<5>(f_plane_count_s<4>(w, m), d);
+    d = f_lshl_add<6>(f_plane_count_s<5>(w, m), d);
+    d = f_lshl_add<7>(f_plane_count_s<6>(w, m), d);
+    d -= f_plane_count_s<7>(w, m) << 8;
+    return (int)d;
+}
+
 // Bit planes B..7 of the wave's 64 quantised values q: lane 2b of `word` receives
 // the low and lane 2b + 1 the high half of plane b's mask (v_writelane_b32 with the
 // lane as an inline constant), and `sum` accumulates sum(q) from the same masks.
@@ -96,35 +119,77 @@ __device__ __forceinline__ void plane_words(int q, uint32_t& word, int& sum) {
         plane_words<B + 1>(q, word, sum);
 }
 
-// Q = clamp(round-half-away(F32(x / s)), -127, 127)  (soft-bnn-accelerator.c:197-208)
-__device__ __forceinline__ int f_quantize(float x, float s) {
-    float r = roundf(x / s);
-    r = r > 127.0f ? 127.0f : r;
-    r = r < -127.0f ? -127.0f : r;
-    return (int)r;
+// Q = clamp(round-half-away(F32(x / s)), -127, 127)  (soft-bnn-accelerator.c:197-208).
+// y = F32(x * F32(1 / s)) is within 1.6e-5 of x / s (|x / s| <= 127) and F32(x / s)
+// within 3.9e-6, so both round to the same integer unless y lies within 2^-14 of a
+// half-integer; those lanes (and all, when s is subnormal: `exact`) divide.
+__device__ __forceinline__ int f_quantize(float x, float s, float rcp, bool exact) {
+    float y = x * rcp;
+    float t = truncf(y), d = y - t;
+    if (exact || fabsf(fabsf(d) - 0.5f) < 0x1p-14f) {
+        y = x / s;
+        t = truncf(y);
+        d = y - t;
+    }
+    const float q = t + (fabsf(d) >= 0.5f ? copysignf(1.0f, y) : 0.0f);
+    return (int)fminf(fmaxf(q, -127.0f), 127.0f);
 }
 
-// sum of p[0..n) in index order (n a multiple of 64): steps of 64 values read with
-// 16-byte loads at constant offsets, two steps per iteration so that the second
-// step's reads are in flight while the first step is added.
-__device__ __forceinline__ float sum_in_order_lds(const float* p, uint32_t n) {
+// The sum of the squares in index order, s_{i+1} = F32(s_i + t_i) from s_0 = +0,
+// evaluated in segments of kSegment terms.  Segment j is run from kWindow candidate
+// starts at once (one lane each): the binary32 values whose bit patterns lie around
+// that of F32(E_j), E_j the sum of the earlier terms in binary64.  Afterwards one
+// wave walks the segments in order: when the running sum is one of segment j's
+// candidates, the lane that started from exactly that value has performed the same
+// additions from the same value, and its end value is taken; otherwise the segment
+// is added term by term.  Either way the result is bit-identical to the sequential
+// loop; the walk costs one table lookup per segment in the usual case, where the
+// accumulated rounding of the sequential sum stays within +-16 ulps of E_j.
+constexpr uint32_t kSegment = 128;
+constexpr uint32_t kWindow = 32;
+constexpr uint32_t kChunk = 64;  // terms per binary64 partial sum (one wave's)
+
+// s plus the n terms at p, one rounding per addition, in index order (n % 16 == 0)
+__device__ __forceinline__ float add_in_order_lds(const float* p, uint32_t n, float s) {
     const float4* p4 = reinterpret_cast<const float4*>(p);
-    float sum = 0.0f;
-#pragma unroll 2
-    for (uint32_t i = 0; i < n / 4u; i += 16u) {
-        float4 v[16];
+#pragma unroll 1
+    for (uint32_t i = 0; i < n / 4u; i += 4u) {
+        float4 v[4];
 #pragma unroll
-        for (int c = 0; c < 16; ++c)
+        for (int c = 0; c < 4; ++c)
             v[c] = p4[i + c];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) {
-            sum = sum + v[c].x;
-            sum = sum + v[c].y;
-            sum = sum + v[c].z;
-            sum = sum + v[c].w;
+        for (int c = 0; c < 4; ++c) {
+            s = s + v[c].x;
+            s = s + v[c].y;
+            s = s + v[c].z;
+            s = s + v[c].w;
         }
     }
-    return sum;
+    return s;
+}
+
+// NC interleaved candidate chains of one wave over kSegment terms each
+template <int NC>
+__device__ __forceinline__ void run_chains(float (&c)[NC], const float4* const (&src)[NC]) {
+#pragma unroll 2
+    for (uint32_t i = 0; i < kSegment / 4u; i += 8u) {
+        float4 v[NC][8];
+#pragma unroll
+        for (int r = 0; r < NC; ++r)
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                v[r][q] = src[r][i + q];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+            for (int r = 0; r < NC; ++r) {
+                c[r] = c[r] + v[r][q].x;
+                c[r] = c[r] + v[r][q].y;
+                c[r] = c[r] + v[r][q].z;
+                c[r] = c[r] + v[r][q].w;
+            }
+    }
 }
 
 // Workgroup barrier for data exchanged through LDS: waits for this wave's LDS
@@ -173,21 +238,36 @@ __device__ __forceinline__ void load_tile(const FusedJob& job, uint32_t tile, ui
 template <int GPW, int EPT>
 __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t tiles_total, uint64_t seq,
                                                          uint64_t* flag, uint64_t* host_status) {
+    static_assert(EPT == 2 * GPW, "a wave quantises exactly the groups of its dots");
     __shared__ float4 scratch4[(kFusedMaxWidth + kFusedPad) / 4];  // squares, then products [2][group][64]
-    __shared__ uint4 planes[kFusedMaxGroups * kPlaneWords / 4];
-    __shared__ int part[kFusedMaxGroups][2];
+    // bit planes of the groups (GPW > 1; one group per wave keeps them in scalar registers),
+    // each written and read by the wave that owns the group
+    __shared__ uint4 planes[GPW > 1 ? kFusedMaxGroups * kPlaneWords / 4 : 1];
     __shared__ uint32_t amax_w[kFusedWaves];
     __shared__ uint64_t exp_tab[32];
     __shared__ float rms_s;
+    // the speculative sum of squares: binary64 sums of 64 terms, the candidates' end
+    // values (segments 2p and 2p + 1 in the two halves of row p), the segments' first
+    // candidate bit pattern
+    constexpr uint32_t kRowMax = EPT * kFusedThreads;
+    constexpr uint32_t kPairs = kRowMax / kSegment / 2u;
+    __shared__ double chunk_sum[kRowMax / kChunk];
+    __shared__ float seg_end[kPairs * 64u];
+    __shared__ int seg_base[kPairs * 2u];
     float* scratch = reinterpret_cast<float*>(scratch4);
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t K = fa.width, G = K / kGroup;
 
+    // row element i of a thread: half i % 2 of group w + 16 (i / 2), w its wave -- the
+    // groups of the wave's dots (whole waves: K % 128 == 0)
+    const auto elem = [&](int i) { return (wave + kFusedWaves * (uint32_t)(i >> 1)) * kGroup + 64u * (i & 1) + lane; };
+    const auto live = [&](int i) { return wave + kFusedWaves * (uint32_t)(i >> 1) < G; };
+
     // 1. the row operands load first and the first tile's weights after them (the
     // load counter completes in order: the row is needed first), arriving while the
-    // row is produced; thread t owns k = t + 1024 i
+    // row is produced
     uint32_t tile = blockIdx.x, ji = 0;
     while (ji + 1u < fa.njobs && fa.jobs[ji + 1u].first_tile <= tile)
         ++ji;
@@ -196,16 +276,16 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     float xv[EPT], bv[EPT], gv[EPT];
 #pragma unroll
     for (int i = 0; i < EPT; ++i)
-        xv[i] = fload(src_a + min(tid + kFusedThreads * i, K - 1u));
+        xv[i] = fload(src_a + min(elem(i), K - 1u));
     if (fa.b) {
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
-            bv[i] = fload(fa.b + min(tid + kFusedThreads * i, K - 1u));
+            bv[i] = fload(fa.b + min(elem(i), K - 1u));
     }
     if (fa.kind == PRE_RMSNORM) {
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
-            gv[i] = fload(fa.gain + min(tid + kFusedThreads * i, K - 1u));
+            gv[i] = fload(fa.gain + min(elem(i), K - 1u));
     }
     TileRegs<GPW> cur, nxt;
     load_tile<GPW>(job, tile - job.first_tile, G, wave, lane, cur);
@@ -217,18 +297,91 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
             for (int i = 0; i < EPT; ++i)
                 xv[i] = xv[i] + bv[i];
         }
+        // the terms, and their binary64 sums per 64 (chunk k / 64)
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
-            const uint32_t k = tid + kFusedThreads * i;
-            if (k < K) {
-                scratch[k] = xv[i] * xv[i];
+            const uint32_t k = elem(i);
+            const float sq = xv[i] * xv[i];
+            if (live(i)) {
+                scratch[k] = sq;
                 if (fa.a_out && blockIdx.x == 0)
                     fstore(fa.a_out + k, xv[i]);
+                const double h = __ockl_wfred_add_f64((double)sq);
+                if (lane == 0)
+                    chunk_sum[k / kChunk] = h;
             }
         }
         lds_barrier();
-        if (tid == 0)
-            rms_s = sqrtf(sum_in_order_lds(scratch, K) / (float)K + fa.eps);
+        // candidate chains: wave w runs pairs w, w + 16, ... (segments 2p, 2p + 1)
+        const uint32_t nseg = K / kSegment, npairs = (nseg + 1u) / 2u;
+        const uint32_t half = lane >> 5, cand = lane & (kWindow - 1u);
+        constexpr int kPairsPerWave = (kPairs + kFusedWaves - 1) / kFusedWaves;
+        float c[kPairsPerWave];
+        const float4* src[kPairsPerWave];
+#pragma unroll
+        for (int r = 0; r < kPairsPerWave; ++r) {
+            const uint32_t p = min(wave + kFusedWaves * r, npairs - 1u);
+            // E_{2p}: the chunks before segment 2p; E_{2p+1} adds segment 2p's two
+            double e = 0.0;
+#pragma unroll
+            for (uint32_t cc = 0; cc < kRowMax / kChunk; cc += 64u)
+                if (cc + lane < 4u * p)
+                    e += chunk_sum[cc + lane];
+            e = __ockl_wfred_add_f64(e);
+            if (half)
+                e = e + chunk_sum[4u * p] + chunk_sum[4u * p + 1u];
+            const int base = __float_as_int((float)e) - (int)(kWindow / 2u);
+            c[r] = __int_as_float(base + (int)cand);
+            const uint32_t j = min(2u * p + half, nseg - 1u);
+            src[r] = reinterpret_cast<const float4*>(scratch + kSegment * j);
+            if (cand == 0 && wave + kFusedWaves * r < npairs && 2u * p + half < nseg)
+                seg_base[2u * p + half] = base;
+        }
+        if (kPairsPerWave > 1 && wave + kFusedWaves < npairs) {
+            run_chains<kPairsPerWave>(c, src);
+        } else if (wave < npairs) {
+            float c1[1] = {c[0]};
+            const float4* const s1[1] = {src[0]};
+            run_chains<1>(c1, s1);
+            c[0] = c1[0];
+        }
+#pragma unroll
+        for (int r = 0; r < kPairsPerWave; ++r)
+            if (wave + kFusedWaves * r < npairs)
+                seg_end[(wave + kFusedWaves * r) * 64u + lane] = c[r];
+        lds_barrier();
+        // the walk (wave 0): bits of the running sum, uniform across the wave
+        if (wave == 0) {
+            float ends[kPairs];
+#pragma unroll
+            for (uint32_t m = 0; m < kPairs; ++m)
+                ends[m] = seg_end[min(m, npairs - 1u) * 64u + lane];
+            const int bases = seg_base[min(lane, nseg - 1u)];
+            // branch-free lookups (a scalar branch per step costs more than the
+            // step); a miss anywhere is noted and the walk repeated below
+            uint32_t v = 0, miss = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < 2u * kPairs; ++j) {
+                const uint32_t idx = v - (uint32_t)__builtin_amdgcn_readlane(bases, j);
+                const uint32_t nv = (uint32_t)__builtin_amdgcn_readlane(__float_as_int(ends[j / 2u]),
+                                                                        (int)((j & 1u) * 32u + (idx & (kWindow - 1u))));
+                const bool live = j < nseg;
+                miss |= live ? idx & ~(kWindow - 1u) : 0u;
+                v = live ? nv : v;
+            }
+            if (miss) {  // the walk with term-by-term additions where the running sum is no candidate
+                v = 0;
+                for (uint32_t j = 0; j < nseg; ++j) {
+                    const uint32_t idx = v - (uint32_t)seg_base[j];
+                    if (idx < kWindow)
+                        v = __float_as_uint(seg_end[(j / 2u) * 64u + (j & 1u) * 32u + idx]);
+                    else
+                        v = __float_as_uint(add_in_order_lds(scratch + kSegment * j, kSegment, __uint_as_float(v)));
+                }
+            }
+            if (lane == 0)
+                rms_s = sqrtf(__uint_as_float(v) / (float)K + fa.eps);
+        }
         lds_barrier();
         const float rms = rms_s;
         if (!__builtin_isfinite(rms) || rms == 0.0f) {
@@ -259,7 +412,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     uint32_t abits = 0;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
-        if (tid + kFusedThreads * i < K) {
+        if (live(i)) {
             const uint32_t a = __float_as_uint(xv[i]) & 0x7fffffffu;
             abits = max(abits, a < 0x7f800000u ? a : 0xffffffffu);
         }
@@ -285,25 +438,39 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
             s = __int_as_float(1);  // smallest subnormal
     }
 
-    // 4. quantise: in step i wave w holds the 64 consecutive k of half (w & 1) of
-    // group 8i + (w >> 1); bit planes by ballot, the group sums from the same masks
-    uint32_t* pw = reinterpret_cast<uint32_t*>(planes);
+    // 4. quantise the wave's own groups: bit planes by ballot, -sum(Q) per group from
+    // the same masks; no exchange between waves
+    const float rcp = 1.0f / s;
+    const bool exact = s < 0x1p-126f;  // 1 / s would overflow
+    uint64_t masks[2][8];  // GPW == 1: the planes of group `wave`
+    int neg_sum[GPW];
 #pragma unroll
-    for (int i = 0; i < EPT; ++i) {
-        const uint32_t chunk = kFusedThreads * i + 64u * wave;
-        if (chunk < K) {  // K % 128 == 0: whole waves
-            const int q = f_quantize(xv[i], s);
-            uint32_t word = 0;
-            int sum = 0;
-            plane_words<0>(q, word, sum);
-            const uint32_t g = (kFusedThreads / kGroup) * i + (wave >> 1), half = wave & 1u;
-            if (lane < 16u)
-                pw[g * kPlaneWords + (lane >> 1) * 4u + half * 2u + (lane & 1u)] = word;
-            if (lane == 0)
-                part[g][half] = sum;
+    for (int gi = 0; gi < GPW; ++gi) {
+        neg_sum[gi] = 0;
+        const uint32_t g = wave + kFusedWaves * gi;
+        if (g < G) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int q = f_quantize(xv[2 * gi + h], s, rcp, exact);
+                if constexpr (GPW == 1) {
+#pragma unroll
+                    for (int b = 0; b < 8; ++b) {
+                        masks[h][b] = __ballot((q >> b) & 1);
+                        const int cnt = __popcll(masks[h][b]);
+                        neg_sum[gi] -= b == 7 ? -(cnt << 7) : (cnt << b);
+                    }
+                } else {
+                    uint32_t word = 0;
+                    int sum = 0;
+                    plane_words<0>(q, word, sum);
+                    neg_sum[gi] -= sum;
+                    if (lane < 16u)
+                        reinterpret_cast<uint32_t*>(planes)[g * kPlaneWords + (lane >> 1) * 4u + h * 2u + (lane & 1u)] =
+                            word;
+                }
+            }
         }
     }
-    lds_barrier();
 
     // 5. per tile: group dots and the rounded products F32(scale) * D into one of two
     // product buffers, then wave 0 adds them in group order (one lane per feature)
@@ -324,7 +491,11 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
         for (int i = 0; i < GPW; ++i) {
             const uint32_t g = wave + kFusedWaves * i;
             if (g < G) {
-                const int d = f_group_dot(cur.w[i], planes + g * (kPlaneWords / 4u), -(part[g][0] + part[g][1]));
+                int d;
+                if constexpr (GPW == 1)
+                    d = f_group_dot_s(cur.w[i], masks, neg_sum[i]);
+                else
+                    d = f_group_dot(cur.w[i], planes + g * (kPlaneWords / 4u), neg_sum[i]);
                 prod[g * 64u + lane] = __half2float(__ushort_as_half((uint16_t)cur.s[i])) * (float)d;
             }
         }

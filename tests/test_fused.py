@@ -153,6 +153,47 @@ def test_fused_rmsnorm(pkg, hipdev, oracle, k, ns, with_b, with_out):
         f.free()
 
 
+def sum_pattern(name, k, rng):
+    """Rows chosen for the sum of squares: rounding that drifts far from the exact
+    prefix sums, terms across many binades, subnormal terms, long zero runs."""
+    if name == "constant":  # the same rounding at every step: hundreds of ulps of drift
+        return np.full(k, 1.1, np.float32)
+    if name == "ramp":  # squares from 2^-70 to 2^20 in index order
+        sign = rng.choice(np.array([-1.0, 1.0], np.float32), k)
+        return (np.exp2(np.linspace(-35.0, 10.0, k)) * sign).astype(np.float32)
+    if name == "tiny":  # subnormal and vanishing squares
+        return f32(rng, k, 1e-22)
+    if name == "zero_head":
+        a = f32(rng, k)
+        a[: k * 3 // 4] = 0.0
+        return a
+    if name == "spikes":  # a few large terms among small ones
+        a = f32(rng, k, 1e-3)
+        a[rng.integers(0, k, 5)] = 300.0
+        return a
+    raise ValueError(name)
+
+
+@pytest.mark.parametrize("pattern", ["constant", "ramp", "tiny", "zero_head", "spikes"])
+@pytest.mark.parametrize("k", [2048, 1152, 6144, 128])
+def test_fused_rmsnorm_sum_patterns(pkg, hipdev, oracle, k, pattern):
+    """The sum of squares is evaluated in parallel segments and resolved exactly;
+    these rows make the resolution fall back to term-by-term addition."""
+    rng = np.random.default_rng(k)
+    f = Fused(pkg, hipdev, k, [64], seed=13)
+    try:
+        a = sum_pattern(pattern, k, rng)
+        gain = np.ones(k, np.float32)
+        f.ops["a"].write(a)
+        f.ops["gain"].write(gain)
+        assert f.create(f.pre(pkg.api.PreOp.RMSNORM, with_b=False, with_out=False)) == 0
+        assert f.run() == 0
+        _, row, _ = host_rmsnorm(a, None, gain, 1e-6)
+        check(f.outputs(), expected(pkg, oracle, f.chunks, row))
+    finally:
+        f.free()
+
+
 @pytest.mark.parametrize("k,ns", [(6144, [2048]), (1024, [300, 64])])
 def test_fused_silu_mul(pkg, hipdev, oracle, k, ns):
     rng = np.random.default_rng(k)
@@ -189,6 +230,10 @@ def test_fused_illegal_rows_write_nothing(pkg, hipdev):
         a[100] = np.inf
         f.ops["a"].write(a)
         assert f.run() == pkg.Status.ERANGE  # rms is inf: the divisor check again
+        assert f.err.read().view(np.int32)[0] == 41
+        f.err.write(np.zeros(1, np.int32))
+        f.ops["a"].write(np.full(k, 1.5e19, np.float32))  # finite squares, the sum overflows
+        assert f.run() == pkg.Status.ERANGE
         assert f.err.read().view(np.int32)[0] == 41
         f.err.write(np.zeros(1, np.int32))
         a[100] = 1.0
