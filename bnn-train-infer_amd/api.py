@@ -128,6 +128,14 @@ class PreOp(ctypes.Structure):  # include/bnn-accelerator-hip.h (BNNX_PreOp)
     ]
 
 
+class PostOp(ctypes.Structure):  # include/bnn-accelerator-hip.h (BNNX_PostOp)
+    NONE, SILU_MUL = 0, 1
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("out", ctypes.c_void_p),
+    ]
+
+
 class BnnError(RuntimeError):
     def __init__(self, status: int, what: str = ""):
         self.status = Status(status) if status in Status._value2member_map_ else status
@@ -174,6 +182,7 @@ class Api:
             "BNNX_ExecuteBatch": (S, [V, P(Job), U32]),
             "BNNX_BatchCreate": (S, [V, P(Job), U32, P(V)]),
             "BNNX_BatchCreateFused": (S, [V, P(Job), U32, P(PreOp), P(V)]),
+            "BNNX_BatchCreateFusedPost": (S, [V, P(Job), U32, P(PreOp), P(PostOp), P(V)]),
             "BNNX_BatchLaunch": (S, [V]),
             "BNNX_BatchCheck": (S, [V]),
             "BNNX_BatchDestroy": (None, [V]),

@@ -1022,14 +1022,20 @@ Span span_of(const void* p, size_t bytes) {
 }
 }  // namespace
 
-EXPORT BNN_Status BNNX_BatchCreateFused(BNN_Device device, const BNN_Job* jobs, uint32_t count, const BNNX_PreOp* pre,
-                                        BNNX_Batch* out_batch) {
+EXPORT BNN_Status BNNX_BatchCreateFusedPost(BNN_Device device, const BNN_Job* jobs, uint32_t count,
+                                            const BNNX_PreOp* pre, const BNNX_PostOp* post, BNNX_Batch* out_batch) {
     if (out_batch == nullptr)
         return BNN_EINVAL;
     *out_batch = nullptr;
     if (device == nullptr || jobs == nullptr || count == 0 || pre == nullptr)
         return BNN_EINVAL;
     if (pre->kind != BNNX_PRE_ROW && pre->kind != BNNX_PRE_RMSNORM && pre->kind != BNNX_PRE_SILU_MUL)
+        return BNN_EINVAL;
+    const int32_t post_kind = post ? post->kind : BNNX_POST_NONE;
+    if (post_kind != BNNX_POST_NONE && post_kind != BNNX_POST_SILU_MUL)
+        return BNN_EINVAL;
+    const bool paired = post_kind == BNNX_POST_SILU_MUL;
+    if (paired && (count % 2u != 0 || post->out == nullptr))
         return BNN_EINVAL;
     const uint32_t width = pre->width;
     if (width == 0 || width % kGroup != 0)
@@ -1055,7 +1061,7 @@ EXPORT BNN_Status BNNX_BatchCreateFused(BNN_Device device, const BNN_Job* jobs, 
             if (spans_overlap(w, reads[r]))
                 return BNN_EINVAL;
     }
-    Span* outs = static_cast<Span*>(malloc(sizeof(Span) * (count + 1u)));
+    Span* outs = static_cast<Span*>(malloc(sizeof(Span) * (count + 2u)));
     FusedJob* table = static_cast<FusedJob*>(malloc(sizeof(FusedJob) * count));
     BNN_Status st = outs && table ? BNN_OK : BNN_ENOMEM;
     uint32_t tiles = 0;
@@ -1090,10 +1096,28 @@ EXPORT BNN_Status BNNX_BatchCreateFused(BNN_Device device, const BNN_Job* jobs, 
         table[i] = FusedJob{p.m->wbits, p.m->wscale, reinterpret_cast<float*>(p.out_base), p.m->n, p.m->tiles, tiles, 0};
         tiles += p.m->tiles;
     }
+    uint32_t post_n = 0;
+    if (st == BNN_OK && paired) {
+        // pairs (p, m + p) of equal length; tiles count half-tiles of the pairs
+        const uint32_t m = count / 2u;
+        tiles = 0;
+        for (uint32_t q = 0; st == BNN_OK && q < m; ++q) {
+            if (table[q].n != table[m + q].n) {
+                st = BNN_EINVAL;
+                break;
+            }
+            table[q].first_tile = tiles;
+            table[q].post_off = post_n;
+            tiles += 2u * table[q].tiles;
+            post_n += table[q].n;
+        }
+    }
     if (st == BNN_OK) {
+        uint32_t nouts = count;
         if (a_out)
-            outs[count] = span_of(a_out, row_bytes);
-        const uint32_t nouts = count + (a_out ? 1u : 0u);
+            outs[nouts++] = span_of(a_out, row_bytes);
+        if (paired)
+            outs[nouts++] = span_of(post->out, (size_t)post_n * 4u);
         std::sort(outs, outs + nouts, [](const Span& x, const Span& y) { return x.begin < y.begin; });
         for (uint32_t i = 0; st == BNN_OK && i < nouts; ++i) {
             if (i > 0 && outs[i].begin < outs[i - 1].end)
@@ -1148,9 +1172,16 @@ EXPORT BNN_Status BNNX_BatchCreateFused(BNN_Device device, const BNN_Job* jobs, 
     fa.row = reinterpret_cast<const float*>(row);
     fa.err = pre->kind == BNNX_PRE_RMSNORM ? pre->err : nullptr;
     fa.err_code = pre->err_code;
+    fa.post = paired ? POST_SILU_MUL : POST_NONE;
+    fa.post_out = paired ? post->out : nullptr;
     device->live_batches++;
     *out_batch = b;
     return BNN_OK;
+}
+
+EXPORT BNN_Status BNNX_BatchCreateFused(BNN_Device device, const BNN_Job* jobs, uint32_t count, const BNNX_PreOp* pre,
+                                        BNNX_Batch* out_batch) {
+    return BNNX_BatchCreateFusedPost(device, jobs, count, pre, nullptr, out_batch);
 }
 
 EXPORT BNN_Status BNNX_BatchCheck(BNNX_Batch batch) {

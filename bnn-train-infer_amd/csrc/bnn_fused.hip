@@ -17,6 +17,8 @@
 //      the row scale, with the next tile's weights already loading.
 // Every workgroup produces the same row from the same inputs, so all of them take
 // the same decisions; workgroup 0 alone stores the pre-operation's residual sum.
+// With the post-operation SILU_MUL the tiles are half-tiles of job pairs (32 features
+// of each job of the pair, the same indices), and each also stores SiLU(y_a) * y_b.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -220,22 +222,77 @@ struct TileRegs {
     uint32_t s[GPW];
 };
 
+// The job table, written by the host only: read through the constant address space
+// (scalar loads through the scalar cache)
+struct JobTable {
+    const FusedJob* t;
+    typedef const __attribute__((address_space(4))) FusedJob* Ptr;
+    __device__ __forceinline__ uint32_t first_tile(uint32_t i) const { return ((Ptr)t)[i].first_tile; }
+    __device__ __forceinline__ FusedJob operator[](uint32_t i) const {
+        const Ptr c = (Ptr)t;
+        FusedJob j;
+        j.wbits = c[i].wbits;
+        j.wscale = c[i].wscale;
+        j.out = c[i].out;
+        j.n = c[i].n;
+        j.tiles = c[i].tiles;
+        j.first_tile = c[i].first_tile;
+        j.post_off = c[i].post_off;
+        return j;
+    }
+};
+
+// The lane's row of a tile: feature `lane` of 64-feature tile `tile` of `job`, or for
+// paired batches (POST_SILU_MUL) half-tile `tile` of the pair (ja, jb): feature
+// 32 (tile % 2) + lane % 32 of 64-feature tile tile / 2, of ja in lanes 0..31 and of jb
+// in lanes 32..63.
+struct LaneRow {
+    const uint4* wbits;
+    const uint16_t* wscale;
+    size_t base;   // the lane's offset in tile units of kTile (group 0)
+    uint32_t row;  // feature index within the job
+};
+// a and b as opaque scalar-register values: a per-lane choice between fields of two
+// descriptors would otherwise become a choice of descriptor address (on the stack)
+template <class T>
+__device__ __forceinline__ T lane_pick(bool second, T a, T b) {
+    uint64_t x = (uint64_t)a, y = (uint64_t)b;
+    asm volatile("" : "+s"(x), "+s"(y));
+    return (T)(second ? y : x);
+}
+
+__device__ __forceinline__ LaneRow lane_row(const FusedJob& ja, const FusedJob& jb, bool paired, uint32_t tile,
+                                            uint32_t G, uint32_t lane) {
+    LaneRow lr;
+    if (paired) {
+        const bool second = lane >= 32u;
+        lr.wbits = lane_pick(second, ja.wbits, jb.wbits);
+        lr.wscale = lane_pick(second, ja.wscale, jb.wscale);
+        lr.row = (tile >> 1) * kTile + 32u * (tile & 1u) + (lane & 31u);
+        lr.base = (size_t)(tile >> 1) * G * kTile + 32u * (tile & 1u) + (lane & 31u);
+    } else {
+        lr.wbits = ja.wbits;
+        lr.wscale = ja.wscale;
+        lr.row = tile * kTile + lane;
+        lr.base = (size_t)tile * G * kTile + lane;
+    }
+    return lr;
+}
+
 template <int GPW>
-__device__ __forceinline__ void load_tile(const FusedJob& job, uint32_t tile, uint32_t G, uint32_t wave,
-                                          uint32_t lane, TileRegs<GPW>& r) {
-    const size_t base = (size_t)tile * G * kTile + lane;
+__device__ __forceinline__ void load_tile(const LaneRow& lr, uint32_t G, uint32_t wave, TileRegs<GPW>& r) {
 #pragma unroll
     for (int i = 0; i < GPW; ++i) {
         const uint32_t g = min(wave + kFusedWaves * i, G - 1u);
-        r.w[i] = fload(job.wbits + base + (size_t)g * kTile);
-        r.s[i] = fload(job.wscale + base + (size_t)g * kTile);
+        r.w[i] = fload(lr.wbits + lr.base + (size_t)g * kTile);
+        r.s[i] = fload(lr.wscale + lr.base + (size_t)g * kTile);
     }
 }
 
 // GPW: groups per wave of a tile's dots; EPT: row elements per thread.  Workgroup
 // b produces the row once and then takes tiles b, b + grid, ... of the batch, the
 // next tile's weights loading while the current one is computed.
-template <int GPW, int EPT>
+template <int GPW, int EPT, bool PAIRED>
 __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t tiles_total, uint64_t seq,
                                                          uint64_t* flag, uint64_t* host_status) {
     static_assert(EPT == 2 * GPW, "a wave quantises exactly the groups of its dots");
@@ -268,10 +325,14 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     // 1. the row operands load first and the first tile's weights after them (the
     // load counter completes in order: the row is needed first), arriving while the
     // row is produced
+    // tiles are walked over the jobs, or over the pairs (the first half of the table)
+    const JobTable jobs{fa.jobs};
+    constexpr bool paired = PAIRED;  // fa.post == POST_SILU_MUL
+    const uint32_t nwalk = paired ? fa.njobs / 2u : fa.njobs, pair_step = paired ? nwalk : 0u;
     uint32_t tile = blockIdx.x, ji = 0;
-    while (ji + 1u < fa.njobs && fa.jobs[ji + 1u].first_tile <= tile)
+    while (ji + 1u < nwalk && jobs.first_tile(ji + 1u) <= tile)
         ++ji;
-    FusedJob job = fa.jobs[ji];
+    FusedJob job = jobs[ji], job2 = jobs[ji + pair_step];
     const float* src_a = fa.kind == PRE_ROW ? fa.row : fa.a;
     float xv[EPT], bv[EPT], gv[EPT];
 #pragma unroll
@@ -288,7 +349,10 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
             gv[i] = fload(fa.gain + min(elem(i), K - 1u));
     }
     TileRegs<GPW> cur, nxt;
-    load_tile<GPW>(job, tile - job.first_tile, G, wave, lane, cur);
+    LaneRow lr = lane_row(job, job2, paired, tile - job.first_tile, G, lane);
+    load_tile<GPW>(lr, G, wave, cur);
+    if (paired && tid < 32u)  // the expf table of the SiLU (read after the first product barrier)
+        exp_tab[tid] = kFusedExp2Table[tid];
 
     // 2. the input row
     if (fa.kind == PRE_RMSNORM) {
@@ -480,11 +544,13 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     for (;;) {
         const uint32_t next = tile + gridDim.x;
         uint32_t nji = ji;
+        LaneRow nlr = lr;
         if (next < tiles_total) {
-            while (nji + 1u < fa.njobs && fa.jobs[nji + 1u].first_tile <= next)
+            while (nji + 1u < nwalk && jobs.first_tile(nji + 1u) <= next)
                 ++nji;
-            const FusedJob nj = fa.jobs[nji];
-            load_tile<GPW>(nj, next - nj.first_tile, G, wave, lane, nxt);
+            const FusedJob nj = jobs[nji], nj2 = jobs[nji + pair_step];
+            nlr = lane_row(nj, nj2, paired, next - nj.first_tile, G, lane);
+            load_tile<GPW>(nlr, G, wave, nxt);
         }
         float* prod = scratch + buf * (kFusedMaxGroups * 64u);
 #pragma unroll
@@ -501,7 +567,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
         }
         lds_barrier();
         if (wave == 0) {
-            const uint32_t n = (tile - job.first_tile) * kTile + lane;
+            const uint32_t n = lr.row;
             float acc = 0.0f;
             uint32_t g = 0;
             for (; g + 8u <= G; g += 8u) {
@@ -517,13 +583,21 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
                 acc = acc + prod[g * 64u + lane];
             acc = acc * s;
             if (n < job.n)
-                fstore(job.out + n, acc);
+                fstore(lane_pick(paired && lane >= 32u, job.out, job2.out) + n, acc);
+            if (paired) {
+                // y_p / (1 + expf(-y_p)) * y_(m+p) (qwen3.c:491-495), y_(m+p) from lane + 32
+                const float second = __shfl(acc, (int)(lane | 32u));
+                if (lane < 32u && n < job.n)
+                    fstore(fa.post_out + job.post_off + n, acc / (1.0f + bnne_expf_libc(-acc, exp_tab)) * second);
+            }
         }
         if (next >= tiles_total)
             break;
         tile = next;
         ji = nji;
-        job = fa.jobs[ji];
+        job = jobs[ji];
+        job2 = jobs[ji + pair_step];
+        lr = nlr;
         cur = nxt;
         buf ^= 1u;
     }
@@ -534,12 +608,17 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
 hipError_t launch_fused(hipStream_t stream, const FusedArgs& args, uint32_t tiles, uint32_t grid, uint64_t seq,
                         uint64_t* flag, uint64_t* host_status) {
     static_assert(kFusedMaxGroups * 64u * 2u <= kFusedMaxWidth, "two product buffers fit the scratch");
-    if (args.width <= 2048u)
-        hipLaunchKernelGGL((k_fused<1, 2>), dim3(grid), dim3(kFusedThreads), 0, stream, args, tiles, seq, flag,
-                           host_status);
+    constexpr int kWideGpw = kFusedMaxGroups / kFusedWaves, kWideEpt = kFusedMaxWidth / kFusedThreads;
+    const bool paired = args.post == POST_SILU_MUL;
+    const dim3 g(grid), b(kFusedThreads);
+    if (args.width <= 2048u && !paired)
+        hipLaunchKernelGGL((k_fused<1, 2, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+    else if (args.width <= 2048u)
+        hipLaunchKernelGGL((k_fused<1, 2, true>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+    else if (!paired)
+        hipLaunchKernelGGL((k_fused<kWideGpw, kWideEpt, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
     else
-        hipLaunchKernelGGL((k_fused<kFusedMaxGroups / kFusedWaves, kFusedMaxWidth / kFusedThreads>), dim3(grid),
-                           dim3(kFusedThreads), 0, stream, args, tiles, seq, flag, host_status);
+        hipLaunchKernelGGL((k_fused<kWideGpw, kWideEpt, true>), g, b, 0, stream, args, tiles, seq, flag, host_status);
     return hipGetLastError();
 }
 

@@ -114,8 +114,13 @@ struct FusedJob {
     const uint4* wbits;
     const uint16_t* wscale;
     float* out;  // output row
-    uint32_t n, tiles, first_tile, pad_;
+    uint32_t n, tiles, first_tile;
+    uint32_t post_off;  // POST_SILU_MUL, first job of a pair: offset of its rows in post_out
 };
+
+// Operation on pairs of outputs of a fused batch: with POST_SILU_MUL the 2m jobs are
+// m pairs (job p, job m + p) of equal n, and post_out receives y_p / (1 + expf(-y_p)) * y_(m+p).
+enum PostKind : int32_t { POST_NONE = 0, POST_SILU_MUL = 1 };
 
 struct FusedArgs {
     const FusedJob* jobs;  // device table
@@ -130,6 +135,8 @@ struct FusedArgs {
     const float* row;      // ROW: the input row
     int32_t* err;          // set to err_code when the RMSNORM check fails (may be null)
     int32_t err_code;
+    int32_t post;          // PostKind
+    float* post_out;       // POST_SILU_MUL
 };
 
 // Host-side launchers (bnn_kernels.hip).  All are asynchronous on `stream`.

@@ -55,12 +55,11 @@ __device__ __forceinline__ float sum_in_order(uint32_t n, Load load) {
     return sum;
 }
 
-// The in-order sum of n floats held in LDS (16-byte aligned): 16-byte loads; the
-// second half of each 64-value step is loading while the first half is added.
-__device__ __forceinline__ float sum_lds_in_order(const float* p, uint32_t n) {
+// sum plus the n floats held in LDS (16-byte aligned), added in index order: 16-byte
+// loads; the second half of each 64-value step is loading while the first is added.
+__device__ __forceinline__ float sum_lds_in_order(const float* p, uint32_t n, float sum = 0.0f) {
     const float4* p4 = reinterpret_cast<const float4*>(p);
     const uint32_t n4 = n / 4u;
-    float sum = 0.0f;
     uint32_t i = 0;
     for (; i + 16u <= n4; i += 16u) {
         float4 a[8], b[8];
@@ -355,31 +354,30 @@ __device__ void set_error_first(int* err, int code) {
     }
 }
 
-// One query head h per workgroup (qwen3.c:419-478 for that head): RMSNorm of the
-// head and of its kv head over head_dim (the two in-order sums run in two waves at
-// once), RoPE of both, the kv head's cache row at pos stored by its first query
-// head, then causal attention against rows 0..pos -- row pos taken from this
-// workgroup's own normalised k and from v, so no workgroup reads a row another is
-// writing.  Every global read the step needs is issued before the first sum: each
-// thread's key row for the scores (one position per thread, 256 per round) into
-// registers, and V rows 0..kAttnVRows-1 straight into LDS (global_load_lds, no
-// registers); longer contexts stream further V rows through the same LDS.  All
-// sums are sequential in index / position order, as in the host step.
-constexpr uint32_t kAttnThreads = 256;
-constexpr uint32_t kAttnHD = 128;                   // head_dim of the register-resident key rows
-constexpr uint32_t kAttnVRows = 192;                // V rows resident in LDS (96 KB)
-constexpr uint32_t kAttnLdsPositions = 4096;        // scores in LDS (16 KB); beyond, `scores`
-constexpr uint32_t kAttnV4 = kAttnVRows * kAttnHD / 4;
+// Attention of the fused step (qwen3.c:417-478) in two launches that spread the
+// layer's K and V rows over many workgroups:
+//   k_attn_scores, workgroup (query head h, block of 64 positions), one wave: the
+//   RMSNorm of the head and of its kv head's new key over head_dim (the two in-order
+//   sums interleaved, in every lane), RoPE of both, the cache row at pos (stored by
+//   the kv head's first query head, in the block that holds pos), then one score per
+//   lane, each an in-order dot over head_dim -- position pos from the wave's own new
+//   key, so no workgroup reads a row another is writing;
+//   k_attn_pv, workgroup (query head h, slice of 32 head dims), one wave: the maximum,
+//   expf, the in-order sum and the probabilities over positions 0..pos, then
+//   value[i] = sum over t in order of p[t] * V[t][i] for the slice's i, the V rows
+//   moved into LDS by DMA at the start.
+// Every sum runs in index / position order, as in the host step.
+constexpr uint32_t kAttnHD = 128;             // head_dim of the fused step
+constexpr uint32_t kScoreBlock = 64;          // positions per k_attn_scores workgroup
+constexpr uint32_t kPvSlice = 32;             // head dims per k_attn_pv workgroup
+constexpr uint32_t kPvRows = 1024;            // V slice rows in LDS per pass (128 KB)
+constexpr uint32_t kPvLdsPositions = 4096;    // probabilities in LDS (16 KB); beyond, recomputed
 
-// Workgroup barrier for data exchanged through LDS: waits for this wave's LDS
-// accesses only.  __syncthreads would also wait for every outstanding global load
-// and store of the wave (its release fence): for the key rows and V rows issued at
-// the start, and for the KV-cache stores, none of which the other waves read.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+// Orders one wave's LDS writes before its later LDS reads of other lanes' data.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // 16 bytes per lane from global memory into LDS at lds_addr + 16 * lane (lds_addr is
@@ -390,210 +388,208 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_addr) : "memory");
 }
 
-// V rows t0 .. t0 + kAttnVRows - 1 (clamped to pos; row pos from v) into vs4: thread
-// tid moves 16-byte piece idx = tid + 256 j, i.e. row idx / 32, column piece idx % 32;
-// waves whose pieces all lie past row pos skip the load.
-__device__ __forceinline__ void attn_dma_v(float4* vs4, const float* __restrict__ vc, const float* __restrict__ v,
-                                           size_t head_off, uint32_t t0, uint32_t pos, uint32_t kv_dim) {
-    constexpr uint32_t hd4 = kAttnHD / 4;
-    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63u;
-    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
-    // pieces of rows t0 .. (pos rounded up to a multiple of 8); rows past pos are copies of row pos
-    const uint32_t live = min(((pos + 8u) & ~7u) - t0, kAttnVRows) * hd4;
-    for (uint32_t j = 0; j < kAttnV4 / kAttnThreads; ++j) {
-        const uint32_t first = kAttnThreads * j + 64u * wave;  // the wave's first piece
-        if (first >= live)
-            break;
-        const uint32_t idx = first + lane, r = idx / hd4, c = idx % hd4;
-        const uint32_t t = min(t0 + r, pos);
-        const float* src = t == pos ? v + head_off : vc + (size_t)t * kv_dim + head_off;
-        dma16(src + 4u * c, base + first * 16u);
-    }
-}
-
-__global__ __launch_bounds__(kAttnThreads) void k_attention_fused(
+__global__ __launch_bounds__(64) void k_attn_scores(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, uint32_t kv_mul, float eps,
     const float* __restrict__ q_gain, const float* __restrict__ k_gain, const float* __restrict__ cosv,
     const float* __restrict__ sinv, float* __restrict__ kc, float* __restrict__ vc, uint32_t pos, uint32_t kv_dim,
-    float scale, float* __restrict__ scores, uint32_t n_ctx, float* __restrict__ y, int* err, int code_base) {
-    constexpr uint32_t HD = kAttnHD, hd4 = HD / 4;
-    __shared__ float4 vs4[kAttnV4];
-    __shared__ float4 lds_sc4[kAttnLdsPositions / 4];
-    __shared__ float4 qs4[HD / 4], ks4[HD / 4];
-    __shared__ float4 sq4[2][HD / 4];
-    __shared__ float red[kAttnThreads / 64];
-    __shared__ float rms_s[2];
-    __shared__ float sum_s;
-    __shared__ uint64_t exp_tab[32];  // the expf table: its lookups are per-lane gathers
-    float* qs = reinterpret_cast<float*>(qs4);
-    float* ks = reinterpret_cast<float*>(ks4);
-    float* lds_sc = reinterpret_cast<float*>(lds_sc4);
-    const float* vs = reinterpret_cast<const float*>(vs4);
-    if (threadIdx.x < 32u)
-        exp_tab[threadIdx.x] = kExp2Table[threadIdx.x];
-    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u;
-    const uint32_t kh = h / kv_mul;
-    const size_t head_off = (size_t)kh * HD;
-    float* sc = pos < kAttnLdsPositions ? lds_sc : scores + (size_t)h * n_ctx;
-    // a barrier after writes to sc: LDS-only unless the scores spill to global memory
-    auto sc_barrier = [&]() {
-        if (pos < kAttnLdsPositions) {
-            lds_barrier();
-        } else {
-            __threadfence_block();
-            __syncthreads();
-        }
-    };
+    float scale, float* __restrict__ scores, uint32_t n_ctx, int* err, int code_base) {
+    constexpr uint32_t HD = kAttnHD, hd4 = HD / 4, half = HD / 2;
+    __shared__ float4 sq4[2][hd4];  // the squares of q and k
+    __shared__ float4 qk4[2][hd4];  // q and k normalised and rotated
+    const uint32_t lane = threadIdx.x, h = blockIdx.x, t = blockIdx.y * kScoreBlock + lane;
+    const size_t head_off = (size_t)(h / kv_mul) * HD;
+    const bool row_owner = h % kv_mul == 0 && blockIdx.y == pos / kScoreBlock;
 
-    // reads, in the order they are needed (the load counter completes in order, so
-    // a small load issued after the big ones would wait for them): the head
-    // vectors, gains, RoPE factors and v, then this thread's key row, then the first
-    // V rows straight into LDS
-    const uint32_t ti = min(tid, HD - 1u), tj = min(tid, HD / 2u - 1u);
-    const float qv = q[(size_t)h * HD + ti], kv = k[head_off + ti];
-    const float qg = q_gain[ti], kg = k_gain[ti];
-    const float rc = cosv[tj], rs = sinv[tj];
-    const float vv = v[head_off + ti];
+    // reads, in the order they are needed: elements lane and lane + 64 of the head
+    // vectors and gains (a RoPE pair), the RoPE factors, then this lane's key row
+    // (rows past pos clamped to pos: loaded, never used)
+    const float qa = q[(size_t)h * HD + lane], qb = q[(size_t)h * HD + lane + half];
+    const float ka = k[head_off + lane], kb = k[head_off + lane + half];
+    const float qga = q_gain[lane], qgb = q_gain[lane + half], kga = k_gain[lane], kgb = k_gain[lane + half];
+    const float c = cosv[lane], s = sinv[lane];
     float4 key[hd4];
-    if (tid < pos) {  // row pos comes from ks
-        const float* row = kc + (size_t)tid * kv_dim + head_off;
+    {
+        const float4* row = reinterpret_cast<const float4*>(kc + (size_t)min(t, pos) * kv_dim + head_off);
 #pragma unroll
-        for (uint32_t c = 0; c < hd4; ++c)
-            key[c] = reinterpret_cast<const float4*>(row)[c];
+        for (uint32_t i = 0; i < hd4; ++i)
+            key[i] = row[i];
     }
-    attn_dma_v(vs4, vc, v, head_off, 0, pos, kv_dim);
 
-    // head norms: the q sum in wave 0, the k sum in wave 1, concurrently
+    // head norms: both in-order sums over head_dim, interleaved, in every lane
     float* sq_q = reinterpret_cast<float*>(sq4[0]);
     float* sq_k = reinterpret_cast<float*>(sq4[1]);
-    if (tid < HD) {
-        qs[tid] = qv;
-        ks[tid] = kv;
-        sq_q[tid] = qv * qv;
-        sq_k[tid] = kv * kv;
+    sq_q[lane] = qa * qa;
+    sq_q[lane + half] = qb * qb;
+    sq_k[lane] = ka * ka;
+    sq_k[lane + half] = kb * kb;
+    wave_lds_sync();
+    float sum_q = 0.0f, sum_k = 0.0f;
+#pragma unroll 8
+    for (uint32_t i = 0; i < hd4; ++i) {
+        const float4 a = sq4[0][i], b = sq4[1][i];
+        sum_q = sum_q + a.x;
+        sum_k = sum_k + b.x;
+        sum_q = sum_q + a.y;
+        sum_k = sum_k + b.y;
+        sum_q = sum_q + a.z;
+        sum_k = sum_k + b.z;
+        sum_q = sum_q + a.w;
+        sum_k = sum_k + b.w;
     }
-    lds_barrier();
-    if (tid == 0 || tid == 64) {
-        const float sum = sum_lds_in_order(tid == 0 ? sq_q : sq_k, HD);
-        rms_s[tid == 0 ? 0 : 1] = sqrtf(sum / (float)HD + eps);
-    }
-    lds_barrier();
-    const float rq = rms_s[0], rk = rms_s[1];
+    const float rq = sqrtf(sum_q / (float)HD + eps), rk = sqrtf(sum_k / (float)HD + eps);
     if (!isfinite(rq) || rq == 0.0f || !isfinite(rk) || rk == 0.0f) {
-        if (tid == 0)
+        if (lane == 0)
             set_error_first(err, code_base + 2);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no LDS DMA outlives the workgroup
         return;
     }
-    if (tid < HD) {
-        qs[tid] = qs[tid] / rq * qg;
-        ks[tid] = ks[tid] / rk * kg;
+    // x / rms * gain, then the rotation of pair (lane, lane + 64)
+    const float nqa = qa / rq * qga, nqb = qb / rq * qgb;
+    const float nka = ka / rk * kga, nkb = kb / rk * kgb;
+    float* qr = reinterpret_cast<float*>(qk4[0]);
+    float* kr = reinterpret_cast<float*>(qk4[1]);
+    qr[lane] = nqa * c - nqb * s;
+    qr[lane + half] = nqa * s + nqb * c;
+    const float rka = nka * c - nkb * s, rkb = nka * s + nkb * c;
+    kr[lane] = rka;
+    kr[lane + half] = rkb;
+    if (row_owner) {
+        kc[(size_t)pos * kv_dim + head_off + lane] = rka;
+        kc[(size_t)pos * kv_dim + head_off + lane + half] = rkb;
+        vc[(size_t)pos * kv_dim + head_off + lane] = v[head_off + lane];
+        vc[(size_t)pos * kv_dim + head_off + lane + half] = v[head_off + lane + half];
     }
-    lds_barrier();
-    // RoPE of pairs (j, j + HD/2); thread j owns pair j of both vectors
-    constexpr uint32_t half = HD / 2u;
-    if (tid < half) {
-        const float c = rc, s = rs;
-        float a = qs[tid], b = qs[tid + half];
-        qs[tid] = a * c - b * s;
-        qs[tid + half] = a * s + b * c;
-        a = ks[tid], b = ks[tid + half];
-        ks[tid] = a * c - b * s;
-        ks[tid + half] = a * s + b * c;
-    }
-    lds_barrier();
-    if (h % kv_mul == 0 && tid < HD) {
-        kc[(size_t)pos * kv_dim + head_off + tid] = ks[tid];
-        vc[(size_t)pos * kv_dim + head_off + tid] = vv;
-    }
+    wave_lds_sync();
 
-    // scores: position t by thread t mod 256; the first round's key rows are in
-    // registers, later rounds load theirs; row pos from ks
-    float mx = -INFINITY;
-    for (uint32_t t = tid; t <= pos; t += kAttnThreads) {
-        if (t != tid && t != pos) {
-            const float* row = kc + (size_t)t * kv_dim + head_off;
+    // the score of position t: in-order dot over head_dim (row pos: the new key)
+    if (t == pos) {
 #pragma unroll
-            for (uint32_t c = 0; c < hd4; ++c)
-                key[c] = reinterpret_cast<const float4*>(row)[c];
-        }
-        float dot = 0.0f;
-        if (t == pos) {
-            for (uint32_t i = 0; i < HD; ++i)
-                dot = dot + qs[i] * ks[i];
-        } else {
+        for (uint32_t i = 0; i < hd4; ++i)
+            key[i] = qk4[1][i];
+    }
+    float dot = 0.0f;
 #pragma unroll
-            for (uint32_t c = 0; c < hd4; ++c) {
-                const float4 qq = qs4[c];
-                dot = dot + qq.x * key[c].x;
-                dot = dot + qq.y * key[c].y;
-                dot = dot + qq.z * key[c].z;
-                dot = dot + qq.w * key[c].w;
-            }
-        }
+    for (uint32_t i = 0; i < hd4; ++i) {
+        const float4 qq = qk4[0][i];
+        dot = dot + qq.x * key[i].x;
+        dot = dot + qq.y * key[i].y;
+        dot = dot + qq.z * key[i].z;
+        dot = dot + qq.w * key[i].w;
+    }
+    if (t <= pos) {
         const float score = dot * scale;
         if (!isfinite(score))
             set_error_first(err, code_base + 3 + 2 * (int)h);
-        sc[t] = score;
-        mx = score > mx ? score : mx;
+        scores[(size_t)h * n_ctx + t] = score;
     }
-    // the maximum over the workgroup (order-free; the scores are finite or flagged)
-    mx = __ockl_wfred_max_f32(mx);
-    if (lane == 0)
-        red[tid >> 6] = mx;
-    lds_barrier();
-    const float maximum = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    // exp, and +0 after pos up to a multiple of 64 positions: adding +0 to this sum of
-    // non-negative terms changes nothing, and the sums below then run whole steps
-    const uint32_t padded = pos < kAttnLdsPositions ? (pos + 64u) & ~63u : pos + 1u;
-    for (uint32_t t = tid; t < padded; t += kAttnThreads)
-        sc[t] = t <= pos ? bnne_expf_libc(sc[t] - maximum, exp_tab) : 0.0f;
-    sc_barrier();
-    if (tid == 0) {
-        const float sum = pos < kAttnLdsPositions ? sum_lds_in_order(sc, padded)
-                                                  : sum_in_order<32>(pos + 1u, [&](uint32_t t) { return sc[t]; });
-        if (!(sum > 0.0f) || !isfinite(sum))
-            set_error_first(err, code_base + 4 + 2 * (int)h);
-        sum_s = sum;
-    }
-    lds_barrier();
-    const float sum = sum_s;
-    for (uint32_t t = tid; t <= pos; t += kAttnThreads)
-        sc[t] = sc[t] / sum;
+}
 
-    // value[i] = sum over t in order of p[t] * V[t][i]; V rows in LDS, kAttnVRows at a
-    // time.  Steps of 8 rows: past pos the probabilities are +0 and the rows finite
-    // copies of row pos, so the extra products are ±0 and the (never -0) sum is unchanged
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's V pieces have landed
-    float acc = 0.0f;
-    for (uint32_t t0 = 0; t0 <= pos; t0 += kAttnVRows) {
-        if (t0 > 0) {
-            lds_barrier();  // every thread is done with the previous rows
-            attn_dma_v(vs4, vc, v, head_off, t0, pos, kv_dim);
-            __builtin_amdgcn_s_waitcnt(0x0F70);
+// V slice rows t0 .. min(t0 + kPvRows, pos + 1) - 1 into LDS, 8 rows of 128 bytes per
+// instruction: lane l moves 16-byte piece l % 8 of row l / 8 (rows past pos clamped).
+__device__ __forceinline__ void dma_v_slice(float4* vs4, const float* __restrict__ vc, size_t off, uint32_t t0,
+                                            uint32_t pos, uint32_t kv_dim) {
+    const uint32_t lane = threadIdx.x;
+    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
+    const uint32_t rows = min(pos + 1u - t0, kPvRows);
+    for (uint32_t r0 = 0; r0 < rows; r0 += 8u) {
+        const uint32_t t = min(t0 + r0 + (lane >> 3), pos);
+        dma16(vc + (size_t)t * kv_dim + off + 4u * (lane & 7u), base + r0 * kPvSlice * 4u);
+    }
+}
+
+__global__ __launch_bounds__(64) void k_attn_pv(const float* __restrict__ scores, const float* __restrict__ vc,
+                                                uint32_t kv_mul, uint32_t pos, uint32_t kv_dim, uint32_t n_ctx,
+                                                float* __restrict__ y, int* err, int code_base) {
+    constexpr uint32_t HD = kAttnHD;
+    __shared__ float4 vs4[kPvRows * kPvSlice / 4];
+    __shared__ float4 p4[kPvLdsPositions / 4];
+    __shared__ uint64_t exp_tab[32];  // the expf table: its lookups are per-lane gathers
+    float* p = reinterpret_cast<float*>(p4);
+    const float* vs = reinterpret_cast<const float*>(vs4);
+    const uint32_t lane = threadIdx.x, h = blockIdx.x, d0 = blockIdx.y * kPvSlice;
+    const size_t off = (size_t)(h / kv_mul) * HD + d0;
+    const float* sc = scores + (size_t)h * n_ctx;
+    const bool in_lds = pos < kPvLdsPositions;
+
+    // the V rows of the first pass, then the scores (into LDS when they fit) and
+    // their maximum (order-free: the scores are finite or flagged)
+    dma_v_slice(vs4, vc, off, 0, pos, kv_dim);
+    if (lane < 32u)
+        exp_tab[lane] = kExp2Table[lane];
+    float mx = -INFINITY;
+    for (uint32_t t = lane; t <= pos; t += 64u) {
+        const float x = sc[t];
+        if (in_lds)
+            p[t] = x;
+        mx = x > mx ? x : mx;
+    }
+    const float maximum = __ockl_wfred_max_f32(mx);
+    wave_lds_sync();
+
+    // expf(score - max) and their sum in position order; in LDS +0 pads the terms to a
+    // multiple of 64 (adding +0 to this sum of non-negative terms changes nothing)
+    float sum = 0.0f;
+    if (in_lds) {
+        const uint32_t padded = (pos + 64u) & ~63u;
+        for (uint32_t t = lane; t < padded; t += 64u)
+            p[t] = t <= pos ? bnne_expf_libc(p[t] - maximum, exp_tab) : 0.0f;
+        wave_lds_sync();
+        sum = sum_lds_in_order(p, padded);
+    } else {
+        // 64 terms at a time through p (unused otherwise), each step padded with +0
+        for (uint32_t t0 = 0; t0 <= pos; t0 += 64u) {
+            p[lane] = t0 + lane <= pos ? bnne_expf_libc(sc[t0 + lane] - maximum, exp_tab) : 0.0f;
+            wave_lds_sync();
+            sum = sum_lds_in_order(p, 64u, sum);
+            wave_lds_sync();
         }
-        sc_barrier();  // the probabilities (first pass) and this thread's V pieces are visible
-        if (tid < HD && pos >= kAttnLdsPositions) {  // scores in global memory: exactly rows t0..pos
-            const uint32_t n = min(kAttnVRows, pos + 1u - t0);
-            for (uint32_t r = 0; r < n; ++r)
-                acc = acc + sc[t0 + r] * vs[r * HD + tid];
-        } else if (tid < HD) {
-            const uint32_t n = min(kAttnVRows, ((pos + 8u) & ~7u) - t0);
-            for (uint32_t r = 0; r < n; r += 8u) {
-                float p8[8], v8[8];
+    }
+    if (!(sum > 0.0f) || !isfinite(sum)) {
+        if (lane == 0)
+            set_error_first(err, code_base + 4 + 2 * (int)h);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no LDS DMA outlives the workgroup
+        return;
+    }
+    if (in_lds) {
+        for (uint32_t t = lane; t <= pos; t += 64u)
+            p[t] = p[t] / sum;
+    }
+
+    // value[i] = sum over t in order of p[t] * V[t][i], lane i < 32 of the slice
+    float acc = 0.0f;
+    for (uint32_t t0 = 0; t0 <= pos; t0 += kPvRows) {
+        if (t0 > 0) {
+            wave_lds_sync();  // every lane is done with the previous rows
+            dma_v_slice(vs4, vc, off, t0, pos, kv_dim);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the wave's V pieces have landed
+        wave_lds_sync();
+        const uint32_t n = min(kPvRows, pos + 1u - t0);
+        if (lane < kPvSlice) {
+            uint32_t r = 0;
+            if (in_lds) {
+                for (; r + 8u <= n; r += 8u) {
+                    float p8[8], v8[8];
 #pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    p8[c] = sc[t0 + r + c];
-                    v8[c] = vs[(r + c) * HD + tid];
+                    for (int i = 0; i < 8; ++i) {
+                        p8[i] = p[t0 + r + i];
+                        v8[i] = vs[(r + i) * kPvSlice + lane];
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        acc = acc + p8[i] * v8[i];
                 }
-#pragma unroll
-                for (int c = 0; c < 8; ++c)
-                    acc = acc + p8[c] * v8[c];
+                for (; r < n; ++r)
+                    acc = acc + p[t0 + r] * vs[r * kPvSlice + lane];
+            } else {
+                for (; r < n; ++r) {
+                    const float pr = bnne_expf_libc(sc[t0 + r] - maximum, exp_tab) / sum;
+                    acc = acc + pr * vs[r * kPvSlice + lane];
+                }
             }
         }
     }
-    if (tid < HD)
-        y[(size_t)h * HD + tid] = acc;
+    if (lane < kPvSlice)
+        y[(size_t)h * HD + d0 + lane] = acc;
 }
 
 // gate = gate / (1 + exp(-gate)) * up (qwen3.c:491-495).
@@ -615,8 +611,8 @@ struct Resident {
     uint32_t C, H, Hk, HD, FF, L, V, kv_dim, n_ctx;
     float eps;
     // activations that linear layers read or write: accelerator buffers
-    BNN_Buffer b_norm, b_q, b_k, b_v, b_y, b_o, b_gate, b_up, b_logits;
-    float *norm, *q, *k, *v, *y, *o, *gate, *up;
+    BNN_Buffer b_norm, b_q, b_k, b_v, b_y, b_o, b_gate, b_up, b_h, b_logits;
+    float *norm, *q, *k, *v, *y, *o, *gate, *up, *h;  // h: SiLU(gate) * up (fused step)
     // everything else: this engine's device memory
     float *x, *x2, *kc, *vc, *scores, *gains, *rope_cos, *rope_sin;
     uint8_t* emb_bits;
@@ -689,7 +685,7 @@ BNNE_Status make_batch(Resident* r, std::initializer_list<std::pair<const Linear
 
 BNNE_Status make_fused(Resident* r, std::initializer_list<std::pair<const Linear*, BNN_Buffer>> parts, BNN_Buffer in,
                        const BNNX_PreOp& pre, BNNX_Batch* out, uint64_t* jobs_total, uint64_t* macs,
-                       BNN_Status* accel_status) {
+                       BNN_Status* accel_status, const BNNX_PostOp* post = nullptr) {
     uint32_t count = 0;
     for (const auto& p : parts)
         count += p.first->n_chunks;
@@ -699,10 +695,10 @@ BNNE_Status make_fused(Resident* r, std::initializer_list<std::pair<const Linear
     uint32_t n = 0;
     for (const auto& p : parts)
         add_jobs(p.first, in, p.second, jobs, &n, macs);
-    *accel_status = BNNX_BatchCreateFused(r->dev, jobs, n, &pre, out);
+    *accel_status = BNNX_BatchCreateFusedPost(r->dev, jobs, n, &pre, post, out);
     std::free(jobs);
     *jobs_total += n;
-    return *accel_status == BNN_OK ? BNNE_OK : accel_error(*accel_status, "BNNX_BatchCreateFused");
+    return *accel_status == BNN_OK ? BNNE_OK : accel_error(*accel_status, "BNNX_BatchCreateFusedPost");
 }
 
 // Error codes of the fused step (see set_error_first).
@@ -738,8 +734,8 @@ void destroy_batches(Resident* r) {
 // Fused batches of every layer and of the lm_head:
 //   qkv:    RMSNorm(x [+ o]) with attn_norm, the sum stored to x2   -> q, k, v
 //   o:      the attention output row y                               -> o
-//   gate/up RMSNorm(x2 + o) with ffn_norm, the sum stored to x       -> gate, up
-//   down:   SiLU(gate) * up                                          -> o
+//   gate/up RMSNorm(x2 + o) with ffn_norm, the sum stored to x       -> gate, up, h = SiLU(gate) * up
+//   down:   the row h                                                -> o
 //   lm_head RMSNorm(x + o) with final_norm                           -> logits
 // so the residual stream alternates between x and x2 within a layer and is in x
 // (plus the down output in o) between layers.  *accel_status is the backend's
@@ -780,16 +776,18 @@ BNNE_Status build_fused(Resident* r, BNN_Status* accel_status) {
             pre.gain = ffn_norm + (size_t)l * C;
             pre.a_out = r->x;
             pre.err_code = base + 3 + 2 * (int)r->H;
+            // the chunks of gate and of up pair up (equal widths): SiLU(gate) * up -> h
+            BNNX_PostOp silu{};
+            silu.kind = BNNX_POST_SILU_MUL;
+            silu.out = r->h;
             st = make_fused(r, {{p[4], r->b_gate}, {p[5], r->b_up}}, r->b_norm, pre, &r->gate_up[l], &r->jobs_per_token,
-                            &r->macs_per_token, accel_status);
+                            &r->macs_per_token, accel_status, &silu);
         }
         if (st == BNNE_OK) {
-            BNNX_PreOp silu{};
-            silu.kind = BNNX_PRE_SILU_MUL;
-            silu.width = r->FF;
-            silu.a = r->gate;
-            silu.b = r->up;
-            st = make_fused(r, {{p[6], r->b_o}}, r->b_gate, silu, &r->down[l], &r->jobs_per_token, &r->macs_per_token,
+            BNNX_PreOp row{};
+            row.kind = BNNX_PRE_ROW;
+            row.width = r->FF;
+            st = make_fused(r, {{p[6], r->b_o}}, r->b_h, row, &r->down[l], &r->jobs_per_token, &r->macs_per_token,
                             accel_status);
         }
     }
@@ -888,6 +886,8 @@ BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, bool fused,
         st = alloc_buffer(r, m.FF, &r->b_gate, &r->gate);
     if (st == BNNE_OK)
         st = alloc_buffer(r, m.FF, &r->b_up, &r->up);
+    if (st == BNNE_OK)
+        st = alloc_buffer(r, m.FF, &r->b_h, &r->h);
     float* logits_dev = nullptr;
     if (st == BNNE_OK)
         st = alloc_buffer(r, m.V, &r->b_logits, &logits_dev);
@@ -973,7 +973,7 @@ void resident_free(Resident* r) {
     std::free(r->gate_up);
     std::free(r->down);
     std::free(r->lin);
-    for (BNN_Buffer b : {r->b_norm, r->b_q, r->b_k, r->b_v, r->b_y, r->b_o, r->b_gate, r->b_up, r->b_logits})
+    for (BNN_Buffer b : {r->b_norm, r->b_q, r->b_k, r->b_v, r->b_y, r->b_o, r->b_gate, r->b_up, r->b_h, r->b_logits})
         BNN_BufferFree(b);
     for (void* p : {(void*)r->x, (void*)r->x2, (void*)r->kc, (void*)r->vc, (void*)r->scores, (void*)r->gains, (void*)r->rope_cos,
                     (void*)r->rope_sin, (void*)r->emb_bits, (void*)r->emb_scales, (void*)r->err})
@@ -1021,11 +1021,14 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         for (uint32_t l = 0; l < r->L && st == BNNE_OK; ++l) {
             const size_t cache_layer = (size_t)l * r->n_ctx * r->kv_dim;
             launch(r->qkv[l]);
-            hipLaunchKernelGGL(k_attention_fused, dim3(r->H), dim3(kAttnThreads), 0, r->stream, r->q, r->k, r->v,
-                               r->H / r->Hk, r->eps, q_norm + (size_t)l * HD, k_norm + (size_t)l * HD,
-                               r->rope_cos + (size_t)pos * half, r->rope_sin + (size_t)pos * half,
-                               r->kc + cache_layer, r->vc + cache_layer, pos, r->kv_dim, scale, r->scores, r->n_ctx,
-                               r->y, r->err, (int)l * code_span(r));
+            hipLaunchKernelGGL(k_attn_scores, dim3(r->H, pos / kScoreBlock + 1u), dim3(kScoreBlock), 0, r->stream,
+                               r->q, r->k, r->v, r->H / r->Hk, r->eps, q_norm + (size_t)l * HD,
+                               k_norm + (size_t)l * HD, r->rope_cos + (size_t)pos * half,
+                               r->rope_sin + (size_t)pos * half, r->kc + cache_layer, r->vc + cache_layer, pos,
+                               r->kv_dim, scale, r->scores, r->n_ctx, r->err, (int)l * code_span(r));
+            hipLaunchKernelGGL(k_attn_pv, dim3(r->H, HD / kPvSlice), dim3(64), 0, r->stream, r->scores,
+                               r->vc + cache_layer, r->H / r->Hk, pos, r->kv_dim, r->n_ctx, r->y, r->err,
+                               (int)l * code_span(r));
             launch(r->attn_out[l]);
             launch(r->gate_up[l]);
             launch(r->down[l]);

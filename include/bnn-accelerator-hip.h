@@ -116,6 +116,24 @@ typedef struct {
 BNN_Status BNNX_BatchCreateFused(BNN_Device device, const BNN_Job* jobs, uint32_t count, const BNNX_PreOp* pre,
                                  BNNX_Batch* out_batch);
 
+/* A fused batch with an operation on pairs of its outputs (post == NULL or kind
+ * BNNX_POST_NONE: BNNX_BatchCreateFused).  BNNX_POST_SILU_MUL: the 2m jobs are m pairs
+ * (job p, job m + p) whose outputs have equal length n_p; besides writing every job's
+ * output as usual, the batch stores
+ *   out[o_p + i] = y_p[i] / (1 + expf(-y_p[i])) * y_(m+p)[i],   o_p = n_0 + ... + n_(p-1)
+ * (each operation rounded to binary32 separately, expf of the host C library): the
+ * SiLU(gate) * up of the qwen3 step (qwen3.c:491-495) for gate/up jobs, as one launch.
+ * `out` is a device address of n_0 + ... + n_(m-1) floats that may not overlap any
+ * operand or job output.  Statuses as BNNX_BatchCreateFused, plus BNN_EINVAL for an
+ * odd job count, pairs of unequal length or a NULL out. */
+enum { BNNX_POST_NONE = 0, BNNX_POST_SILU_MUL = 1 };
+typedef struct {
+    int32_t kind; /* BNNX_POST_* */
+    float* out;   /* SILU_MUL: the products */
+} BNNX_PostOp;
+BNN_Status BNNX_BatchCreateFusedPost(BNN_Device device, const BNN_Job* jobs, uint32_t count, const BNNX_PreOp* pre,
+                                     const BNNX_PostOp* post, BNNX_Batch* out_batch);
+
 /* Device address of a buffer's memory, for kernels a caller runs on the device's
  * stream between batch launches.  Valid until BNN_BufferFree. */
 BNN_Status BNNX_BufferDevicePointer(BNN_Buffer buffer, void** out_pointer);

@@ -7,7 +7,7 @@ them, and stores its outputs (per decode step: greedy token and an FNV-1a-64 has
 of the logits bytes; for classification: every logit's float32 bits, hashed) as
 JSON fixtures under tests/golden/.  Run from the repository root:
 
-    python tests/golden/make_e2e_fixtures.py [tiny] [mlp] [full FULL_OUTPUT.txt]
+    python tests/golden/make_e2e_fixtures.py [tiny] [mlp] [long] [full FULL_OUTPUT.txt]
 
 'full' converts the output of a full-size run made beforehand (it takes ~15 min on
 one core):  oracle/_ref/engine_run_soft llm MODEL.gguf PROMPT.txt 127 1024
@@ -32,6 +32,9 @@ TINY = dict(layers=2, hidden=256, heads=2, kv_heads=1, head_dim=128, ffn=512, vo
 TINY_PROMPT, TINY_STEPS, TINY_CTX = 8, 12, 64
 MLP_SAMPLES, MLP_BATCH = 1000, 64
 FULL_PROMPT, FULL_STEPS, FULL_CTX = 32, 127, 1024
+# a one-layer model decoding past 4096 positions (attention over long contexts)
+LONG = dict(layers=1, hidden=256, heads=2, kv_heads=1, head_dim=128, ffn=256, vocab=256, context=4608, seed=23)
+LONG_PROMPT, LONG_STEPS, LONG_CTX = 4160, 6, 4400
 
 
 def package():
@@ -69,6 +72,19 @@ def tiny(pkg):
     (GOLDEN / "e2e_qwen3_tiny.json").write_text(json.dumps(res, indent=1) + "\n")
 
 
+def long(pkg):
+    with tempfile.TemporaryDirectory() as d:
+        model, ids = Path(d) / "long.gguf", Path(d) / "ids.txt"
+        pkg.gguf.qwen3_random(model, **LONG)
+        prompt = pkg.gguf.prompt_ids(LONG_PROMPT, LONG["vocab"], seed=LONG["seed"])
+        ids.write_text(" ".join(map(str, prompt)) + "\n")
+        out = subprocess.run([str(RUN), "llm", str(model), str(ids), str(LONG_STEPS), str(LONG_CTX)], check=True,
+                             capture_output=True, text=True).stdout
+    res = {"model": LONG, "prompt_count": LONG_PROMPT, "prompt_seed": LONG["seed"], "steps_arg": LONG_STEPS,
+           "ctx": LONG_CTX, **parse_llm(out)}
+    (GOLDEN / "e2e_qwen3_long.json").write_text(json.dumps(res, indent=1) + "\n")
+
+
 def mlp(pkg):
     with tempfile.TemporaryDirectory() as d:
         model, inp = Path(d) / "mlp.gguf", Path(d) / "in.f32"
@@ -102,6 +118,8 @@ if __name__ == "__main__":
         tiny(pkg)
     if "mlp" in args:
         mlp(pkg)
+    if "long" in args:
+        long(pkg)
     if "full" in args:
         i = args.index("full")
         full(pkg, Path(args[i + 1]), float(args[i + 2]) if len(args) > i + 2 else None)

@@ -26,6 +26,7 @@ ENGINE_RUN_SOFT = REF_DIR / "engine_run_soft"
 ENGINE_RUN_REFHIP = REF_DIR / "engine_run_refhip"
 TINY = json.loads((GOLDEN / "e2e_qwen3_tiny.json").read_text())
 MLP = json.loads((GOLDEN / "e2e_bnn_mlp.json").read_text())
+LONG = json.loads((GOLDEN / "e2e_qwen3_long.json").read_text())
 FULL_FIXTURE = GOLDEN / "e2e_qwen3_1p7b.json"
 
 
@@ -229,6 +230,23 @@ def test_engine_qwen3_tiny_bit_exact(pkg, tmp_path, runner):
     if runner != "refhip":
         assert parse_path(out) == runner.split("-")[1]
     assert parse_llm(out) == TINY["steps"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["device", "prepared"])
+def test_engine_qwen3_long_context_bit_exact(pkg, tmp_path, path):
+    """Decoding past 4096 positions: the device attention's multi-pass V rows (more
+    than 1024 positions) and its probabilities recomputed beyond the LDS capacity
+    (more than 4096), against the reference engine + soft backend."""
+    model, ids = tmp_path / "long.gguf", tmp_path / "ids.txt"
+    pkg.gguf.qwen3_random(model, **LONG["model"])
+    prompt = pkg.gguf.prompt_ids(LONG["prompt_count"], LONG["model"]["vocab"], seed=LONG["prompt_seed"])
+    ids.write_text(" ".join(map(str, prompt)) + "\n")
+    print(f"engine qwen3 long context, {path} path", flush=True)
+    out = subprocess.run([str(ENGINE_RUN_OWN), "llm", str(model), str(ids), str(LONG["steps_arg"]), str(LONG["ctx"]),
+                          path], capture_output=True, text=True, timeout=300, check=True).stdout
+    assert parse_path(out) == path
+    assert parse_llm(out) == LONG["steps"]
 
 
 @pytest.mark.gpu

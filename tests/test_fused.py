@@ -210,6 +210,82 @@ def test_fused_silu_mul(pkg, hipdev, oracle, k, ns):
         f.free()
 
 
+@pytest.mark.parametrize("k,ns,kind", [
+    (2048, [640, 640], "rmsnorm"),           # the gate/up shape, scaled down
+    (2048, [256, 96, 256, 96], "rmsnorm"),   # two pairs of different lengths
+    (1024, [100, 100], "row"),               # a partial last tile, the ROW input
+    (6144, [128, 128], "rmsnorm"),           # the wide template
+])
+def test_fused_post_silu_mul(pkg, hipdev, oracle, k, ns, kind):
+    """SiLU(y_p) * y_(m+p) of the pairs stored next to the jobs' own outputs."""
+    rng = np.random.default_rng(k + len(ns))
+    f = Fused(pkg, hipdev, k, ns, seed=17)
+    m = len(ns) // 2
+    post_buf = hipdev.buffer(4 * sum(ns[:m]))
+    try:
+        post = pkg.api.PostOp()
+        post.kind, post.out = post.SILU_MUL, post_buf.device_pointer()
+        if kind == "rmsnorm":
+            a, b = f32(rng, k, 3.0), f32(rng, k, 0.5)
+            gain = (1.0 + 0.02 * rng.standard_normal(k)).astype(np.float32)
+            f.ops["a"].write(a)
+            f.ops["b"].write(b)
+            f.ops["gain"].write(gain)
+            pre = f.pre(pkg.api.PreOp.RMSNORM, True, False)
+            _, row, _ = host_rmsnorm(a, b, gain, 1e-6)
+        else:
+            row = f32(rng, k, 2.0)
+            f.row.write(row)
+            pre = f.pre(pkg.api.PreOp.ROW)
+        jobs = f.jobs()
+        st = hipdev.api.BNNX_BatchCreateFusedPost(hipdev.handle, jobs, len(jobs), ctypes.byref(pre),
+                                                  ctypes.byref(post), ctypes.byref(f.batch))
+        assert st == 0
+        assert f.run() == 0
+        want = expected(pkg, oracle, f.chunks, row)
+        check(f.outputs(), want)
+        prod = np.concatenate([host_silu_mul(want[p], want[m + p]) for p in range(m)])
+        got = post_buf.read().view(np.float32)
+        assert np.array_equal(got.view(np.uint32), prod.view(np.uint32)), first_mismatch(got, prod)
+    finally:
+        f.free()
+        post_buf.free()
+
+
+def test_fused_post_create_checks(pkg, hipdev):
+    S = pkg.Status
+    f = Fused(pkg, hipdev, 1024, [128, 128, 64], seed=19)
+    post_buf = hipdev.buffer(4 * 256)
+    try:
+        P = pkg.api.PreOp
+        post = pkg.api.PostOp()
+        post.kind, post.out = post.SILU_MUL, post_buf.device_pointer()
+
+        def create(jobs, post_op):
+            return hipdev.api.BNNX_BatchCreateFusedPost(hipdev.handle, jobs, len(jobs), ctypes.byref(f.pre(P.ROW)),
+                                                        ctypes.byref(post_op), ctypes.byref(f.batch))
+        jobs = f.jobs()
+        assert create(jobs, post) == S.EINVAL  # three jobs: no pairs
+        two = (pkg.Job * 2)(jobs[0], jobs[2])
+        assert create(two, post) == S.EINVAL  # a pair of unequal lengths
+        two = (pkg.Job * 2)(jobs[0], jobs[1])
+        bad = pkg.api.PostOp()
+        bad.kind, bad.out = 7, post_buf.device_pointer()
+        assert create(two, bad) == S.EINVAL
+        bad.kind, bad.out = bad.SILU_MUL, None
+        assert create(two, bad) == S.EINVAL
+        bad.out = f.outs[1].device_pointer()  # the products may not overlap a job output
+        assert create(two, bad) == S.EINVAL
+        bad.out = f.row.device_pointer()  # nor the input row
+        assert create(two, bad) == S.EINVAL
+        assert not f.batch
+        none = pkg.api.PostOp()
+        assert create(f.jobs(), none) == 0  # POST_NONE: a plain fused batch
+    finally:
+        f.free()
+        post_buf.free()
+
+
 def test_fused_illegal_rows_write_nothing(pkg, hipdev):
     """A failed RMSNorm divisor stores err_code and raises the device error; a
     non-finite produced row raises it without err_code; outputs stay untouched and
