@@ -69,7 +69,7 @@ __device__ __forceinline__ uint32_t f_plane_count(uint4 w, const uint4* p) {
     c = f_bcnt_acc(w.z & pb.z, c);
     return f_bcnt_acc(w.w & pb.w, c);
 }
-// D = sum_{b<7} 2^(b+1) popc(w & P_b) - 2^8 popc(w & P_7) - sum(Q)  (exact)
+// (planes in LDS) D = sum_{b<7} 2^(b+1) popc(w & P_b) - 2^8 popc(w & P_7) - sum(Q)  (exact)
 __device__ __forceinline__ int f_group_dot(uint4 w, const uint4* p, int neg_sum) {
     uint32_t d = (uint32_t)neg_sum;
     d = f_lshl_add<1>(f_plane_count<0>(w, p), d);
@@ -83,8 +83,8 @@ __device__ __forceinline__ int f_group_dot(uint4 w, const uint4* p, int neg_sum)
     return (int)d;
 }
 
-// The same with the group's planes as wave-uniform values: bit b of mask m[h][b] is
-// bit b of element 64 h + lane (plane words 2h and 2h + 1)
+// popc(w & P_B) of a group's sign bits w and plane B of the quantised row, the plane
+// as wave-uniform ballot masks: bit l of m[h][B] is bit B of element 64 h + l
 template <int B>
 __device__ __forceinline__ uint32_t f_plane_count_s(uint4 w, const uint64_t (&m)[2][8]) {
     uint32_t c = (uint32_t)__builtin_popcount(w.x & (uint32_t)m[0][B]);
@@ -92,6 +92,7 @@ __device__ __forceinline__ uint32_t f_plane_count_s(uint4 w, const uint64_t (&m)
     c = f_bcnt_acc(w.z & (uint32_t)m[1][B], c);
     return f_bcnt_acc(w.w & (uint32_t)(m[1][B] >> 32), c);
 }
+// D = sum_{b<7} 2^(b+1) popc(w & P_b) - 2^8 popc(w & P_7) - sum(Q)  (exact)
 __device__ __forceinline__ int f_group_dot_s(uint4 w, const uint64_t (&m)[2][8], int neg_sum) {
     uint32_t d = (uint32_t)neg_sum;
     d = f_lshl_add<1>(f_plane_count_s<0>(w, m), d);
@@ -502,31 +503,38 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
             s = __int_as_float(1);  // smallest subnormal
     }
 
-    // 4. quantise the wave's own groups: bit planes by ballot, -sum(Q) per group from
-    // the same masks; no exchange between waves
+    // 4. quantise the wave's own groups; their bit planes are ballots (wave-uniform
+    // masks: kept in scalar registers for one group per wave, else in LDS), and
+    // -sum(Q) per group from the same masks; no exchange between waves
     const float rcp = 1.0f / s;
     const bool exact = s < 0x1p-126f;  // 1 / s would overflow
+    int q[EPT];
+#pragma unroll
+    for (int i = 0; i < EPT; ++i)
+        q[i] = live(i) ? f_quantize(xv[i], s, rcp, exact) : 0;
     uint64_t masks[2][8];  // GPW == 1: the planes of group `wave`
     int neg_sum[GPW];
+    if constexpr (GPW == 1) {
+        neg_sum[0] = 0;
 #pragma unroll
-    for (int gi = 0; gi < GPW; ++gi) {
-        neg_sum[gi] = 0;
-        const uint32_t g = wave + kFusedWaves * gi;
-        if (g < G) {
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int q = f_quantize(xv[2 * gi + h], s, rcp, exact);
-                if constexpr (GPW == 1) {
+            for (int b = 0; b < 8; ++b) {
+                masks[h][b] = __ballot((q[h] >> b) & 1);
+                const int cnt = __popcll(masks[h][b]);
+                neg_sum[0] -= b == 7 ? -(cnt << 7) : (cnt << b);
+            }
+    } else {
 #pragma unroll
-                    for (int b = 0; b < 8; ++b) {
-                        masks[h][b] = __ballot((q >> b) & 1);
-                        const int cnt = __popcll(masks[h][b]);
-                        neg_sum[gi] -= b == 7 ? -(cnt << 7) : (cnt << b);
-                    }
-                } else {
+        for (int gi = 0; gi < GPW; ++gi) {
+            neg_sum[gi] = 0;
+            const uint32_t g = wave + kFusedWaves * gi;
+            if (g < G) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
                     uint32_t word = 0;
                     int sum = 0;
-                    plane_words<0>(q, word, sum);
+                    plane_words<0>(q[2 * gi + h], word, sum);
                     neg_sum[gi] -= sum;
                     if (lane < 16u)
                         reinterpret_cast<uint32_t*>(planes)[g * kPlaneWords + (lane >> 1) * 4u + h * 2u + (lane & 1u)] =
@@ -558,10 +566,11 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
             const uint32_t g = wave + kFusedWaves * i;
             if (g < G) {
                 int d;
-                if constexpr (GPW == 1)
+                if constexpr (GPW == 1) {
                     d = f_group_dot_s(cur.w[i], masks, neg_sum[i]);
-                else
+                } else {
                     d = f_group_dot(cur.w[i], planes + g * (kPlaneWords / 4u), neg_sum[i]);
+                }
                 prod[g * 64u + lane] = __half2float(__ushort_as_half((uint16_t)cur.s[i])) * (float)d;
             }
         }

@@ -362,15 +362,14 @@ __device__ void set_error_first(int* err, int code) {
 //   the kv head's first query head, in the block that holds pos), then one score per
 //   lane, each an in-order dot over head_dim -- position pos from the wave's own new
 //   key, so no workgroup reads a row another is writing;
-//   k_attn_pv, workgroup (query head h, slice of 32 head dims), one wave: the maximum,
+//   k_attn_pv, workgroup (query head h, slice of 32 head dims), two waves: the maximum,
 //   expf, the in-order sum and the probabilities over positions 0..pos, then
 //   value[i] = sum over t in order of p[t] * V[t][i] for the slice's i, the V rows
-//   moved into LDS by DMA at the start.
+//   moved into LDS by DMA by a second wave meanwhile.
 // Every sum runs in index / position order, as in the host step.
 constexpr uint32_t kAttnHD = 128;             // head_dim of the fused step
 constexpr uint32_t kScoreBlock = 64;          // positions per k_attn_scores workgroup
 constexpr uint32_t kPvSlice = 32;             // head dims per k_attn_pv workgroup
-constexpr uint32_t kPvRows = 1024;            // V slice rows in LDS per pass (128 KB)
 constexpr uint32_t kPvLdsPositions = 4096;    // probabilities in LDS (16 KB); beyond, recomputed
 
 // Orders one wave's LDS writes before its later LDS reads of other lanes' data.
@@ -378,14 +377,6 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// 16 bytes per lane from global memory into LDS at lds_addr + 16 * lane (lds_addr is
-// the wave's base, in M0).  Inline assembly: the kernel waits for these loads
-// itself (vmcnt(0) before the first read).  The s_nop covers the wait state between
-// writing M0 and the LDS DMA reading it.
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_addr) : "memory");
 }
 
 __global__ __launch_bounds__(64) void k_attn_scores(
@@ -483,49 +474,76 @@ __global__ __launch_bounds__(64) void k_attn_scores(
     }
 }
 
-// V slice rows t0 .. min(t0 + kPvRows, pos + 1) - 1 into LDS, 8 rows of 128 bytes per
-// instruction: lane l moves 16-byte piece l % 8 of row l / 8 (rows past pos clamped).
-__device__ __forceinline__ void dma_v_slice(float4* vs4, const float* __restrict__ vc, size_t off, uint32_t t0,
-                                            uint32_t pos, uint32_t kv_dim) {
-    const uint32_t lane = threadIdx.x;
-    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
-    const uint32_t rows = min(pos + 1u - t0, kPvRows);
-    for (uint32_t r0 = 0; r0 < rows; r0 += 8u) {
-        const uint32_t t = min(t0 + r0 + (lane >> 3), pos);
-        dma16(vc + (size_t)t * kv_dim + off + 4u * (lane & 7u), base + r0 * kPvSlice * 4u);
-    }
+// 16 bytes per lane from global memory into LDS at lds_addr + 16 * lane (lds_addr is
+// the wave's base, in M0).  Inline assembly: the wave waits for these loads itself
+// (vmcnt(0)).  The s_nop covers the wait state between writing M0 and the LDS DMA
+// reading it.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_addr) : "memory");
 }
 
-__global__ __launch_bounds__(64) void k_attn_pv(const float* __restrict__ scores, const float* __restrict__ vc,
-                                                uint32_t kv_mul, uint32_t pos, uint32_t kv_dim, uint32_t n_ctx,
-                                                float* __restrict__ y, int* err, int code_base) {
+constexpr uint32_t kPvRows = 1024;  // V slice rows in LDS per pass (128 KB)
+constexpr uint32_t kPvPad = 16;     // rows / probabilities read past the end by the pipelined loop
+
+__global__ __launch_bounds__(128) void k_attn_pv(const float* __restrict__ scores, const float* __restrict__ vc,
+                                                 uint32_t kv_mul, uint32_t pos, uint32_t kv_dim, uint32_t n_ctx,
+                                                 float* __restrict__ y, int* err, int code_base) {
     constexpr uint32_t HD = kAttnHD;
-    __shared__ float4 vs4[kPvRows * kPvSlice / 4];
-    __shared__ float4 p4[kPvLdsPositions / 4];
-    __shared__ uint64_t exp_tab[32];  // the expf table: its lookups are per-lane gathers
+    constexpr uint32_t kBatch = 8;  // score loads per lane in flight
+    __shared__ float4 vs4[(kPvRows + kPvPad) * kPvSlice / 4];
+    __shared__ float4 p4[(kPvLdsPositions + 64u) / 4];  // probabilities (or one pass's), padded
+    __shared__ uint64_t exp_tab[32];                      // the expf table: its lookups are per-lane gathers
     float* p = reinterpret_cast<float*>(p4);
     const float* vs = reinterpret_cast<const float*>(vs4);
-    const uint32_t lane = threadIdx.x, h = blockIdx.x, d0 = blockIdx.y * kPvSlice;
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t h = blockIdx.x, d0 = blockIdx.y * kPvSlice;
     const size_t off = (size_t)(h / kv_mul) * HD + d0;
     const float* sc = scores + (size_t)h * n_ctx;
-    const bool in_lds = pos < kPvLdsPositions;
+    const bool in_lds = pos < kPvLdsPositions;  // every probability in LDS, else per pass of V rows
 
-    // the V rows of the first pass, then the scores (into LDS when they fit) and
-    // their maximum (order-free: the scores are finite or flagged)
-    dma_v_slice(vs4, vc, off, 0, pos, kv_dim);
+    if (wave == 1) {
+        // the V rows of each pass into LDS, 8 rows of 128 bytes per instruction (lane l:
+        // piece l % 8 of row l / 8; rows past pos clamped), between the barriers that
+        // hand the rows to wave 0 and take them back
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
+        for (uint32_t t0 = 0; t0 <= pos; t0 += kPvRows) {
+            if (t0 > 0)
+                __builtin_amdgcn_s_barrier();  // wave 0 is done with the previous rows
+            const uint32_t rows = min(pos + 1u - t0, kPvRows);
+            for (uint32_t r0 = 0; r0 < rows; r0 += 8u) {
+                const uint32_t t = min(t0 + r0 + (lane >> 3), pos);
+                dma16(vc + (size_t)t * kv_dim + off + 4u * (lane & 7u), base + r0 * kPvSlice * 4u);
+            }
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+            __builtin_amdgcn_s_barrier();         // the rows are in LDS
+        }
+        return;
+    }
+
+    // wave 0: the scores into LDS when they fit, and their maximum (order-free: finite
+    // or flagged)
     if (lane < 32u)
         exp_tab[lane] = kExp2Table[lane];
     float mx = -INFINITY;
-    for (uint32_t t = lane; t <= pos; t += 64u) {
-        const float x = sc[t];
-        if (in_lds)
-            p[t] = x;
-        mx = x > mx ? x : mx;
+    for (uint32_t t0 = 0; t0 <= pos; t0 += 64u * kBatch) {
+        float x[kBatch];
+#pragma unroll
+        for (uint32_t c = 0; c < kBatch; ++c)
+            x[c] = sc[min(t0 + 64u * c + lane, pos)];
+#pragma unroll
+        for (uint32_t c = 0; c < kBatch; ++c) {
+            const uint32_t t = t0 + 64u * c + lane;
+            if (t <= pos) {
+                if (in_lds)
+                    p[t] = x[c];
+                mx = x[c] > mx ? x[c] : mx;
+            }
+        }
     }
     const float maximum = __ockl_wfred_max_f32(mx);
     wave_lds_sync();
 
-    // expf(score - max) and their sum in position order; in LDS +0 pads the terms to a
+    // expf(score - max) and their sum in position order; +0 pads the terms to a
     // multiple of 64 (adding +0 to this sum of non-negative terms changes nothing)
     float sum = 0.0f;
     if (in_lds) {
@@ -535,7 +553,6 @@ __global__ __launch_bounds__(64) void k_attn_pv(const float* __restrict__ scores
         wave_lds_sync();
         sum = sum_lds_in_order(p, padded);
     } else {
-        // 64 terms at a time through p (unused otherwise), each step padded with +0
         for (uint32_t t0 = 0; t0 <= pos; t0 += 64u) {
             p[lane] = t0 + lane <= pos ? bnne_expf_libc(sc[t0 + lane] - maximum, exp_tab) : 0.0f;
             wave_lds_sync();
@@ -543,49 +560,64 @@ __global__ __launch_bounds__(64) void k_attn_pv(const float* __restrict__ scores
             wave_lds_sync();
         }
     }
+    // a failed softmax is flagged; the wave still runs its barriers (y is then unused)
     if (!(sum > 0.0f) || !isfinite(sum)) {
         if (lane == 0)
             set_error_first(err, code_base + 4 + 2 * (int)h);
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no LDS DMA outlives the workgroup
-        return;
     }
     if (in_lds) {
         for (uint32_t t = lane; t <= pos; t += 64u)
             p[t] = p[t] / sum;
     }
 
-    // value[i] = sum over t in order of p[t] * V[t][i], lane i < 32 of the slice
+    // value[i] = sum over t in order of p[t] * V[t][i] (lane i < 32 of the slice) per
+    // pass of V rows; the next 8 rows' reads are issued before the current 8 are added
     float acc = 0.0f;
     for (uint32_t t0 = 0; t0 <= pos; t0 += kPvRows) {
-        if (t0 > 0) {
-            wave_lds_sync();  // every lane is done with the previous rows
-            dma_v_slice(vs4, vc, off, t0, pos, kv_dim);
-        }
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the wave's V pieces have landed
-        wave_lds_sync();
         const uint32_t n = min(kPvRows, pos + 1u - t0);
+        if (t0 > 0)
+            __builtin_amdgcn_s_barrier();  // the previous rows are read: wave 1 may reload
+        if (!in_lds) {                     // this pass's probabilities
+            for (uint32_t r = lane; r < n; r += 64u)
+                p[r] = bnne_expf_libc(sc[t0 + r] - maximum, exp_tab) / sum;
+        }
+        wave_lds_sync();
+        __builtin_amdgcn_s_barrier();  // the rows are in LDS
         if (lane < kPvSlice) {
+            const float4* pp = reinterpret_cast<const float4*>(in_lds ? p + t0 : p);
+            const float* vl = vs + lane;
+            float4 pa0 = pp[0], pa1 = pp[1];
+            float va[8];
+#pragma unroll
+            for (uint32_t c = 0; c < 8; ++c)
+                va[c] = vl[c * kPvSlice];
             uint32_t r = 0;
-            if (in_lds) {
-                for (; r + 8u <= n; r += 8u) {
-                    float p8[8], v8[8];
+#pragma unroll 2
+            for (; r + 8u <= n; r += 8u) {
+                const float4 pb0 = pp[(r + 8u) / 4u], pb1 = pp[(r + 8u) / 4u + 1u];
+                float vb[8];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        p8[i] = p[t0 + r + i];
-                        v8[i] = vs[(r + i) * kPvSlice + lane];
-                    }
+                for (uint32_t c = 0; c < 8; ++c)
+                    vb[c] = vl[(r + 8u + c) * kPvSlice];
+                acc = acc + pa0.x * va[0];
+                acc = acc + pa0.y * va[1];
+                acc = acc + pa0.z * va[2];
+                acc = acc + pa0.w * va[3];
+                acc = acc + pa1.x * va[4];
+                acc = acc + pa1.y * va[5];
+                acc = acc + pa1.z * va[6];
+                acc = acc + pa1.w * va[7];
+                pa0 = pb0;
+                pa1 = pb1;
 #pragma unroll
-                    for (int i = 0; i < 8; ++i)
-                        acc = acc + p8[i] * v8[i];
-                }
-                for (; r < n; ++r)
-                    acc = acc + p[t0 + r] * vs[r * kPvSlice + lane];
-            } else {
-                for (; r < n; ++r) {
-                    const float pr = bnne_expf_libc(sc[t0 + r] - maximum, exp_tab) / sum;
-                    acc = acc + pr * vs[r * kPvSlice + lane];
-                }
+                for (uint32_t c = 0; c < 8; ++c)
+                    va[c] = vb[c];
             }
+            const float pr[8] = {pa0.x, pa0.y, pa0.z, pa0.w, pa1.x, pa1.y, pa1.z, pa1.w};
+#pragma unroll
+            for (uint32_t c = 0; c < 7; ++c)
+                if (r + c < n)
+                    acc = acc + pr[c] * va[c];
         }
     }
     if (lane < kPvSlice)
@@ -1026,7 +1058,7 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
                                k_norm + (size_t)l * HD, r->rope_cos + (size_t)pos * half,
                                r->rope_sin + (size_t)pos * half, r->kc + cache_layer, r->vc + cache_layer, pos,
                                r->kv_dim, scale, r->scores, r->n_ctx, r->err, (int)l * code_span(r));
-            hipLaunchKernelGGL(k_attn_pv, dim3(r->H, HD / kPvSlice), dim3(64), 0, r->stream, r->scores,
+            hipLaunchKernelGGL(k_attn_pv, dim3(r->H, HD / kPvSlice), dim3(128), 0, r->stream, r->scores,
                                r->vc + cache_layer, r->H / r->Hk, pos, r->kv_dim, r->n_ctx, r->y, r->err,
                                (int)l * code_span(r));
             launch(r->attn_out[l]);
