@@ -47,6 +47,7 @@ __device__ __forceinline__ void fstore(float* p, float v) { *(__attribute__((add
 
 extern "C" __device__ uint32_t __ockl_wfred_max_u32(uint32_t);
 extern "C" __device__ double __ockl_wfred_add_f64(double);
+extern "C" __device__ int __ockl_wfred_add_i32(int);
 
 // popc(x) + acc and (c << SHIFT) + acc as single instructions (the compiler would
 // otherwise re-associate the chains)
@@ -515,15 +516,14 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     uint64_t masks[2][8];  // GPW == 1: the planes of group `wave`
     int neg_sum[GPW];
     if constexpr (GPW == 1) {
-        neg_sum[0] = 0;
+        // -sum(Q) as a wave reduction (the 16 waves' scalar popcount chains would share one
+        // scalar unit)
+        neg_sum[0] = -__ockl_wfred_add_i32(q[0] + q[1]);
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int b = 0; b < 8; ++b) {
+            for (int b = 0; b < 8; ++b)
                 masks[h][b] = __ballot((q[h] >> b) & 1);
-                const int cnt = __popcll(masks[h][b]);
-                neg_sum[0] -= b == 7 ? -(cnt << 7) : (cnt << b);
-            }
     } else {
 #pragma unroll
         for (int gi = 0; gi < GPW; ++gi) {
