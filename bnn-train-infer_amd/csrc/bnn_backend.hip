@@ -762,7 +762,8 @@ struct BatchPlan {
     uint64_t prep_blocks = 0, dot_items_total = 0;
     size_t scratch_bytes = 0;
     uint32_t max_groups = 0;
-    // tables: PrepJob[count] | DotJob[count] | prep block->job | dot item->job (non-uniform only)
+    // tables: PrepJob[count] | DotJob[count] | prep block->job (unless one row per job) |
+    // dot item->job (non-uniform only)
     size_t prep_tab = 0, dot_tab = 0, prep_map = 0, dot_map = 0, tables = 0;
     ~BatchPlan() { free(plans); }
 };
@@ -817,7 +818,7 @@ BNN_Status plan_batch(BNN_Device device, const BNN_Job* jobs, uint32_t count, Ba
     if (st == BNN_OK) {
         bp->prep_tab = round_up(sizeof(PrepJob) * count, 256);
         bp->dot_tab = round_up(sizeof(DotJob) * count, 256);
-        bp->prep_map = round_up(4u * bp->prep_blocks, 256);
+        bp->prep_map = bp->prep_blocks == count ? 0 : round_up(4u * bp->prep_blocks, 256);
         bp->dot_map = bp->uniform ? 0 : round_up(4u * bp->dot_items_total, 256);
         bp->tables = bp->prep_tab + bp->dot_tab + bp->prep_map + bp->dot_map;
     }
@@ -842,8 +843,9 @@ void fill_batch_tables(const BatchPlan& bp, const BNN_Job* jobs, unsigned char* 
         soff += row_scratch_bytes(p, rows, &a, &b, &c);
         hd[i] = make_dot(p, hp[i], p.out_base, p.out_stride);
         hd[i].first_block = di;
-        for (uint32_t r = 0; r < rows; ++r)
-            hpm[pb++] = i;
+        for (uint32_t r = 0; r < rows; ++r, ++pb)
+            if (bp.prep_map)
+                hpm[pb] = i;
         const uint32_t items = dot_items(p.m->tiles, rows, bp.max_groups);
         if (!bp.uniform)
             for (uint32_t r = 0; r < items; ++r)
@@ -858,11 +860,13 @@ hipError_t launch_batch(BNN_Device device, const unsigned char* tables, size_t p
                         uint32_t max_groups, uint64_t seq) {
     const PrepJob* dp = reinterpret_cast<const PrepJob*>(tables);
     const DotJob* dd = reinterpret_cast<const DotJob*>(tables + prep_tab);
-    const uint32_t* dpm = reinterpret_cast<const uint32_t*>(tables + prep_tab + dot_tab);
+    // no map (prep_map == 0) when every job has one row: prep block b is job b
+    const uint32_t* dpm = prep_map ? reinterpret_cast<const uint32_t*>(tables + prep_tab + dot_tab) : nullptr;
     const uint32_t* ddm =
         uniform_items ? nullptr : reinterpret_cast<const uint32_t*>(tables + prep_tab + dot_tab + prep_map);
     hipError_t e = timed(device, KK_PREP, [&] {
-        return launch_prep_batch(device->stream, dp, dpm, prep_blocks, seq, device->flag_dev, device->status_host);
+        return launch_prep_batch(device->stream, dp, dpm, prep_blocks, max_groups, seq, device->flag_dev,
+                                 device->status_host);
     });
     if (e == hipSuccess)
         e = timed(device, KK_DOT, [&] {

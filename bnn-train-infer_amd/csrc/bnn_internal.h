@@ -153,7 +153,8 @@ uint32_t dot_items(uint32_t tiles, uint32_t rows, uint32_t max_groups);
 // Dot: items = sum of rows*tiles; job of an item = item / uniform_items when every
 // job has that many items, else item_job[item].
 hipError_t launch_prep_batch(hipStream_t stream, const PrepJob* jobs, const uint32_t* block_job,
-                             uint32_t blocks, uint64_t seq, uint64_t* flag, uint64_t* host_status);
+                             uint32_t blocks, uint32_t max_groups, uint64_t seq, uint64_t* flag,
+                             uint64_t* host_status);
 hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32_t* item_job, uint32_t items,
                             uint32_t uniform_items, uint32_t max_groups, uint32_t cu_count, uint64_t seq,
                             const uint64_t* flag);
