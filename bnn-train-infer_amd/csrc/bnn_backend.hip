@@ -639,6 +639,30 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
     if (st != BNN_OK)
         return st;
 
+    // One GEMV_F32 row (the reference engine's only call, linear.c:169-200): the row is
+    // checked, quantised and multiplied in one launch of the fused kernel, read straight
+    // from the input view -- no scratch, no second launch.
+    if (job->operation == BNN_OP_GEMV_F32 && p.in_aligned && p.out_aligned && p.m->k <= kFusedMaxWidth &&
+        p.m->k % kGroup == 0) {
+        if (hipSetDevice(device->ordinal) != hipSuccess)
+            return BNN_EIO;
+        FusedArgs fa = {};
+        fa.jobs = nullptr;
+        fa.njobs = 1;
+        fa.kind = PRE_ROW;
+        fa.width = p.m->k;
+        fa.row = reinterpret_cast<const float*>(p.in_base);
+        fa.post = POST_NONE;
+        fa.single = FusedJob{p.m->wbits, p.m->wscale, reinterpret_cast<float*>(p.out_base), p.m->n, p.m->tiles, 0, 0};
+        const uint32_t cus = device->cu_count ? device->cu_count : 256u;
+        const uint32_t grid = p.m->tiles < 2u * cus ? p.m->tiles : 2u * cus;
+        const uint64_t seq = ++device->seq;
+        const hipError_t e = timed(device, KK_DOT, [&] {
+            return launch_fused(device->stream, fa, p.m->tiles, grid, seq, device->flag_dev, device->status_host);
+        });
+        return finish(device, e, seq);
+    }
+
     // rows per launch chunk, bounded by the scratch cap
     const uint32_t rows = job->rows;
     const bool mfma = rows >= kMfmaMinRows;

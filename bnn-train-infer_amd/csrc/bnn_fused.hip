@@ -225,12 +225,18 @@ struct TileRegs {
 };
 
 // The job table, written by the host only: read through the constant address space
-// (scalar loads through the scalar cache)
+// (scalar loads through the scalar cache).  A single job (BNN_Execute) comes in the
+// kernel arguments instead (t == null), with no table in device memory.
 struct JobTable {
     const FusedJob* t;
+    const FusedJob& single;
     typedef const __attribute__((address_space(4))) FusedJob* Ptr;
-    __device__ __forceinline__ uint32_t first_tile(uint32_t i) const { return ((Ptr)t)[i].first_tile; }
+    __device__ __forceinline__ uint32_t first_tile(uint32_t i) const {
+        return t ? ((Ptr)t)[i].first_tile : single.first_tile;
+    }
     __device__ __forceinline__ FusedJob operator[](uint32_t i) const {
+        if (t == nullptr)
+            return single;
         const Ptr c = (Ptr)t;
         FusedJob j;
         j.wbits = c[i].wbits;
@@ -328,7 +334,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     // load counter completes in order: the row is needed first), arriving while the
     // row is produced
     // tiles are walked over the jobs, or over the pairs (the first half of the table)
-    const JobTable jobs{fa.jobs};
+    const JobTable jobs{fa.jobs, fa.single};
     constexpr bool paired = PAIRED;  // fa.post == POST_SILU_MUL
     const uint32_t nwalk = paired ? fa.njobs / 2u : fa.njobs, pair_step = paired ? nwalk : 0u;
     uint32_t tile = blockIdx.x, ji = 0;

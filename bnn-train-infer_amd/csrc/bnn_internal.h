@@ -123,7 +123,7 @@ struct FusedJob {
 enum PostKind : int32_t { POST_NONE = 0, POST_SILU_MUL = 1 };
 
 struct FusedArgs {
-    const FusedJob* jobs;  // device table
+    const FusedJob* jobs;  // device table, or null: the one job is `single`
     uint32_t njobs;
     int32_t kind;          // PreKind
     uint32_t width;        // K
@@ -137,6 +137,7 @@ struct FusedArgs {
     int32_t err_code;
     int32_t post;          // PostKind
     float* post_out;       // POST_SILU_MUL
+    FusedJob single;       // jobs == null (njobs == 1): the job, passed in the kernel arguments
 };
 
 // Host-side launchers (bnn_kernels.hip).  All are asynchronous on `stream`.
