@@ -427,6 +427,211 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 }
 
 // ---------------------------------------------------------------------------
+// k_gemm_pipe<MI>: F32-accumulating jobs on (32*MI) x 128 workgroup tiles (4 waves,
+// 2 x 2, each (16*MI) x 64 = MI x 4 MFMA subtiles).  K streams through LDS in
+// stages of half a group (64 bytes of every A and B row: one MFMA step), with four
+// LDS slots: stage h+3 is issued right after the barrier of stage h, so three
+// stages in flight (about 1.5 groups of compute) cover the global->LDS latency.
+//   * every wave issues the same DMAs per stage (its share of the A and B blocks,
+//     plus, for the first half of a group, its 64 columns' scales), so the wait for
+//     stage h is a fixed count of younger DMAs (vmcnt), then one barrier;
+//   * the DMA source is a uniform 64-bit base in SGPRs (advanced by K per stage)
+//     plus a per-lane offset fixed for the whole loop: no VALU work per DMA;
+//   * the epilogue of group g-1 (RN(scale * D) added in group order, as in
+//     k_gemm_big) is interleaved subtile by subtile with the first-half MFMAs of
+//     group g, which restart that subtile's integer accumulator.
+// LDS layout of a stage block: 16-byte chunk c (0..3) of row r at r*64 + 16*(c ^ ((r >> 1) & 3)):
+// the 16 lanes reading one fragment (16 rows, one chunk) are spread over the banks.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kPipeSlots = 4;
+constexpr uint32_t kHalf = 64;  // K bytes per stage
+
+__device__ __forceinline__ uint32_t swz64(uint32_t r, uint32_t c) { return r * 64u + 16u * (c ^ ((r >> 1) & 3u)); }
+
+// 16 bytes per lane from sbase + voff into LDS at lds_addr + 16 * lane (see dma16)
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
+}
+
+// vmcnt(N) and lgkmcnt(0): at most N of this wave's DMAs still in flight, and its LDS
+// reads done -- before a barrier after which other waves refill the slot it read
+template <int N>
+__device__ __forceinline__ void wait_stage() {
+    static_assert(N >= 0 && N < 16, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt(0x0070 | N);
+}
+
+template <int MI>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_pipe(
+    GemmJob j, uint32_t mtiles, uint64_t seq, const uint64_t* __restrict__ flag) {
+    constexpr uint32_t TM = 32u * MI, TN = 128u;
+    constexpr uint32_t A_BYTES = TM * kHalf, B_BYTES = TN * kHalf, SLOT = A_BYTES + B_BYTES;
+    constexpr uint32_t A_INS = A_BYTES / 1024u / 4u, B_INS = B_BYTES / 1024u / 4u;  // DMAs per wave and stage
+    constexpr int P = (int)(A_INS + B_INS);
+    static_assert(A_INS >= 1 && 2 * P + 1 < 16, "stage DMAs");
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[kPipeSlots][SLOT];
+    __shared__ __attribute__((aligned(16))) unsigned char lds_sc[4][4][128];  // [group % 4][wave]
+    if (*flag == seq)
+        return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave >> 1, wn = wave & 1u;
+    const uint32_t tile = gemm_tile_of_block(blockIdx.x, gridDim.x);
+    const uint32_t mt = tile % mtiles, nt = tile / mtiles;
+    const uint32_t m0 = mt * TM, n0 = nt * TN;
+    const uint32_t groups = j.groups, stages = 2u * groups;
+
+    // DMA instruction i of wave w fills block positions p = (w * INS + i) * 64 + lane:
+    // row p / 4, stored chunk p % 4 = logical chunk ^ ((row >> 1) & 3); A rows past
+    // the job are clamped (never stored), B rows stay below n_pad
+    uint32_t a_off[A_INS], b_off[B_INS];
+#pragma unroll
+    for (uint32_t i = 0; i < A_INS; ++i) {
+        const uint32_t p = (wave * A_INS + i) * 64u + lane, r = p >> 2;
+        const uint32_t c = (p & 3u) ^ ((r >> 1) & 3u);
+        a_off[i] = (min(m0 + r, j.rows - 1u) - m0) * j.k + 16u * c;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < B_INS; ++i) {
+        const uint32_t p = (wave * B_INS + i) * 64u + lane, r = p >> 2;
+        const uint32_t c = (p & 3u) ^ ((r >> 1) & 3u);
+        b_off[i] = r * j.k + 16u * c;
+    }
+    const uint8_t* a_base = reinterpret_cast<const uint8_t*>(j.q) + (size_t)m0 * j.k;
+    const uint8_t* b_base = reinterpret_cast<const uint8_t*>(j.wbytes) + (size_t)n0 * j.k;
+    // this wave's 64 columns' scales: one 64-feature tile of the scale layout (clamped
+    // into the array for columns past the last tile; those are never stored)
+    const uint32_t stile = min((n0 + wn * 64u) >> 6, j.tiles - 1u);
+    const uint8_t* sc_base = reinterpret_cast<const uint8_t*>(j.wscale) + (size_t)stile * groups * 128u;
+    const uint32_t lds0 = lds_offset(lds);
+    const uint32_t lds_sc0 = lds_offset(lds_sc) + wave * 128u;
+    // stage h (h past the last stage reloads the last one into a free slot: every
+    // stage issues the same DMAs, so the wait counts are the same throughout)
+    auto issue = [&](uint32_t h, bool first_half) {
+        const uint32_t hs = min(h, stages - 1u);
+        const uint32_t koff = (hs >> 1) * kGroup + (hs & 1u) * kHalf;
+        const uint32_t slot = lds0 + (h % kPipeSlots) * SLOT;
+#pragma unroll
+        for (uint32_t i = 0; i < A_INS; ++i)
+            dma16s(a_base + koff, a_off[i], slot + (wave * A_INS + i) * 1024u);
+#pragma unroll
+        for (uint32_t i = 0; i < B_INS; ++i)
+            dma16s(b_base + koff, b_off[i], slot + A_BYTES + (wave * B_INS + i) * 1024u);
+        if (first_half && lane < 8u)
+            dma16s(sc_base + (size_t)(hs >> 1) * 128u, 16u * lane, lds_sc0 + ((h >> 1) & 3u) * 512u);
+    };
+
+    float acc[MI][4][4];
+    v4i d[MI][4];
+    const v4i c_init = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            d[mi][ni] = c_init;  // with scale 0 the first epilogue adds +0
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mi][ni][r] = 0.0f;
+        }
+    float sc_prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    issue(0, true);
+    issue(1, false);
+    issue(2, true);
+
+    const uint32_t arow0 = wm * 16u * MI + (lane & 15u), brow0 = wn * 64u + (lane & 15u);
+    const uint32_t chunk = lane >> 4;
+    for (uint32_t g = 0; g < groups; ++g) {
+        // ---- first half of group g (stage 2g): stages 2g+1 and 2g+2 stay in flight
+        wait_stage<2 * P + 1>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue(2u * g + 3u, false);
+        const unsigned char* blk = lds[(2u * g) % kPipeSlots];
+        const uint16_t* scl = reinterpret_cast<const uint16_t*>(lds_sc[g & 3u][wave]);
+        float sc_cur[4];
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+            sc_cur[ni] = __half2float(__ushort_as_half(scl[16u * ni + (lane & 15u)]));
+        v4i a[MI], b[4];
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+            a[mi] = *reinterpret_cast<const v4i*>(blk + swz64(arow0 + 16u * mi, chunk));
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+            b[ni] = *reinterpret_cast<const v4i*>(blk + A_BYTES + swz64(brow0 + 16u * ni, chunk));
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            const float sc = sc_prev[ni];
+            const float cneg = sc * -kMagicValue;  // exact
+#pragma unroll
+            for (int mi = 0; mi < MI; ++mi) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc, __int_as_float(d[mi][ni][r]), cneg);
+                d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], c_init, 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, MI + 8, 0);
+#pragma unroll
+        for (int i = 0; i < 4 * MI; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        // ---- second half (stage 2g+1): stages 2g+2 and 2g+3 stay in flight
+        wait_stage<2 * P + 1>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        issue(2u * g + 4u, true);
+        blk = lds[(2u * g + 1u) % kPipeSlots];
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+            a[mi] = *reinterpret_cast<const v4i*>(blk + swz64(arow0 + 16u * mi, chunk));
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+            b[ni] = *reinterpret_cast<const v4i*>(blk + A_BYTES + swz64(brow0 + 16u * ni, chunk));
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int mi = 0; mi < MI; ++mi)
+                d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], d[mi][ni], 0, 0, 0);
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+            sc_prev[ni] = sc_cur[ni];
+    }
+    // no DMA may still be writing this workgroup's LDS when it ends
+    wait_stage<0>();
+    // epilogue of the last group, then store Z (or Z * s)
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) {
+        const float sc = sc_prev[ni];
+        const float cneg = sc * -kMagicValue;
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc, __int_as_float(d[mi][ni][r]), cneg);
+    }
+    const uint32_t ncol0 = n0 + wn * 64u + (lane & 15u);
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + wm * 16u * MI + 16u * mi + 4u * (lane >> 4) + r;
+            if (m >= j.rows)
+                continue;
+            const float s = j.mode == MODE_SUM_SCALED ? j.rscale[m] : 1.0f;
+            float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const uint32_t n = ncol0 + 16u * ni;
+                if (n < j.n)
+                    orow[n] = j.mode == MODE_SUM_SCALED ? acc[mi][ni][r] * s : acc[mi][ni][r];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // k_gemm_ks: F32-accumulating jobs too small to give every CU a 128 x 128 tile.
 // Workgroup tile (16*TMS) x (16*TNS); the W waves split the K dimension instead of
 // the tile: wave w computes groups w, w+W, w+2W, ... for the whole tile, with its
@@ -633,6 +838,9 @@ hipError_t launch_expand(hipStream_t stream, const uint4* wbits, uint32_t tiles,
 #ifndef BNN_GEMM_KS
 #define BNN_GEMM_KS 0  // tuning: TMS TNS W DEPTH (four digits) forces k_gemm_ks with that shape
 #endif
+#ifndef BNN_GEMM_PIPE
+#define BNN_GEMM_PIPE 1  // k_gemm_pipe for F32-accumulating jobs with enough 128 x 128 or 64 x 128 tiles
+#endif
 #ifndef BNN_GEMM_BIG
 #define BNN_GEMM_BIG 1  // k_gemm_big for F32-accumulating jobs with a 128 x 128 tile per CU
 #endif
@@ -642,6 +850,16 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
     auto blocks = [&](uint32_t tm, uint32_t tn) {
         return (uint64_t)((job.rows + tm - 1u) / tm) * ((job.n + tn - 1u) / tn);
     };
+#if BNN_GEMM_PIPE
+    // 128 x 128 tiles for every CU: k_gemm_big (measured 30.9 vs 32.5 us for k_gemm_pipe<4>
+    // at 1024 x 2048 x 6144); fewer: the pipelined kernel on 64 x 128 tiles when those
+    // give most CUs one (6144 -> 2048 at 1024 rows: 35 vs 62 us for 64 x 128 k_gemm)
+    if (job.mode != MODE_DOT_I16 && blocks(128, 128) < cus && blocks(64, 128) >= cus * 3u / 4u) {
+        const uint32_t mtiles = (job.rows + 63u) / 64u, ntiles = (job.n + 127u) / 128u;
+        hipLaunchKernelGGL(k_gemm_pipe<2>, dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq, flag);
+        return hipGetLastError();
+    }
+#endif
     if (BNN_GEMM_BIG && job.mode != MODE_DOT_I16 && blocks(kBigTile, kBigTile) >= cus) {
         const uint32_t mtiles = (job.rows + kBigTile - 1u) / kBigTile;
         const uint32_t ntiles = (job.n + kBigTile - 1u) / kBigTile;
