@@ -65,6 +65,17 @@ __device__ __forceinline__ void gstore(float* p, float v) { *(__attribute__((add
 __device__ __forceinline__ void gstore(int16_t* p, int16_t v) {
     *(__attribute__((address_space(1))) int16_t*)p = v;
 }
+// 16 bytes at a 16-byte aligned address
+__device__ __forceinline__ void gstore16(int16_t* p, u32x4 v) { *(__attribute__((address_space(1))) u32x4*)p = v; }
+// eight D values (|D| <= 16256) as int16 pairs, element 2i in the low half of word i
+__device__ __forceinline__ u32x4 pack8(const int* d) {
+    u32x4 v;
+    v.x = ((uint32_t)d[0] & 0xffffu) | ((uint32_t)d[1] << 16);
+    v.y = ((uint32_t)d[2] & 0xffffu) | ((uint32_t)d[3] << 16);
+    v.z = ((uint32_t)d[4] & 0xffffu) | ((uint32_t)d[5] << 16);
+    v.w = ((uint32_t)d[6] & 0xffffu) | ((uint32_t)d[7] << 16);
+    return v;
+}
 
 __device__ __forceinline__ float load_f32(const unsigned char* row, uint32_t k, bool aligned) {
     if (aligned)
@@ -616,10 +627,19 @@ void k_dot_wave(const DotJob* __restrict__ jobs, const uint32_t* __restrict__ it
                 dv[g] = group_dot_v(w[g], lp + g * (kPlaneWords / 4), -__shfl(sum, g));
         }
         int16_t* o = reinterpret_cast<int16_t*>(orow) + (size_t)(n0 + lane) * groups;
+        if (live && !failed) {
+            if (groups % 8u == 0 && ((uintptr_t)o & 15u) == 0) {
+                // the lane's groups are contiguous: 16-byte stores of 8 D values each
 #pragma unroll
-        for (int g = 0; g < kWaveMaxGroups; ++g) {
-            if ((uint32_t)g < groups && live && !failed)
-                gstore(o + g, (int16_t)dv[g]);
+                for (int c = 0; c < kWaveMaxGroups / 8; ++c)
+                    if ((uint32_t)(8 * c) < groups)
+                        gstore16(o + 8 * c, pack8(dv + 8 * c));
+            } else {
+#pragma unroll
+                for (int g = 0; g < kWaveMaxGroups; ++g)
+                    if ((uint32_t)g < groups)
+                        gstore(o + g, (int16_t)dv[g]);
+            }
         }
     }
 }
@@ -684,21 +704,28 @@ void k_dot_wave_long(const DotJob* __restrict__ jobs, const uint32_t* __restrict
     const bool store = live && !failed;
     int16_t* od = reinterpret_cast<int16_t*>(orow) + (size_t)(n0 + lane) * groups;
     float acc = 0.0f;
+    // DOT_GROUPS: a block's 8 D values are one 16-byte store when the lane's row is aligned
+    const bool packed = groups % 8u == 0 && ((uintptr_t)od & 15u) == 0;
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
         if (blk + 1 < NB)
             load_block((blk + 1) & 1, blk + 1);
+        int dv[kLongBlock];
 #pragma unroll
         for (int i = 0; i < kLongBlock; ++i) {
             const uint32_t g = blk * kLongBlock + i;
+            dv[i] = 0;
             if (g < groups) {
                 const int d = group_dot_v(w[blk & 1][i], lp + g * (kPlaneWords / 4), -__shfl(sum, g));
+                dv[i] = d;
                 if (sum_mode)
                     acc = acc + __half2float(__ushort_as_half((uint16_t)sc[blk & 1][i])) * (float)d;
-                else if (store)
+                else if (store && !packed)
                     gstore(od + g, (int16_t)d);
             }
         }
+        if (!sum_mode && store && packed && (uint32_t)(blk * kLongBlock) < groups)
+            gstore16(od + blk * kLongBlock, pack8(dv));
     }
     if (sum_mode) {
         if (it.j.mode == MODE_SUM_SCALED)
