@@ -123,21 +123,6 @@ __device__ __forceinline__ void plane_words(int q, uint32_t& word, int& sum) {
         plane_words<B + 1>(q, word, sum);
 }
 
-// Q = clamp(round-half-away(F32(x / s)), -127, 127)  (soft-bnn-accelerator.c:197-208).
-// y = F32(x * F32(1 / s)) is within 1.6e-5 of x / s (|x / s| <= 127) and F32(x / s)
-// within 3.9e-6, so both round to the same integer unless y lies within 2^-14 of a
-// half-integer; those lanes (and all, when s is subnormal: `exact`) divide.
-__device__ __forceinline__ int f_quantize(float x, float s, float rcp, bool exact) {
-    float y = x * rcp;
-    float t = truncf(y), d = y - t;
-    if (exact || fabsf(fabsf(d) - 0.5f) < 0x1p-14f) {
-        y = x / s;
-        t = truncf(y);
-        d = y - t;
-    }
-    const float q = t + (fabsf(d) >= 0.5f ? copysignf(1.0f, y) : 0.0f);
-    return (int)fminf(fmaxf(q, -127.0f), 127.0f);
-}
 
 // The sum of the squares in index order, s_{i+1} = F32(s_i + t_i) from s_0 = +0,
 // evaluated in segments of kSegment terms.  Segment j is run from kWindow candidate
@@ -518,7 +503,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     int q[EPT];
 #pragma unroll
     for (int i = 0; i < EPT; ++i)
-        q[i] = live(i) ? f_quantize(xv[i], s, rcp, exact) : 0;
+        q[i] = live(i) ? quantize_rcp(xv[i], s, rcp, exact) : 0;
     uint64_t masks[2][8];  // GPW == 1: the planes of group `wave`
     int neg_sum[GPW];
     if constexpr (GPW == 1) {

@@ -93,14 +93,6 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
     return __uint_as_float(__ockl_wfred_max_u32(__float_as_uint(v)));
 }
 
-// Q = clamp(round-half-away(F32(x / s)), -127, 127)  (soft-bnn-accelerator.c:197-208)
-__device__ __forceinline__ int quantize(float x, float s) {
-    float y = x / s;      // correctly rounded IEEE division
-    float r = roundf(y);  // half away from zero
-    r = r > 127.0f ? 127.0f : r;
-    r = r < -127.0f ? -127.0f : r;
-    return (int)r;
-}
 
 __device__ __forceinline__ void raise_flag(uint64_t seq, uint64_t* flag, uint64_t* host_status) {
     __hip_atomic_store(flag, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -184,6 +176,8 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
         }
     }
 
+    const float rcp = 1.0f / s;
+    const bool exact = s < 0x1p-126f;  // 1 / s would overflow
     // pass 2: quantise; in iteration i wave w owns the 64 consecutive k of half (w & 1)
     // of group kPrepGroupsPerIter*i + (w >> 1)
     uint32_t* planes = j.planes ? j.planes + (size_t)m * groups * kPlaneWords : nullptr;
@@ -191,7 +185,7 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
     for (int i = 0; i < kPrepPerThread; ++i) {
         const uint32_t base = (uint32_t)kPrepThreads * i;
         if ((uint32_t)i < iters && base + wave * 64u < k_total) {  // K % 128 == 0: whole waves
-            const int q = f32 ? quantize(__int_as_float(raw[i]), s) : raw[i];
+            const int q = f32 ? quantize_rcp(__int_as_float(raw[i]), s, rcp, exact) : raw[i];
             if (j.q)
                 j.q[(size_t)m * k_total + base + tid] = (int8_t)q;
             // bit planes of these 64 values; the wave's sum follows from the same
