@@ -639,17 +639,17 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
     if (st != BNN_OK)
         return st;
 
-    // One GEMV_F32 row (the reference engine's only call, linear.c:169-200): the row is
-    // checked, quantised and multiplied in one launch of the fused kernel, read straight
-    // from the input view -- no scratch, no second launch.
-    if (job->operation == BNN_OP_GEMV_F32 && p.in_aligned && p.out_aligned && p.m->k <= kFusedMaxWidth &&
-        p.m->k % kGroup == 0) {
+    // One row of GEMV_F32 (the reference engine's only call, linear.c:169-200), GEMV or
+    // DOT_GROUPS: the row is checked, quantised (F32) and multiplied in one launch of the
+    // fused kernel, read straight from the input view -- no scratch, no second launch.
+    if (job->rows == 1 && p.in_aligned && p.out_aligned && p.m->k <= kFusedMaxWidth && p.m->k % kGroup == 0) {
         if (hipSetDevice(device->ordinal) != hipSuccess)
             return BNN_EIO;
         FusedArgs fa = {};
         fa.jobs = nullptr;
         fa.njobs = 1;
-        fa.kind = PRE_ROW;
+        fa.kind = p.f32_in ? PRE_ROW : PRE_ROW_I8;
+        fa.dot_out = p.dot_out ? 1 : 0;
         fa.width = p.m->k;
         fa.row = reinterpret_cast<const float*>(p.in_base);
         fa.post = POST_NONE;

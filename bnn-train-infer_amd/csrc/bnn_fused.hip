@@ -327,10 +327,18 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
         ++ji;
     FusedJob job = jobs[ji], job2 = jobs[ji + pair_step];
     const float* src_a = fa.kind == PRE_ROW ? fa.row : fa.a;
+    const bool int_row = fa.kind == PRE_ROW_I8;
     float xv[EPT], bv[EPT], gv[EPT];
+    if (int_row) {  // int8 values, exact in binary32
+        const int8_t* src8 = reinterpret_cast<const int8_t*>(fa.row);
 #pragma unroll
-    for (int i = 0; i < EPT; ++i)
-        xv[i] = fload(src_a + min(elem(i), K - 1u));
+        for (int i = 0; i < EPT; ++i)
+            xv[i] = (float)(int)*(const __attribute__((address_space(1))) int8_t*)(src8 + min(elem(i), K - 1u));
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPT; ++i)
+            xv[i] = fload(src_a + min(elem(i), K - 1u));
+    }
     if (fa.b) {
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
@@ -464,14 +472,16 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
         }
     }
 
-    // 3. the GEMV_F32 input check and the row scale, in one exchange: a wave with a
-    // non-finite value posts the all-ones word (above every finite |x| bit pattern)
+    // 3. the input check and the row scale, in one exchange: a wave with an illegal
+    // value (non-finite; -128 in an int8 row: soft-bnn-accelerator.c:278-308) posts the
+    // all-ones word (above every finite |x| bit pattern)
     uint32_t abits = 0;
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         if (live(i)) {
             const uint32_t a = __float_as_uint(xv[i]) & 0x7fffffffu;
-            abits = max(abits, a < 0x7f800000u ? a : 0xffffffffu);
+            const bool bad = int_row ? xv[i] == -128.0f : a >= 0x7f800000u;
+            abits = max(abits, bad ? 0xffffffffu : a);
         }
     }
     abits = __ockl_wfred_max_u32(abits);
@@ -489,7 +499,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     }
     float amax = __uint_as_float(abits);
     float s = 1.0f;
-    if (amax != 0.0f) {
+    if (amax != 0.0f && !int_row) {
         s = amax / 127.0f;
         if (s == 0.0f)
             s = __int_as_float(1);  // smallest subnormal
@@ -503,7 +513,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     int q[EPT];
 #pragma unroll
     for (int i = 0; i < EPT; ++i)
-        q[i] = live(i) ? quantize_rcp(xv[i], s, rcp, exact) : 0;
+        q[i] = !live(i) ? 0 : int_row ? (int)xv[i] : quantize_rcp(xv[i], s, rcp, exact);
     uint64_t masks[2][8];  // GPW == 1: the planes of group `wave`
     int neg_sum[GPW];
     if constexpr (GPW == 1) {
@@ -562,11 +572,34 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
                 } else {
                     d = f_group_dot(cur.w[i], planes + g * (kPlaneWords / 4u), neg_sum[i]);
                 }
-                prod[g * 64u + lane] = __half2float(__ushort_as_half((uint16_t)cur.s[i])) * (float)d;
+                // DOT_GROUPS: D itself goes through the exchange
+                prod[g * 64u + lane] = fa.dot_out ? __int_as_float(d)
+                                                  : __half2float(__ushort_as_half((uint16_t)cur.s[i])) * (float)d;
             }
         }
         lds_barrier();
-        if (wave == 0) {
+        if (wave == 0 && fa.dot_out) {
+            // int16 D[n][g]: a lane's groups are contiguous, 16-byte stores of 8 when aligned
+            const uint32_t n = lr.row;
+            if (n < job.n) {
+                int16_t* o = reinterpret_cast<int16_t*>(job.out) + (size_t)n * G;
+                if (G % 8u == 0 && ((uintptr_t)o & 15u) == 0) {
+                    for (uint32_t g = 0; g < G; g += 8u) {
+                        uint32_t v[8];
+#pragma unroll
+                        for (int c = 0; c < 8; ++c)
+                            v[c] = (uint32_t)__float_as_int(prod[(g + c) * 64u + lane]) & 0xffffu;
+                        const u32x4 w = {v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
+                                         v[6] | (v[7] << 16)};
+                        *(__attribute__((address_space(1))) u32x4*)(o + g) = w;
+                    }
+                } else {
+                    for (uint32_t g = 0; g < G; ++g)
+                        *(__attribute__((address_space(1))) int16_t*)(o + g) =
+                            (int16_t)__float_as_int(prod[g * 64u + lane]);
+                }
+            }
+        } else if (wave == 0) {
             const uint32_t n = lr.row;
             float acc = 0.0f;
             uint32_t g = 0;

@@ -107,7 +107,9 @@ constexpr uint32_t kMfmaMinRows = BNN_MFMA_MIN_ROWS;
 // Fused batches (bnn_fused.hip): GEMV_F32 jobs sharing one input row produced on
 // the device by a pre-operation.  One entry per job; the job's tiles are the
 // workgroups first_tile .. first_tile + tiles - 1 of the launch.
-enum PreKind : int32_t { PRE_ROW = 0, PRE_RMSNORM = 1, PRE_SILU_MUL = 2 };
+// PRE_ROW_I8: the row is int8 (GEMV / DOT_GROUPS input: checked for -128, used as Q
+// with row scale 1; single jobs only)
+enum PreKind : int32_t { PRE_ROW = 0, PRE_RMSNORM = 1, PRE_SILU_MUL = 2, PRE_ROW_I8 = 3 };
 constexpr uint32_t kFusedMaxWidth = 6144;  // K of a fused batch (LDS holds the whole row)
 
 struct FusedJob {
@@ -138,6 +140,7 @@ struct FusedArgs {
     int32_t post;          // PostKind
     float* post_out;       // POST_SILU_MUL
     FusedJob single;       // jobs == null (njobs == 1): the job, passed in the kernel arguments
+    int32_t dot_out;       // DOT_GROUPS: out receives int16 D[n][group] instead of the sums
 };
 
 // Host-side launchers (bnn_kernels.hip).  All are asynchronous on `stream`.

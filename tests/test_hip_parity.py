@@ -211,34 +211,43 @@ def test_two_devices_are_isolated(pkg, hip):
     b.close()
 
 
+@pytest.mark.parametrize("op", ["GEMV_F32", "GEMV", "DOT_GROUPS"])
 @pytest.mark.parametrize("k", [128, 1152, 6144, 6272, 8192])
-def test_single_row_gemv_f32_both_paths(pkg, hipdev, oracle, k):
-    """BNN_Execute GEMV_F32 with one row: K <= 6144 runs as one fused launch, wider rows as
-    prep + dot.  Both against the oracle on ragged tile counts, with outliers and a row of
-    one non-zero value; a non-finite input is ERANGE with the output left untouched."""
+def test_single_row_both_paths(pkg, hipdev, oracle, k, op):
+    """BNN_Execute with one row: K <= 6144 runs as one fused launch, wider rows as prep +
+    dot.  Both against the oracle on ragged tile counts, with outliers and a row of one
+    non-zero value; an illegal input (Inf; -128 for int8 rows) is ERANGE with the output
+    left untouched, and the next call succeeds."""
     rng = np.random.default_rng(k)
+    f32 = op == "GEMV_F32"
+    in_t, out_t = pkg.api.OP_TYPES[pkg.Op[op]]
     for n in (1, 65, 8192):
-        print(f"k={k} n={n}", flush=True)
+        print(f"{op} k={k} n={n}", flush=True)
         bits, scales = pkg.synth.matrix(n, k, seed=k + n)
-        x = pkg.synth.normal_f32(3, k, seed=k)
-        x[0, rng.integers(0, k, 8)] *= 20.0
-        x[1] = 0.0
-        x[1, k // 2] = -3.5
+        if f32:
+            x = pkg.synth.normal_f32(3, k, seed=k)
+            x[0, rng.integers(0, k, 8)] *= 20.0
+            x[1] = 0.0
+            x[1, k // 2] = -3.5
+        else:
+            x = pkg.synth.int8_uniform(3, k, seed=k)
+            x[1] = 0
+            x[1, k // 2] = -127
+        out_bytes = n * (k // 128) * 2 if op == "DOT_GROUPS" else 4 * n
         with pkg.Device(oracle, 0) as odev:
             mh, mo = hipdev.matrix(bits, scales), odev.matrix(bits, scales)
             try:
                 for r in range(3):
-                    got = hipdev.run(pkg.Op.GEMV_F32, mh, x[r:r + 1])
-                    want = odev.run(pkg.Op.GEMV_F32, mo, x[r:r + 1])
-                    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (k, n, r)
+                    got = hipdev.run(pkg.Op[op], mh, x[r:r + 1])
+                    want = odev.run(pkg.Op[op], mo, x[r:r + 1])
+                    assert got.tobytes() == want.tobytes(), (op, k, n, r)
                 bad = x[:1].copy()
-                bad[0, k - 1] = np.inf
-                bi, bo = hipdev.buffer(bad.nbytes), hipdev.buffer(4 * n)
+                bad[0, k - 1] = np.inf if f32 else -128
+                bi, bo = hipdev.buffer(bad.nbytes), hipdev.buffer(out_bytes)
                 try:
                     bi.write(bad)
-                    bo.write(np.full(4 * n, 0x5A, np.uint8))
-                    job = pkg.Job(int(pkg.Op.GEMV_F32), mh.handle.value, bi.view(pkg.Type.F32),
-                                  bo.view(pkg.Type.F32), 1)
+                    bo.write(np.full(out_bytes, 0x5A, np.uint8))
+                    job = pkg.Job(int(pkg.Op[op]), mh.handle.value, bi.view(in_t), bo.view(out_t), 1)
                     assert hipdev.execute(job) == pkg.Status.ERANGE
                     assert np.all(bo.read() == 0x5A)
                     bi.write(x[:1])
