@@ -38,6 +38,12 @@ constexpr int kMagicBits = 0x4B400000;     // bit pattern of 12582912.0f = 1.5 *
 constexpr float kMagicValue = 12582912.0f;
 constexpr int kPitch = 144;                // LDS bytes per staged row: 128 + 16 (bank spread)
 
+// Output elements as nontemporal stores: written once, not kept dirty in the L2s for
+// the end-of-kernel release to write back.
+__device__ __forceinline__ void store_out(float* p, float v) {
+    __builtin_nontemporal_store(v, (__attribute__((address_space(1))) float*)p);
+}
+
 __device__ __forceinline__ u32x4 gload16(const void* p) {
     return *(const __attribute__((address_space(1))) u32x4*)p;
 }
@@ -221,7 +227,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmJob j, uint32_t mtiles, uint64
             for (int ni = 0; ni < NS; ++ni) {
                 const uint32_t n = lane_n0 + 16u * ni;
                 if (n < j.n)
-                    orow[n] = j.mode == MODE_SUM_SCALED ? acc[mi][ni][r] * s : acc[mi][ni][r];
+                    store_out(orow + n, j.mode == MODE_SUM_SCALED ? acc[mi][ni][r] * s : acc[mi][ni][r]);
             }
         }
     }
@@ -420,7 +426,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int ni = 0; ni < 4; ++ni) {
                 const uint32_t n = ncol0 + 16u * ni;
                 if (n < j.n)
-                    orow[n] = j.mode == MODE_SUM_SCALED ? acc[mi][ni][r] * s : acc[mi][ni][r];
+                    store_out(orow + n, j.mode == MODE_SUM_SCALED ? acc[mi][ni][r] * s : acc[mi][ni][r]);
             }
         }
     }
@@ -625,7 +631,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int ni = 0; ni < 4; ++ni) {
                 const uint32_t n = ncol0 + 16u * ni;
                 if (n < j.n)
-                    orow[n] = j.mode == MODE_SUM_SCALED ? acc[mi][ni][r] * s : acc[mi][ni][r];
+                    store_out(orow + n, j.mode == MODE_SUM_SCALED ? acc[mi][ni][r] * s : acc[mi][ni][r]);
             }
         }
     }
@@ -792,7 +798,7 @@ __global__ __launch_bounds__(64 * W) void k_gemm_ks(GemmJob j, uint32_t mtiles, 
             if (m >= j.rows || n >= j.n)
                 continue;
             float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
-            orow[n] = j.mode == MODE_SUM_SCALED ? acc[i][r] * j.rscale[m] : acc[i][r];
+            store_out(orow + n, j.mode == MODE_SUM_SCALED ? acc[i][r] * j.rscale[m] : acc[i][r]);
         }
     }
 }
