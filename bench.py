@@ -357,8 +357,10 @@ def main():
         copy_calibration()
         return
     if args.gpus != 1:
-        print("bench.py: this build runs on exactly one GPU (the BNN_* path has no multi-GPU form here; "
-              "see DESIGN.md for how it would shard).", file=sys.stderr)
+        print("bench.py: this build runs on exactly one GPU. The BNN_* path has no multi-GPU form here: "
+              "it would shard on output features (each matrix chunk on its own GPU, the input row "
+              "broadcast and the outputs gathered, no floating-point reduction across GPUs).",
+              file=sys.stderr)
         sys.exit(2)
 
     pkg = load_pkg()
