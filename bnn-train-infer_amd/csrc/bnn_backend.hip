@@ -28,6 +28,8 @@ using namespace bnnhip;
 namespace {
 
 constexpr size_t kPinnedCap = size_t(8) << 20;       // largest transfer staged through pinned memory
+constexpr size_t kWriteRingBytes = size_t(1) << 20;  // pinned ring for small writes
+constexpr size_t kAsyncWriteMax = size_t(64) << 10;  // writes up to this size return before the copy ends
 constexpr size_t kScratchRowsCap = 4096;              // rows per launch chunk
 constexpr size_t kScratchBytesCap = size_t(256) << 20;
 
@@ -250,6 +252,8 @@ EXPORT BNN_Status BNN_DeviceClose(BNN_Device device) {
         (void)hipFree(device->scratch);
     if (device->pinned)
         (void)hipHostFree(device->pinned);
+    if (device->wring)
+        (void)hipHostFree(device->wring);
     if (device->table_host)
         (void)hipHostFree(device->table_host);
     if (device->table_dev)
@@ -448,6 +452,37 @@ EXPORT BNN_Status BNN_BufferWrite(BNN_Buffer buffer, size_t offset, const void* 
     hipError_t e = hipSetDevice(d->ordinal);
     if (e != hipSuccess)
         return BNN_EIO;
+    if (bytes <= kAsyncWriteMax) {
+        // Small writes (a linear's input row: linear.c:169-175): the bytes are copied into
+        // the pinned ring and the host->device copy is queued on the device stream, which
+        // orders it before every later kernel, read or write of this device.  The caller's
+        // memory is free on return; the ring restarts after a synchronisation.
+        if (d->wring == nullptr) {
+            void* p = nullptr;
+            if (hipHostMalloc(&p, kWriteRingBytes, hipHostMallocDefault) != hipSuccess) {
+                (void)hipGetLastError();
+                return BNN_ENOMEM;
+            }
+            d->wring = static_cast<unsigned char*>(p);
+            d->wring_off = 0;
+        }
+        if (d->wring_off + bytes > kWriteRingBytes) {
+            if (hipStreamSynchronize(d->stream) != hipSuccess) {
+                (void)hipGetLastError();
+                return BNN_EIO;
+            }
+            d->wring_off = 0;
+        }
+        unsigned char* slot = d->wring + d->wring_off;
+        memcpy(slot, src, bytes);
+        e = hipMemcpyAsync(buffer->dev + offset, slot, bytes, hipMemcpyHostToDevice, d->stream);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return BNN_EIO;
+        }
+        d->wring_off += round_up(bytes, 256);
+        return BNN_OK;
+    }
     if (bytes <= kPinnedCap && ensure_pinned(d, bytes) == BNN_OK) {
         memcpy(d->pinned, src, bytes);
         e = hipMemcpyAsync(buffer->dev + offset, d->pinned, bytes, hipMemcpyHostToDevice, d->stream);

@@ -210,6 +210,8 @@ struct bnn_accel_device {
     size_t scratch_bytes;
     unsigned char* pinned;     // grow-only pinned host staging for transfers
     size_t pinned_bytes;
+    unsigned char* wring;      // pinned ring for small writes, copied asynchronously on `stream`
+    size_t wring_off;          // next free byte; the ring restarts after a stream synchronisation
     unsigned char* table_host; // grow-only pinned staging for batch job tables
     size_t table_host_bytes;
     unsigned char* table_dev;  // grow-only device copy of the batch job tables
