@@ -105,6 +105,18 @@ BNN_Status ensure_pinned(BNN_Device d, size_t bytes) {
     return BNN_OK;
 }
 
+BNN_Status ensure_mirror(BNN_Device d) {
+    if (d->mirror)
+        return BNN_OK;
+    void* p = nullptr;
+    if (hipHostMalloc(&p, sizeof(float) * kMaxFeatures, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return BNN_ENOMEM;
+    }
+    d->mirror = static_cast<float*>(p);
+    return BNN_OK;
+}
+
 // Adds the elapsed time of every recorded event pair; the stream must be idle.
 hipError_t resolve_timing(BNN_Device d) {
     hipError_t result = hipSuccess;
@@ -254,6 +266,8 @@ EXPORT BNN_Status BNN_DeviceClose(BNN_Device device) {
         (void)hipHostFree(device->pinned);
     if (device->wring)
         (void)hipHostFree(device->wring);
+    if (device->mirror)
+        (void)hipHostFree(device->mirror);
     if (device->table_host)
         (void)hipHostFree(device->table_host);
     if (device->table_dev)
@@ -434,6 +448,8 @@ EXPORT void BNN_BufferFree(BNN_Buffer buffer) {
         return;
     (void)hipSetDevice(buffer->device->ordinal);
     (void)hipStreamSynchronize(buffer->device->stream);
+    if (buffer->device->mirror_buf == buffer)
+        buffer->device->mirror_buf = nullptr;
     (void)hipFree(buffer->dev);
     buffer->device->live_buffers--;
     buffer->device->generation++;
@@ -449,6 +465,7 @@ EXPORT BNN_Status BNN_BufferWrite(BNN_Buffer buffer, size_t offset, const void* 
     if (bytes == 0)
         return BNN_OK;
     BNN_Device d = buffer->device;
+    d->mirror_buf = nullptr;
     hipError_t e = hipSetDevice(d->ordinal);
     if (e != hipSuccess)
         return BNN_EIO;
@@ -502,6 +519,12 @@ EXPORT BNN_Status BNN_BufferRead(BNN_Buffer buffer, size_t offset, void* dst, si
     if (bytes == 0)
         return BNN_OK;
     BNN_Device d = buffer->device;
+    if (d->mirror_buf == buffer && offset >= d->mirror_off && bytes <= d->mirror_bytes &&
+        offset - d->mirror_off <= d->mirror_bytes - bytes) {
+        // the last BNN_Execute's output, already in host memory (the call synchronised)
+        memcpy(dst, reinterpret_cast<const unsigned char*>(d->mirror) + (offset - d->mirror_off), bytes);
+        return BNN_OK;
+    }
     hipError_t e = hipSetDevice(d->ordinal);
     if (e != hipSuccess)
         return BNN_EIO;
@@ -669,6 +692,8 @@ BNN_Status finish(BNN_Device device, hipError_t e, uint64_t seq) {
 }  // namespace
 
 EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
+    if (device != nullptr)
+        device->mirror_buf = nullptr;
     JobPlan p;
     BNN_Status st = plan_job(device, job, &p);
     if (st != BNN_OK)
@@ -689,13 +714,23 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
         fa.row = reinterpret_cast<const float*>(p.in_base);
         fa.post = POST_NONE;
         fa.single = FusedJob{p.m->wbits, p.m->wscale, reinterpret_cast<float*>(p.out_base), p.m->n, p.m->tiles, 0, 0};
+        // F32 outputs of buffers whose device address was never handed out are mirrored
+        // into pinned host memory by the same kernel
+        const bool mirror = !p.dot_out && !job->output.buffer->exposed && ensure_mirror(device) == BNN_OK;
+        fa.mirror = mirror ? device->mirror : nullptr;
         const uint32_t cus = device->cu_count ? device->cu_count : 256u;
         const uint32_t grid = p.m->tiles < 2u * cus ? p.m->tiles : 2u * cus;
         const uint64_t seq = ++device->seq;
         const hipError_t e = timed(device, KK_DOT, [&] {
             return launch_fused(device->stream, fa, p.m->tiles, grid, seq, device->flag_dev, device->status_host);
         });
-        return finish(device, e, seq);
+        const BNN_Status result = finish(device, e, seq);
+        if (result == BNN_OK && mirror) {
+            device->mirror_buf = job->output.buffer;
+            device->mirror_off = job->output.offset;
+            device->mirror_bytes = p.out_row;
+        }
+        return result;
     }
 
     // rows per launch chunk, bounded by the scratch cap
@@ -940,6 +975,8 @@ hipError_t launch_batch(BNN_Device device, const unsigned char* tables, size_t p
 static BNN_Status run_cached_batch(BNN_Device device);
 
 EXPORT BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint32_t count) {
+    if (device != nullptr)
+        device->mirror_buf = nullptr;
     if (device == nullptr || jobs == nullptr || count == 0)
         return BNN_EINVAL;
     // An identical job array of the same resource generation reuses the tables
@@ -1260,6 +1297,7 @@ EXPORT BNN_Status BNNX_BatchLaunch(BNNX_Batch batch) {
     if (st != BNN_OK)
         return st;
     BNN_Device device = batch->device;
+    device->mirror_buf = nullptr;
     if (hipSetDevice(device->ordinal) != hipSuccess)
         return BNN_EIO;
     const uint64_t seq = ++device->seq;
@@ -1315,6 +1353,9 @@ EXPORT BNN_Status BNNX_BufferDevicePointer(BNN_Buffer buffer, void** out_pointer
     *out_pointer = nullptr;
     if (buffer == nullptr)
         return BNN_EINVAL;
+    buffer->exposed = true;
+    if (buffer->device->mirror_buf == buffer)
+        buffer->device->mirror_buf = nullptr;
     *out_pointer = buffer->dev;
     return BNN_OK;
 }

@@ -615,8 +615,11 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
             for (; g < G; ++g)
                 acc = acc + prod[g * 64u + lane];
             acc = acc * s;
-            if (n < job.n)
+            if (n < job.n) {
                 fstore(lane_pick(paired && lane >= 32u, job.out, job2.out) + n, acc);
+                if (fa.mirror)
+                    fa.mirror[n] = acc;
+            }
             if (paired) {
                 // y_p / (1 + expf(-y_p)) * y_(m+p) (qwen3.c:491-495), y_(m+p) from lane + 32
                 const float second = __shfl(acc, (int)(lane | 32u));

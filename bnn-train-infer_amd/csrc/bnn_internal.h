@@ -140,6 +140,7 @@ struct FusedArgs {
     int32_t post;          // PostKind
     float* post_out;       // POST_SILU_MUL
     FusedJob single;       // jobs == null (njobs == 1): the job, passed in the kernel arguments
+    float* mirror;         // single F32 job: host memory that also receives the output row (may be null)
     int32_t dot_out;       // DOT_GROUPS: out receives int16 D[n][group] instead of the sums
 };
 
@@ -212,6 +213,12 @@ struct bnn_accel_device {
     size_t pinned_bytes;
     unsigned char* wring;      // pinned ring for small writes, copied asynchronously on `stream`
     size_t wring_off;          // next free byte; the ring restarts after a stream synchronisation
+    // Host mirror of the last single-row BNN_Execute output: the fused kernel also writes
+    // the row into this pinned memory, so a BNN_BufferRead of (part of) that output right
+    // after the call is a host copy.  Any other call that could change buffers drops it.
+    float* mirror;             // pinned, kMaxFeatures floats
+    BNN_Buffer mirror_buf;     // null: no valid mirror
+    size_t mirror_off, mirror_bytes;
     unsigned char* table_host; // grow-only pinned staging for batch job tables
     size_t table_host_bytes;
     unsigned char* table_dev;  // grow-only device copy of the batch job tables
@@ -269,4 +276,5 @@ struct bnn_accel_buffer {
     BNN_Device device;
     size_t size;
     unsigned char* dev;
+    bool exposed;  // its device pointer was handed out (BNNX_BufferDevicePointer): never mirrored
 };

@@ -258,3 +258,60 @@ def test_single_row_both_paths(pkg, hipdev, oracle, k, op):
             finally:
                 mh.destroy()
                 mo.destroy()
+
+
+def test_read_after_single_row_execute(pkg, hipdev, oracle):
+    """A single-row F32 output is also written to host memory by the kernel; a read of
+    (part of) it right after the call is served from there.  Every other call that can
+    change buffers must drop that copy: later writes, other jobs on the same buffer, an
+    error, and a buffer whose device pointer was handed out."""
+    k, n = 2048, 300
+    bits, scales = pkg.synth.matrix(n, k, seed=11)
+    x = pkg.synth.normal_f32(2, k, seed=11)
+    with pkg.Device(oracle, 0) as odev:
+        mo = odev.matrix(bits, scales)
+        want = [odev.run(pkg.Op.GEMV_F32, mo, x[r:r + 1])[0] for r in range(2)]
+        mo.destroy()
+    m = hipdev.matrix(bits, scales)
+    bi, bo = hipdev.buffer(x.nbytes), hipdev.buffer(4 * 2 * n + 64)
+    try:
+        bi.write(x)
+        jobs = [pkg.Job(int(pkg.Op.GEMV_F32), m.handle.value, bi.view(pkg.Type.F32, r * 4 * k),
+                        bo.view(pkg.Type.F32, 64 + r * 4 * n), 1) for r in range(2)]
+        f = lambda raw: np.frombuffer(raw, np.float32)
+        assert hipdev.execute(jobs[0]) == pkg.Status.OK
+        assert np.array_equal(f(bo.read(4 * n, 64)).view(np.uint32), want[0].view(np.uint32))
+        assert np.array_equal(f(bo.read(80, 64 + 40)).view(np.uint32), want[0][10:30].view(np.uint32))
+        # a write to the output buffer: the next read sees the write
+        bo.write(np.full(16, 7.0, np.float32), 64 + 8)
+        got = f(bo.read(4 * n, 64))
+        assert np.all(got[2:18] == 7.0) and np.array_equal(got[18:].view(np.uint32), want[0][18:].view(np.uint32))
+        # a second job into the same buffer: both rows read back from the device
+        assert hipdev.execute(jobs[0]) == pkg.Status.OK
+        assert hipdev.execute(jobs[1]) == pkg.Status.OK
+        both = f(bo.read(8 * n, 64))
+        assert np.array_equal(both[:n].view(np.uint32), want[0].view(np.uint32))
+        assert np.array_equal(both[n:].view(np.uint32), want[1].view(np.uint32))
+        # an illegal input: ERANGE, the output keeps the previous row
+        bad = x[1].copy()
+        bad[5] = np.nan
+        bi.write(bad, 4 * k)
+        assert hipdev.execute(jobs[1]) == pkg.Status.ERANGE
+        assert np.array_equal(f(bo.read(4 * n, 64 + 4 * n)).view(np.uint32), want[1].view(np.uint32))
+        # a buffer whose device address is known may change behind the library's back
+        bi.write(x[1], 4 * k)
+        assert hipdev.execute(jobs[1]) == pkg.Status.OK
+        dptr = bo.device_pointer()
+        rt = ctypes.CDLL("libamdhip64.so")
+        zeros = np.zeros(n, np.float32)
+        assert rt.hipMemcpy(ctypes.c_void_p(dptr + 64 + 4 * n), zeros.ctypes.data_as(ctypes.c_void_p),
+                            ctypes.c_size_t(4 * n), 1) == 0
+        assert np.all(f(bo.read(4 * n, 64 + 4 * n)) == 0.0)
+        assert hipdev.execute(jobs[1]) == pkg.Status.OK  # never mirrored again
+        assert rt.hipMemcpy(ctypes.c_void_p(dptr + 64 + 4 * n), zeros.ctypes.data_as(ctypes.c_void_p),
+                            ctypes.c_size_t(4 * n), 1) == 0
+        assert np.all(f(bo.read(4 * n, 64 + 4 * n)) == 0.0)
+    finally:
+        bi.free()
+        bo.free()
+        m.destroy()
