@@ -210,17 +210,21 @@ struct TileRegs {
 };
 
 // The job table, written by the host only: read through the constant address space
-// (scalar loads through the scalar cache).  A single job (BNN_Execute) comes in the
-// kernel arguments instead (t == null), with no table in device memory.
+// (scalar loads through the scalar cache).  A single job (BNN_Execute, SINGLE) comes in
+// the kernel arguments instead, with no table in device memory.
+template <bool SINGLE>
 struct JobTable {
     const FusedJob* t;
     const FusedJob& single;
     typedef const __attribute__((address_space(4))) FusedJob* Ptr;
     __device__ __forceinline__ uint32_t first_tile(uint32_t i) const {
-        return t ? ((Ptr)t)[i].first_tile : single.first_tile;
+        if constexpr (SINGLE)
+            return single.first_tile;
+        else
+            return ((Ptr)t)[i].first_tile;
     }
     __device__ __forceinline__ FusedJob operator[](uint32_t i) const {
-        if (t == nullptr)
+        if constexpr (SINGLE)
             return single;
         const Ptr c = (Ptr)t;
         FusedJob j;
@@ -285,7 +289,9 @@ __device__ __forceinline__ void load_tile(const LaneRow& lr, uint32_t G, uint32_
 // GPW: groups per wave of a tile's dots; EPT: row elements per thread.  Workgroup
 // b produces the row once and then takes tiles b, b + grid, ... of the batch, the
 // next tile's weights loading while the current one is computed.
-template <int GPW, int EPT, bool PAIRED>
+// SINGLE: one job in the kernel arguments (BNN_Execute): its row may be int8, its output
+// DOT_GROUPS' D or mirrored into host memory.  Batches compile without those branches.
+template <int GPW, int EPT, bool PAIRED, bool SINGLE>
 __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t tiles_total, uint64_t seq,
                                                          uint64_t* flag, uint64_t* host_status) {
     static_assert(EPT == 2 * GPW, "a wave quantises exactly the groups of its dots");
@@ -319,7 +325,7 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     // load counter completes in order: the row is needed first), arriving while the
     // row is produced
     // tiles are walked over the jobs, or over the pairs (the first half of the table)
-    const JobTable jobs{fa.jobs, fa.single};
+    const JobTable<SINGLE> jobs{fa.jobs, fa.single};
     constexpr bool paired = PAIRED;  // fa.post == POST_SILU_MUL
     const uint32_t nwalk = paired ? fa.njobs / 2u : fa.njobs, pair_step = paired ? nwalk : 0u;
     uint32_t tile = blockIdx.x, ji = 0;
@@ -327,7 +333,9 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
         ++ji;
     FusedJob job = jobs[ji], job2 = jobs[ji + pair_step];
     const float* src_a = fa.kind == PRE_ROW ? fa.row : fa.a;
-    const bool int_row = fa.kind == PRE_ROW_I8;
+    const bool int_row = SINGLE && fa.kind == PRE_ROW_I8;
+    const bool dot_out = SINGLE && fa.dot_out;
+    float* const mirror = SINGLE ? fa.mirror : nullptr;
     float xv[EPT], bv[EPT], gv[EPT];
     if (int_row) {  // int8 values, exact in binary32
         const int8_t* src8 = reinterpret_cast<const int8_t*>(fa.row);
@@ -573,12 +581,12 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
                     d = f_group_dot(cur.w[i], planes + g * (kPlaneWords / 4u), neg_sum[i]);
                 }
                 // DOT_GROUPS: D itself goes through the exchange
-                prod[g * 64u + lane] = fa.dot_out ? __int_as_float(d)
+                prod[g * 64u + lane] = dot_out ? __int_as_float(d)
                                                   : __half2float(__ushort_as_half((uint16_t)cur.s[i])) * (float)d;
             }
         }
         lds_barrier();
-        if (wave == 0 && fa.dot_out) {
+        if (wave == 0 && dot_out) {
             // int16 D[n][g]: a lane's groups are contiguous, 16-byte stores of 8 when aligned
             const uint32_t n = lr.row;
             if (n < job.n) {
@@ -617,8 +625,8 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
             acc = acc * s;
             if (n < job.n) {
                 fstore(lane_pick(paired && lane >= 32u, job.out, job2.out) + n, acc);
-                if (fa.mirror)
-                    fa.mirror[n] = acc;
+                if (mirror)
+                    mirror[n] = acc;
             }
             if (paired) {
                 // y_p / (1 + expf(-y_p)) * y_(m+p) (qwen3.c:491-495), y_(m+p) from lane + 32
@@ -647,14 +655,23 @@ hipError_t launch_fused(hipStream_t stream, const FusedArgs& args, uint32_t tile
     constexpr int kWideGpw = kFusedMaxGroups / kFusedWaves, kWideEpt = kFusedMaxWidth / kFusedThreads;
     const bool paired = args.post == POST_SILU_MUL;
     const dim3 g(grid), b(kFusedThreads);
-    if (args.width <= 2048u && !paired)
-        hipLaunchKernelGGL((k_fused<1, 2, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
-    else if (args.width <= 2048u)
-        hipLaunchKernelGGL((k_fused<1, 2, true>), g, b, 0, stream, args, tiles, seq, flag, host_status);
-    else if (!paired)
-        hipLaunchKernelGGL((k_fused<kWideGpw, kWideEpt, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
-    else
-        hipLaunchKernelGGL((k_fused<kWideGpw, kWideEpt, true>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+    if (args.jobs == nullptr) {  // a single job in the kernel arguments
+        if (args.width <= 2048u)
+            hipLaunchKernelGGL((k_fused<1, 2, false, true>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+        else
+            hipLaunchKernelGGL((k_fused<kWideGpw, kWideEpt, false, true>), g, b, 0, stream, args, tiles, seq, flag,
+                               host_status);
+    } else if (args.width <= 2048u && !paired) {
+        hipLaunchKernelGGL((k_fused<1, 2, false, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+    } else if (args.width <= 2048u) {
+        hipLaunchKernelGGL((k_fused<1, 2, true, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+    } else if (!paired) {
+        hipLaunchKernelGGL((k_fused<kWideGpw, kWideEpt, false, false>), g, b, 0, stream, args, tiles, seq, flag,
+                           host_status);
+    } else {
+        hipLaunchKernelGGL((k_fused<kWideGpw, kWideEpt, true, false>), g, b, 0, stream, args, tiles, seq, flag,
+                           host_status);
+    }
     return hipGetLastError();
 }
 
