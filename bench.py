@@ -346,6 +346,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--prewarm", type=float, default=0.5,
+                    help="seconds of back-to-back steps before the declared warmup (GPU clock ramp)")
+    ap.add_argument("--no-timed-events", action="store_true",
+                    help="no HIP events in the timed steps (kernel durations from a separate pass)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary legs (ops, gemm, e2e, mlp)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -423,6 +427,35 @@ def main():
         if st != 0:
             raise pkg.BnnError(st, "BNNX_DeviceSynchronize")
 
+    # Pre-warm: the GPU leaves its idle clocks only after some milliseconds of work, so
+    # steps are launched back to back (in bursts closed by a synchronisation) until
+    # PREWARM_S seconds have passed; then the declared warmup steps, one
+    # synchronisation, and the timed steps.
+    t0, prewarm_steps = time.perf_counter(), 0
+    while time.perf_counter() - t0 < args.prewarm:
+        for _ in range(64):
+            launch()
+        synchronize()
+        prewarm_steps += 64
+    for _ in range(args.warmup):
+        launch()
+    synchronize()
+    # HIP events around every launch on the device stream (recorded by the library,
+    # resolved at the synchronisation) give the kernels' own durations in the same
+    # timed steps; --no-timed-events leaves them out (their cost: see config.event_overhead)
+    dev.kernel_timing(not args.no_timed_events)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        launch()
+    synchronize()
+    wall = time.perf_counter() - t0
+    dot_ms, dot_n = dev.kernel_timing_read(1)
+    prep_ms, prep_n = dev.kernel_timing_read(0)
+    dev.kernel_timing(False)
+    print(f"timed: {args.steps} steps in {wall:.4f} s after {prewarm_steps} pre-warm steps", flush=True)
+    y_stream = bout.read().view(np.float32).reshape(MATRICES, N_OUT)
+    assert np.array_equal(y_stream.view(np.uint32), y_batch.view(np.uint32)), "streamed steps differ"
+    # the same number of steps again without events: what the events cost per step
     for _ in range(args.warmup):
         launch()
     synchronize()
@@ -430,28 +463,26 @@ def main():
     for _ in range(args.steps):
         launch()
     synchronize()
-    wall = time.perf_counter() - t0
-    print(f"timed: {args.steps} steps in {wall:.3f} s", flush=True)
-    y_stream = bout.read().view(np.float32).reshape(MATRICES, N_OUT)
-    assert np.array_equal(y_stream.view(np.uint32), y_batch.view(np.uint32)), "streamed steps differ"
+    plain_wall = time.perf_counter() - t0
 
     hip.BNNX_BatchDestroy(batch)
 
-    # the same step through the synchronous BNNX_ExecuteBatch (returns with results
-    # readable), with kernel durations from HIP events recorded around each launch on
-    # the device stream (event pairs between back-to-back launches would stretch them)
+    # the same step through the synchronous BNNX_ExecuteBatch (returns with results readable)
     sync_steps = max(1, args.steps // 4)
-    dev.kernel_timing(True)
     t0 = time.perf_counter()
     for _ in range(sync_steps):
         step()
     sync_wall = time.perf_counter() - t0
-    dot_ms, dot_n = dev.kernel_timing_read(1)
-    prep_ms, prep_n = dev.kernel_timing_read(0)
-    dev.kernel_timing(False)
 
     step_bytes = MATRICES * BYTES_PER_JOB
     value = step_bytes * args.steps / wall / 1e9
+    if dot_n == 0:  # --no-timed-events: kernel durations from a separate pass with events
+        dev.kernel_timing(True)
+        for _ in range(args.steps):
+            step()
+        dot_ms, dot_n = dev.kernel_timing_read(1)
+        prep_ms, prep_n = dev.kernel_timing_read(0)
+        dev.kernel_timing(False)
     dot_avg_s = dot_ms / 1e3 / max(dot_n, 1)
     achieved = step_bytes / dot_avg_s / 1e9
 
@@ -502,6 +533,10 @@ def main():
             "bytes_per_step": step_bytes,
             "step": "one prepared batch launch (BNNX_BatchLaunch: prep + group-dot), back to back, "
                     "one BNNX_DeviceSynchronize at the end",
+            "prewarm_s": args.prewarm,
+            "timed_events": not args.no_timed_events,
+            "event_overhead": round(wall / plain_wall - 1.0, 4),
+            "no_event_GBps": round(step_bytes * args.steps / plain_wall / 1e9, 2),
             "sync_GBps": round(step_bytes * sync_steps / sync_wall / 1e9, 2),
             "sync_ms_per_step": round(sync_wall / sync_steps * 1e3, 4),
             "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
@@ -516,7 +551,9 @@ def main():
             "traffic": traffic_from_profiles(),
             "kernel": "k_dot_wave (batched group-dot, one wave per 64-feature tile)",
             "kernel_avg_us": round(dot_avg_s * 1e6, 2),
+            "kernel_launches_timed": dot_n,
             "prep_kernel_avg_us": round(prep_ms / max(prep_n, 1) * 1e3, 2),
+            "step_frac": round(value / HBM_PEAK_GBS, 4),
         },
         "per_call": per_call,
     }

@@ -175,6 +175,7 @@ class Api:
             setattr(self, name, fn)
         # HIP-backend extensions (include/bnn-accelerator-hip.h); absent elsewhere.
         ext = {
+            "BNNX_DeviceOpenOrdinal": (S, [U32, P(V)]),
             "BNNX_DeviceStream": (S, [V, P(V)]),
             "BNNX_KernelTiming": (S, [V, ctypes.c_int]),
             "BNNX_KernelTimingRead": (S, [V, U32, P(ctypes.c_double), P(ctypes.c_uint64)]),

@@ -134,6 +134,38 @@ hipError_t resolve_timing(BNN_Device d) {
     return result;
 }
 
+void destroy_events(BNN_Device d) {
+    for (int i = 0; i < bnn_accel_device::kTimingSlots; ++i) {
+        if (d->ev_begin[i])
+            (void)hipEventDestroy(d->ev_begin[i]);
+        if (d->ev_end[i])
+            (void)hipEventDestroy(d->ev_end[i]);
+        d->ev_begin[i] = d->ev_end[i] = nullptr;
+    }
+    d->events_created = false;
+}
+
+// The timing event pairs, created on the first BNNX_KernelTiming(device, 1).
+BNN_Status ensure_events(BNN_Device d) {
+    if (d->events_created)
+        return BNN_OK;
+    if (hipSetDevice(d->ordinal) != hipSuccess)
+        return BNN_EIO;
+    hipError_t e = hipSuccess;
+    for (int i = 0; e == hipSuccess && i < bnn_accel_device::kTimingSlots; ++i) {
+        e = hipEventCreate(&d->ev_begin[i]);
+        if (e == hipSuccess)
+            e = hipEventCreate(&d->ev_end[i]);
+    }
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        destroy_events(d);
+        return hip_status(e);
+    }
+    d->events_created = true;
+    return BNN_OK;
+}
+
 // Launch helper: when timing is on, brackets `launch` with an event pair on the
 // device stream (no extra synchronisation unless the slots run out).
 template <typename F>
@@ -187,16 +219,16 @@ BNN_Status op_types(BNN_Operation op, BNN_Type* in, BNN_Type* out) {
 // Devices (soft-bnn-accelerator.c:310-356)
 // ---------------------------------------------------------------------------
 
-EXPORT BNN_Status BNN_DeviceOpen(uint32_t device_index, BNN_Device* out_device) {
-    if (out_device == nullptr)
-        return BNN_EINVAL;
-    *out_device = nullptr;
+namespace {
+
+// Opens HIP device `ordinal` (BNN_DeviceOpen: 0; BNNX_DeviceOpenOrdinal: any).
+BNN_Status open_device(int ordinal, BNN_Device* out_device) {
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
         (void)hipGetLastError();
         return BNN_ENOTSUP;
     }
-    if (device_index >= (uint32_t)count)
+    if (ordinal < 0 || ordinal >= count)
         return BNN_ENOTSUP;
     float one = 1.0f;
     uint32_t one_bits;
@@ -207,7 +239,7 @@ EXPORT BNN_Status BNN_DeviceOpen(uint32_t device_index, BNN_Device* out_device) 
     BNN_Device d = static_cast<BNN_Device>(calloc(1, sizeof(bnn_accel_device)));
     if (d == nullptr)
         return BNN_ENOMEM;
-    d->ordinal = (int)device_index;
+    d->ordinal = ordinal;
     hipError_t e = hipSetDevice(d->ordinal);
     int cus = 0;
     if (e == hipSuccess)
@@ -219,13 +251,9 @@ EXPORT BNN_Status BNN_DeviceOpen(uint32_t device_index, BNN_Device* out_device) 
         e = hipMalloc(reinterpret_cast<void**>(&d->flag_dev), 256);
     if (e == hipSuccess)
         e = hipHostMalloc(reinterpret_cast<void**>(&d->status_host), 256, hipHostMallocCoherent);
-    for (int i = 0; e == hipSuccess && i < bnn_accel_device::kTimingSlots; ++i) {
-        e = hipEventCreate(&d->ev_begin[i]);
-        if (e == hipSuccess)
-            e = hipEventCreate(&d->ev_end[i]);
-    }
     if (e == hipSuccess) {
-        *d->status_host = 0;
+        d->status_host[0] = 0;
+        d->status_host[1] = 0;
         const uint64_t zero = 0;
         e = hipMemcpyAsync(d->flag_dev, &zero, sizeof zero, hipMemcpyHostToDevice, d->stream);
         if (e == hipSuccess)
@@ -234,12 +262,6 @@ EXPORT BNN_Status BNN_DeviceOpen(uint32_t device_index, BNN_Device* out_device) 
     if (e != hipSuccess) {
         BNN_Status st = hip_status(e);
         (void)hipGetLastError();
-        for (int i = 0; i < bnn_accel_device::kTimingSlots; ++i) {
-            if (d->ev_end[i])
-                (void)hipEventDestroy(d->ev_end[i]);
-            if (d->ev_begin[i])
-                (void)hipEventDestroy(d->ev_begin[i]);
-        }
         if (d->status_host)
             (void)hipHostFree(d->status_host);
         if (d->flag_dev)
@@ -251,6 +273,28 @@ EXPORT BNN_Status BNN_DeviceOpen(uint32_t device_index, BNN_Device* out_device) 
     }
     *out_device = d;
     return BNN_OK;
+}
+
+}  // namespace
+
+// (soft-bnn-accelerator.c:309-325) index 0 only; it names the process's first visible
+// HIP device.  Other GPUs of a host: BNNX_DeviceOpenOrdinal.
+EXPORT BNN_Status BNN_DeviceOpen(uint32_t device_index, BNN_Device* out_device) {
+    if (out_device == nullptr)
+        return BNN_EINVAL;
+    *out_device = nullptr;
+    if (device_index != 0)
+        return BNN_ENOTSUP;
+    return open_device(0, out_device);
+}
+
+EXPORT BNN_Status BNNX_DeviceOpenOrdinal(uint32_t hip_ordinal, BNN_Device* out_device) {
+    if (out_device == nullptr)
+        return BNN_EINVAL;
+    *out_device = nullptr;
+    if (hip_ordinal > (uint32_t)INT32_MAX)
+        return BNN_ENOTSUP;
+    return open_device((int)hip_ordinal, out_device);
 }
 
 EXPORT BNN_Status BNN_DeviceClose(BNN_Device device) {
@@ -273,10 +317,7 @@ EXPORT BNN_Status BNN_DeviceClose(BNN_Device device) {
     if (device->table_dev)
         (void)hipFree(device->table_dev);
     free(device->batch_jobs);
-    for (int i = 0; i < bnn_accel_device::kTimingSlots; ++i) {
-        (void)hipEventDestroy(device->ev_begin[i]);
-        (void)hipEventDestroy(device->ev_end[i]);
-    }
+    destroy_events(device);
     (void)hipHostFree(device->status_host);
     (void)hipFree(device->flag_dev);
     (void)hipStreamDestroy(device->stream);
@@ -684,97 +725,87 @@ BNN_Status finish(BNN_Device device, hipError_t e, uint64_t seq) {
         (void)hipGetLastError();
         return BNN_EIO;
     }
-    if (__atomic_load_n(device->status_host, __ATOMIC_ACQUIRE) == seq)
+    if (__atomic_load_n(&device->status_host[0], __ATOMIC_ACQUIRE) == seq)
         return BNN_ERANGE;
     return BNN_OK;
 }
 
 }  // namespace
 
-EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
-    if (device != nullptr)
-        device->mirror_buf = nullptr;
-    JobPlan p;
-    BNN_Status st = plan_job(device, job, &p);
-    if (st != BNN_OK)
-        return st;
+namespace {
 
-    // One row of GEMV_F32 (the reference engine's only call, linear.c:169-200), GEMV or
-    // DOT_GROUPS: the row is checked, quantised (F32) and multiplied in one launch of the
-    // fused kernel, read straight from the input view -- no scratch, no second launch.
-    if (job->rows == 1 && p.in_aligned && p.out_aligned && p.m->k <= kFusedMaxWidth && p.m->k % kGroup == 0) {
-        if (hipSetDevice(device->ordinal) != hipSuccess)
-            return BNN_EIO;
-        FusedArgs fa = {};
-        fa.jobs = nullptr;
-        fa.njobs = 1;
-        fa.kind = p.f32_in ? PRE_ROW : PRE_ROW_I8;
-        fa.dot_out = p.dot_out ? 1 : 0;
-        fa.width = p.m->k;
-        fa.row = reinterpret_cast<const float*>(p.in_base);
-        fa.post = POST_NONE;
-        fa.single = FusedJob{p.m->wbits, p.m->wscale, reinterpret_cast<float*>(p.out_base), p.m->n, p.m->tiles, 0, 0};
-        // F32 outputs of buffers whose device address was never handed out are mirrored
-        // into pinned host memory by the same kernel
-        const bool mirror = !p.dot_out && !job->output.buffer->exposed && ensure_mirror(device) == BNN_OK;
-        fa.mirror = mirror ? device->mirror : nullptr;
-        const uint32_t cus = device->cu_count ? device->cu_count : 256u;
-        const uint32_t grid = p.m->tiles < 2u * cus ? p.m->tiles : 2u * cus;
-        const uint64_t seq = ++device->seq;
-        const hipError_t e = timed(device, KK_DOT, [&] {
-            return launch_fused(device->stream, fa, p.m->tiles, grid, seq, device->flag_dev, device->status_host);
-        });
-        const BNN_Status result = finish(device, e, seq);
-        if (result == BNN_OK && mirror) {
-            device->mirror_buf = job->output.buffer;
-            device->mirror_off = job->output.offset;
-            device->mirror_bytes = p.out_row;
-        }
-        return result;
-    }
-
-    // rows per launch chunk, bounded by the scratch cap
-    const uint32_t rows = job->rows;
-    const bool mfma = rows >= kMfmaMinRows;
+// Rows per launch chunk of a multi-row job and the scratch bytes of one chunk's
+// quantised rows, for a scratch of `cap` bytes that also holds the chunk's staging
+// rows when the output view is not naturally aligned.  chunk = 0: not even one row fits.
+void chunk_rows(const JobPlan& p, uint32_t rows, bool mfma, size_t cap, size_t* chunk_out, size_t* rows_bytes) {
     size_t a, b, c;
-    const size_t per_row = row_scratch_bytes(p, 1, &a, &b, &c, nullptr, mfma) + (p.out_aligned ? 0u : p.out_row);
+    // planes + group sums + row scale (+ Q rows) (+ staging), unrounded
+    const size_t per_row = (size_t)p.m->groups * (kPlaneWords * 4u + 4u) + 4u + (mfma ? p.m->k : 0u) +
+                           (p.out_aligned ? 0u : p.out_row);
+    // each of the (at most five) regions is rounded up to 256 bytes once per chunk
+    const size_t slack = 5 * 256;
     size_t chunk = rows < kScratchRowsCap ? rows : kScratchRowsCap;
-    while (chunk > 1 && chunk * per_row + 4096 > kScratchBytesCap)
-        chunk /= 2;
-    const size_t rows_bytes = row_scratch_bytes(p, chunk, &a, &b, &c, nullptr, mfma);
-    const size_t staging_bytes = p.out_aligned ? 0 : round_up(chunk * p.out_row, 256);
+    const size_t fit = cap > slack ? (cap - slack) / per_row : 0;
+    if (chunk > fit)
+        chunk = fit;
+    *chunk_out = chunk;
+    *rows_bytes = chunk ? row_scratch_bytes(p, chunk, &a, &b, &c, nullptr, mfma) : 0;
+}
 
+// One row, aligned views, K <= kFusedMaxWidth: check, quantisation and dots in one
+// launch of the fused kernel, read straight from the input view -- no scratch.
+// `mirror`: also write an F32 output row into the device's pinned host mirror.
+BNN_Status run_single_row(BNN_Device device, const BNN_Job* job, const JobPlan& p, bool allow_mirror) {
     if (hipSetDevice(device->ordinal) != hipSuccess)
         return BNN_EIO;
-    st = ensure_scratch(device, rows_bytes + staging_bytes);
-    if (st != BNN_OK)
-        return st;
-    unsigned char* staging = device->scratch + rows_bytes;
-
-    hipError_t e = hipSuccess;
-    if (mfma && p.m->wbytes == nullptr) {
-        // first multi-row job on this matrix: create its +1/-1 byte copy
-        const uint32_t n_pad = (p.m->n + kGemmRowPad - 1u) / kGemmRowPad * kGemmRowPad;
-        void* w = nullptr;
-        if (hipMalloc(&w, (size_t)n_pad * p.m->k) != hipSuccess) {
-            (void)hipGetLastError();
-            return BNN_ENOMEM;
-        }
-        p.m->wbytes = static_cast<int8_t*>(w);
-        p.m->n_pad = n_pad;
-        e = launch_expand(device->stream, p.m->wbits, p.m->tiles, p.m->groups, n_pad, p.m->wbytes);
+    FusedArgs fa = {};
+    fa.jobs = nullptr;
+    fa.njobs = 1;
+    fa.kind = p.f32_in ? PRE_ROW : PRE_ROW_I8;
+    fa.dot_out = p.dot_out ? 1 : 0;
+    fa.width = p.m->k;
+    fa.row = reinterpret_cast<const float*>(p.in_base);
+    fa.post = POST_NONE;
+    fa.single = FusedJob{p.m->wbits, p.m->wscale, reinterpret_cast<float*>(p.out_base), p.m->n, p.m->tiles, 0, 0};
+    // F32 outputs of buffers whose device address was never handed out are mirrored
+    // into pinned host memory by the same kernel
+    const bool mirror =
+        allow_mirror && !p.dot_out && !job->output.buffer->exposed && ensure_mirror(device) == BNN_OK;
+    fa.mirror = mirror ? device->mirror : nullptr;
+    const uint32_t cus = device->cu_count ? device->cu_count : 256u;
+    const uint32_t grid = p.m->tiles < 2u * cus ? p.m->tiles : 2u * cus;
+    const uint64_t seq = ++device->seq;
+    const hipError_t e = timed(device, KK_DOT, [&] {
+        return launch_fused(device->stream, fa, p.m->tiles, grid, seq, device->flag_dev, device->status_host);
+    });
+    const BNN_Status result = finish(device, e, seq);
+    if (result == BNN_OK && mirror) {
+        device->mirror_buf = job->output.buffer;
+        device->mirror_off = job->output.offset;
+        device->mirror_bytes = p.out_row;
     }
+    return result;
+}
+
+// A multi-row job (or a single row the fused kernel does not take) in chunks of
+// `chunk` rows whose quantised forms occupy the first `rows_bytes` of `scratch`,
+// followed by the chunk's staging rows when the output view is not aligned.
+// mfma: the rows run on the matrix cores (the matrix's +1/-1 copy must exist).
+BNN_Status run_rows(BNN_Device device, const BNN_Job* job, const JobPlan& p, bool mfma, unsigned char* scratch,
+                    size_t chunk, size_t rows_bytes, hipError_t e) {
+    const uint32_t rows = job->rows;
+    unsigned char* staging = scratch + rows_bytes;
     const uint64_t seq = ++device->seq;
     if (e == hipSuccess && chunk < rows) {
         // every row is checked before any chunk writes output
-        const PrepJob all = make_prep(p, p.in_base, rows, device->scratch);
+        const PrepJob all = make_prep(p, p.in_base, rows, scratch);
         e = timed(device, KK_PREP, [&] {
             return launch_prep(device->stream, all, true, seq, device->flag_dev, device->status_host);
         });
     }
     for (size_t r0 = 0; e == hipSuccess && r0 < rows; r0 += chunk) {
         const uint32_t rc = (uint32_t)((rows - r0) < chunk ? (rows - r0) : chunk);
-        const PrepJob pj = make_prep(p, p.in_base + r0 * p.in_stride, rc, device->scratch, mfma);
+        const PrepJob pj = make_prep(p, p.in_base + r0 * p.in_stride, rc, scratch, mfma);
         e = timed(device, KK_PREP, [&] {
             return launch_prep(device->stream, pj, false, seq, device->flag_dev, device->status_host);
         });
@@ -798,6 +829,58 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
             });
     }
     return finish(device, e, seq);
+}
+
+bool single_row_path(const BNN_Job* job, const JobPlan& p) {
+    return job->rows == 1 && p.in_aligned && p.out_aligned && p.m->k <= kFusedMaxWidth && p.m->k % kGroup == 0;
+}
+
+}  // namespace
+
+EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
+    if (device != nullptr)
+        device->mirror_buf = nullptr;
+    JobPlan p;
+    BNN_Status st = plan_job(device, job, &p);
+    if (st != BNN_OK)
+        return st;
+    // one row of GEMV_F32 (the reference engine's only call, linear.c:169-200), GEMV or DOT_GROUPS
+    if (single_row_path(job, p))
+        return run_single_row(device, job, p, true);
+
+    const bool mfma = job->rows >= kMfmaMinRows;
+    size_t chunk = 0, rows_bytes = 0;
+    chunk_rows(p, job->rows, mfma, kScratchBytesCap, &chunk, &rows_bytes);
+    if (chunk == 0)
+        return BNN_ENOMEM;
+    const size_t staging_bytes = p.out_aligned ? 0 : round_up(chunk * p.out_row, 256);
+    if (hipSetDevice(device->ordinal) != hipSuccess)
+        return BNN_EIO;
+    st = ensure_scratch(device, rows_bytes + staging_bytes);
+    if (st != BNN_OK)
+        return st;
+
+    hipError_t e = hipSuccess;
+    if (mfma && p.m->wbytes == nullptr) {
+        // first multi-row job on this matrix: create its +1/-1 byte copy; the matrix
+        // records it only once the expansion is enqueued
+        const uint32_t n_pad = (p.m->n + kGemmRowPad - 1u) / kGemmRowPad * kGemmRowPad;
+        void* w = nullptr;
+        if (hipMalloc(&w, (size_t)n_pad * p.m->k) != hipSuccess) {
+            (void)hipGetLastError();
+            return BNN_ENOMEM;
+        }
+        e = launch_expand(device->stream, p.m->wbits, p.m->tiles, p.m->groups, n_pad, static_cast<int8_t*>(w));
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipStreamSynchronize(device->stream);
+            (void)hipFree(w);
+            return BNN_EIO;
+        }
+        p.m->wbytes = static_cast<int8_t*>(w);
+        p.m->n_pad = n_pad;
+    }
+    return run_rows(device, job, p, mfma, device->scratch, chunk, rows_bytes, e);
 }
 
 // ---------------------------------------------------------------------------
@@ -951,7 +1034,7 @@ void fill_batch_tables(const BatchPlan& bp, const BNN_Job* jobs, unsigned char* 
 // The two launches of a batch whose tables start at 'tables' on the device.
 hipError_t launch_batch(BNN_Device device, const unsigned char* tables, size_t prep_tab, size_t dot_tab,
                         size_t prep_map, uint32_t prep_blocks, uint32_t items, uint32_t uniform_items,
-                        uint32_t max_groups, uint64_t seq) {
+                        uint32_t max_groups, uint64_t seq, uint64_t* status) {
     const PrepJob* dp = reinterpret_cast<const PrepJob*>(tables);
     const DotJob* dd = reinterpret_cast<const DotJob*>(tables + prep_tab);
     // no map (prep_map == 0) when every job has one row: prep block b is job b
@@ -959,8 +1042,7 @@ hipError_t launch_batch(BNN_Device device, const unsigned char* tables, size_t p
     const uint32_t* ddm =
         uniform_items ? nullptr : reinterpret_cast<const uint32_t*>(tables + prep_tab + dot_tab + prep_map);
     hipError_t e = timed(device, KK_PREP, [&] {
-        return launch_prep_batch(device->stream, dp, dpm, prep_blocks, max_groups, seq, device->flag_dev,
-                                 device->status_host);
+        return launch_prep_batch(device->stream, dp, dpm, prep_blocks, max_groups, seq, device->flag_dev, status);
     });
     if (e == hipSuccess)
         e = timed(device, KK_DOT, [&] {
@@ -1049,7 +1131,8 @@ static BNN_Status run_cached_batch(BNN_Device device) {
     const uint64_t seq = ++device->seq;
     const hipError_t e = launch_batch(device, device->table_dev, device->batch_prep_tab, device->batch_dot_tab,
                                       device->batch_prep_map, device->batch_prep_blocks, device->batch_items,
-                                      device->batch_uniform_items, device->batch_max_groups, seq);
+                                      device->batch_uniform_items, device->batch_max_groups, seq,
+                                      device->status_host);
     if (e != hipSuccess)
         device->batch_count = 0;
     return finish(device, e, seq);
@@ -1307,10 +1390,12 @@ EXPORT BNN_Status BNNX_BatchLaunch(BNNX_Batch batch) {
         batch->fused ? timed(device, KK_DOT,
                              [&] {
                                  return launch_fused(device->stream, batch->fused_args, batch->fused_tiles,
-                                                     batch->fused_grid, seq, device->flag_dev, device->status_host);
+                                                     batch->fused_grid, seq, device->flag_dev,
+                                                     device->status_host + 1);
                              })
                      : launch_batch(device, batch->mem, batch->prep_tab, batch->dot_tab, batch->prep_map,
-                                    batch->prep_blocks, batch->items, batch->uniform_items, batch->max_groups, seq);
+                                    batch->prep_blocks, batch->items, batch->uniform_items, batch->max_groups, seq,
+                                    device->status_host + 1);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return BNN_EIO;
@@ -1342,7 +1427,7 @@ EXPORT BNN_Status BNNX_DeviceSynchronize(BNN_Device device) {
         (void)hipGetLastError();
         return BNN_EIO;
     }
-    if (first != 0 && __atomic_load_n(device->status_host, __ATOMIC_ACQUIRE) >= first)
+    if (first != 0 && __atomic_load_n(&device->status_host[1], __ATOMIC_ACQUIRE) >= first)
         return BNN_ERANGE;
     return BNN_OK;
 }
@@ -1397,6 +1482,11 @@ EXPORT BNN_Status BNNX_DeviceStream(BNN_Device device, void** out_stream) {
 EXPORT BNN_Status BNNX_KernelTiming(BNN_Device device, int enable) {
     if (device == nullptr)
         return BNN_EINVAL;
+    if (enable) {
+        const BNN_Status st = ensure_events(device);
+        if (st != BNN_OK)
+            return st;
+    }
     device->timing = enable != 0;
     device->ev_used = 0;
     for (int i = 0; i < KK_COUNT; ++i) {

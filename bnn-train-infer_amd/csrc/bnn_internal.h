@@ -206,7 +206,9 @@ struct bnn_accel_device {
     uint64_t async_first_seq;  // first seq launched asynchronously since the last synchronise (0: none)
     uint64_t retired;          // matrices and buffers destroyed so far
     uint64_t* flag_dev;        // device word: seq of the last job that met an illegal input
-    uint64_t* status_host;     // pinned host word, same meaning, written by the kernels
+    // pinned host words, same meaning, written by the kernels: [0] for synchronous calls,
+    // [1] for asynchronous launches (read by BNNX_DeviceSynchronize)
+    uint64_t* status_host;
     unsigned char* scratch;    // grow-only device scratch
     size_t scratch_bytes;
     unsigned char* pinned;     // grow-only pinned host staging for transfers
@@ -237,7 +239,8 @@ struct bnn_accel_device {
     // optional kernel timing (extension API): event pairs recorded around
     // launches, resolved after the call's synchronisation
     int timing;
-    static constexpr int kTimingSlots = 64;
+    bool events_created;       // the event pairs exist (made by the first BNNX_KernelTiming(.., 1))
+    static constexpr int kTimingSlots = 1024;
     hipEvent_t ev_begin[kTimingSlots], ev_end[kTimingSlots];
     int ev_kind[kTimingSlots];
     int ev_used;

@@ -22,6 +22,14 @@ enum {
     BNNX_KERNEL_GEMM = 3     /* multi-row jobs on the matrix cores */
 };
 
+/*
+ * BNN_DeviceOpen accepts index 0 only, as the reference's soft backend does
+ * (soft-bnn-accelerator.c:317-318); index 0 is the process's first visible HIP
+ * device.  This opens HIP device `hip_ordinal` (0 .. hipGetDeviceCount() - 1) with
+ * the same semantics, for hosts with several GPUs; BNN_ENOTSUP for any other value.
+ */
+BNN_Status BNNX_DeviceOpenOrdinal(uint32_t hip_ordinal, BNN_Device* out_device);
+
 /* The hipStream_t (as void*) on which every transfer and kernel of the device runs. */
 BNN_Status BNNX_DeviceStream(BNN_Device device, void** out_stream);
 

@@ -196,3 +196,90 @@ def test_prepared_batch_launches(pkg, hipdev):
     assert api.BNNX_BatchCreate(hipdev.handle, bad, 2, ctypes.byref(b)) == pkg.Status.EINVAL
     assert not b.value
     _free(mats, bi, bo)
+
+
+def test_async_status_is_separate_from_synchronous_calls(pkg, hipdev):
+    """An illegal input met by a synchronous call after an asynchronous launch is that
+    call's own BNN_ERANGE; the next BNNX_DeviceSynchronize reports only the launches
+    (and the other way round: a failed launch is not hidden by a later good call)."""
+    import ctypes
+    api = hipdev.api
+    specs = [("GEMV_F32", 2048, 1024, 1), ("GEMV_F32", 2048, 512, 1)]
+    mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs, seed=9)
+    b = ctypes.c_void_p()
+    assert api.BNNX_BatchCreate(hipdev.handle, jobs, 1, ctypes.byref(b)) == pkg.Status.OK
+    bad = xs[1].copy()
+    bad[0, 7] = np.nan
+    raw = bi.read()
+    o1 = jobs[1].input.offset
+    raw[o1:o1 + bad.nbytes] = bad.view(np.uint8).reshape(-1)
+    bi.write(raw)
+    assert api.BNNX_BatchLaunch(b) == pkg.Status.OK             # job 0: legal
+    assert hipdev.execute(jobs[1]) == pkg.Status.ERANGE         # synchronous, illegal
+    assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.OK
+    # the reverse order: a failed launch, then a good synchronous call
+    raw[o1:o1 + xs[1].nbytes] = xs[1].view(np.uint8).reshape(-1)
+    o0 = jobs[0].input.offset
+    bad0 = xs[0].copy()
+    bad0[0, 3] = np.inf
+    raw[o0:o0 + bad0.nbytes] = bad0.view(np.uint8).reshape(-1)
+    bi.write(raw)
+    assert api.BNNX_BatchLaunch(b) == pkg.Status.OK
+    assert hipdev.execute(jobs[1]) == pkg.Status.OK
+    assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.ERANGE
+    assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.OK
+    api.BNNX_BatchDestroy(b)
+    _free(mats, bi, bo)
+
+
+def test_batches_drop_the_single_row_mirror(pkg, hipdev):
+    """A single-row F32 BNN_Execute output is mirrored in host memory; a later
+    BNNX_ExecuteBatch or prepared batch launch that rewrites the same range must make
+    BNN_BufferRead return the new device contents."""
+    import ctypes
+    api = hipdev.api
+    k, n = 2048, 700
+    mats = [hipdev.matrix(*pkg.synth.matrix(n, k, seed=s)) for s in (21, 22, 23)]
+    x = pkg.synth.normal_f32(1, k, seed=21)
+    bi, bo = hipdev.buffer(x.nbytes), hipdev.buffer(4 * n)
+    bi.write(x)
+    want = [hipdev.run(pkg.Op.GEMV_F32, m, x)[0] for m in mats]
+    jobs = [pkg.Job(int(pkg.Op.GEMV_F32), m.handle.value, bi.view(pkg.Type.F32), bo.view(pkg.Type.F32), 1)
+            for m in mats]
+    f = lambda raw: np.frombuffer(raw, np.float32).view(np.uint32)
+    assert hipdev.execute(jobs[0]) == pkg.Status.OK
+    assert np.array_equal(f(bo.read()), want[0].view(np.uint32))
+    one = (pkg.Job * 1)(jobs[1])
+    assert api.BNNX_ExecuteBatch(hipdev.handle, one, 1) == pkg.Status.OK
+    assert np.array_equal(f(bo.read()), want[1].view(np.uint32))
+    assert hipdev.execute(jobs[0]) == pkg.Status.OK
+    assert np.array_equal(f(bo.read(40, 80)), want[0][20:30].view(np.uint32))
+    b = ctypes.c_void_p()
+    three = (pkg.Job * 1)(jobs[2])
+    assert api.BNNX_BatchCreate(hipdev.handle, three, 1, ctypes.byref(b)) == pkg.Status.OK
+    assert hipdev.execute(jobs[0]) == pkg.Status.OK                 # mirror valid again
+    assert api.BNNX_BatchLaunch(b) == pkg.Status.OK
+    assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.OK
+    assert np.array_equal(f(bo.read()), want[2].view(np.uint32))
+    api.BNNX_BatchDestroy(b)
+    bi.free()
+    bo.free()
+    for m in mats:
+        m.destroy()
+
+
+def test_device_index_contract(pkg, hip):
+    """BNN_DeviceOpen takes index 0 only (soft-bnn-accelerator.c:317-318); other GPUs
+    are opened through BNNX_DeviceOpenOrdinal."""
+    import ctypes
+    h = ctypes.c_void_p(1234)
+    assert hip.BNN_DeviceOpen(1, ctypes.byref(h)) == pkg.Status.ENOTSUP and h.value is None
+    count = ctypes.c_int()
+    assert ctypes.CDLL("libamdhip64.so").hipGetDeviceCount(ctypes.byref(count)) == 0 and count.value >= 1
+    h = ctypes.c_void_p(1234)
+    assert hip.lib.BNNX_DeviceOpenOrdinal(ctypes.c_uint32(count.value), ctypes.byref(h)) == pkg.Status.ENOTSUP
+    assert h.value is None
+    assert hip.lib.BNNX_DeviceOpenOrdinal(ctypes.c_uint32(0), ctypes.byref(h)) == pkg.Status.OK and h.value
+    caps = pkg.Caps()
+    assert hip.BNN_DeviceGetCaps(h, ctypes.byref(caps)) == pkg.Status.OK and caps.max_in_features == 8192
+    assert hip.BNN_DeviceClose(h) == pkg.Status.OK

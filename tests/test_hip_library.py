@@ -63,6 +63,15 @@ def test_device_open_arguments(pkg, hip):
     h = ctypes.c_void_p(1234)
     assert hip.BNN_DeviceOpen(2**32 - 1, ctypes.byref(h)) == pkg.Status.ENOTSUP
     assert h.value is None
+    # index != 0 is rejected before any device is touched (soft-bnn-accelerator.c:317-318)
+    h = ctypes.c_void_p(1234)
+    assert hip.BNN_DeviceOpen(1, ctypes.byref(h)) == pkg.Status.ENOTSUP
+    assert h.value is None
+    fn = hip.lib.BNNX_DeviceOpenOrdinal
+    assert fn(ctypes.c_uint32(0), None) == pkg.Status.EINVAL
+    h = ctypes.c_void_p(1234)
+    assert fn(ctypes.c_uint32(2**32 - 1), ctypes.byref(h)) == pkg.Status.ENOTSUP
+    assert h.value is None
     assert hip.BNN_DeviceClose(None) == pkg.Status.EINVAL
     caps = pkg.Caps()
     assert hip.BNN_DeviceGetCaps(None, ctypes.byref(caps)) == pkg.Status.EINVAL
