@@ -5,15 +5,19 @@ One step = one pass of the hot path over one batch of synthetic input: 608
 GEMV_F32 jobs, each on its own resident 2048 -> 6144 matrix (1.0 GiB of sign
 bits + scales in total, 4x the 256 MB Infinity Cache) with its own input row,
 issued as one prepared batch launch (one prep launch + one group-dot launch).
-Steps are launched back to back and the timed region ends with one
-BNNX_DeviceSynchronize.  Inputs are resident in HBM before timing starts.
+Inputs are resident in HBM before timing starts.  The GPU is pre-warmed with
+0.5 s of back-to-back steps (it leaves its idle clocks only after some
+milliseconds of work), then the declared warmup steps, a kernel pass (K steps
+with HIP events on every dispatch), and the K timed steps, launched back to
+back and closed by one BNNX_DeviceSynchronize.
 
   value            algorithmic bytes of the step / wall time of the step (GB/s);
                    per GEMV_F32 job 1,802,240 B = 1.125 bit per weight + 4K + 4N;
                    config.sync_GBps is the same step through the synchronous
                    BNNX_ExecuteBatch (one host round trip per step)
   roofline         the dot kernel: algorithmic bytes per launch / its average
-                   duration from HIP events on the device stream, against 8 TB/s
+                   duration from HIP events on the device stream (kernel pass),
+                   against 8 TB/s; step_frac is value / 8 TB/s
   per_call         the same operation through the reference's synchronous
                    BNN_Execute, one job per call (latency-bound at this size)
   cpu_baseline     the reference soft backend (compiled from its source into
@@ -348,8 +352,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--prewarm", type=float, default=0.5,
                     help="seconds of back-to-back steps before the declared warmup (GPU clock ramp)")
-    ap.add_argument("--no-timed-events", action="store_true",
-                    help="no HIP events in the timed steps (kernel durations from a separate pass)")
+    ap.add_argument("--timed-events", action="store_true",
+                    help="also record HIP events in the timed steps (kernel durations from them)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the secondary legs (ops, gemm, e2e, mlp)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -440,30 +444,33 @@ def main():
     for _ in range(args.warmup):
         launch()
     synchronize()
-    # HIP events around every launch on the device stream (recorded by the library,
-    # resolved at the synchronisation) give the kernels' own durations in the same
-    # timed steps; --no-timed-events leaves them out (their cost: see config.event_overhead)
-    dev.kernel_timing(not args.no_timed_events)
+    # Kernel pass: the same K steps with HIP events on every kernel launch of the device
+    # stream (the dispatches' own start and end timestamps, recorded through
+    # hipExtLaunchKernel by the library and resolved at the synchronisation).  Timing
+    # every dispatch slows a step by ~5% (config.event_overhead), so the timed steps
+    # that follow run without events; --timed-events puts them in the timed steps.
+    dev.kernel_timing(True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        launch()
+    synchronize()
+    event_wall = time.perf_counter() - t0
+    dot_ms, dot_n = dev.kernel_timing_read(1)
+    prep_ms, prep_n = dev.kernel_timing_read(0)
+    dev.kernel_timing(bool(args.timed_events))
     t0 = time.perf_counter()
     for _ in range(args.steps):
         launch()
     synchronize()
     wall = time.perf_counter() - t0
-    dot_ms, dot_n = dev.kernel_timing_read(1)
-    prep_ms, prep_n = dev.kernel_timing_read(0)
-    dev.kernel_timing(False)
-    print(f"timed: {args.steps} steps in {wall:.4f} s after {prewarm_steps} pre-warm steps", flush=True)
+    if args.timed_events:
+        dot_ms, dot_n = dev.kernel_timing_read(1)
+        prep_ms, prep_n = dev.kernel_timing_read(0)
+        dev.kernel_timing(False)
+    print(f"timed: {args.steps} steps in {wall:.4f} s after {prewarm_steps} pre-warm steps "
+          f"(kernel pass with events: {event_wall:.4f} s)", flush=True)
     y_stream = bout.read().view(np.float32).reshape(MATRICES, N_OUT)
     assert np.array_equal(y_stream.view(np.uint32), y_batch.view(np.uint32)), "streamed steps differ"
-    # the same number of steps again without events: what the events cost per step
-    for _ in range(args.warmup):
-        launch()
-    synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        launch()
-    synchronize()
-    plain_wall = time.perf_counter() - t0
 
     hip.BNNX_BatchDestroy(batch)
 
@@ -476,13 +483,6 @@ def main():
 
     step_bytes = MATRICES * BYTES_PER_JOB
     value = step_bytes * args.steps / wall / 1e9
-    if dot_n == 0:  # --no-timed-events: kernel durations from a separate pass with events
-        dev.kernel_timing(True)
-        for _ in range(args.steps):
-            step()
-        dot_ms, dot_n = dev.kernel_timing_read(1)
-        prep_ms, prep_n = dev.kernel_timing_read(0)
-        dev.kernel_timing(False)
     dot_avg_s = dot_ms / 1e3 / max(dot_n, 1)
     achieved = step_bytes / dot_avg_s / 1e9
 
@@ -534,9 +534,10 @@ def main():
             "step": "one prepared batch launch (BNNX_BatchLaunch: prep + group-dot), back to back, "
                     "one BNNX_DeviceSynchronize at the end",
             "prewarm_s": args.prewarm,
-            "timed_events": not args.no_timed_events,
-            "event_overhead": round(wall / plain_wall - 1.0, 4),
-            "no_event_GBps": round(step_bytes * args.steps / plain_wall / 1e9, 2),
+            "timed_events": bool(args.timed_events),
+            "kernel_pass": "the same K steps right before the timed ones, HIP events on every dispatch",
+            "event_overhead": round(event_wall / wall - 1.0, 4),
+            "kernel_pass_GBps": round(step_bytes * args.steps / event_wall / 1e9, 2),
             "sync_GBps": round(step_bytes * sync_steps / sync_wall / 1e9, 2),
             "sync_ms_per_step": round(sync_wall / sync_steps * 1e3, 4),
             "hbm_fraction": round(value / HBM_PEAK_GBS, 4),

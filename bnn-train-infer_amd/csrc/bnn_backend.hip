@@ -166,8 +166,17 @@ BNN_Status ensure_events(BNN_Device d) {
     return BNN_OK;
 }
 
-// Launch helper: when timing is on, brackets `launch` with an event pair on the
-// device stream (no extra synchronisation unless the slots run out).
+}  // namespace
+
+namespace bnnhip {
+thread_local LaunchEvents t_launch_events = {nullptr, nullptr};
+}  // namespace bnnhip
+
+namespace {
+
+// Launch helper: when timing is on, the kernel that `launch` enqueues records its own
+// start and end into an event pair (hipExtLaunchKernel: timestamps of the dispatch
+// itself, no marker packets between kernels; no synchronisation unless the slots run out).
 template <typename F>
 hipError_t timed(BNN_Device d, int kind, F&& launch) {
     if (!d->timing)
@@ -180,11 +189,9 @@ hipError_t timed(BNN_Device d, int kind, F&& launch) {
             return e;
     }
     const int slot = d->ev_used;
-    hipError_t e = hipEventRecord(d->ev_begin[slot], d->stream);
-    if (e == hipSuccess)
-        e = launch();
-    if (e == hipSuccess)
-        e = hipEventRecord(d->ev_end[slot], d->stream);
+    t_launch_events = LaunchEvents{d->ev_begin[slot], d->ev_end[slot]};
+    hipError_t e = launch();
+    t_launch_events = LaunchEvents{nullptr, nullptr};
     if (e == hipSuccess) {
         d->ev_kind[slot] = kind;
         d->ev_used = slot + 1;

@@ -657,19 +657,19 @@ hipError_t launch_fused(hipStream_t stream, const FusedArgs& args, uint32_t tile
     const dim3 g(grid), b(kFusedThreads);
     if (args.jobs == nullptr) {  // a single job in the kernel arguments
         if (args.width <= 2048u)
-            hipLaunchKernelGGL((k_fused<1, 2, false, true>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+            launch_kernel((k_fused<1, 2, false, true>), g, b, 0, stream, args, tiles, seq, flag, host_status);
         else
-            hipLaunchKernelGGL((k_fused<kWideGpw, kWideEpt, false, true>), g, b, 0, stream, args, tiles, seq, flag,
+            launch_kernel((k_fused<kWideGpw, kWideEpt, false, true>), g, b, 0, stream, args, tiles, seq, flag,
                                host_status);
     } else if (args.width <= 2048u && !paired) {
-        hipLaunchKernelGGL((k_fused<1, 2, false, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+        launch_kernel((k_fused<1, 2, false, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
     } else if (args.width <= 2048u) {
-        hipLaunchKernelGGL((k_fused<1, 2, true, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+        launch_kernel((k_fused<1, 2, true, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
     } else if (!paired) {
-        hipLaunchKernelGGL((k_fused<kWideGpw, kWideEpt, false, false>), g, b, 0, stream, args, tiles, seq, flag,
+        launch_kernel((k_fused<kWideGpw, kWideEpt, false, false>), g, b, 0, stream, args, tiles, seq, flag,
                            host_status);
     } else {
-        hipLaunchKernelGGL((k_fused<kWideGpw, kWideEpt, true, false>), g, b, 0, stream, args, tiles, seq, flag,
+        launch_kernel((k_fused<kWideGpw, kWideEpt, true, false>), g, b, 0, stream, args, tiles, seq, flag,
                            host_status);
     }
     return hipGetLastError();

@@ -807,7 +807,7 @@ template <int TMS, int TNS, int W, int DEPTH>
 hipError_t launch_ks(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
     const uint32_t mtiles = (job.rows + 16u * TMS - 1u) / (16u * TMS);
     const uint32_t ntiles = (job.n + 16u * TNS - 1u) / (16u * TNS);
-    hipLaunchKernelGGL((k_gemm_ks<TMS, TNS, W, DEPTH>), dim3(mtiles * ntiles), dim3(64 * W), 0, stream, job, mtiles,
+    launch_kernel((k_gemm_ks<TMS, TNS, W, DEPTH>), dim3(mtiles * ntiles), dim3(64 * W), 0, stream, job, mtiles,
                        seq, flag);
     return hipGetLastError();
 }
@@ -817,10 +817,10 @@ hipError_t launch_t(hipStream_t stream, const GemmJob& job, uint64_t seq, const 
     const uint32_t mtiles = (job.rows + 32u * MS - 1u) / (32u * MS);
     const uint32_t ntiles = (job.n + 32u * NS - 1u) / (32u * NS);
     if (job.mode == MODE_DOT_I16)
-        hipLaunchKernelGGL((k_gemm<MS, NS, true>), dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq,
+        launch_kernel((k_gemm<MS, NS, true>), dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq,
                            flag);
     else
-        hipLaunchKernelGGL((k_gemm<MS, NS, false>), dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq,
+        launch_kernel((k_gemm<MS, NS, false>), dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq,
                            flag);
     return hipGetLastError();
 }
@@ -833,7 +833,7 @@ hipError_t launch_expand(hipStream_t stream, const uint4* wbits, uint32_t tiles,
     uint64_t blocks = (total + 255u) / 256u;
     if (blocks > 4096u)
         blocks = 4096u;
-    hipLaunchKernelGGL(k_expand, dim3((uint32_t)blocks), dim3(256), 0, stream, wbits, tiles, groups, n_pad, wbytes);
+    launch_kernel(k_expand, dim3((uint32_t)blocks), dim3(256), 0, stream, wbits, tiles, groups, n_pad, wbytes);
     return hipGetLastError();
 }
 
@@ -862,14 +862,14 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
     // give most CUs one (6144 -> 2048 at 1024 rows: 35 vs 62 us for 64 x 128 k_gemm)
     if (job.mode != MODE_DOT_I16 && blocks(128, 128) < cus && blocks(64, 128) >= cus * 3u / 4u) {
         const uint32_t mtiles = (job.rows + 63u) / 64u, ntiles = (job.n + 127u) / 128u;
-        hipLaunchKernelGGL(k_gemm_pipe<2>, dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq, flag);
+        launch_kernel(k_gemm_pipe<2>, dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq, flag);
         return hipGetLastError();
     }
 #endif
     if (BNN_GEMM_BIG && job.mode != MODE_DOT_I16 && blocks(kBigTile, kBigTile) >= cus) {
         const uint32_t mtiles = (job.rows + kBigTile - 1u) / kBigTile;
         const uint32_t ntiles = (job.n + kBigTile - 1u) / kBigTile;
-        hipLaunchKernelGGL(k_gemm_big, dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq, flag);
+        launch_kernel(k_gemm_big, dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq, flag);
         return hipGetLastError();
     }
 #if BNN_GEMM_KS

@@ -16,6 +16,7 @@
 //   q     [row][K]  i8       : the quantised row itself (matrix-core path)
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -143,6 +144,25 @@ struct FusedArgs {
     float* mirror;         // single F32 job: host memory that also receives the output row (may be null)
     int32_t dot_out;       // DOT_GROUPS: out receives int16 D[n][group] instead of the sums
 };
+
+// Kernel timing: when `start` is set, the next kernel launched through launch_kernel
+// records its own start and end into these events (taken from the dispatch itself,
+// so timing adds no packet between kernels); the launch clears them.
+struct LaunchEvents {
+    hipEvent_t start, stop;
+};
+extern thread_local LaunchEvents t_launch_events;
+
+template <typename F, typename... Args>
+inline void launch_kernel(F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t stream, Args... args) {
+    if (t_launch_events.start != nullptr) {
+        const LaunchEvents ev = t_launch_events;
+        t_launch_events = LaunchEvents{nullptr, nullptr};
+        hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, ev.start, ev.stop, 0u, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, shmem, stream, args...);
+    }
+}
 
 // Host-side launchers (bnn_kernels.hip).  All are asynchronous on `stream`.
 // Single job: descriptor passed by value.  `validate_only` runs only the

@@ -745,12 +745,12 @@ hipError_t launch_dot_long(hipStream_t stream, const DotJob* jobs, const uint32_
     const uint32_t grid = (items + kLongWaves - 1u) / kLongWaves;
     const dim3 block(64 * kLongWaves);
     switch ((max_groups + kLongBlock - 1u) / kLongBlock) {
-    case 3: hipLaunchKernelGGL((k_dot_wave_long<MAP, 3>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
-    case 4: hipLaunchKernelGGL((k_dot_wave_long<MAP, 4>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
-    case 5: hipLaunchKernelGGL((k_dot_wave_long<MAP, 5>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
-    case 6: hipLaunchKernelGGL((k_dot_wave_long<MAP, 6>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
-    case 7: hipLaunchKernelGGL((k_dot_wave_long<MAP, 7>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
-    default: hipLaunchKernelGGL((k_dot_wave_long<MAP, 8>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 3: launch_kernel((k_dot_wave_long<MAP, 3>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 4: launch_kernel((k_dot_wave_long<MAP, 4>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 5: launch_kernel((k_dot_wave_long<MAP, 5>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 6: launch_kernel((k_dot_wave_long<MAP, 6>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 7: launch_kernel((k_dot_wave_long<MAP, 7>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    default: launch_kernel((k_dot_wave_long<MAP, 8>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
     }
     return hipGetLastError();
 }
@@ -758,7 +758,7 @@ hipError_t launch_dot_long(hipStream_t stream, const DotJob* jobs, const uint32_
 template <int MAXG, int MAP, int TPI>
 hipError_t launch_dot_t(hipStream_t stream, const DotJob& single, const DotJob* jobs, const uint32_t* item_job,
                         uint32_t items, uint32_t uniform_items, uint32_t grid, uint64_t seq, const uint64_t* flag) {
-    hipLaunchKernelGGL((k_dot<MAXG, MAP, TPI, BNN_DOT_PREFETCH != 0>), dim3(grid), dim3(64 * kDotWaves), 0, stream,
+    launch_kernel((k_dot<MAXG, MAP, TPI, BNN_DOT_PREFETCH != 0>), dim3(grid), dim3(64 * kDotWaves), 0, stream,
                        single, jobs, item_job, items, uniform_items, seq, flag);
     return hipGetLastError();
 }
@@ -785,13 +785,13 @@ hipError_t launch_prep_nt(hipStream_t stream, uint32_t blocks, uint32_t max_k, c
     constexpr int kMaxPer = (int)kMaxFeatures / NT;
     const uint32_t per = (max_k + NT - 1u) / NT;
     if (per <= (uint32_t)kMaxPer / 4u)
-        hipLaunchKernelGGL((k_prep<BATCH, NT, kMaxPer / 4>), dim3(blocks), dim3(NT), 0, stream, single, jobs,
+        launch_kernel((k_prep<BATCH, NT, kMaxPer / 4>), dim3(blocks), dim3(NT), 0, stream, single, jobs,
                            block_job, validate_only, seq, flag, host_status);
     else if (per <= (uint32_t)kMaxPer / 2u)
-        hipLaunchKernelGGL((k_prep<BATCH, NT, kMaxPer / 2>), dim3(blocks), dim3(NT), 0, stream, single, jobs,
+        launch_kernel((k_prep<BATCH, NT, kMaxPer / 2>), dim3(blocks), dim3(NT), 0, stream, single, jobs,
                            block_job, validate_only, seq, flag, host_status);
     else
-        hipLaunchKernelGGL((k_prep<BATCH, NT, kMaxPer>), dim3(blocks), dim3(NT), 0, stream, single, jobs,
+        launch_kernel((k_prep<BATCH, NT, kMaxPer>), dim3(blocks), dim3(NT), 0, stream, single, jobs,
                            block_job, validate_only, seq, flag, host_status);
     return hipGetLastError();
 }
@@ -853,10 +853,10 @@ hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32
         const uint32_t grid = (items + BNN_DOT_WAVE_WG_WAVES - 1u) / BNN_DOT_WAVE_WG_WAVES;
         const dim3 block(64 * BNN_DOT_WAVE_WG_WAVES);
         if (uniform_items)
-            hipLaunchKernelGGL(k_dot_wave<MAP_UNIFORM>, dim3(grid), block, 0, stream, jobs, item_job, items,
+            launch_kernel(k_dot_wave<MAP_UNIFORM>, dim3(grid), block, 0, stream, jobs, item_job, items,
                                uniform_items, seq, flag);
         else
-            hipLaunchKernelGGL(k_dot_wave<MAP_TABLE>, dim3(grid), block, 0, stream, jobs, item_job, items, 0u, seq,
+            launch_kernel(k_dot_wave<MAP_TABLE>, dim3(grid), block, 0, stream, jobs, item_job, items, 0u, seq,
                                flag);
         return hipGetLastError();
     }
@@ -882,7 +882,7 @@ hipError_t launch_scatter(hipStream_t stream, const unsigned char* src, size_t s
     size_t blocks = (row_bytes + 255u) / 256u;
     if (blocks > 1024u)
         blocks = 1024u;
-    hipLaunchKernelGGL(k_scatter, dim3((uint32_t)blocks, rows), dim3(256), 0, stream, src, src_stride, dst,
+    launch_kernel(k_scatter, dim3((uint32_t)blocks, rows), dim3(256), 0, stream, src, src_stride, dst,
                        dst_stride, row_bytes, seq, flag);
     return hipGetLastError();
 }

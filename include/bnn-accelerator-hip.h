@@ -34,9 +34,11 @@ BNN_Status BNNX_DeviceOpenOrdinal(uint32_t hip_ordinal, BNN_Device* out_device);
 BNN_Status BNNX_DeviceStream(BNN_Device device, void** out_stream);
 
 /*
- * enable != 0: start recording HIP events around every kernel launch of the
- * device and reset the totals; enable == 0: stop.  Timing adds one event pair
- * and one synchronisation per launch, so leave it off outside measurement.
+ * enable != 0: every kernel launch of the device records its own start and end
+ * into a HIP event pair (hipExtLaunchKernel), and the totals are reset; enable == 0:
+ * stop.  Events are resolved at the next synchronisation of the call or of
+ * BNNX_DeviceSynchronize (and every 1024 launches).  Profiled dispatches run a few
+ * percent slower, so leave timing off outside measurement.
  */
 BNN_Status BNNX_KernelTiming(BNN_Device device, int enable);
 
