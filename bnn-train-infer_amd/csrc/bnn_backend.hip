@@ -12,6 +12,7 @@
 #include <fenv.h>
 #include <float.h>
 #include <hip/hip_runtime.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -226,7 +227,40 @@ BNN_Status op_types(BNN_Operation op, BNN_Type* in, BNN_Type* out) {
 // Devices (soft-bnn-accelerator.c:310-356)
 // ---------------------------------------------------------------------------
 
+// ---------------------------------------------------------------------------
+// Fixed device scratch of BNNX_ExecuteNoAlloc: one copy per GPU, resident until the
+// process ends.  Host code never passes the symbol itself to a kernel (on the host it
+// is only a stand-in for the device variable): open_device resolves each GPU's copy
+// once with hipGetSymbolAddress, and every later use goes through that address.
+// ---------------------------------------------------------------------------
+constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
 namespace {
+
+constexpr int kMaxOrdinals = 64;
+pthread_mutex_t g_static_lock = PTHREAD_MUTEX_INITIALIZER;
+unsigned char* g_static_scratch[kMaxOrdinals];  // per HIP ordinal, null until resolved
+
+// The current device's copy of `scratch` (the caller has made `ordinal` current).
+hipError_t resolve_static_scratch(int ordinal, unsigned char** out) {
+    *out = nullptr;
+    if (ordinal < 0 || ordinal >= kMaxOrdinals)
+        return hipErrorInvalidDevice;
+    pthread_mutex_lock(&g_static_lock);
+    hipError_t e = hipSuccess;
+    if (g_static_scratch[ordinal] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e == hipSuccess && p == nullptr)
+            e = hipErrorInvalidSymbol;
+        if (e == hipSuccess)
+            g_static_scratch[ordinal] = static_cast<unsigned char*>(p);
+    }
+    *out = g_static_scratch[ordinal];
+    pthread_mutex_unlock(&g_static_lock);
+    return e;
+}
 
 // Opens HIP device `ordinal` (BNN_DeviceOpen: 0; BNNX_DeviceOpenOrdinal: any).
 BNN_Status open_device(int ordinal, BNN_Device* out_device) {
@@ -235,7 +269,7 @@ BNN_Status open_device(int ordinal, BNN_Device* out_device) {
         (void)hipGetLastError();
         return BNN_ENOTSUP;
     }
-    if (ordinal < 0 || ordinal >= count)
+    if (ordinal < 0 || ordinal >= count || ordinal >= kMaxOrdinals)
         return BNN_ENOTSUP;
     float one = 1.0f;
     uint32_t one_bits;
@@ -248,6 +282,8 @@ BNN_Status open_device(int ordinal, BNN_Device* out_device) {
         return BNN_ENOMEM;
     d->ordinal = ordinal;
     hipError_t e = hipSetDevice(d->ordinal);
+    if (e == hipSuccess)
+        e = resolve_static_scratch(d->ordinal, &d->static_scratch);
     int cus = 0;
     if (e == hipSuccess)
         e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, d->ordinal);
@@ -888,6 +924,28 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
         p.m->n_pad = n_pad;
     }
     return run_rows(device, job, p, mfma, device->scratch, chunk, rows_bytes, e);
+}
+
+// BNN_Execute without any allocation: the quantised rows (and staging rows for
+// unaligned output views) live in this GPU's fixed `scratch` array, multi-row jobs
+// run on the bit-plane kernels in chunks that fit it, and single-row outputs are
+// not mirrored into host memory.
+EXPORT BNN_Status BNNX_ExecuteNoAlloc(BNN_Device device, const BNN_Job* job) {
+    if (device != nullptr)
+        device->mirror_buf = nullptr;
+    JobPlan p;
+    BNN_Status st = plan_job(device, job, &p);
+    if (st != BNN_OK)
+        return st;
+    if (single_row_path(job, p))
+        return run_single_row(device, job, p, false);
+    size_t chunk = 0, rows_bytes = 0;
+    chunk_rows(p, job->rows, false, kStaticScratchBytes, &chunk, &rows_bytes);
+    if (chunk == 0 || device->static_scratch == nullptr)
+        return BNN_ENOMEM;  // one row's quantised form and staging exceed the fixed scratch
+    if (hipSetDevice(device->ordinal) != hipSuccess)
+        return BNN_EIO;
+    return run_rows(device, job, p, false, device->static_scratch, chunk, rows_bytes, hipSuccess);
 }
 
 // ---------------------------------------------------------------------------

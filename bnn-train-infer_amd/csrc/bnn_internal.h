@@ -231,6 +231,7 @@ struct bnn_accel_device {
     uint64_t* status_host;
     unsigned char* scratch;    // grow-only device scratch
     size_t scratch_bytes;
+    unsigned char* static_scratch;  // this GPU's fixed scratch array (BNNX_ExecuteNoAlloc)
     unsigned char* pinned;     // grow-only pinned host staging for transfers
     size_t pinned_bytes;
     unsigned char* wring;      // pinned ring for small writes, copied asynchronously on `stream`

@@ -61,6 +61,22 @@ BNN_Status BNNX_KernelTimingRead(BNN_Device device, uint32_t kind, double* total
 BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint32_t count);
 
 /*
+ * BNN_Execute that allocates nothing.  No counterpart in the reference API: it is
+ * for callers that cannot allocate memory at call time (tight serving loops,
+ * harnesses that forbid hipMalloc).  Same checks, statuses and results as
+ * BNN_Execute for every job.  A multi-row job keeps its rows' quantised forms (and,
+ * for an output view that is not naturally aligned, its staged output rows) in one
+ * fixed 8 MiB device array per GPU, created with the library's code object and held
+ * until the process ends; the rows run in chunks that fit it, on the bit-plane dot
+ * kernels (never on the matrix cores, whose +1/-1 weight copy BNN_Execute allocates).
+ * A job whose single row does not fit the array is rejected with BNN_ENOMEM (none
+ * does within the 8192-feature limits of BNN_DeviceGetCaps).  Single-row outputs are
+ * not mirrored in host memory.  Every call on one GPU, from any BNN_Device handle
+ * opened on it, shares that array: calls that overlap in time on one GPU race.
+ */
+BNN_Status BNNX_ExecuteNoAlloc(BNN_Device device, const BNN_Job* job);
+
+/*
  * Prepared batches: the checks and job tables of BNNX_ExecuteBatch done once, for
  * callers that run the same set of jobs many times (a model's layers, token after
  * token) and keep their activations on the device.
