@@ -507,17 +507,14 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     }
     float amax = __uint_as_float(abits);
     float s = 1.0f;
-    if (amax != 0.0f && !int_row) {
-        s = amax / 127.0f;
-        if (s == 0.0f)
-            s = __int_as_float(1);  // smallest subnormal
-    }
+    if (!int_row)
+        s = quant_row_scale(amax);
 
     // 4. quantise the wave's own groups; their bit planes are ballots (wave-uniform
     // masks: kept in scalar registers for one group per wave, else in LDS), and
     // -sum(Q) per group from the same masks; no exchange between waves
     const float rcp = 1.0f / s;
-    const bool exact = s < 0x1p-126f;  // 1 / s would overflow
+    const bool exact = quant_exact(s);  // 1 / s may overflow
     int q[EPT];
 #pragma unroll
     for (int i = 0; i < EPT; ++i)

@@ -22,6 +22,7 @@
 #include <stdint.h>
 
 #include "bnn-accelerator.h"
+#include "bnn_quant.h"
 
 namespace bnnhip {
 
@@ -195,23 +196,6 @@ hipError_t launch_expand(hipStream_t stream, const uint4* wbits, uint32_t tiles,
 hipError_t launch_scatter(hipStream_t stream, const unsigned char* src, size_t src_stride,
                           unsigned char* dst, size_t dst_stride, size_t row_bytes, uint32_t rows,
                           uint64_t seq, const uint64_t* flag);
-
-// Q = clamp(round-half-away(F32(x / s)), -127, 127)  (soft-bnn-accelerator.c:197-208),
-// given rcp = F32(1 / s) and exact = (s is subnormal, where 1 / s overflows).
-// y = F32(x * F32(1 / s)) is within 1.6e-5 of x / s (|x / s| <= 127) and F32(x / s)
-// within 3.9e-6, so both round to the same integer unless y lies within 2^-14 of a
-// half-integer; those lanes (and all, when s is subnormal: `exact`) divide.
-__device__ __forceinline__ int quantize_rcp(float x, float s, float rcp, bool exact) {
-    float y = x * rcp;
-    float t = truncf(y), d = y - t;
-    if (exact || fabsf(fabsf(d) - 0.5f) < 0x1p-14f) {
-        y = x / s;
-        t = truncf(y);
-        d = y - t;
-    }
-    const float q = t + (fabsf(d) >= 0.5f ? copysignf(1.0f, y) : 0.0f);
-    return (int)fminf(fmaxf(q, -127.0f), 127.0f);
-}
 
 }  // namespace bnnhip
 

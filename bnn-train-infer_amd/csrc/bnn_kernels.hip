@@ -31,7 +31,6 @@ namespace {
 
 constexpr int kLdsPitch = 65;                     // words per group row of the D/term exchange
 
-__device__ __forceinline__ float f32_min_subnormal() { return __int_as_float(1); }
 
 // Pointers taken from job descriptors are generic; loading through these
 // global-address-space views makes the compiler emit global_load, not flat_load.
@@ -176,15 +175,11 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
 #pragma unroll
         for (int w = 1; w < kPrepWaves; ++w)
             amax = fmaxf(amax, red_max[w]);
-        if (amax != 0.0f) {
-            s = amax / 127.0f;
-            if (s == 0.0f)
-                s = f32_min_subnormal();
-        }
+        s = quant_row_scale(amax);
     }
 
     const float rcp = 1.0f / s;
-    const bool exact = s < 0x1p-126f;  // 1 / s would overflow
+    const bool exact = quant_exact(s);  // 1 / s may overflow
     // pass 2: quantise; in iteration i wave w owns the 64 consecutive k of half (w & 1)
     // of group kPrepGroupsPerIter*i + (w >> 1)
     uint32_t* planes = j.planes ? j.planes + (size_t)m * groups * kPlaneWords : nullptr;
