@@ -292,8 +292,8 @@ __device__ __forceinline__ void load_tile(const LaneRow& lr, uint32_t G, uint32_
 // SINGLE: one job in the kernel arguments (BNN_Execute): its row may be int8, its output
 // DOT_GROUPS' D or mirrored into host memory.  Batches compile without those branches.
 template <int GPW, int EPT, bool PAIRED, bool SINGLE>
-__global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t tiles_total, uint64_t seq,
-                                                         uint64_t* flag, uint64_t* host_status) {
+__device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_total, uint64_t seq, uint64_t* flag,
+                                           uint64_t* host_status) {
     static_assert(EPT == 2 * GPW, "a wave quantises exactly the groups of its dots");
     __shared__ float4 scratch4[(kFusedMaxWidth + kFusedPad) / 4];  // squares, then products [2][group][64]
     // bit planes of the groups (GPW > 1; one group per wave keeps them in scalar registers),
@@ -641,6 +641,25 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
         lr = nlr;
         cur = nxt;
         buf ^= 1u;
+    }
+}
+
+template <int GPW, int EPT, bool PAIRED, bool SINGLE>
+__global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t tiles_total, uint64_t seq,
+                                                         uint64_t* flag, uint64_t* host_status) {
+    fused_body<GPW, EPT, PAIRED, SINGLE>(fa, tiles_total, seq, flag, host_status);
+    // Completion signal of a single job, so that the host need not wait for the end of the
+    // kernel: in this form every global store (outputs, host mirror, error words) comes from
+    // wave 0, which makes them visible system-wide before its workgroup counts itself; the
+    // last workgroup to count then stores seq into the pinned host word.
+    if (SINGLE && fa.done_host != nullptr && threadIdx.x < 64u) {
+        __threadfence_system();
+        if (threadIdx.x == 0) {
+            const uint64_t prev =
+                __hip_atomic_fetch_add(fa.done_count, (uint64_t)1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            if (prev + 1u == fa.done_target)
+                __hip_atomic_store(fa.done_host, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
     }
 }
 
