@@ -1,12 +1,14 @@
-// GGUF v3 reader: memory-maps the file, parses the metadata the engine needs and the
-// tensor table, and checks every tensor's extent against the mapping.
+// GGUF v3 files: memory-mapped, indexed once, values decoded on request.
 //
-// Accepts and rejects what the reference reader does (bnn-sw-v2/gguf.c:404-490):
-// version 3 only, at most 4096 metadata entries, alignment 1..4096 (default 32),
-// tensor types F32 (0), F16 (1) and Q1_0 (41, 18-byte blocks over [in, out] with
-// in % 128 == 0), rank 1..4, non-empty tensor table, general.architecture present.
-// Typed keys with the wrong type are format errors; unknown keys are skipped.
-#include "engine_internal.h"
+// What is accepted follows the reference reader (bnn-sw-v2/gguf.c:404-490), whose
+// files and statuses callers share: version 3 only; at most 4096 metadata entries;
+// values nest at most four arrays deep; general.alignment in 1..4096 (default 32);
+// tensor ranks 1..4 and types F32 (0), F16 (1) and Q1_0 (41, 18-byte blocks over
+// [in, out] with in % 128 == 0); a non-empty tensor table; general.architecture
+// present; every tensor inside the data section.  The keys this engine reads have a
+// fixed kind (integer, real, text, text array, word array) and a present key of the
+// wrong kind -- or a repeated array key -- makes the file malformed.
+#include "engine.hpp"
 
 #include <fcntl.h>
 #include <sys/mman.h>
@@ -14,478 +16,456 @@
 #include <unistd.h>
 
 #include <cmath>
-#include <cstdlib>
 #include <cstring>
 
 namespace bnne {
 namespace {
 
+// GGUF value types
 enum : uint32_t {
-    kU8 = 0, kI8 = 1, kU16 = 2, kI16 = 3, kU32 = 4, kI32 = 5, kF32 = 6, kBool = 7,
-    kString = 8, kArray = 9, kU64 = 10, kI64 = 11, kF64 = 12
+    tU8 = 0, tI8 = 1, tU16 = 2, tI16 = 3, tU32 = 4, tI32 = 5, tF32 = 6, tBool = 7,
+    tString = 8, tArray = 9, tU64 = 10, tI64 = 11, tF64 = 12
 };
 
-// Little-endian reader over [p, end); any overrun clears ok and yields zeros.
-struct Reader {
-    const uint8_t* p;
-    const uint8_t* end;
-    bool ok;
+constexpr uint64_t kMaxEntries = 4096;
+constexpr unsigned kMaxNesting = 4;
 
-    bool need(uint64_t n) {
-        if (!ok || n > (uint64_t)(end - p))
-            ok = false;
-        return ok;
-    }
-    uint64_t uint(unsigned bytes) {
-        if (!need(bytes))
-            return 0;
-        uint64_t v = 0;
-        for (unsigned i = 0; i < bytes; ++i)
-            v |= (uint64_t)p[i] << (8 * i);
-        p += bytes;
-        return v;
-    }
-    uint32_t u32() { return (uint32_t)uint(4); }
-    uint64_t u64() { return uint(8); }
-    GgufString str() {
-        GgufString s = {nullptr, 0};
-        const uint64_t n = u64();
-        if (!ok || n > UINT32_MAX || !need(n)) {
-            ok = false;
-            return s;
-        }
-        s.data = p;
-        s.length = (uint32_t)n;
-        p += n;
-        return s;
-    }
-};
-
-unsigned scalar_bytes(uint32_t type) {
+unsigned fixed_size(uint32_t type) {
     switch (type) {
-    case kU8: case kI8: case kBool: return 1;
-    case kU16: case kI16: return 2;
-    case kU32: case kI32: case kF32: return 4;
-    case kU64: case kI64: case kF64: return 8;
+    case tU8: case tI8: case tBool: return 1;
+    case tU16: case tI16: return 2;
+    case tU32: case tI32: case tF32: return 4;
+    case tU64: case tI64: case tF64: return 8;
     default: return 0;
     }
 }
 
-bool skip(Reader& r, uint32_t type, unsigned depth) {
-    if (!r.ok || depth > 4)
-        return false;
-    if (const unsigned n = scalar_bytes(type)) {
-        r.uint(n);
-        return r.ok;
-    }
-    if (type == kString) {
-        r.str();
-        return r.ok;
-    }
-    if (type != kArray)
-        return false;
-    const uint32_t element = r.u32();
-    const uint64_t count = r.u64();
-    for (uint64_t i = 0; r.ok && i < count; ++i)
-        if (!skip(r, element, depth + 1))
-            return false;
-    return r.ok;
+uint64_t le(const uint8_t* p, unsigned n) {
+    uint64_t v = 0;
+    for (unsigned i = 0; i < n; ++i)
+        v |= (uint64_t)p[i] << (8 * i);
+    return v;
 }
 
-// Integer-typed value (any width, signed values sign-extended), as gguf.c:126-140.
-bool read_integer(Reader& r, uint32_t type, uint64_t* out) {
-    switch (type) {
-    case kU8: case kBool: *out = r.uint(1); break;
-    case kI8: *out = (uint64_t)(int64_t)(int8_t)r.uint(1); break;
-    case kU16: *out = r.uint(2); break;
-    case kI16: *out = (uint64_t)(int64_t)(int16_t)r.uint(2); break;
-    case kU32: *out = r.uint(4); break;
-    case kI32: *out = (uint64_t)(int64_t)(int32_t)r.uint(4); break;
-    case kU64: case kI64: *out = r.uint(8); break;
+// A forward-only view of [at, end).  Every read checks its own bounds; a failed read
+// leaves `at` at null, after which all reads fail.
+struct Bytes {
+    const uint8_t* at;
+    const uint8_t* end;
+
+    bool have(uint64_t n) const { return at && n <= (uint64_t)(end - at); }
+    uint64_t take(unsigned n) {
+        if (!have(n)) {
+            at = nullptr;
+            return 0;
+        }
+        const uint64_t v = le(at, n);
+        at += n;
+        return v;
+    }
+    std::string_view string() {
+        const uint64_t n = take(8);
+        if (n > UINT32_MAX || !have(n)) {
+            at = nullptr;
+            return {};
+        }
+        const std::string_view s(reinterpret_cast<const char*>(at), (size_t)n);
+        at += n;
+        return s;
+    }
+    // moves past one value of `type`; false for an unknown type or too deep a nesting
+    bool skip(uint32_t type, unsigned depth) {
+        if (!at || depth > kMaxNesting)
+            return false;
+        if (const unsigned n = fixed_size(type)) {
+            take(n);
+        } else if (type == tString) {
+            string();
+        } else if (type == tArray) {
+            const uint32_t element = (uint32_t)take(4);
+            const uint64_t count = take(8);
+            if (const unsigned n = fixed_size(element)) {  // a block of fixed-size elements
+                if (!at || count > UINT64_MAX / n || !have(count * n))
+                    return at = nullptr, false;
+                at += count * n;
+                return true;
+            }
+            for (uint64_t i = 0; at && i < count; ++i)
+                if (!skip(element, depth + 1))
+                    return false;
+        } else {
+            return false;
+        }
+        return at != nullptr;
+    }
+};
+
+[[noreturn]] void malformed(const char* path, const char* what) { raise(BNNE_EFORMAT, "%s: %s", path, what); }
+
+// The kinds of the keys this engine reads.
+enum class Kind { Integer, Real, Text, Texts, Words };
+
+struct KnownKey {
+    const char* key;
+    Kind kind;
+};
+const KnownKey kKnownKeys[] = {
+    {"general.architecture", Kind::Text},
+    {"general.alignment", Kind::Integer},
+    {"qwen3.block_count", Kind::Integer},
+    {"qwen3.context_length", Kind::Integer},
+    {"qwen3.embedding_length", Kind::Integer},
+    {"qwen3.feed_forward_length", Kind::Integer},
+    {"qwen3.attention.head_count", Kind::Integer},
+    {"qwen3.attention.head_count_kv", Kind::Integer},
+    {"qwen3.attention.key_length", Kind::Integer},
+    {"qwen3.attention.value_length", Kind::Integer},
+    {"qwen3.attention.layer_norm_rms_epsilon", Kind::Real},
+    {"qwen3.rope.freq_base", Kind::Real},
+    {"qwen3.rope.scaling.type", Kind::Text},
+    {"qwen3.rope.scaling.factor", Kind::Real},
+    {"qwen3.rope.scaling.original_context_length", Kind::Integer},
+    {"bnn-mlp.block_count", Kind::Integer},
+    {"bnn-mlp.class_count", Kind::Integer},
+    {"bnn-mlp.input_features", Kind::Integer},
+    {"bnn-mlp.input_pixels", Kind::Integer},
+    {"bnn-mlp.input_mean", Kind::Real},
+    {"bnn-mlp.input_std", Kind::Real},
+    {"bnn-mlp.labels", Kind::Texts},
+    {"tokenizer.ggml.model", Kind::Text},
+    {"tokenizer.ggml.pre", Kind::Text},
+    {"tokenizer.ggml.tokens", Kind::Texts},
+    {"tokenizer.ggml.token_type", Kind::Words},
+    {"tokenizer.ggml.merges", Kind::Texts},
+    {"tokenizer.ggml.eos_token_id", Kind::Integer},
+    {"tokenizer.ggml.bos_token_id", Kind::Integer},
+    {"tokenizer.ggml.padding_token_id", Kind::Integer},
+    {"tokenizer.ggml.add_bos_token", Kind::Integer},
+};
+
+// "bnn-mlp.block.<i>.activation" with i in decimal: its block index (capped at 1000).
+std::optional<uint32_t> activation_index(std::string_view key) {
+    constexpr std::string_view head = "bnn-mlp.block.", tail = ".activation";
+    if (key.size() <= head.size() + tail.size() || key.substr(0, head.size()) != head ||
+        key.substr(key.size() - tail.size()) != tail)
+        return std::nullopt;
+    uint32_t index = 0;
+    for (char ch : key.substr(head.size(), key.size() - head.size() - tail.size())) {
+        if (ch < '0' || ch > '9')
+            return std::nullopt;
+        index = index * 10u + (uint32_t)(ch - '0');
+        if (index > 1000u)
+            index = 1000u;
+    }
+    return index;
+}
+bool is_activation_key(std::string_view key) { return activation_index(key).has_value(); }
+
+std::optional<Kind> kind_of(std::string_view key) {
+    for (const KnownKey& k : kKnownKeys)
+        if (key == k.key)
+            return k.kind;
+    if (is_activation_key(key))
+        return Kind::Text;
+    return std::nullopt;
+}
+
+// Integer value of a scalar entry (any integer type); false for other types.
+bool decode_integer(const GgufFile::Entry& e, uint64_t* out) {
+    const uint8_t* p = e.value;
+    switch (e.type) {
+    case tU8: case tBool: *out = p[0]; return true;
+    case tI8: *out = (uint64_t)(int64_t)(int8_t)p[0]; return true;
+    case tU16: *out = le(p, 2); return true;
+    case tI16: *out = (uint64_t)(int64_t)(int16_t)le(p, 2); return true;
+    case tU32: *out = le(p, 4); return true;
+    case tI32: *out = (uint64_t)(int64_t)(int32_t)le(p, 4); return true;
+    case tU64: case tI64: *out = le(p, 8); return true;
     default: return false;
     }
-    return r.ok;
 }
 
-bool read_float(Reader& r, uint32_t type, float* out) {
-    if (type == kF32) {
-        const uint32_t bits = r.u32();
+bool decode_real(const GgufFile::Entry& e, float* out) {
+    if (e.type == tF32) {
+        const uint32_t bits = (uint32_t)le(e.value, 4);
         std::memcpy(out, &bits, 4);
-    } else if (type == kF64) {
-        const uint64_t bits = r.u64();
+    } else if (e.type == tF64) {
+        const uint64_t bits = le(e.value, 8);
         double d;
         std::memcpy(&d, &bits, 8);
         *out = (float)d;
     } else {
         return false;
     }
-    return r.ok && std::isfinite(*out);
+    return std::isfinite(*out);
 }
 
-bool read_text(Reader& r, uint32_t type, char* dst, size_t size) {
-    if (type != kString)
+// Element type and count of an array entry.
+bool array_header(const GgufFile::Entry& e, uint32_t* element, uint64_t* count) {
+    if (e.type != tArray)
         return false;
-    const GgufString s = r.str();
-    if (!r.ok)
-        return false;
-    const size_t n = s.length < size - 1 ? s.length : size - 1;
-    std::memcpy(dst, s.data, n);
-    dst[n] = '\0';
+    *element = (uint32_t)le(e.value, 4);
+    *count = le(e.value + 4, 8);
     return true;
 }
 
-bool key_is(const GgufString& key, const char* name) {
-    const size_t n = std::strlen(name);
-    return key.length == n && std::memcmp(key.data, name, n) == 0;
-}
-
-// "bnn-mlp.block.<decimal>.activation" -> index (gguf.c:168-186)
-bool mlp_activation_index(const GgufString& key, uint32_t* index) {
-    static const char pre[] = "bnn-mlp.block.", post[] = ".activation";
-    const size_t np = sizeof pre - 1, ns = sizeof post - 1;
-    if (key.length <= np + ns || std::memcmp(key.data, pre, np) != 0 ||
-        std::memcmp(key.data + key.length - ns, post, ns) != 0)
-        return false;
-    uint64_t v = 0;
-    for (size_t i = np; i < key.length - ns; ++i) {
-        const uint8_t ch = key.data[i];
-        if (ch < '0' || ch > '9' || v > 63)
-            return false;
-        v = v * 10 + (ch - '0');
+bool entry_has_kind(const GgufFile::Entry& e, Kind kind) {
+    uint64_t v;
+    float f;
+    uint32_t element;
+    uint64_t count;
+    switch (kind) {
+    case Kind::Integer: return decode_integer(e, &v);
+    case Kind::Real: return decode_real(e, &f);
+    case Kind::Text: return e.type == tString;
+    case Kind::Texts: return array_header(e, &element, &count) && element == tString;
+    case Kind::Words: return array_header(e, &element, &count) && (element == tI32 || element == tU32);
     }
-    *index = (uint32_t)v;
-    return true;
+    return false;
 }
 
-BNNE_Status store_activation(Gguf* g, uint32_t index, Reader& r, uint32_t type) {
-    if (type != kString)
-        return BNNE_EFORMAT;
-    if (index >= g->mlp_activation_count) {
-        const uint64_t count = (uint64_t)index + 1;
-        if (count > 64)
-            return BNNE_EFORMAT;
-        auto* grown = static_cast<char(*)[16]>(std::realloc(g->mlp_activations, count * sizeof *g->mlp_activations));
-        if (!grown)
-            return BNNE_ENOMEM;
-        std::memset(grown + g->mlp_activation_count, 0, (count - g->mlp_activation_count) * sizeof *grown);
-        g->mlp_activations = grown;
-        g->mlp_activation_count = count;
-    }
-    return read_text(r, type, g->mlp_activations[index], sizeof g->mlp_activations[index]) ? BNNE_OK
-                                                                                             : BNNE_EFORMAT;
-}
-
-// A string array: checked for type, counted, and (when 'keep' is given) its strings
-// recorded as views into the mapping.  'seen' rejects a repeated key.
-BNNE_Status string_array(Reader& r, uint32_t type, bool* seen, uint64_t* count_out, GgufString** keep = nullptr) {
-    if (*seen || type != kArray)
-        return BNNE_EFORMAT;
-    *seen = true;
-    const uint32_t element = r.u32();
-    const uint64_t count = r.u64();
-    if (!r.ok || element != kString || count > SIZE_MAX / sizeof(GgufString))
-        return BNNE_EFORMAT;
-    GgufString* out = nullptr;
-    if (keep && count) {
-        out = static_cast<GgufString*>(std::calloc(count, sizeof(GgufString)));
-        if (!out)
-            return BNNE_ENOMEM;
-    }
-    for (uint64_t i = 0; i < count; ++i) {
-        const GgufString v = r.str();
-        if (!r.ok) {
-            std::free(out);
-            return BNNE_EFORMAT;
-        }
-        if (out)
-            out[i] = v;
-    }
-    if (keep)
-        *keep = out;
-    if (count_out)
-        *count_out = count;
-    return BNNE_OK;
-}
-
-BNNE_Status int_array(Reader& r, uint32_t type, bool* seen, uint32_t** out, uint64_t* count_out) {
-    if (*seen || type != kArray)
-        return BNNE_EFORMAT;
-    *seen = true;
-    const uint32_t element = r.u32();
-    const uint64_t count = r.u64();
-    if (!r.ok || (element != kI32 && element != kU32) || count > SIZE_MAX / 4)
-        return BNNE_EFORMAT;
-    if (!r.need(count * 4))
-        return BNNE_EFORMAT;
-    uint32_t* v = count ? static_cast<uint32_t*>(std::malloc(count * 4)) : nullptr;
-    if (count && !v)
-        return BNNE_ENOMEM;
-    for (uint64_t i = 0; i < count; ++i)
-        v[i] = r.u32();
-    *out = v;
-    *count_out = count;
-    return BNNE_OK;
-}
-
-struct IntKey {
-    const char* name;
-    uint64_t Gguf::*field;
-};
-const IntKey kIntKeys[] = {
-    {"qwen3.block_count", &Gguf::block_count},
-    {"qwen3.context_length", &Gguf::context_length},
-    {"qwen3.embedding_length", &Gguf::embedding_length},
-    {"qwen3.feed_forward_length", &Gguf::feed_forward_length},
-    {"qwen3.attention.head_count", &Gguf::head_count},
-    {"qwen3.attention.head_count_kv", &Gguf::head_count_kv},
-    {"qwen3.attention.key_length", &Gguf::key_length},
-    {"qwen3.attention.value_length", &Gguf::value_length},
-    {"qwen3.rope.scaling.original_context_length", &Gguf::rope_original_context},
-    {"bnn-mlp.block_count", &Gguf::mlp_block_count},
-    {"bnn-mlp.class_count", &Gguf::mlp_class_count},
-    {"bnn-mlp.input_features", &Gguf::mlp_input_features},
-    {"bnn-mlp.input_pixels", &Gguf::mlp_input_pixels},
-};
-struct FloatKey {
-    const char* name;
-    float Gguf::*field;
-};
-const FloatKey kFloatKeys[] = {
-    {"qwen3.attention.layer_norm_rms_epsilon", &Gguf::rms_epsilon},
-    {"qwen3.rope.freq_base", &Gguf::rope_freq_base},
-    {"qwen3.rope.scaling.factor", &Gguf::rope_factor},
-    {"bnn-mlp.input_mean", &Gguf::mlp_input_mean},
-    {"bnn-mlp.input_std", &Gguf::mlp_input_std},
-};
-
-BNNE_Status parse_metadata(Reader& r, Gguf* g, uint64_t count) {
-    if (!r.ok || count > 4096)
-        return BNNE_EFORMAT;
-    bool labels = false, tokens = false, types = false, merges = false;
-    for (uint64_t i = 0; i < count; ++i) {
-        const GgufString key = r.str();
-        const uint32_t type = r.u32();
-        if (!r.ok)
-            return BNNE_EFORMAT;
-        uint64_t v = 0;
-        uint32_t index = 0;
-        BNNE_Status st = BNNE_OK;
-        bool handled = false;
-        for (const IntKey& k : kIntKeys)
-            if (key_is(key, k.name)) {
-                if (!read_integer(r, type, &(g->*k.field)))
-                    return BNNE_EFORMAT;
-                handled = true;
-            }
-        for (const FloatKey& k : kFloatKeys)
-            if (key_is(key, k.name)) {
-                if (!read_float(r, type, &(g->*k.field)))
-                    return BNNE_EFORMAT;
-                handled = true;
-            }
-        if (handled)
-            continue;
-        if (key_is(key, "general.architecture")) {
-            if (!read_text(r, type, g->architecture, sizeof g->architecture))
-                return BNNE_EFORMAT;
-        } else if (key_is(key, "general.alignment")) {
-            if (!read_integer(r, type, &v) || v == 0 || v > 4096)
-                return BNNE_EFORMAT;
-            g->alignment = (uint32_t)v;
-        } else if (key_is(key, "qwen3.rope.scaling.type")) {
-            if (!read_text(r, type, g->rope_scaling_type, sizeof g->rope_scaling_type))
-                return BNNE_EFORMAT;
-        } else if (key_is(key, "bnn-mlp.labels")) {
-            st = string_array(r, type, &labels, nullptr);
-        } else if (mlp_activation_index(key, &index)) {
-            st = store_activation(g, index, r, type);
-        } else if (key_is(key, "tokenizer.ggml.model") || key_is(key, "tokenizer.ggml.pre")) {
-            char scratch[32];
-            if (!read_text(r, type, scratch, sizeof scratch))
-                return BNNE_EFORMAT;
-        } else if (key_is(key, "tokenizer.ggml.tokens")) {
-            st = string_array(r, type, &tokens, &g->token_count, &g->tokens);
-        } else if (key_is(key, "tokenizer.ggml.token_type")) {
-            st = int_array(r, type, &types, &g->token_types, &g->token_type_count);
-        } else if (key_is(key, "tokenizer.ggml.merges")) {
-            st = string_array(r, type, &merges, nullptr);
-        } else if (key_is(key, "tokenizer.ggml.eos_token_id")) {
-            if (!read_integer(r, type, &v))
-                return BNNE_EFORMAT;
-            g->eos_token_id = (uint32_t)v;
-            g->has_eos = 1;
-        } else if (key_is(key, "tokenizer.ggml.bos_token_id")) {
-            if (!read_integer(r, type, &v))
-                return BNNE_EFORMAT;
-            g->bos_token_id = (uint32_t)v;
-            g->has_bos = 1;
-        } else if (key_is(key, "tokenizer.ggml.padding_token_id") || key_is(key, "tokenizer.ggml.add_bos_token")) {
-            if (!read_integer(r, type, &v))
-                return BNNE_EFORMAT;
-        } else if (!skip(r, type, 0)) {
-            return BNNE_EFORMAT;
-        }
-        if (st != BNNE_OK)
-            return st;
-    }
-    return r.ok ? BNNE_OK : BNNE_EFORMAT;
-}
-
-BNNE_Status parse_tensors(Reader& r, Gguf* g, uint64_t count) {
-    if (!r.ok || count == 0 || count > SIZE_MAX / sizeof(GgufTensor))
-        return BNNE_EFORMAT;
-    g->tensors = static_cast<GgufTensor*>(std::calloc(count, sizeof(GgufTensor)));
-    if (!g->tensors)
-        return BNNE_ENOMEM;
-    g->tensor_count = count;
-    for (uint64_t i = 0; i < count; ++i) {
-        GgufTensor& t = g->tensors[i];
-        t.name = r.str();
-        t.rank = r.u32();
-        if (!r.ok || t.rank == 0 || t.rank > kMaxDims)
-            return BNNE_EFORMAT;
-        for (uint32_t d = 0; d < t.rank; ++d)
-            t.dims[d] = r.u64();
-        t.type = r.u32();
-        t.offset = r.u64();
-        if (!r.ok)
-            return BNNE_EFORMAT;
-    }
-    return BNNE_OK;
-}
-
-BNNE_Status tensor_bytes(GgufTensor& t) {
-    uint64_t count = 1;
+// Bytes of a tensor's data; throws for types this engine does not read or bad shapes.
+uint64_t tensor_bytes(const TensorRef& t, const char* path) {
+    uint64_t elements = 1;
     for (uint32_t d = 0; d < t.rank; ++d) {
-        if (t.dims[d] == 0 || count > UINT64_MAX / t.dims[d])
-            return BNNE_EFORMAT;
-        count *= t.dims[d];
+        if (t.dims[d] == 0 || elements > UINT64_MAX / t.dims[d])
+            malformed(path, "tensor with an empty or overflowing shape");
+        elements *= t.dims[d];
     }
-    if (t.type == kTypeF32) {
-        if (count > UINT64_MAX / 4)
-            return BNNE_EFORMAT;
-        t.bytes = count * 4;
-    } else if (t.type == kTypeF16) {
-        if (count > UINT64_MAX / 2)
-            return BNNE_EFORMAT;
-        t.bytes = count * 2;
-    } else if (t.type == kTypeQ1_0) {
-        if (t.rank != 2 || t.dims[0] % kGroup != 0 || t.dims[1] > UINT64_MAX / 18)
-            return BNNE_EFORMAT;
-        const uint64_t groups = t.dims[0] / kGroup;
-        if (t.dims[1] > UINT64_MAX / groups)
-            return BNNE_EFORMAT;
-        t.bytes = t.dims[1] * groups * 18;
-    } else {
-        return BNNE_ENOTSUP;
+    switch (t.type) {
+    case kF32:
+        if (elements > UINT64_MAX / 4)
+            malformed(path, "tensor too large");
+        return elements * 4;
+    case kF16:
+        if (elements > UINT64_MAX / 2)
+            malformed(path, "tensor too large");
+        return elements * 2;
+    case kQ1_0: {
+        if (t.rank != 2 || t.dims[0] % kGroup != 0)
+            malformed(path, "Q1_0 tensor that is not [in, out] with in a multiple of 128");
+        const uint64_t blocks_per_row = t.dims[0] / kGroup;
+        if (t.dims[1] > UINT64_MAX / 18 / blocks_per_row)
+            malformed(path, "tensor too large");
+        return t.dims[1] * blocks_per_row * 18;
     }
-    return BNNE_OK;
+    default:
+        raise(BNNE_ENOTSUP, "%s: tensor '%.*s' has type %u (F32, F16 and Q1_0 are read)", path, (int)t.name.size(),
+              t.name.data(), t.type);
+    }
 }
 
 }  // namespace
 
-BNNE_Status gguf_open(const char* path, Gguf** out) {
-    if (!path || !out)
-        return BNNE_EINVAL;
-    *out = nullptr;
+std::unique_ptr<GgufFile> GgufFile::open(const char* path) {
     const int fd = ::open(path, O_RDONLY);
     if (fd < 0)
-        return error(BNNE_EIO, "%s: cannot open GGUF file", path);
+        raise(BNNE_EIO, "%s: cannot be opened", path);
     struct stat st;
     if (::fstat(fd, &st) != 0 || st.st_size <= 0) {
         ::close(fd);
-        return error(BNNE_EIO, "%s: cannot stat GGUF file", path);
+        raise(BNNE_EIO, "%s: empty or unreadable", path);
     }
-    const size_t size = (size_t)st.st_size;
-    void* map = ::mmap(nullptr, size, PROT_READ, MAP_PRIVATE, fd, 0);
+    void* map = ::mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
     ::close(fd);
     if (map == MAP_FAILED)
-        return error(BNNE_EIO, "%s: cannot mmap GGUF file", path);
+        raise(BNNE_EIO, "%s: cannot be mapped", path);
+    std::unique_ptr<GgufFile> f(new GgufFile);
+    f->map_ = map;
+    f->map_bytes_ = (size_t)st.st_size;
 
-    Gguf* g = static_cast<Gguf*>(std::calloc(1, sizeof(Gguf)));
-    if (!g) {
-        ::munmap(map, size);
-        return error(BNNE_ENOMEM, "out of memory");
-    }
-    g->mapping = static_cast<uint8_t*>(map);
-    g->mapping_bytes = size;
-    g->alignment = 32;
+    const uint8_t* base = static_cast<const uint8_t*>(map);
+    Bytes in{base, base + f->map_bytes_};
+    const bool magic = in.have(4) && std::memcmp(in.at, "GGUF", 4) == 0;
+    in.take(4);
+    const uint32_t version = (uint32_t)in.take(4);
+    const uint64_t n_tensors = in.take(8), n_entries = in.take(8);
+    if (!in.at || !magic || version != 3)
+        malformed(path, "not a GGUF version 3 file");
+    if (n_entries > kMaxEntries)
+        malformed(path, "too many metadata entries");
 
-    Reader r = {g->mapping, g->mapping + size, true};
-    const bool magic = r.need(4) && std::memcmp(r.p, "GGUF", 4) == 0;
-    r.p += r.ok ? 4 : 0;
-    const uint32_t version = r.u32();
-    const uint64_t tensor_count = r.u64();
-    const uint64_t metadata_count = r.u64();
-    if (!r.ok || !magic || version != 3) {
-        gguf_close(g);
-        return error(BNNE_EFORMAT, "%s: unsupported GGUF header or version", path);
+    f->entries_.reserve((size_t)n_entries);
+    for (uint64_t i = 0; i < n_entries; ++i) {
+        Entry e;
+        e.key = in.string();
+        e.type = (uint32_t)in.take(4);
+        e.value = in.at;
+        if (!in.skip(e.type, 0))
+            malformed(path, "truncated or malformed metadata");
+        e.end = in.at;
+        f->entries_.push_back(e);
     }
-    BNNE_Status status = parse_metadata(r, g, metadata_count);
-    if (status == BNNE_OK)
-        status = parse_tensors(r, g, tensor_count);
-    if (status != BNNE_OK) {
-        gguf_close(g);
-        return error(status, "%s: invalid GGUF metadata or tensor table", path);
+    // a tensor record takes at least 32 bytes (name length, rank, one dimension, type,
+    // offset): a count the rest of the file cannot hold is malformed, not an allocation
+    if (n_tensors == 0)
+        malformed(path, "no tensor table");
+    if (!in.at || n_tensors > (uint64_t)(in.end - in.at) / 32u)
+        malformed(path, "tensor table longer than the file");
+    f->tensors_.reserve((size_t)n_tensors);
+    std::vector<uint64_t> offsets;  // relative to the data section, whose start is known later
+    offsets.reserve((size_t)n_tensors);
+    for (uint64_t i = 0; i < n_tensors; ++i) {
+        TensorRef t{};
+        t.name = in.string();
+        t.rank = (uint32_t)in.take(4);
+        if (!in.at || t.rank == 0 || t.rank > 4)
+            malformed(path, "truncated tensor table or tensor rank outside 1..4");
+        for (uint32_t d = 0; d < t.rank; ++d)
+            t.dims[d] = in.take(8);
+        t.type = (uint32_t)in.take(4);
+        const uint64_t offset = in.take(8);
+        if (!in.at)
+            malformed(path, "truncated tensor table");
+        offsets.push_back(offset);
+        f->tensors_.push_back(t);
     }
-    if (!g->architecture[0]) {
-        gguf_close(g);
-        return error(BNNE_EFORMAT, "%s: missing general.architecture", path);
-    }
-    const size_t info_end = (size_t)(r.p - g->mapping);
-    const size_t align = g->alignment;
-    g->data_offset = (info_end + align - 1) / align * align;
-    if (g->data_offset > size) {
-        gguf_close(g);
-        return error(BNNE_EFORMAT, "%s: GGUF data section is out of bounds", path);
-    }
-    for (uint64_t i = 0; i < g->tensor_count; ++i) {
-        GgufTensor& t = g->tensors[i];
-        status = tensor_bytes(t);
-        if (status != BNNE_OK) {
-            gguf_close(g);
-            return error(status, "%s: unsupported tensor type or shape", path);
+
+    // the keys this engine reads: usable kind, arrays not repeated
+    std::vector<std::string_view> arrays_seen;
+    for (const Entry& e : f->entries_) {
+        const std::optional<Kind> kind = kind_of(e.key);
+        if (!kind)
+            continue;
+        if (!entry_has_kind(e, *kind))
+            raise(BNNE_EFORMAT, "%s: metadata '%.*s' has the wrong type", path, (int)e.key.size(), e.key.data());
+        if (*kind == Kind::Texts || *kind == Kind::Words) {
+            for (std::string_view seen : arrays_seen)
+                if (seen == e.key)
+                    raise(BNNE_EFORMAT, "%s: metadata '%.*s' appears twice", path, (int)e.key.size(), e.key.data());
+            arrays_seen.push_back(e.key);
         }
-        const uint64_t available = size - g->data_offset;
-        if (t.offset > available || t.bytes > available - t.offset) {
-            gguf_close(g);
-            return error(BNNE_EFORMAT, "%s: GGUF tensor data is out of bounds", path);
-        }
     }
-    if (g->rope_factor <= 0.0f)
-        g->rope_factor = 1.0f;
-    if (g->rope_original_context == 0)
-        g->rope_original_context = g->context_length;
-    *out = g;
-    return BNNE_OK;
+    for (const Entry& e : f->entries_)
+        if (activation_index(e.key).value_or(0) > 63u)
+            malformed(path, "activation of a bnn-mlp block beyond the 64th");
+    const std::optional<std::string_view> arch = f->text("general.architecture");
+    if (!arch || arch->empty())
+        malformed(path, "general.architecture is missing");
+    f->architecture_.assign(arch->data(), arch->size());
+    uint64_t alignment = f->integer("general.alignment").value_or(32);
+    if (alignment == 0 || alignment > 4096)
+        malformed(path, "general.alignment outside 1..4096");
+
+    // the data section starts at the next multiple of the alignment
+    const uint64_t header_end = (uint64_t)(in.at - base);
+    const uint64_t data_start = (header_end + alignment - 1) / alignment * alignment;
+    if (data_start > f->map_bytes_)
+        malformed(path, "data section beyond the end of the file");
+    const uint64_t room = f->map_bytes_ - data_start;
+    for (size_t i = 0; i < f->tensors_.size(); ++i) {
+        TensorRef& t = f->tensors_[i];
+        const uint64_t offset = offsets[i];
+        t.bytes = tensor_bytes(t, path);
+        if (offset > room || t.bytes > room - offset)
+            malformed(path, "tensor data beyond the end of the file");
+        t.data = base + data_start + offset;
+    }
+    return f;
 }
 
-void gguf_close(Gguf* g) {
-    if (!g)
-        return;
-    std::free(g->tensors);
-    std::free(g->mlp_activations);
-    std::free(g->tokens);
-    std::free(g->token_types);
-    if (g->mapping)
-        ::munmap(g->mapping, g->mapping_bytes);
-    std::free(g);
+GgufFile::~GgufFile() {
+    if (map_)
+        ::munmap(map_, map_bytes_);
 }
 
-const GgufTensor* gguf_find(const Gguf* g, const char* name) {
-    if (!g || !name)
-        return nullptr;
-    const size_t n = std::strlen(name);
-    for (uint64_t i = 0; i < g->tensor_count; ++i) {
-        const GgufTensor& t = g->tensors[i];
-        if (t.name.length == n && std::memcmp(t.name.data, name, n) == 0)
-            return &t;
-    }
+const GgufFile::Entry* GgufFile::entry(std::string_view key) const {
+    for (auto it = entries_.rbegin(); it != entries_.rend(); ++it)
+        if (it->key == key)
+            return &*it;
     return nullptr;
 }
 
-const uint8_t* gguf_data(const Gguf* g, const GgufTensor* t) {
-    return g && t ? g->mapping + g->data_offset + t->offset : nullptr;
+bool GgufFile::has(std::string_view key) const { return entry(key) != nullptr; }
+
+const TensorRef* GgufFile::tensor(std::string_view name) const {
+    for (const TensorRef& t : tensors_)
+        if (t.name == name)
+            return &t;
+    return nullptr;
+}
+
+std::optional<uint64_t> GgufFile::integer(std::string_view key) const {
+    const Entry* e = entry(key);
+    uint64_t v;
+    if (!e)
+        return std::nullopt;
+    if (!decode_integer(*e, &v))
+        raise(BNNE_EFORMAT, "metadata '%.*s' is not an integer", (int)key.size(), key.data());
+    return v;
+}
+
+std::optional<float> GgufFile::real(std::string_view key) const {
+    const Entry* e = entry(key);
+    float v;
+    if (!e)
+        return std::nullopt;
+    if (!decode_real(*e, &v))
+        raise(BNNE_EFORMAT, "metadata '%.*s' is not a finite real", (int)key.size(), key.data());
+    return v;
+}
+
+std::optional<std::string_view> GgufFile::text(std::string_view key) const {
+    const Entry* e = entry(key);
+    if (!e)
+        return std::nullopt;
+    if (e->type != tString)
+        raise(BNNE_EFORMAT, "metadata '%.*s' is not a string", (int)key.size(), key.data());
+    Bytes b{e->value, e->end};
+    return b.string();
+}
+
+std::vector<std::string_view> GgufFile::texts(std::string_view key) const {
+    std::vector<std::string_view> out;
+    const Entry* e = entry(key);
+    uint32_t element;
+    uint64_t count;
+    if (!e)
+        return out;
+    if (!array_header(*e, &element, &count) || element != tString)
+        raise(BNNE_EFORMAT, "metadata '%.*s' is not a string array", (int)key.size(), key.data());
+    Bytes b{e->value + 12, e->end};
+    out.reserve((size_t)count);
+    for (uint64_t i = 0; i < count; ++i)
+        out.push_back(b.string());
+    return out;
+}
+
+std::vector<uint32_t> GgufFile::words(std::string_view key) const {
+    std::vector<uint32_t> out;
+    const Entry* e = entry(key);
+    uint32_t element;
+    uint64_t count;
+    if (!e)
+        return out;
+    if (!array_header(*e, &element, &count) || (element != tI32 && element != tU32))
+        raise(BNNE_EFORMAT, "metadata '%.*s' is not a 32-bit integer array", (int)key.size(), key.data());
+    out.resize((size_t)count);
+    for (uint64_t i = 0; i < count; ++i)
+        out[i] = (uint32_t)le(e->value + 12 + 4 * i, 4);
+    return out;
+}
+
+std::vector<float> read_floats(const GgufFile& file, std::string_view name, size_t count) {
+    const TensorRef* t = file.tensor(name);
+    if (!t || (t->type != kF32 && t->type != kF16))
+        raise(BNNE_EFORMAT, "no F32/F16 tensor '%.*s'", (int)name.size(), name.data());
+    const uint64_t elements = t->bytes / (t->type == kF32 ? 4u : 2u);
+    if (elements != count)
+        raise(BNNE_EFORMAT, "tensor '%.*s' holds %llu values where %zu belong", (int)name.size(), name.data(),
+              (unsigned long long)elements, count);
+    std::vector<float> v(count);
+    for (size_t i = 0; i < count; ++i) {
+        if (t->type == kF32) {
+            const uint32_t bits = (uint32_t)le(t->data + 4 * i, 4);
+            std::memcpy(&v[i], &bits, 4);
+        } else {
+            v[i] = half_to_float((uint16_t)le(t->data + 2 * i, 2));
+        }
+        if (!std::isfinite(v[i]))
+            raise(BNNE_EFORMAT, "tensor '%.*s' holds a NaN or infinity", (int)name.size(), name.data());
+    }
+    return v;
 }
 
 }  // namespace bnne

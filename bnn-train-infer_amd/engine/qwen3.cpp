@@ -1,538 +1,416 @@
-// Qwen3 decoder (architecture "qwen3"): loading from GGUF and the per-token step.
+// Qwen3 decoders (general.architecture "qwen3"), the model of the reference's LLM path.
 //
-// Every linear layer goes through linear_forward (BNN_Execute GEMV_F32); the rest of
-// the step runs on the host.  The host arithmetic follows the reference's
-// qwen3_step (bnn-sw-v2/qwen3/qwen3.c:396-512) operation for operation -- the same
-// sequential sums, the same division-then-multiply in RMSNorm, the same libm calls
-// (sqrtf, expf, powf, cosf, sinf, logf) -- and is compiled without FP contraction,
-// so that with bit-exact linear results the logits are bit-identical.
+// Weights: token_embd.weight is Q1_0 [C, V]: a token's row is its embedding (+scale
+// where the sign bit is 1, -scale where it is 0) and the same matrix is the output
+// layer (tied embeddings); per layer blk.<l>.attn_norm, ffn_norm (C values),
+// attn_q_norm, attn_k_norm (head_dim values) as F32/F16 and the Q1_0 projections
+// attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up, ffn_down; output_norm.
 //
-// Model layout (qwen3.c:144-274): token_embd.weight is Q1_0 [C, V] and doubles as the
-// lm_head (tied embeddings); per layer attn_norm, ffn_norm (C), attn_q_norm,
-// attn_k_norm (head_dim) in F32/F16, and Q1_0 attn_q/k/v/output, ffn_gate/up/down.
-#include "engine_internal.h"
+// A context decodes on one of two paths with the same results: the device path
+// (resident.hip: everything on the GPU, the linear layers as fused batches) or the
+// host step below, which runs every linear layer through SignLinear::apply (one
+// BNN_Execute per shard) and the rest on the host.  The host step performs the
+// floating-point operations of the reference's qwen3_step
+// (bnn-sw-v2/qwen3/qwen3.c:342-512) in the same order -- sequential sums, RMSNorm as
+// x / rms * gain, softmax as exp(s - max) / sum, SiLU as g / (1 + exp(-g)) * u --
+// compiled without contraction and with the same libm, so equal linear results
+// give equal logits.
+#include "engine.hpp"
 #include "resident.h"
 
 #include <cmath>
 #include <cstdio>
-#include <cstdlib>
 #include <cstring>
-#include <initializer_list>
 #include <math.h>
+#include <string>
 
 namespace bnne {
 namespace {
 
-constexpr uint32_t kMaxLayers = 128, kMaxHeads = 256, kMaxVocab = 1u << 20;
+constexpr uint64_t kMaxLayers = 128, kMaxHeads = 256, kMaxVocab = 1u << 20;
 constexpr double kPi = 3.14159265358979323846;
 
-struct Block {
-    float *attn_norm, *q_norm, *k_norm, *ffn_norm;
-    Linear wq, wk, wv, wo, gate, up, down;
+struct Shape {
+    uint32_t layers = 0, width = 0, ffn = 0, heads = 0, kv_heads = 0, head_dim = 0, vocab = 0, kv_width = 0;
+    uint32_t trained_ctx = 0;
+    float eps = 0, rope_base = 0;
+    // RoPE scaling: frequencies times freq_scale; YaRN ramps between scaled and
+    // unscaled frequencies over the pairs [ramp_lo, ramp_hi] and multiplies by mscale
+    float freq_scale = 1.0f, mscale = 1.0f;
+    int32_t ramp_lo = 0, ramp_hi = 0;
+    bool yarn = false;
 };
 
-struct Model {
-    uint32_t C, H, Hk, HD, FF, L, V, kv_dim;
-    float eps, rope_base, rope_freq_scale, rope_mscale;
-    int32_t rope_corr0, rope_corr1;
-    bool rope_yarn;
-    uint8_t* emb_bits;
-    uint16_t* emb_scales;
-    Linear lm_head;
-    float* final_norm;
-    Block* blocks;
+struct Layer {
+    std::vector<float> attn_norm, ffn_norm, q_norm, k_norm;
+    SignLinear q, k, v, o, gate, up, down;
 };
 
-struct State {
-    uint32_t n_ctx;
-    float *x, *norm, *q, *k, *v, *y, *o, *gate, *up, *scores, *probs;
-    float *k_cache, *v_cache, *rope_cos, *rope_sin;  // host KV cache: host step only
-    Resident* resident;  // device-resident step when non-null
+class Qwen3Model final : public bnne_model {
+public:
+    void load() override;
+    bnne_context* new_context(const BNNE_ContextParams& p) override;
+
+    Shape shape;
+    SignWeights embedding;  // token rows (and the output layer's weights)
+    SignLinear lm_head;
+    std::vector<float> final_norm;
+    std::vector<std::unique_ptr<Layer>> layers;
+
+private:
+    void read_shape();
 };
 
-float* alloc_f32(size_t count) {
-    if (!count || count > SIZE_MAX / sizeof(float))
-        return nullptr;
-    return static_cast<float*>(std::malloc(count * sizeof(float)));
+uint32_t bounded(const GgufFile& f, const char* key, uint64_t max) {
+    const uint64_t v = f.integer(key).value_or(0);
+    if (v == 0 || v > max)
+        raise(BNNE_EFORMAT, "Qwen3 metadata %s = %llu is outside 1..%llu", key, (unsigned long long)v,
+              (unsigned long long)max);
+    return (uint32_t)v;
 }
 
-void unload(void* impl) {
-    Model* m = static_cast<Model*>(impl);
-    if (!m)
-        return;
-    if (m->blocks) {
-        for (uint32_t l = 0; l < m->L; ++l) {
-            Block& b = m->blocks[l];
-            std::free(b.attn_norm);
-            std::free(b.q_norm);
-            std::free(b.k_norm);
-            std::free(b.ffn_norm);
-            for (Linear* lin : {&b.wq, &b.wk, &b.wv, &b.wo, &b.gate, &b.up, &b.down})
-                linear_free(lin);
-        }
+int32_t clamp_pair(double v, int32_t lo, int32_t hi) { return v <= (double)lo ? lo : v >= (double)hi ? hi : (int32_t)v; }
+
+void Qwen3Model::read_shape() {
+    const GgufFile& f = *file;
+    Shape& s = shape;
+    const TensorRef* emb = f.tensor("token_embd.weight");
+    if (!emb || emb->type != kQ1_0 || emb->rank != 2)
+        raise(BNNE_EFORMAT, "no Q1_0 token_embd.weight");
+    s.layers = bounded(f, "qwen3.block_count", kMaxLayers);
+    s.width = bounded(f, "qwen3.embedding_length", UINT32_MAX);
+    s.ffn = bounded(f, "qwen3.feed_forward_length", UINT32_MAX);
+    s.heads = bounded(f, "qwen3.attention.head_count", kMaxHeads);
+    s.kv_heads = bounded(f, "qwen3.attention.head_count_kv", kMaxHeads);
+    s.head_dim = bounded(f, "qwen3.attention.key_length", UINT32_MAX);
+    if (f.integer("qwen3.attention.value_length").value_or(0) != s.head_dim)
+        raise(BNNE_EFORMAT, "Qwen3 value heads differ from key heads");
+    s.trained_ctx = bounded(f, "qwen3.context_length", UINT32_MAX);
+    s.eps = f.real("qwen3.attention.layer_norm_rms_epsilon").value_or(0.0f);
+    s.rope_base = f.real("qwen3.rope.freq_base").value_or(0.0f);
+    if (!(s.eps > 0.0f) || !(s.rope_base > 0.0f))
+        raise(BNNE_EFORMAT, "Qwen3 RMSNorm epsilon and RoPE base must be positive");
+    if (emb->dims[0] != s.width || emb->dims[1] == 0 || emb->dims[1] > kMaxVocab)
+        raise(BNNE_EFORMAT, "token_embd.weight is not [%u, vocabulary <= 2^20]", s.width);
+    s.vocab = (uint32_t)emb->dims[1];
+    if (s.head_dim > s.width || (uint64_t)s.heads * s.head_dim != s.width || s.heads % s.kv_heads != 0 ||
+        s.width % kGroup != 0 || s.ffn % kGroup != 0 || s.head_dim % 2 != 0)
+        raise(BNNE_EFORMAT, "Qwen3 widths do not fit together (heads x head_dim = width, groups of 128)");
+    s.kv_width = s.kv_heads * s.head_dim;
+    if (s.kv_width % kGroup != 0)
+        raise(BNNE_EFORMAT, "Qwen3 key/value width %u is not a multiple of 128", s.kv_width);
+    if (caps.group_size != kGroup || !(caps.supported_ops & BNN_CAP_GEMV_F32))
+        raise(BNNE_ENOTSUP, "Qwen3 layers need an accelerator with 128-weight groups and GEMV_F32");
+
+    // RoPE scaling (YaRN when qwen3.rope.scaling.type is "yarn")
+    const float factor = f.real("qwen3.rope.scaling.factor").value_or(0.0f);
+    s.freq_scale = 1.0f / (factor > 0.0f ? factor : 1.0f);
+    s.yarn = f.text("qwen3.rope.scaling.type").value_or("") == "yarn";
+    s.ramp_lo = 0;
+    s.ramp_hi = (int32_t)s.head_dim - 1;
+    uint64_t original = f.integer("qwen3.rope.scaling.original_context_length").value_or(0);
+    if (original == 0)
+        original = s.trained_ctx;
+    if (s.yarn && original) {
+        // the pairs whose wavelength spans 32 and 1 rotations of the original context
+        const double dims = (double)s.head_dim, log_base2 = 2.0 * std::log((double)s.rope_base);
+        const double lo = std::floor(dims * std::log((double)original / (32.0 * 2.0 * kPi)) / log_base2);
+        const double hi = std::ceil(dims * std::log((double)original / (2.0 * kPi)) / log_base2);
+        s.ramp_lo = clamp_pair(lo, 0, (int32_t)s.head_dim - 1);
+        s.ramp_hi = clamp_pair(hi, 0, (int32_t)s.head_dim - 1);
+        s.mscale = 1.0f + 0.1f * logf(1.0f / s.freq_scale);
     }
-    std::free(m->blocks);
-    linear_free(&m->lm_head);
-    std::free(m->final_norm);
-    std::free(m->emb_bits);
-    std::free(m->emb_scales);
-    std::free(m);
+    if (!(s.freq_scale > 0.0f) || !std::isfinite(s.mscale))
+        raise(BNNE_EFORMAT, "Qwen3 RoPE scaling gives no usable frequencies");
 }
 
-BNNE_Status read_vector(const Gguf* g, const char* name, uint32_t count, float** out) {
-    float* data = nullptr;
-    size_t n = 0;
-    const BNNE_Status st = tensor_f32(g, name, &data, &n);
-    if (st != BNNE_OK)
-        return st;
-    if (n != count) {
-        std::free(data);
-        return error(BNNE_EFORMAT, "tensor '%s' has %zu elements, expected %u", name, n, count);
-    }
-    *out = data;
-    return BNNE_OK;
+std::string layer_key(uint32_t l, const char* what) {
+    char name[80];
+    std::snprintf(name, sizeof name, "blk.%u.%s.weight", l, what);
+    return name;
 }
 
-BNNE_Status load_linear(bnne_model* mm, const Gguf* g, const char* name, uint32_t in, uint32_t out, Linear* l) {
-    const BNNE_Status st = linear_load(mm, g, name, l);
-    if (st != BNNE_OK)
-        return st;
-    if (l->in != in || l->out != out) {
-        const uint32_t ai = l->in, ao = l->out;
-        linear_free(l);
-        return error(BNNE_EFORMAT, "tensor '%s' has shape %u->%u, expected %u->%u", name, ai, ao, in, out);
+void Qwen3Model::load() {
+    read_shape();
+    const Shape& s = shape;
+    const GgufFile& f = *file;
+    final_norm = read_floats(f, "output_norm.weight", s.width);
+    for (uint32_t l = 0; l < s.layers; ++l) {
+        std::unique_ptr<Layer> layer(new Layer);
+        layer->attn_norm = read_floats(f, layer_key(l, "attn_norm"), s.width);
+        layer->ffn_norm = read_floats(f, layer_key(l, "ffn_norm"), s.width);
+        layer->q_norm = read_floats(f, layer_key(l, "attn_q_norm"), s.head_dim);
+        layer->k_norm = read_floats(f, layer_key(l, "attn_k_norm"), s.head_dim);
+        layers.push_back(std::move(layer));
     }
-    return BNNE_OK;
-}
-
-int32_t clamp_dim(double v, int32_t lo, int32_t hi) {
-    if (v <= (double)lo)
-        return lo;
-    if (v >= (double)hi)
-        return hi;
-    return (int32_t)v;
-}
-
-// RoPE scaling parameters (qwen3.c:125-142): plain scaling by 1/factor, or YaRN with
-// the correction range from the original context length.
-BNNE_Status init_rope(Model* m, const Gguf* g) {
-    const float freq_scale = 1.0f / g->rope_factor;
-    const bool yarn = std::strcmp(g->rope_scaling_type, "yarn") == 0;
-    int32_t corr0 = 0, corr1 = (int32_t)(m->HD - 1);
-    float mscale = 1.0f;
-    if (yarn && g->rope_original_context) {
-        const double base = m->rope_base, orig = (double)g->rope_original_context;
-        const double lo = std::floor((double)m->HD * std::log(orig / (32.0 * 2.0 * kPi)) / (2.0 * std::log(base)));
-        const double hi = std::ceil((double)m->HD * std::log(orig / (2.0 * kPi)) / (2.0 * std::log(base)));
-        corr0 = clamp_dim(lo, 0, (int32_t)m->HD - 1);
-        corr1 = clamp_dim(hi, 0, (int32_t)m->HD - 1);
-        mscale = 1.0f + 0.1f * logf(1.0f / freq_scale);
-    }
-    if (!(freq_scale > 0.0f) || !std::isfinite(mscale))
-        return error(BNNE_EFORMAT, "invalid Qwen3 rope scaling");
-    m->rope_freq_scale = freq_scale;
-    m->rope_mscale = mscale;
-    m->rope_corr0 = corr0;
-    m->rope_corr1 = corr1;
-    m->rope_yarn = yarn;
-    return BNNE_OK;
-}
-
-BNNE_Status load(bnne_model* mm, const Gguf* g, void** out_impl) {
-    *out_impl = nullptr;
-    Model* m = static_cast<Model*>(std::calloc(1, sizeof(Model)));
-    if (!m)
-        return error(BNNE_ENOMEM, "out of memory");
-    const GgufTensor* emb = gguf_find(g, "token_embd.weight");
-    if (!emb || emb->type != kTypeQ1_0 || emb->rank != 2) {
-        unload(m);
-        return error(BNNE_EFORMAT, "missing token_embd.weight");
-    }
-    if (g->block_count == 0 || g->block_count > kMaxLayers || g->embedding_length == 0 ||
-        g->embedding_length > UINT32_MAX || g->feed_forward_length == 0 || g->feed_forward_length > UINT32_MAX ||
-        g->head_count == 0 || g->head_count > kMaxHeads || g->head_count_kv == 0 || g->head_count_kv > kMaxHeads ||
-        g->key_length == 0 || g->key_length > UINT32_MAX || g->key_length != g->value_length ||
-        g->context_length == 0 || g->context_length > UINT32_MAX || g->rms_epsilon <= 0.0f ||
-        g->rope_freq_base <= 0.0f || emb->dims[0] != g->embedding_length || emb->dims[1] == 0 ||
-        emb->dims[1] > kMaxVocab) {
-        unload(m);
-        return error(BNNE_EFORMAT, "unsupported Qwen3 dimensions");
-    }
-    m->L = (uint32_t)g->block_count;
-    m->C = (uint32_t)g->embedding_length;
-    m->FF = (uint32_t)g->feed_forward_length;
-    m->H = (uint32_t)g->head_count;
-    m->Hk = (uint32_t)g->head_count_kv;
-    m->HD = (uint32_t)g->key_length;
-    m->V = (uint32_t)emb->dims[1];
-    m->eps = g->rms_epsilon;
-    m->rope_base = g->rope_freq_base;
-    if (m->HD > m->C || (uint64_t)m->H * m->HD != m->C || m->H % m->Hk != 0 || m->C % kGroup != 0 ||
-        m->FF % kGroup != 0 || m->HD % 2 != 0) {
-        unload(m);
-        return error(BNNE_EFORMAT, "inconsistent Qwen3 dimensions");
-    }
-    m->kv_dim = m->Hk * m->HD;
-    if (m->kv_dim % kGroup != 0) {
-        unload(m);
-        return error(BNNE_EFORMAT, "Qwen3 KV width is not group aligned");
-    }
-    if (mm->caps.group_size != kGroup || !(mm->caps.supported_ops & BNN_CAP_GEMV_F32)) {
-        unload(m);
-        return error(BNNE_ENOTSUP, "Qwen3 requires group 128 with F32 GEMV support");
-    }
-    m->blocks = static_cast<Block*>(std::calloc(m->L, sizeof(Block)));
-    if (!m->blocks) {
-        unload(m);
-        return error(BNNE_ENOMEM, "out of memory");
-    }
-    BNNE_Status st = init_rope(m, g);
-    if (st == BNNE_OK)
-        st = read_vector(g, "output_norm.weight", m->C, &m->final_norm);
-    char name[64];
-    for (uint32_t l = 0; st == BNNE_OK && l < m->L; ++l) {
-        Block& b = m->blocks[l];
-        std::snprintf(name, sizeof name, "blk.%u.attn_norm.weight", l);
-        st = read_vector(g, name, m->C, &b.attn_norm);
-        if (st != BNNE_OK)
-            break;
-        std::snprintf(name, sizeof name, "blk.%u.ffn_norm.weight", l);
-        st = read_vector(g, name, m->C, &b.ffn_norm);
-        if (st != BNNE_OK)
-            break;
-        std::snprintf(name, sizeof name, "blk.%u.attn_q_norm.weight", l);
-        st = read_vector(g, name, m->HD, &b.q_norm);
-        if (st != BNNE_OK)
-            break;
-        std::snprintf(name, sizeof name, "blk.%u.attn_k_norm.weight", l);
-        st = read_vector(g, name, m->HD, &b.k_norm);
-    }
-    if (st == BNNE_OK)
-        st = q1_0_read(g, "token_embd.weight", m->C, m->V, &m->emb_bits, &m->emb_scales);
-    if (st == BNNE_OK)
-        st = linear_init(mm, m->C, m->V, m->emb_bits, m->emb_scales, &m->lm_head);
-    for (uint32_t l = 0; st == BNNE_OK && l < m->L; ++l) {
-        Block& b = m->blocks[l];
-        struct {
-            const char* suffix;
+    embedding = read_sign_weights(f, "token_embd.weight", s.width, s.vocab);
+    lm_head.upload(*this, embedding);
+    for (uint32_t l = 0; l < s.layers; ++l) {
+        Layer& L = *layers[l];
+        const struct {
+            const char* name;
             uint32_t in, out;
-            Linear* lin;
-        } const parts[] = {
-            {"attn_q", m->C, m->C, &b.wq},       {"attn_k", m->C, m->kv_dim, &b.wk},
-            {"attn_v", m->C, m->kv_dim, &b.wv},  {"attn_output", m->C, m->C, &b.wo},
-            {"ffn_gate", m->C, m->FF, &b.gate},  {"ffn_up", m->C, m->FF, &b.up},
-            {"ffn_down", m->FF, m->C, &b.down},
+            SignLinear* dst;
+        } projections[] = {
+            {"attn_q", s.width, s.width, &L.q},     {"attn_k", s.width, s.kv_width, &L.k},
+            {"attn_v", s.width, s.kv_width, &L.v},  {"attn_output", s.width, s.width, &L.o},
+            {"ffn_gate", s.width, s.ffn, &L.gate},  {"ffn_up", s.width, s.ffn, &L.up},
+            {"ffn_down", s.ffn, s.width, &L.down},
         };
-        for (const auto& p : parts) {
-            std::snprintf(name, sizeof name, "blk.%u.%s.weight", l, p.suffix);
-            st = load_linear(mm, g, name, p.in, p.out, p.lin);
-            if (st != BNNE_OK)
-                break;
-        }
+        for (const auto& p : projections)
+            p.dst->upload(*this, read_sign_weights(f, layer_key(l, p.name), p.in, p.out));
     }
-    if (st != BNNE_OK) {
-        unload(m);
-        return st;
-    }
-    mm->info.n_vocab = m->V;
-    mm->info.n_ctx_train = (uint32_t)g->context_length;
-    *out_impl = m;
-    return BNNE_OK;
+    info.n_vocab = s.vocab;
+    info.n_ctx_train = s.trained_ctx;
 }
 
-void ctx_free(void* state) {
-    State* s = static_cast<State*>(state);
-    if (!s)
-        return;
-    resident_free(s->resident);
-    for (float* p : {s->x, s->norm, s->q, s->k, s->v, s->y, s->o, s->gate, s->up, s->scores, s->probs, s->k_cache,
-                     s->v_cache, s->rope_cos, s->rope_sin})
-        std::free(p);
-    std::free(s);
-}
+// ---------------------------------------------------------------------------- context
 
-// cos/sin tables per (position, pair) (qwen3.c:276-299).
-void init_rope_tables(const Model* m, State* s) {
-    const uint32_t half = m->HD / 2;
-    for (uint32_t pos = 0; pos < s->n_ctx; ++pos) {
+class Qwen3Context final : public bnne_context {
+public:
+    Qwen3Context(Qwen3Model& m, const BNNE_ContextParams& p);
+    ~Qwen3Context() override { resident_free(device_); }
+    void decode(const int32_t* tokens, uint32_t n, float* logits) override;
+
+    // 0 host step, 1 device path with fused batches, 2 device path with prepared batches
+    int path() const { return device_ ? (resident_fused(device_) ? 1 : 2) : 0; }
+    void select_path(int path);
+
+private:
+    BNNE_Status open_device_path(bool fused, Resident** out);
+    void step(uint32_t token, uint32_t pos, float* logits);
+    void attend(uint32_t layer, uint32_t pos);
+
+    Qwen3Model& m_;
+    const Shape& s_;
+    // host step: the activation rows, attention scratch and the KV cache
+    std::vector<float> x_, norm_, q_, k_, v_, y_, o_, gate_, up_, scores_, probs_;
+    std::vector<float> keys_, values_;  // [layer][position][kv_width], host step only
+    std::vector<float> cos_, sin_;      // RoPE rotation of pair j at position p: [p][head_dim / 2]
+    Resident* device_ = nullptr;
+};
+
+Qwen3Context::Qwen3Context(Qwen3Model& m, const BNNE_ContextParams& p)
+    : bnne_context(m, p), m_(m), s_(m.shape), x_(s_.width), norm_(s_.width), q_(s_.width), k_(s_.kv_width),
+      v_(s_.kv_width), y_(s_.width), o_(s_.width), gate_(s_.ffn), up_(s_.ffn), scores_(p.n_ctx), probs_(p.n_ctx) {
+    // rotation tables (qwen3.c:276-299): theta = pos * base^(-2j / head_dim), scaled
+    const uint32_t half = s_.head_dim / 2;
+    cos_.resize((size_t)p.n_ctx * half);
+    sin_.resize((size_t)p.n_ctx * half);
+    const float span = (float)(s_.ramp_hi - s_.ramp_lo);
+    const float ramp_width = span > 0.001f ? span : 0.001f;
+    for (uint32_t pos = 0; pos < p.n_ctx; ++pos)
         for (uint32_t j = 0; j < half; ++j) {
-            const float theta_extrap = (float)pos * powf(m->rope_base, -2.0f * (float)j / (float)m->HD);
-            float theta = m->rope_freq_scale * theta_extrap;
-            if (m->rope_yarn) {
-                const float span = (float)(m->rope_corr1 - m->rope_corr0);
-                const float denom = span > 0.001f ? span : 0.001f;
-                const float y = ((float)j - (float)m->rope_corr0) / denom;
-                const float ramp = 1.0f - fminf(1.0f, fmaxf(0.0f, y));
-                theta = (m->rope_freq_scale * theta_extrap) * (1.0f - ramp) + theta_extrap * ramp;
+            const float unscaled = (float)pos * powf(s_.rope_base, -2.0f * (float)j / (float)s_.head_dim);
+            float theta = s_.freq_scale * unscaled;
+            if (s_.yarn) {
+                const float t = ((float)j - (float)s_.ramp_lo) / ramp_width;
+                const float keep = 1.0f - fminf(1.0f, fmaxf(0.0f, t));  // share of the unscaled frequency
+                theta = (s_.freq_scale * unscaled) * (1.0f - keep) + unscaled * keep;
             }
-            s->rope_cos[(size_t)pos * half + j] = cosf(theta) * m->rope_mscale;
-            s->rope_sin[(size_t)pos * half + j] = sinf(theta) * m->rope_mscale;
+            cos_[(size_t)pos * half + j] = cosf(theta) * s_.mscale;
+            sin_[(size_t)pos * half + j] = sinf(theta) * s_.mscale;
         }
-    }
-}
-
-BNNE_Status alloc_host_cache(const Model* m, State* s) {
-    const size_t cache = (size_t)m->L * s->n_ctx * m->kv_dim;
-    s->k_cache = alloc_f32(cache);
-    s->v_cache = alloc_f32(cache);
-    if (!s->k_cache || !s->v_cache) {
-        std::free(s->k_cache);
-        std::free(s->v_cache);
-        s->k_cache = s->v_cache = nullptr;
-        return error(BNNE_ENOMEM, "out of memory");
-    }
-    return BNNE_OK;
-}
-
-BNNE_Status make_resident(bnne_context* c, const Model* m, State* s, bool fused) {
-    const float* attn[kMaxLayers];
-    const float* ffn[kMaxLayers];
-    const float* qn[kMaxLayers];
-    const float* kn[kMaxLayers];
-    const Linear* lin[7][kMaxLayers];
-    for (uint32_t l = 0; l < m->L; ++l) {
-        const Block& b = m->blocks[l];
-        attn[l] = b.attn_norm, ffn[l] = b.ffn_norm, qn[l] = b.q_norm, kn[l] = b.k_norm;
-        lin[0][l] = &b.wq, lin[1][l] = &b.wk, lin[2][l] = &b.wv, lin[3][l] = &b.wo;
-        lin[4][l] = &b.gate, lin[5][l] = &b.up, lin[6][l] = &b.down;
-    }
-    ResidentModel rm = {};
-    rm.C = m->C, rm.H = m->H, rm.Hk = m->Hk, rm.HD = m->HD, rm.FF = m->FF, rm.L = m->L, rm.V = m->V;
-    rm.kv_dim = m->kv_dim, rm.n_ctx = s->n_ctx, rm.eps = m->eps;
-    rm.attn_norm = attn, rm.ffn_norm = ffn, rm.q_norm = qn, rm.k_norm = kn, rm.final_norm = m->final_norm;
-    rm.emb_bits = m->emb_bits, rm.emb_scales = m->emb_scales, rm.rope_cos = s->rope_cos, rm.rope_sin = s->rope_sin;
-    rm.wq = lin[0], rm.wk = lin[1], rm.wv = lin[2], rm.wo = lin[3], rm.gate = lin[4], rm.up = lin[5];
-    rm.down = lin[6], rm.lm_head = &m->lm_head;
-    return resident_create(c, rm, fused, &s->resident);
-}
-
-// Every context starts on the device-resident step; one whose shapes that step
-// does not support (resident_create: ENOTSUP) runs the host step.
-BNNE_Status ctx_init(bnne_context* c, void** out_state) {
-    *out_state = nullptr;
-    const Model* m = static_cast<const Model*>(c->model->impl);
-    State* s = static_cast<State*>(std::calloc(1, sizeof(State)));
-    if (!s)
-        return error(BNNE_ENOMEM, "out of memory");
-    s->n_ctx = c->params.n_ctx;
-    const size_t half = m->HD / 2;
-    s->x = alloc_f32(m->C);
-    s->norm = alloc_f32(m->C);
-    s->q = alloc_f32(m->C);
-    s->y = alloc_f32(m->C);
-    s->o = alloc_f32(m->C);
-    s->k = alloc_f32(m->kv_dim);
-    s->v = alloc_f32(m->kv_dim);
-    s->gate = alloc_f32(m->FF);
-    s->up = alloc_f32(m->FF);
-    s->scores = alloc_f32(s->n_ctx);
-    s->probs = alloc_f32(s->n_ctx);
-    s->rope_cos = alloc_f32((size_t)s->n_ctx * half);
-    s->rope_sin = alloc_f32((size_t)s->n_ctx * half);
-    if (!s->x || !s->norm || !s->q || !s->y || !s->o || !s->k || !s->v || !s->gate || !s->up || !s->scores ||
-        !s->probs || !s->rope_cos || !s->rope_sin) {
-        ctx_free(s);
-        return error(BNNE_ENOMEM, "out of memory");
-    }
-    init_rope_tables(m, s);
-    BNNE_Status st = make_resident(c, m, s, true);
+    // the device path where the backend and the shapes allow it, else the host step
+    const BNNE_Status st = open_device_path(true, &device_);
     if (st == BNNE_ENOTSUP) {
-        error_clear();
-        st = alloc_host_cache(m, s);
+        forget_message();
+        keys_.resize((size_t)s_.layers * p.n_ctx * s_.kv_width);
+        values_.resize(keys_.size());
+    } else if (st != BNNE_OK) {
+        throw Failure{st};
     }
-    if (st != BNNE_OK) {
-        ctx_free(s);
-        return st;
-    }
-    *out_state = s;
-    return BNNE_OK;
 }
 
-// out = x / rms * gain, rms = sqrt(sum x^2 / n + eps), sum in index order (qwen3.c:342-353).
-BNNE_Status rmsnorm(const float* x, uint32_t n, float eps, const float* gain, float* out) {
-    float sum = 0.0f;
+BNNE_Status Qwen3Context::open_device_path(bool fused, Resident** out) {
+    std::vector<const float*> norms[4];
+    std::vector<const SignLinear*> lin[7];
+    for (const auto& l : m_.layers) {
+        norms[0].push_back(l->attn_norm.data());
+        norms[1].push_back(l->ffn_norm.data());
+        norms[2].push_back(l->q_norm.data());
+        norms[3].push_back(l->k_norm.data());
+        const SignLinear* proj[7] = {&l->q, &l->k, &l->v, &l->o, &l->gate, &l->up, &l->down};
+        for (int i = 0; i < 7; ++i)
+            lin[i].push_back(proj[i]);
+    }
+    ResidentModel rm{};
+    rm.C = s_.width, rm.H = s_.heads, rm.Hk = s_.kv_heads, rm.HD = s_.head_dim, rm.FF = s_.ffn;
+    rm.L = s_.layers, rm.V = s_.vocab, rm.kv_dim = s_.kv_width, rm.n_ctx = params.n_ctx, rm.eps = s_.eps;
+    rm.attn_norm = norms[0].data(), rm.ffn_norm = norms[1].data();
+    rm.q_norm = norms[2].data(), rm.k_norm = norms[3].data(), rm.final_norm = m_.final_norm.data();
+    rm.emb_bits = m_.embedding.bits.data(), rm.emb_scales = m_.embedding.scales.data();
+    rm.rope_cos = cos_.data(), rm.rope_sin = sin_.data();
+    rm.wq = lin[0].data(), rm.wk = lin[1].data(), rm.wv = lin[2].data(), rm.wo = lin[3].data();
+    rm.gate = lin[4].data(), rm.up = lin[5].data(), rm.down = lin[6].data(), rm.lm_head = &m_.lm_head;
+    return resident_create(this, rm, fused, out);
+}
+
+void Qwen3Context::select_path(int path) {
+    if (path < 0 || path > 2)
+        raise(BNNE_EINVAL, "decode path %d (0 host, 1 device with fused batches, 2 device)", path);
+    if (path == this->path())
+        return;
+    if (pos != 0)
+        raise(BNNE_EINVAL, "the decode path is chosen before the first token");
+    if (path == 0) {
+        keys_.resize((size_t)s_.layers * params.n_ctx * s_.kv_width);
+        values_.resize(keys_.size());
+        resident_free(device_);
+        device_ = nullptr;
+        return;
+    }
+    Resident* fresh = nullptr;
+    const BNNE_Status st = open_device_path(path == 1, &fresh);
+    if (st != BNNE_OK)
+        throw Failure{st};
+    resident_free(device_);
+    device_ = fresh;
+    std::vector<float>().swap(keys_);
+    std::vector<float>().swap(values_);
+}
+
+// out = x / rms * gain with rms = sqrt(sum of x_i^2 in index order / n + eps) (qwen3.c:342-353);
+// out may be x.
+void rmsnorm(const float* x, uint32_t n, float eps, const float* gain, float* out) {
+    float squares = 0.0f;
     for (uint32_t i = 0; i < n; ++i)
-        sum += x[i] * x[i];
-    const float rms = sqrtf(sum / (float)n + eps);
+        squares += x[i] * x[i];
+    const float rms = sqrtf(squares / (float)n + eps);
     if (!std::isfinite(rms) || rms == 0.0f)
-        return error(BNNE_ECOMPUTE, "Qwen3 RMSNorm produced a non-finite divisor");
+        raise(BNNE_ECOMPUTE, "RMSNorm divisor is zero or not finite");
     for (uint32_t i = 0; i < n; ++i)
         out[i] = x[i] / rms * gain[i];
-    return BNNE_OK;
 }
 
-// Embedding row: +scale where the sign bit is 1, -scale where 0 (qwen3.c:355-366).
-void embed(const Model* m, uint32_t token, float* out) {
-    const uint8_t* bits = m->emb_bits + (size_t)token * (m->C / 8u);
-    const uint16_t* scales = m->emb_scales + (size_t)token * (m->C / kGroup);
-    for (uint32_t g = 0; g < m->C / kGroup; ++g) {
-        const float s = fp16_to_fp32(scales[g]);
-        for (uint32_t j = 0; j < kGroup; ++j) {
-            const bool bit = (bits[g * 16 + (j >> 3)] >> (j & 7u)) & 1u;
-            out[g * kGroup + j] = bit ? s : -s;
-        }
-    }
-}
-
-// Rotation of the pairs (j, j + half) (qwen3.c:368-376).
-void rope(float* v, const float* cs, const float* sn, uint32_t half) {
+// Rotates the pairs (j, j + half) of one head (qwen3.c:368-376).
+void rotate(float* head, const float* c, const float* s, uint32_t half) {
     for (uint32_t j = 0; j < half; ++j) {
-        const float a = v[j], b = v[j + half];
-        v[j] = a * cs[j] - b * sn[j];
-        v[j + half] = a * sn[j] + b * cs[j];
+        const float a = head[j], b = head[j + half];
+        head[j] = a * c[j] - b * s[j];
+        head[j + half] = a * s[j] + b * c[j];
     }
 }
 
-// Causal attention of all heads against cache rows 0..pos (qwen3.c:441-478).
-BNNE_Status attention(const Model* m, State* s, uint32_t layer, uint32_t pos) {
-    const uint32_t kv_mul = m->H / m->Hk;
-    const float scale = 1.0f / sqrtf((float)m->HD);
-    const float* kc = s->k_cache + (size_t)layer * s->n_ctx * m->kv_dim;
-    const float* vc = s->v_cache + (size_t)layer * s->n_ctx * m->kv_dim;
-    for (uint32_t h = 0; h < m->H; ++h) {
-        const size_t head_off = (size_t)(h / kv_mul) * m->HD;
-        const float* q = s->q + (size_t)h * m->HD;
-        float maximum = -INFINITY;
+// Every query head against cache rows 0..pos of its key/value head (qwen3.c:441-478):
+// scores q.k * (1 / sqrt(head_dim)), softmax, probability-weighted sum of the values.
+void Qwen3Context::attend(uint32_t layer, uint32_t pos) {
+    const uint32_t HD = s_.head_dim, group = s_.heads / s_.kv_heads;
+    const float scale = 1.0f / sqrtf((float)HD);
+    const float* keys = keys_.data() + (size_t)layer * params.n_ctx * s_.kv_width;
+    const float* values = values_.data() + (size_t)layer * params.n_ctx * s_.kv_width;
+    for (uint32_t h = 0; h < s_.heads; ++h) {
+        const float* q = q_.data() + (size_t)h * HD;
+        const size_t kv_head = (size_t)(h / group) * HD;
+        float top = -INFINITY;
         for (uint32_t t = 0; t <= pos; ++t) {
-            const float* key = kc + (size_t)t * m->kv_dim + head_off;
+            const float* key = keys + (size_t)t * s_.kv_width + kv_head;
             float dot = 0.0f;
-            for (uint32_t i = 0; i < m->HD; ++i)
+            for (uint32_t i = 0; i < HD; ++i)
                 dot += q[i] * key[i];
             const float score = dot * scale;
             if (!std::isfinite(score))
-                return error(BNNE_ECOMPUTE, "Qwen3 attention score is not finite");
-            s->scores[t] = score;
-            if (score > maximum)
-                maximum = score;
+                raise(BNNE_ECOMPUTE, "non-finite attention score");
+            scores_[t] = score;
+            if (score > top)
+                top = score;
         }
-        float sum = 0.0f;
+        float total = 0.0f;
         for (uint32_t t = 0; t <= pos; ++t) {
-            const float p = expf(s->scores[t] - maximum);
-            s->probs[t] = p;
-            sum += p;
+            probs_[t] = expf(scores_[t] - top);
+            total += probs_[t];
         }
-        if (!(sum > 0.0f) || !std::isfinite(sum))
-            return error(BNNE_ECOMPUTE, "Qwen3 attention softmax failed");
+        if (!(total > 0.0f) || !std::isfinite(total))
+            raise(BNNE_ECOMPUTE, "softmax normaliser is zero or not finite");
         for (uint32_t t = 0; t <= pos; ++t)
-            s->probs[t] /= sum;
-        for (uint32_t i = 0; i < m->HD; ++i) {
+            probs_[t] /= total;
+        float* out = y_.data() + (size_t)h * HD;
+        for (uint32_t i = 0; i < HD; ++i) {
             float acc = 0.0f;
             for (uint32_t t = 0; t <= pos; ++t)
-                acc += s->probs[t] * vc[(size_t)t * m->kv_dim + head_off + i];
-            s->y[(size_t)h * m->HD + i] = acc;
+                acc += probs_[t] * values[(size_t)t * s_.kv_width + kv_head + i];
+            out[i] = acc;
         }
     }
-    return BNNE_OK;
 }
 
-#define TRY(expr)                          \
-    do {                                   \
-        const BNNE_Status st_ = (expr);    \
-        if (st_ != BNNE_OK)                \
-            return st_;                    \
-    } while (0)
-
-BNNE_Status step(bnne_context* c, uint32_t token, uint32_t pos, float* logits) {
-    const Model* m = static_cast<const Model*>(c->model->impl);
-    State* s = static_cast<State*>(c->state);
-    const uint32_t half = m->HD / 2;
-    embed(m, token, s->x);
-    for (uint32_t l = 0; l < m->L; ++l) {
-        const Block& b = m->blocks[l];
-        TRY(rmsnorm(s->x, m->C, m->eps, b.attn_norm, s->norm));
-        TRY(linear_forward(c, &b.wq, s->norm, s->q));
-        TRY(linear_forward(c, &b.wk, s->norm, s->k));
-        TRY(linear_forward(c, &b.wv, s->norm, s->v));
-        for (uint32_t h = 0; h < m->H; ++h)
-            TRY(rmsnorm(s->q + (size_t)h * m->HD, m->HD, m->eps, b.q_norm, s->q + (size_t)h * m->HD));
-        for (uint32_t h = 0; h < m->Hk; ++h)
-            TRY(rmsnorm(s->k + (size_t)h * m->HD, m->HD, m->eps, b.k_norm, s->k + (size_t)h * m->HD));
-        const float* cs = s->rope_cos + (size_t)pos * half;
-        const float* sn = s->rope_sin + (size_t)pos * half;
-        for (uint32_t h = 0; h < m->H; ++h)
-            rope(s->q + (size_t)h * m->HD, cs, sn, half);
-        for (uint32_t h = 0; h < m->Hk; ++h)
-            rope(s->k + (size_t)h * m->HD, cs, sn, half);
-        const size_t at = ((size_t)l * s->n_ctx + pos) * m->kv_dim;
-        std::memcpy(s->k_cache + at, s->k, (size_t)m->kv_dim * sizeof(float));
-        std::memcpy(s->v_cache + at, s->v, (size_t)m->kv_dim * sizeof(float));
-        TRY(attention(m, s, l, pos));
-        TRY(linear_forward(c, &b.wo, s->y, s->o));
-        for (uint32_t i = 0; i < m->C; ++i)
-            s->x[i] += s->o[i];
-        TRY(rmsnorm(s->x, m->C, m->eps, b.ffn_norm, s->norm));
-        TRY(linear_forward(c, &b.gate, s->norm, s->gate));
-        TRY(linear_forward(c, &b.up, s->norm, s->up));
-        for (uint32_t i = 0; i < m->FF; ++i) {
-            const float g = s->gate[i];
+void Qwen3Context::step(uint32_t token, uint32_t pos, float* logits) {
+    const uint32_t C = s_.width, HD = s_.head_dim, half = HD / 2;
+    // embedding row: +scale / -scale by sign bit (qwen3.c:355-366)
+    const uint8_t* bits = m_.embedding.bits.data() + (size_t)token * (C / 8u);
+    const uint16_t* scales = m_.embedding.scales.data() + (size_t)token * (C / kGroup);
+    for (uint32_t i = 0; i < C; ++i) {
+        const float scale = half_to_float(scales[i / kGroup]);
+        x_[i] = (bits[i / 8u] >> (i % 8u)) & 1u ? scale : -scale;
+    }
+    for (uint32_t l = 0; l < s_.layers; ++l) {
+        const Layer& L = *m_.layers[l];
+        rmsnorm(x_.data(), C, s_.eps, L.attn_norm.data(), norm_.data());
+        L.q.apply(*this, norm_.data(), q_.data());
+        L.k.apply(*this, norm_.data(), k_.data());
+        L.v.apply(*this, norm_.data(), v_.data());
+        for (uint32_t h = 0; h < s_.heads; ++h)
+            rmsnorm(q_.data() + (size_t)h * HD, HD, s_.eps, L.q_norm.data(), q_.data() + (size_t)h * HD);
+        for (uint32_t h = 0; h < s_.kv_heads; ++h)
+            rmsnorm(k_.data() + (size_t)h * HD, HD, s_.eps, L.k_norm.data(), k_.data() + (size_t)h * HD);
+        const float* c = cos_.data() + (size_t)pos * half;
+        const float* sn = sin_.data() + (size_t)pos * half;
+        for (uint32_t h = 0; h < s_.heads; ++h)
+            rotate(q_.data() + (size_t)h * HD, c, sn, half);
+        for (uint32_t h = 0; h < s_.kv_heads; ++h)
+            rotate(k_.data() + (size_t)h * HD, c, sn, half);
+        const size_t row = ((size_t)l * params.n_ctx + pos) * s_.kv_width;
+        std::memcpy(keys_.data() + row, k_.data(), (size_t)s_.kv_width * sizeof(float));
+        std::memcpy(values_.data() + row, v_.data(), (size_t)s_.kv_width * sizeof(float));
+        attend(l, pos);
+        L.o.apply(*this, y_.data(), o_.data());
+        for (uint32_t i = 0; i < C; ++i)
+            x_[i] += o_[i];
+        rmsnorm(x_.data(), C, s_.eps, L.ffn_norm.data(), norm_.data());
+        L.gate.apply(*this, norm_.data(), gate_.data());
+        L.up.apply(*this, norm_.data(), up_.data());
+        for (uint32_t i = 0; i < s_.ffn; ++i) {
+            const float g = gate_[i];
             const float silu = g / (1.0f + expf(-g));
-            s->gate[i] = silu * s->up[i];
+            gate_[i] = silu * up_[i];
         }
-        TRY(linear_forward(c, &b.down, s->gate, s->o));
-        for (uint32_t i = 0; i < m->C; ++i)
-            s->x[i] += s->o[i];
+        L.down.apply(*this, gate_.data(), o_.data());
+        for (uint32_t i = 0; i < C; ++i)
+            x_[i] += o_[i];
     }
     if (logits) {
-        TRY(rmsnorm(s->x, m->C, m->eps, m->final_norm, s->norm));
-        TRY(linear_forward(c, &m->lm_head, s->norm, logits));
+        rmsnorm(x_.data(), C, s_.eps, m_.final_norm.data(), norm_.data());
+        m_.lm_head.apply(*this, norm_.data(), logits);
     }
-    return BNNE_OK;
 }
 
-BNNE_Status decode(bnne_context* c, const int32_t* tokens, uint32_t n, float* logits) {
-    State* s = static_cast<State*>(c->state);
-    if (s->resident)
-        return resident_step(c, s->resident, tokens, n, c->pos, logits);
+void Qwen3Context::decode(const int32_t* tokens, uint32_t n, float* logits) {
+    if (device_) {
+        const BNNE_Status st = resident_step(this, device_, tokens, n, pos, logits);
+        if (st != BNNE_OK)
+            throw Failure{st};
+        return;
+    }
     for (uint32_t i = 0; i < n; ++i)
-        TRY(step(c, (uint32_t)tokens[i], c->pos + i, i + 1 == n ? logits : nullptr));
-    return BNNE_OK;
+        step((uint32_t)tokens[i], pos + i, i + 1 == n ? logits : nullptr);
 }
 
-// Positions beyond 'pos' are simply overwritten by later steps.
-BNNE_Status truncate(bnne_context*, uint32_t) { return BNNE_OK; }
+bnne_context* Qwen3Model::new_context(const BNNE_ContextParams& p) { return new Qwen3Context(*this, p); }
 
 }  // namespace
 
-const Arch kArchQwen3 = {"qwen3", BNNE_TASK_LLM, load, unload, ctx_init, ctx_free, nullptr, decode, truncate};
+bnne_model* make_qwen3() { return new Qwen3Model; }
 
-BNNE_Status qwen3_set_resident(bnne_context* c, int mode) {
-    if (c->model->arch != &kArchQwen3)
-        return error(BNNE_ENOTSUP, "only qwen3 contexts have a device-resident step");
-    if (mode < 0 || mode > 2)
-        return error(BNNE_EINVAL, "unknown decode path %d", mode);
-    State* s = static_cast<State*>(c->state);
-    if (mode == qwen3_resident_mode(c))
-        return BNNE_OK;
-    if (c->pos != 0)
-        return error(BNNE_EINVAL, "the decode path can only change before the first token");
-    const Model* m = static_cast<const Model*>(c->model->impl);
-    if (mode != 0) {
-        Resident* old = s->resident;
-        s->resident = nullptr;
-        const BNNE_Status st = make_resident(c, m, s, mode == 1);
-        if (st != BNNE_OK) {
-            s->resident = old;
-            return st;
-        }
-        resident_free(old);
-        std::free(s->k_cache);
-        std::free(s->v_cache);
-        s->k_cache = s->v_cache = nullptr;
-        return BNNE_OK;
-    }
-    const BNNE_Status st = alloc_host_cache(m, s);
-    if (st != BNNE_OK)
-        return st;
-    resident_free(s->resident);
-    s->resident = nullptr;
-    return BNNE_OK;
+BNNE_Status qwen3_select_path(bnne_context* ctx, int path) {
+    Qwen3Context* q = dynamic_cast<Qwen3Context*>(ctx);
+    if (!q)
+        return complain(BNNE_ENOTSUP, "only qwen3 contexts have a device path");
+    return guarded([&] { q->select_path(path); });
 }
 
-int qwen3_resident_mode(const bnne_context* c) {
-    if (c->model->arch != &kArchQwen3)
-        return 0;
-    const Resident* r = static_cast<const State*>(c->state)->resident;
-    return r == nullptr ? 0 : resident_fused(r) ? 1 : 2;
+int qwen3_path(const bnne_context* ctx) {
+    const Qwen3Context* q = dynamic_cast<const Qwen3Context*>(ctx);
+    return q ? q->path() : 0;
 }
 
 }  // namespace bnne

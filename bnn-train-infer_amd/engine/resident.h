@@ -13,7 +13,7 @@
 #ifndef BNNE_RESIDENT_H
 #define BNNE_RESIDENT_H
 
-#include "engine_internal.h"
+#include "engine.hpp"
 
 namespace bnne {
 
@@ -29,14 +29,14 @@ struct ResidentModel {  // host views of the model, used once to build the devic
     const uint16_t* emb_scales;     // [V][C/128]
     const float* rope_cos;          // [n_ctx][HD/2]
     const float* rope_sin;
-    const Linear* const* wq;  // [L] each
-    const Linear* const* wk;
-    const Linear* const* wv;
-    const Linear* const* wo;
-    const Linear* const* gate;
-    const Linear* const* up;
-    const Linear* const* down;
-    const Linear* lm_head;
+    const SignLinear* const* wq;  // [L] each
+    const SignLinear* const* wk;
+    const SignLinear* const* wv;
+    const SignLinear* const* wo;
+    const SignLinear* const* gate;
+    const SignLinear* const* up;
+    const SignLinear* const* down;
+    const SignLinear* lm_head;
 };
 
 struct Resident;

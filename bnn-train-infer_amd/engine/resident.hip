@@ -656,7 +656,7 @@ struct Resident {
     bool allow_fused, fused;
     BNNX_Batch *qkv, *attn_out, *gate_up, *down;
     BNNX_Batch lm_head;
-    const Linear** lin;  // [7 * L + 1]: per layer q, k, v, o, gate, up, down; then lm_head
+    const SignLinear** lin;  // [7 * L + 1]: per layer q, k, v, o, gate, up, down; then lm_head
     uint64_t jobs_per_token, macs_per_token, lm_jobs, lm_macs;
 };
 
@@ -664,13 +664,13 @@ namespace {
 
 BNNE_Status hip_error(hipError_t e, const char* what) {
     (void)hipGetLastError();
-    return error(e == hipErrorOutOfMemory ? BNNE_ENOMEM : BNNE_EIO, "%s: %s", what, hipGetErrorString(e));
+    return complain(e == hipErrorOutOfMemory ? BNNE_ENOMEM : BNNE_EIO, "%s: %s", what, hipGetErrorString(e));
 }
 
 BNNE_Status alloc_buffer(Resident* r, size_t floats, BNN_Buffer* b, float** ptr) {
-    BNNE_Status st = accel_error(BNN_BufferAlloc(r->dev, floats * sizeof(float), b), "BNN_BufferAlloc");
+    BNNE_Status st = accel_status(BNN_BufferAlloc(r->dev, floats * sizeof(float), b), "BNN_BufferAlloc");
     if (st == BNNE_OK)
-        st = accel_error(BNNX_BufferDevicePointer(*b, reinterpret_cast<void**>(ptr)), "BNNX_BufferDevicePointer");
+        st = accel_status(BNNX_BufferDevicePointer(*b, reinterpret_cast<void**>(ptr)), "BNNX_BufferDevicePointer");
     return st;
 }
 
@@ -682,55 +682,55 @@ BNNE_Status upload(T** dst, const void* src, size_t bytes) {
     return e == hipSuccess ? BNNE_OK : hip_error(e, "device upload");
 }
 
-void add_jobs(const Linear* l, BNN_Buffer in, BNN_Buffer out, BNN_Job* jobs, uint32_t* n, uint64_t* macs) {
-    for (uint32_t c = 0; c < l->n_chunks; ++c) {
+void add_jobs(const SignLinear* l, BNN_Buffer in, BNN_Buffer out, BNN_Job* jobs, uint32_t* n, uint64_t* macs) {
+    for (uint32_t c = 0; c < (uint32_t)l->shards().size(); ++c) {
         BNN_Job& j = jobs[(*n)++];
         j = BNN_Job{};
         j.operation = BNN_OP_GEMV_F32;
-        j.matrix = l->chunks[c].matrix;
+        j.matrix = l->shards()[c].matrix;
         j.input.buffer = in;
         j.input.type = BNN_TYPE_F32;
         j.output.buffer = out;
         j.output.type = BNN_TYPE_F32;
-        j.output.offset = (size_t)l->chunks[c].out_off * sizeof(float);
+        j.output.offset = (size_t)l->shards()[c].first * sizeof(float);
         j.rows = 1;
     }
-    *macs += (uint64_t)l->in * l->out;
+    *macs += (uint64_t)l->in() * l->out();
 }
 
-BNNE_Status make_batch(Resident* r, std::initializer_list<std::pair<const Linear*, BNN_Buffer>> parts, BNN_Buffer in,
+BNNE_Status make_batch(Resident* r, std::initializer_list<std::pair<const SignLinear*, BNN_Buffer>> parts, BNN_Buffer in,
                        BNNX_Batch* out, uint64_t* jobs_total, uint64_t* macs) {
     uint32_t count = 0;
     for (const auto& p : parts)
-        count += p.first->n_chunks;
+        count += (uint32_t)p.first->shards().size();
     BNN_Job* jobs = static_cast<BNN_Job*>(std::calloc(count, sizeof(BNN_Job)));
     if (!jobs)
-        return error(BNNE_ENOMEM, "out of memory");
+        return complain(BNNE_ENOMEM, "out of memory");
     uint32_t n = 0;
     for (const auto& p : parts)
         add_jobs(p.first, in, p.second, jobs, &n, macs);
-    const BNNE_Status st = accel_error(BNNX_BatchCreate(r->dev, jobs, n, out), "BNNX_BatchCreate");
+    const BNNE_Status st = accel_status(BNNX_BatchCreate(r->dev, jobs, n, out), "BNNX_BatchCreate");
     std::free(jobs);
     *jobs_total += n;
     return st;
 }
 
-BNNE_Status make_fused(Resident* r, std::initializer_list<std::pair<const Linear*, BNN_Buffer>> parts, BNN_Buffer in,
+BNNE_Status make_fused(Resident* r, std::initializer_list<std::pair<const SignLinear*, BNN_Buffer>> parts, BNN_Buffer in,
                        const BNNX_PreOp& pre, BNNX_Batch* out, uint64_t* jobs_total, uint64_t* macs,
-                       BNN_Status* accel_status, const BNNX_PostOp* post = nullptr) {
+                       BNN_Status* refused, const BNNX_PostOp* post = nullptr) {
     uint32_t count = 0;
     for (const auto& p : parts)
-        count += p.first->n_chunks;
+        count += (uint32_t)p.first->shards().size();
     BNN_Job* jobs = static_cast<BNN_Job*>(std::calloc(count, sizeof(BNN_Job)));
     if (!jobs)
-        return error(BNNE_ENOMEM, "out of memory");
+        return complain(BNNE_ENOMEM, "out of memory");
     uint32_t n = 0;
     for (const auto& p : parts)
         add_jobs(p.first, in, p.second, jobs, &n, macs);
-    *accel_status = BNNX_BatchCreateFusedPost(r->dev, jobs, n, &pre, post, out);
+    *refused = BNNX_BatchCreateFusedPost(r->dev, jobs, n, &pre, post, out);
     std::free(jobs);
     *jobs_total += n;
-    return *accel_status == BNN_OK ? BNNE_OK : accel_error(*accel_status, "BNNX_BatchCreateFusedPost");
+    return *refused == BNN_OK ? BNNE_OK : accel_status(*refused, "BNNX_BatchCreateFusedPost");
 }
 
 // Error codes of the fused step (see set_error_first).
@@ -770,18 +770,18 @@ void destroy_batches(Resident* r) {
 //   down:   the row h                                                -> o
 //   lm_head RMSNorm(x + o) with final_norm                           -> logits
 // so the residual stream alternates between x and x2 within a layer and is in x
-// (plus the down output in o) between layers.  *accel_status is the backend's
+// (plus the down output in o) between layers.  *refused is the backend's
 // status of the first batch it refused.
-BNNE_Status build_fused(Resident* r, BNN_Status* accel_status) {
+BNNE_Status build_fused(Resident* r, BNN_Status* refused) {
     r->jobs_per_token = r->macs_per_token = r->lm_jobs = r->lm_macs = 0;
-    *accel_status = BNN_OK;
+    *refused = BNN_OK;
     const uint32_t C = r->C;
     const float* attn_norm = r->gains;
     const float* ffn_norm = r->gains + (size_t)r->L * C;
     const float* final_norm = r->gains + 2 * (size_t)r->L * C + 2 * (size_t)r->L * r->HD;
     BNNE_Status st = BNNE_OK;
     for (uint32_t l = 0; st == BNNE_OK && l < r->L; ++l) {
-        const Linear* const* p = r->lin + 7 * (size_t)l;
+        const SignLinear* const* p = r->lin + 7 * (size_t)l;
         const int base = (int)l * code_span(r);
         BNNX_PreOp pre{};
         pre.kind = BNNX_PRE_RMSNORM;
@@ -794,13 +794,13 @@ BNNE_Status build_fused(Resident* r, BNN_Status* accel_status) {
         pre.err = r->err;
         pre.err_code = base + 1;
         st = make_fused(r, {{p[0], r->b_q}, {p[1], r->b_k}, {p[2], r->b_v}}, r->b_norm, pre, &r->qkv[l],
-                        &r->jobs_per_token, &r->macs_per_token, accel_status);
+                        &r->jobs_per_token, &r->macs_per_token, refused);
         if (st == BNNE_OK) {
             BNNX_PreOp row{};
             row.kind = BNNX_PRE_ROW;
             row.width = C;
             st = make_fused(r, {{p[3], r->b_o}}, r->b_y, row, &r->attn_out[l], &r->jobs_per_token, &r->macs_per_token,
-                            accel_status);
+                            refused);
         }
         if (st == BNNE_OK) {
             pre.a = r->x2;
@@ -813,14 +813,14 @@ BNNE_Status build_fused(Resident* r, BNN_Status* accel_status) {
             silu.kind = BNNX_POST_SILU_MUL;
             silu.out = r->h;
             st = make_fused(r, {{p[4], r->b_gate}, {p[5], r->b_up}}, r->b_norm, pre, &r->gate_up[l], &r->jobs_per_token,
-                            &r->macs_per_token, accel_status, &silu);
+                            &r->macs_per_token, refused, &silu);
         }
         if (st == BNNE_OK) {
             BNNX_PreOp row{};
             row.kind = BNNX_PRE_ROW;
             row.width = r->FF;
             st = make_fused(r, {{p[6], r->b_o}}, r->b_h, row, &r->down[l], &r->jobs_per_token, &r->macs_per_token,
-                            accel_status);
+                            refused);
         }
     }
     if (st == BNNE_OK) {
@@ -834,7 +834,7 @@ BNNE_Status build_fused(Resident* r, BNN_Status* accel_status) {
         pre.err = r->err;
         pre.err_code = (int)r->L * code_span(r) + 1;
         st = make_fused(r, {{r->lin[7 * (size_t)r->L], r->b_logits}}, r->b_norm, pre, &r->lm_head, &r->lm_jobs,
-                        &r->lm_macs, accel_status);
+                        &r->lm_macs, refused);
     }
     return st;
 }
@@ -861,7 +861,7 @@ BNNE_Status build_unfused(Resident* r) {
     r->jobs_per_token = r->macs_per_token = r->lm_jobs = r->lm_macs = 0;
     BNNE_Status st = BNNE_OK;
     for (uint32_t l = 0; st == BNNE_OK && l < r->L; ++l) {
-        const Linear* const* p = r->lin + 7 * (size_t)l;
+        const SignLinear* const* p = r->lin + 7 * (size_t)l;
         st = make_batch(r, {{p[0], r->b_q}, {p[1], r->b_k}, {p[2], r->b_v}}, r->b_norm, &r->qkv[l], &r->jobs_per_token,
                         &r->macs_per_token);
         if (st == BNNE_OK)
@@ -884,16 +884,16 @@ bool resident_fused(const Resident* r) { return r->fused; }
 BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, bool fused, Resident** out) {
     *out = nullptr;
     if (m.HD > kMaxHeadDim || m.HD % 4u != 0 || m.C > kMaxNormWidth)
-        return error(BNNE_ENOTSUP, "device-resident decode supports head_dim <= %u (a multiple of 4) and width <= %u",
+        return complain(BNNE_ENOTSUP, "device-resident decode supports head_dim <= %u (a multiple of 4) and width <= %u",
                      kMaxHeadDim, kMaxNormWidth);
     Resident* r = static_cast<Resident*>(std::calloc(1, sizeof(Resident)));
     if (!r)
-        return error(BNNE_ENOMEM, "out of memory");
+        return complain(BNNE_ENOMEM, "out of memory");
     r->dev = c->model->device;
     r->C = m.C, r->H = m.H, r->Hk = m.Hk, r->HD = m.HD, r->FF = m.FF, r->L = m.L, r->V = m.V;
     r->kv_dim = m.kv_dim, r->n_ctx = m.n_ctx, r->eps = m.eps;
     r->allow_fused = fused;
-    BNNE_Status st = accel_error(BNNX_DeviceStream(r->dev, reinterpret_cast<void**>(&r->stream)), "BNNX_DeviceStream");
+    BNNE_Status st = accel_status(BNNX_DeviceStream(r->dev, reinterpret_cast<void**>(&r->stream)), "BNNX_DeviceStream");
     hipError_t e = hipSuccess;
     if (st == BNNE_OK) {
         e = hipStreamGetDevice(r->stream, &r->ordinal);
@@ -939,7 +939,7 @@ BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, bool fused,
         const size_t n = 2 * (size_t)m.L * m.C + 2 * (size_t)m.L * m.HD + m.C;
         float* host = static_cast<float*>(std::malloc(n * sizeof(float)));
         if (!host) {
-            st = error(BNNE_ENOMEM, "out of memory");
+            st = complain(BNNE_ENOMEM, "out of memory");
         } else {
             float* p = host;
             for (uint32_t l = 0; l < m.L; ++l, p += m.C)
@@ -973,13 +973,13 @@ BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, bool fused,
         r->attn_out = static_cast<BNNX_Batch*>(std::calloc(m.L, sizeof(BNNX_Batch)));
         r->gate_up = static_cast<BNNX_Batch*>(std::calloc(m.L, sizeof(BNNX_Batch)));
         r->down = static_cast<BNNX_Batch*>(std::calloc(m.L, sizeof(BNNX_Batch)));
-        r->lin = static_cast<const Linear**>(std::calloc(7 * (size_t)m.L + 1, sizeof(Linear*)));
+        r->lin = static_cast<const SignLinear**>(std::calloc(7 * (size_t)m.L + 1, sizeof(SignLinear*)));
         if (!r->qkv || !r->attn_out || !r->gate_up || !r->down || !r->lin)
-            st = error(BNNE_ENOMEM, "out of memory");
+            st = complain(BNNE_ENOMEM, "out of memory");
     }
     if (st == BNNE_OK) {
         for (uint32_t l = 0; l < m.L; ++l) {
-            const Linear** p = r->lin + 7 * (size_t)l;
+            const SignLinear** p = r->lin + 7 * (size_t)l;
             p[0] = m.wq[l], p[1] = m.wk[l], p[2] = m.wv[l], p[3] = m.wo[l];
             p[4] = m.gate[l], p[5] = m.up[l], p[6] = m.down[l];
         }
@@ -1017,7 +1017,7 @@ void resident_free(Resident* r) {
 BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, uint32_t n, uint32_t pos0,
                           float* logits) {
     const bool stats = c->params.enable_stats != 0;
-    const uint64_t t0 = stats ? now_ns() : 0;
+    const uint64_t t0 = stats ? clock_ns() : 0;
     hipError_t e = hipSetDevice(r->ordinal);
     if (e != hipSuccess)
         return hip_error(e, "hipSetDevice");
@@ -1040,11 +1040,11 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         if (st != BNNE_OK)
             return st;
     } else if (valid != BNN_OK) {
-        return accel_error(valid, "BNNX_BatchCheck");
+        return accel_status(valid, "BNNX_BatchCheck");
     }
     auto launch = [&](BNNX_Batch b) {
         if (st == BNNE_OK)
-            st = accel_error(BNNX_BatchLaunch(b), "BNNX_BatchLaunch");
+            st = accel_status(BNNX_BatchLaunch(b), "BNNX_BatchLaunch");
     };
     for (uint32_t i = 0; i < n && st == BNNE_OK && r->fused; ++i) {
         const uint32_t pos = pos0 + i;
@@ -1099,9 +1099,9 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         }
     }
     e = hipGetLastError();
-    const uint64_t t1 = stats ? now_ns() : 0;
+    const uint64_t t1 = stats ? clock_ns() : 0;
     const BNN_Status sync = BNNX_DeviceSynchronize(r->dev);
-    const uint64_t t2 = stats ? now_ns() : 0;
+    const uint64_t t2 = stats ? clock_ns() : 0;
     if (st != BNNE_OK)
         return st;
     if (e != hipSuccess)
@@ -1118,21 +1118,21 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         kind = p == 1 || p == 2 || p == code_span(r) - 1 ? kErrNorm : ((p - 3) % 2 == 0 ? kErrScore : kErrSoftmax);
     }
     if (kind == kErrNorm)
-        return error(BNNE_ECOMPUTE, "Qwen3 RMSNorm produced a non-finite divisor");
+        return complain(BNNE_ECOMPUTE, "RMSNorm divisor is zero or not finite");
     if (kind == kErrScore)
-        return error(BNNE_ECOMPUTE, "Qwen3 attention score is not finite");
+        return complain(BNNE_ECOMPUTE, "non-finite attention score");
     if (kind == kErrSoftmax)
-        return error(BNNE_ECOMPUTE, "Qwen3 attention softmax failed");
-    st = accel_error(sync, "BNN_Execute");
+        return complain(BNNE_ECOMPUTE, "softmax normaliser is zero or not finite");
+    st = accel_status(sync, "BNN_Execute");
     if (st != BNNE_OK)
         return st;
     if (logits) {
-        st = accel_error(BNN_BufferRead(r->b_logits, 0, logits, (size_t)r->V * sizeof(float)), "BNN_BufferRead");
+        st = accel_status(BNN_BufferRead(r->b_logits, 0, logits, (size_t)r->V * sizeof(float)), "BNN_BufferRead");
         if (st != BNNE_OK)
             return st;
     }
     if (stats) {
-        const uint64_t t3 = now_ns();
+        const uint64_t t3 = clock_ns();
         c->stats.execute_ns += t2 - t1;
         c->stats.transfer_ns += t3 - t2;
         const uint64_t lm = logits ? 1 : 0;

@@ -8,11 +8,12 @@
 // and 4) keep their text.  The vocabulary must spell all 256 bytes.  End of
 // generation: the declared EOS id and the tokens "<|endoftext|>" and "<|im_end|>".
 // Text encoding (BNNE_Tokenize) is not part of this build.
-#include "engine_internal.h"
+#include "engine.hpp"
 
-#include <cstdlib>
 #include <cstring>
+#include <optional>
 #include <string>
+#include <string_view>
 #include <unordered_set>
 
 namespace bnne {
@@ -75,94 +76,76 @@ std::string utf8_of(uint32_t cp) {
 
 }  // namespace
 
-void vocab_free(Vocab* v) {
-    if (!v)
-        return;
-    std::free(v->text);
-    std::free(v->off);
-    std::free(v->len);
-    std::free(v);
-}
-
-BNNE_Status vocab_build(const Gguf* g, Vocab** out) {
-    *out = nullptr;
-    if (!g->tokens || !g->token_count)
-        return error(BNNE_EFORMAT, "tokenizer has no vocabulary");
-    if (g->token_count > UINT32_MAX)
-        return error(BNNE_ERANGE, "tokenizer vocabulary is too large");
+Vocab::Vocab(const GgufFile& file) {
+    const std::vector<std::string_view> tokens = file.texts("tokenizer.ggml.tokens");
+    const std::vector<uint32_t> types = file.words("tokenizer.ggml.token_type");
+    if (tokens.empty())
+        raise(BNNE_EFORMAT, "the model has no token list");
+    if (tokens.size() > UINT32_MAX)
+        raise(BNNE_ERANGE, "the token list is too long");
     uint32_t cp_of[256];
     byte_code_points(cp_of);
     {
-        std::unordered_set<std::string> spelled;
-        spelled.reserve(g->token_count * 2);
-        for (uint64_t i = 0; i < g->token_count; ++i)
-            spelled.emplace(reinterpret_cast<const char*>(g->tokens[i].data), g->tokens[i].length);
+        std::unordered_set<std::string_view> spelled(tokens.begin(), tokens.end());
         for (uint32_t b = 0; b < 256; ++b)
             if (!spelled.count(utf8_of(cp_of[b])))
-                return error(BNNE_EFORMAT, "vocabulary is missing a byte token");
+                raise(BNNE_EFORMAT, "the token list does not spell every byte");
     }
     int byte_of_cp[512];
     std::memset(byte_of_cp, 0xff, sizeof byte_of_cp);
     for (uint32_t b = 0; b < 256; ++b)
         byte_of_cp[cp_of[b]] = (int)b;
 
-    Vocab* v = static_cast<Vocab*>(std::calloc(1, sizeof(Vocab)));
-    uint64_t total = 0;
-    for (uint64_t i = 0; i < g->token_count; ++i)
-        total += g->tokens[i].length + 1u;
-    if (v) {
-        v->text = static_cast<char*>(std::malloc(total));
-        v->off = static_cast<uint32_t*>(std::malloc(g->token_count * sizeof(uint32_t)));
-        v->len = static_cast<uint32_t*>(std::malloc(g->token_count * sizeof(uint32_t)));
-    }
-    if (!v || !v->text || !v->off || !v->len || total > UINT32_MAX) {
-        vocab_free(v);
-        return error(total > UINT32_MAX ? BNNE_ERANGE : BNNE_ENOMEM, "vocabulary table");
-    }
-    v->count = g->token_count;
-    size_t used = 0;
-    for (uint64_t i = 0; i < g->token_count; ++i) {
-        const GgufString& t = g->tokens[i];
-        const uint32_t type = g->token_types && i < g->token_type_count ? g->token_types[i] : 1u;
-        v->off[i] = (uint32_t)used;
-        if (type == 3 || type == 4) {
-            std::memcpy(v->text + used, t.data, t.length);
-            used += t.length;
+    offset_.resize(tokens.size());
+    length_.resize(tokens.size());
+    for (size_t i = 0; i < tokens.size(); ++i) {
+        const std::string_view t = tokens[i];
+        const uint8_t* p = reinterpret_cast<const uint8_t*>(t.data());
+        const uint32_t type = i < types.size() ? types[i] : 1u;
+        if (text_.size() > UINT32_MAX - t.size() - 1)
+            raise(BNNE_ERANGE, "the token list is too long");
+        offset_[i] = (uint32_t)text_.size();
+        if (type == 3 || type == 4) {  // control and user-defined tokens keep their text
+            text_.append(t);
         } else {
             size_t pos = 0;
-            while (pos < t.length) {
+            while (pos < t.size()) {
                 uint32_t cp = 0;
-                size_t n = utf8_next(t.data + pos, t.length - pos, &cp);
+                size_t n = utf8_next(p + pos, t.size() - pos, &cp);
                 if (n && cp < 512 && byte_of_cp[cp] >= 0) {
-                    v->text[used++] = (char)byte_of_cp[cp];
+                    text_.push_back((char)byte_of_cp[cp]);
                 } else {
                     n = n ? n : 1;
-                    std::memcpy(v->text + used, t.data + pos, n);
-                    used += n;
+                    text_.append(t.substr(pos, n));
                 }
                 pos += n;
             }
         }
-        v->len[i] = (uint32_t)(used - v->off[i]);
-        v->text[used++] = '\0';
+        length_[i] = (uint32_t)(text_.size() - offset_[i]);
+        text_.push_back('\0');
     }
-    auto add_eog = [&](uint32_t id) {
-        for (uint32_t k = 0; k < v->n_eog; ++k)
-            if (v->eog[k] == id)
+    const auto add_eog = [&](uint32_t id) {
+        for (uint32_t e : eog_)
+            if (e == id)
                 return;
-        if (v->n_eog < 8)
-            v->eog[v->n_eog++] = id;
+        if (eog_.size() < 8)
+            eog_.push_back(id);
     };
-    if (g->has_eos && g->eos_token_id < g->token_count)
-        add_eog(g->eos_token_id);
-    for (uint64_t i = 0; i < g->token_count; ++i) {
-        const GgufString& t = g->tokens[i];
-        if ((t.length == 13 && std::memcmp(t.data, "<|endoftext|>", 13) == 0) ||
-            (t.length == 10 && std::memcmp(t.data, "<|im_end|>", 10) == 0))
+    if (const std::optional<uint64_t> eos = file.integer("tokenizer.ggml.eos_token_id"))
+        if ((uint32_t)*eos < tokens.size())
+            add_eog((uint32_t)*eos);
+    for (size_t i = 0; i < tokens.size(); ++i)
+        if (tokens[i] == "<|endoftext|>" || tokens[i] == "<|im_end|>")
             add_eog((uint32_t)i);
-    }
-    *out = v;
-    return BNNE_OK;
+}
+
+std::string_view Vocab::piece(uint32_t id) const { return std::string_view(text_.data() + offset_[id], length_[id]); }
+
+bool Vocab::ends_generation(uint32_t id) const {
+    for (uint32_t e : eog_)
+        if (e == id)
+            return true;
+    return false;
 }
 
 }  // namespace bnne

@@ -1,0 +1,25 @@
+// Test infrastructure: the device-path entry points (engine/resident.h) for a build of
+// the engine's host code without HIP, linked to the CPU oracle backend (oracle/bnn_cpu.c)
+// so that the engine's host step runs -- and runs under AddressSanitizer and
+// UndefinedBehaviorSanitizer -- on a machine without a GPU.  Every context then
+// decodes on the host step.  Not part of the product.
+#include "resident.h"
+
+namespace bnne {
+
+struct Resident {};
+
+BNNE_Status resident_create(bnne_context*, const ResidentModel&, bool, Resident** out) {
+    *out = nullptr;
+    return complain(BNNE_ENOTSUP, "this build of the engine has no device path");
+}
+
+bool resident_fused(const Resident*) { return false; }
+
+BNNE_Status resident_step(bnne_context*, Resident*, const int32_t*, uint32_t, uint32_t, float*) {
+    return complain(BNNE_ENOTSUP, "this build of the engine has no device path");
+}
+
+void resident_free(Resident*) {}
+
+}  // namespace bnne

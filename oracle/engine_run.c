@@ -53,40 +53,48 @@ static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint3
     BNNE_Status st = BNNE_ModelGetInfo(model, &info);
     if (st != BNNE_OK)
         return fail("BNNE_ModelGetInfo", st);
+    int rc = 2;
+    BNNE_Context c = NULL;
     int32_t* ids = malloc((size_t)ctx * sizeof *ids);
     float* logits = malloc((size_t)info.n_vocab * sizeof *logits);
     FILE* f = fopen(ids_path, "r");
     if (!ids || !logits || !f)
-        return 2;
+        goto done;
     uint32_t count = 0;
     long v;
     while (count < ctx && fscanf(f, "%ld", &v) == 1)
         ids[count++] = (int32_t)v;
-    fclose(f);
     BNNE_ContextParams params;
     BNNE_ContextParamsInit(&params);
     params.n_ctx = ctx;
-    BNNE_Context c = NULL;
     st = BNNE_ContextCreate(model, &params, &c);
-    if (st != BNNE_OK)
-        return fail("BNNE_ContextCreate", st);
+    if (st != BNNE_OK) {
+        rc = fail("BNNE_ContextCreate", st);
+        goto done;
+    }
 #ifdef OWN_ENGINE
-    if ((st = BNNEX_ContextSetResident(c, mode)) != BNNE_OK)
-        return fail("BNNEX_ContextSetResident", st);
+    if ((st = BNNEX_ContextSetResident(c, mode)) != BNNE_OK) {
+        rc = fail("BNNEX_ContextSetResident", st);
+        goto done;
+    }
     static const char* const kPath[] = {"host", "device", "prepared"};
     printf("path %s\n", kPath[BNNEX_ContextIsResident(c)]);
 #else
     (void)mode;
 #endif
     st = BNNE_Decode(c, ids, count, logits);
-    if (st != BNNE_OK)
-        return fail("BNNE_Decode(prefill)", st);
+    if (st != BNNE_OK) {
+        rc = fail("BNNE_Decode(prefill)", st);
+        goto done;
+    }
     int32_t next = (int32_t)argmax(logits, info.n_vocab);
     printf("step 0 %d %016" PRIx64 "\n", next, fnv64(logits, (size_t)info.n_vocab * 4));
     for (uint32_t s = 1; s <= steps; s++) {
         st = BNNE_Decode(c, &next, 1, logits);
-        if (st != BNNE_OK)
-            return fail("BNNE_Decode", st);
+        if (st != BNNE_OK) {
+            rc = fail("BNNE_Decode", st);
+            goto done;
+        }
         next = (int32_t)argmax(logits, info.n_vocab);
         printf("step %u %d %016" PRIx64 "\n", s, next, fnv64(logits, (size_t)info.n_vocab * 4));
         fflush(stdout);
@@ -97,10 +105,14 @@ static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint3
            " execute_ns=%" PRIu64 " host_ns=%" PRIu64 " device_calls=%" PRIu64 "\n",
            stats.calls, stats.items, stats.total_ns, stats.transfer_ns, stats.execute_ns, stats.host_ns,
            stats.device_calls);
+    rc = 0;
+done:
+    if (f)
+        fclose(f);
     BNNE_ContextFree(c);
     free(ids);
     free(logits);
-    return 0;
+    return rc;
 }
 
 static int run_classify(BNNE_Model model, const char* input_path, uint32_t samples, uint32_t batch) {
@@ -108,25 +120,29 @@ static int run_classify(BNNE_Model model, const char* input_path, uint32_t sampl
     BNNE_Status st = BNNE_ModelGetInfo(model, &info);
     if (st != BNNE_OK)
         return fail("BNNE_ModelGetInfo", st);
+    int rc = 2;
+    BNNE_Context c = NULL;
     float* x = malloc((size_t)samples * info.input_size * sizeof *x);
     float* logits = malloc((size_t)batch * info.n_classes * sizeof *logits);
     FILE* f = fopen(input_path, "rb");
     if (!x || !logits || !f || fread(x, sizeof *x, (size_t)samples * info.input_size, f) !=
                                    (size_t)samples * info.input_size)
-        return 2;
-    fclose(f);
+        goto done;
     BNNE_ContextParams params;
     BNNE_ContextParamsInit(&params);
     params.n_batch = batch;
-    BNNE_Context c = NULL;
     st = BNNE_ContextCreate(model, &params, &c);
-    if (st != BNNE_OK)
-        return fail("BNNE_ContextCreate", st);
+    if (st != BNNE_OK) {
+        rc = fail("BNNE_ContextCreate", st);
+        goto done;
+    }
     for (uint32_t s0 = 0; s0 < samples; s0 += batch) {
         const uint32_t n = samples - s0 < batch ? samples - s0 : batch;
         st = BNNE_Classify(c, x + (size_t)s0 * info.input_size, n, logits);
-        if (st != BNNE_OK)
-            return fail("BNNE_Classify", st);
+        if (st != BNNE_OK) {
+            rc = fail("BNNE_Classify", st);
+            goto done;
+        }
         for (uint32_t i = 0; i < n; i++) {
             for (uint32_t k = 0; k < info.n_classes; k++) {
                 uint32_t bits;
@@ -135,10 +151,14 @@ static int run_classify(BNNE_Model model, const char* input_path, uint32_t sampl
             }
         }
     }
+    rc = 0;
+done:
+    if (f)
+        fclose(f);
     BNNE_ContextFree(c);
     free(x);
     free(logits);
-    return 0;
+    return rc;
 }
 
 int main(int argc, char** argv) {
@@ -158,8 +178,10 @@ int main(int argc, char** argv) {
     }
     BNNE_Model model = NULL;
     BNNE_Status st = BNNE_ModelLoad(dev, argv[2], &model);
-    if (st != BNNE_OK)
+    if (st != BNNE_OK) {
+        BNN_DeviceClose(dev);
         return fail("BNNE_ModelLoad", st);
+    }
     const uint32_t a = (uint32_t)strtoul(argv[4], NULL, 10), b = (uint32_t)strtoul(argv[5], NULL, 10);
     const int rc = strcmp(argv[1], "llm") == 0 ? run_llm(model, argv[3], a, b, mode) : run_classify(model, argv[3], a, b);
     BNNE_ModelFree(model);

@@ -213,6 +213,106 @@ def test_reference_engine_reproduces_fixtures(pkg, tmp_path):
     check_mlp_output(out)
 
 
+ENGINE_RUN_CPU = ROOT / "oracle" / "lib" / "engine_run_cpu"
+ENGINE_RUN_ASAN = ROOT / "oracle" / "lib" / "engine_run_asan"
+ASAN_ENV = {"ASAN_OPTIONS": "detect_leaks=1:abort_on_error=0:exitcode=99", "UBSAN_OPTIONS": "print_stacktrace=1"}
+
+
+@pytest.mark.parametrize("exe", [ENGINE_RUN_CPU, ENGINE_RUN_ASAN], ids=["plain", "sanitized"])
+def test_engine_host_step_on_cpu_oracle(pkg, tmp_path, exe):
+    """This engine's host code (GGUF reader, Q1_0 layers, the Qwen3 host step, bnn-mlp)
+    linked to the CPU oracle backend reproduces the reference engine + soft backend:
+    every step's token and logits hash of the tiny model, all 1000x10 classifier logits.
+    The sanitized build runs the same under AddressSanitizer + UndefinedBehaviorSanitizer."""
+    import os
+    env = dict(os.environ, **ASAN_ENV)
+    model, ids = write_tiny(pkg, tmp_path)
+    out = subprocess.run([str(exe), "llm", str(model), str(ids), str(TINY["steps_arg"]), str(TINY["ctx"]), "host"],
+                         capture_output=True, text=True, timeout=300, env=env)
+    assert out.returncode == 0, out.stderr[-2000:]
+    assert parse_path(out.stdout) == "host"
+    assert parse_llm(out.stdout) == TINY["steps"]
+    model, inp = write_mlp(pkg, tmp_path)
+    out = subprocess.run([str(exe), "classify", str(model), str(inp), str(MLP["samples"]), str(MLP["batch"])],
+                         capture_output=True, text=True, timeout=300, env=env)
+    assert out.returncode == 0, out.stderr[-2000:]
+    check_mlp_output(out.stdout)
+
+
+def _run_sanitized(args, env):
+    out = subprocess.run([str(ENGINE_RUN_ASAN), *args], capture_output=True, text=True, timeout=60, env=env)
+    report = "AddressSanitizer" in out.stderr or "runtime error" in out.stderr or "LeakSanitizer" in out.stderr
+    return out.returncode, report, out.stderr
+
+
+@pytest.mark.parametrize("case", ["missing", "magic", "version", "truncated", "no_tensors", "arch", "tensor_type"])
+def test_engine_format_errors_sanitized(pkg, tmp_path, case):
+    """The malformed files of test_engine_format_errors_without_device, read by the
+    sanitized host build: an engine error (exit 2), no sanitizer report."""
+    import os
+    w = pkg.gguf.Writer()
+    w.string("general.architecture", "nosuch" if case == "arch" else "qwen3")
+    if case == "tensor_type":
+        w.tensors.append(("t", (4,), 2, b"\0" * 8))
+    elif case != "no_tensors":
+        w.tensor("t", (4,), pkg.gguf.TYPE_F32, b"\0" * 16)
+    path = tmp_path / "bad.gguf"
+    w.write(path)
+    raw = bytearray(path.read_bytes())
+    if case == "magic":
+        raw[0:4] = b"GGUX"
+    elif case == "version":
+        raw[4:8] = struct.pack("<I", 2)
+    elif case == "truncated":
+        raw = raw[:40]
+    path.write_bytes(bytes(raw))
+    if case == "missing":
+        path = tmp_path / "absent.gguf"
+    ids = tmp_path / "ids.txt"
+    ids.write_text("1 2\n")
+    rc, report, err = _run_sanitized(["llm", str(path), str(ids), "1", "8", "host"], dict(os.environ, **ASAN_ENV))
+    assert rc == 2 and not report, err[-2000:]
+
+
+def test_engine_gguf_mutation_fuzz_sanitized(pkg, tmp_path):
+    """Bounded mutation fuzz of the GGUF reader and model loaders under ASan/UBSan: the
+    tiny Qwen3 and bnn-mlp files with bytes of their header, metadata and tensor table
+    overwritten, lengths and counts set to extremes, or the file cut short.  Each run
+    must end with success or an engine error -- never a sanitizer report, a crash or a
+    hang.  Stops at the first failure."""
+    import os
+    import random
+    env = dict(os.environ, **ASAN_ENV)
+    model, ids = write_tiny(pkg, tmp_path)
+    mlp, inp = write_mlp(pkg, tmp_path)
+    rng = random.Random(20261202)
+    extremes = [b"\xff" * 8, b"\x00" * 8, struct.pack("<Q", 2 ** 32), struct.pack("<Q", 2 ** 63 + 1),
+                struct.pack("<I", 0xffffffff), struct.pack("<I", 13), struct.pack("<I", 9)]
+    for base, run in ((model, ["llm", None, str(ids), "1", "16", "host"]),
+                      (mlp, ["classify", None, str(inp), "2", "2"])):
+        pristine = base.read_bytes()
+        # the header, metadata and tensor table: everything before the first tensor's data
+        _, _, _, data_start, _ = read_gguf(base)
+        for trial in range(60):
+            raw = bytearray(pristine)
+            kind = trial % 3
+            if kind == 0:
+                for _ in range(rng.randint(1, 8)):
+                    raw[rng.randrange(data_start)] = rng.randrange(256)
+            elif kind == 1:
+                at = rng.randrange(data_start - 8)
+                v = rng.choice(extremes)
+                raw[at:at + len(v)] = v
+            else:
+                raw = raw[:rng.randrange(1, len(raw))]
+            path = tmp_path / "fuzz.gguf"
+            path.write_bytes(bytes(raw))
+            args = list(run)
+            args[1] = str(path)
+            rc, report, err = _run_sanitized(args, env)
+            assert rc in (0, 2) and not report, (base.name, trial, kind, rc, err[-2000:])
+
+
 # ----------------------------------------------------------------------------- GPU
 
 
