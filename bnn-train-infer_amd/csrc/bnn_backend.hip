@@ -32,7 +32,7 @@ constexpr size_t kPinnedCap = size_t(8) << 20;       // largest transfer staged 
 constexpr size_t kWriteRingBytes = size_t(1) << 20;  // pinned ring for small writes
 constexpr size_t kAsyncWriteMax = size_t(64) << 10;  // writes up to this size return before the copy ends
 constexpr size_t kScratchRowsCap = 4096;              // rows per launch chunk
-constexpr size_t kScratchBytesCap = size_t(256) << 20;
+constexpr size_t kExecuteScratchBytes = size_t(32) << 20;  // allocated with the device
 
 bool mul_size(size_t a, size_t b, size_t* out) {
     if (a != 0 && b > SIZE_MAX / a)
@@ -292,6 +292,10 @@ BNN_Status open_device(int ordinal, BNN_Device* out_device) {
         e = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
     if (e == hipSuccess)
         e = hipMalloc(reinterpret_cast<void**>(&d->flag_dev), 256);
+    if (e == hipSuccess) {  // BNN_Execute's scratch: quantised rows (and staging rows) of a chunk of rows
+        e = hipMalloc(reinterpret_cast<void**>(&d->scratch), kExecuteScratchBytes);
+        d->scratch_bytes = e == hipSuccess ? kExecuteScratchBytes : 0;
+    }
     if (e == hipSuccess)
         e = hipHostMalloc(reinterpret_cast<void**>(&d->status_host), 256, hipHostMallocCoherent);
     if (e == hipSuccess) {
@@ -310,6 +314,8 @@ BNN_Status open_device(int ordinal, BNN_Device* out_device) {
             (void)hipHostFree(d->status_host);
         if (d->flag_dev)
             (void)hipFree(d->flag_dev);
+        if (d->scratch)
+            (void)hipFree(d->scratch);
         if (d->stream)
             (void)hipStreamDestroy(d->stream);
         free(d);
@@ -487,8 +493,6 @@ EXPORT void BNN_MatrixDestroy(BNN_Matrix matrix) {
     (void)hipSetDevice(matrix->device->ordinal);
     (void)hipStreamSynchronize(matrix->device->stream);
     (void)hipFree(matrix->wbits);
-    if (matrix->wbytes)
-        (void)hipFree(matrix->wbytes);
     matrix->device->live_matrices--;
     matrix->device->generation++;
     matrix->device->retired++;
@@ -745,7 +749,7 @@ DotJob make_dot(const JobPlan& p, const PrepJob& pj, unsigned char* out, size_t 
 
 GemmJob make_gemm(const JobPlan& p, const PrepJob& pj, unsigned char* out, size_t out_stride) {
     GemmJob j = {};
-    j.wbytes = p.m->wbytes;
+    j.wbits = p.m->wbits;
     j.wscale = p.m->wscale;
     j.q = pj.q;
     j.rscale = pj.rscale;
@@ -927,39 +931,15 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
     if (single_row_path(job, p))
         return run_single_row(device, job, p, true);
 
+    // rows in chunks that fit the device's scratch (allocated with the device)
     const bool mfma = job->rows >= kMfmaMinRows;
     size_t chunk = 0, rows_bytes = 0;
-    chunk_rows(p, job->rows, mfma, kScratchBytesCap, &chunk, &rows_bytes);
+    chunk_rows(p, job->rows, mfma, device->scratch_bytes, &chunk, &rows_bytes);
     if (chunk == 0)
         return BNN_ENOMEM;
-    const size_t staging_bytes = p.out_aligned ? 0 : round_up(chunk * p.out_row, 256);
     if (hipSetDevice(device->ordinal) != hipSuccess)
         return BNN_EIO;
-    st = ensure_scratch(device, rows_bytes + staging_bytes);
-    if (st != BNN_OK)
-        return st;
-
-    hipError_t e = hipSuccess;
-    if (mfma && p.m->wbytes == nullptr) {
-        // first multi-row job on this matrix: create its +1/-1 byte copy; the matrix
-        // records it only once the expansion is enqueued
-        const uint32_t n_pad = (p.m->n + kGemmRowPad - 1u) / kGemmRowPad * kGemmRowPad;
-        void* w = nullptr;
-        if (hipMalloc(&w, (size_t)n_pad * p.m->k) != hipSuccess) {
-            (void)hipGetLastError();
-            return BNN_ENOMEM;
-        }
-        e = launch_expand(device->stream, p.m->wbits, p.m->tiles, p.m->groups, n_pad, static_cast<int8_t*>(w));
-        if (e != hipSuccess) {
-            (void)hipGetLastError();
-            (void)hipStreamSynchronize(device->stream);
-            (void)hipFree(w);
-            return BNN_EIO;
-        }
-        p.m->wbytes = static_cast<int8_t*>(w);
-        p.m->n_pad = n_pad;
-    }
-    return run_rows(device, job, p, mfma, device->scratch, chunk, rows_bytes, e);
+    return run_rows(device, job, p, mfma, device->scratch, chunk, rows_bytes, hipSuccess);
 }
 
 // BNN_Execute without any allocation: the quantised rows (and staging rows for

@@ -86,9 +86,10 @@ struct DotJob {
     uint32_t first_block;
 };
 
-// One multi-row job on the matrix cores (rows >= kMfmaMinRows).
+// One multi-row job on the matrix cores (rows >= kMfmaMinRows), read from the
+// matrix's resident layout (sign bits unpacked in LDS by the kernel).
 struct GemmJob {
-    const int8_t* wbytes;     // [n_pad][k] +1/-1
+    const uint4* wbits;       // matrix layout [tiles][groups][64] x 16 bytes
     const uint16_t* wscale;   // matrix layout [tiles][groups][64]
     const int8_t* q;          // [rows][k] quantised rows
     const float* rscale;      // [rows]
@@ -98,7 +99,6 @@ struct GemmJob {
     uint32_t rows;
     int32_t mode;
 };
-constexpr uint32_t kGemmRowPad = 128;  // n_pad granularity = largest workgroup tile
 
 // Rows from which a job runs on the matrix cores instead of the bit-plane kernel.
 #ifndef BNN_MFMA_MIN_ROWS
@@ -196,9 +196,6 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
 // (bnn_fused.hip).
 hipError_t launch_fused(hipStream_t stream, const FusedArgs& args, uint32_t tiles, uint32_t grid, uint64_t seq,
                         uint64_t* flag, uint64_t* host_status);
-// wbytes[n_pad][k] <- sign bits of the matrix layout (once per matrix).
-hipError_t launch_expand(hipStream_t stream, const uint4* wbits, uint32_t tiles, uint32_t groups,
-                         uint32_t n_pad, int8_t* wbytes);
 hipError_t launch_scatter(hipStream_t stream, const unsigned char* src, size_t src_stride,
                           unsigned char* dst, size_t dst_stride, size_t row_bytes, uint32_t rows,
                           uint64_t seq, const uint64_t* flag);
@@ -267,11 +264,6 @@ struct bnn_accel_matrix {
     uint32_t k, n, groups, tiles;
     uint4* wbits;
     uint16_t* wscale;
-    // Matrix-core copy of the weights, created on the first multi-row job:
-    // wbytes[n_pad][k] int8 of +1/-1 (n_pad = N rounded up to 128; padding rows
-    // are -1 and never stored).  8 bits per weight, freed with the matrix.
-    int8_t* wbytes;
-    uint32_t n_pad;
 };
 
 // A prepared batch: job tables and the rows' scratch in one device allocation,

@@ -105,9 +105,10 @@ def test_quantiser_edge_rows(pkg, hipdev, oracle, i):
 
 @pytest.mark.parametrize("op", ["GEMM", "GEMM_F32"])
 @pytest.mark.parametrize("rows,k,n", [
-    (1000, 384, 4100), (2049, 128, 2000), (1152, 640, 8128),  # 128 x 128 tiles, one wave per subtile block
-    (50, 640, 1000), (100, 3200, 3000), (120, 1152, 5000),    # K split over 8 waves: 32x16, 32x32, 64x32 tiles
-    (250, 1152, 6100), (1000, 640, 2000),                      # 64 x 128 tiles through the 4-slot DMA pipeline
+    (1000, 384, 4100), (2049, 128, 2000), (1152, 640, 8128),  # 128 x 128 workgroup tiles
+    (1000, 640, 2000),                                         # 64 x 128
+    (250, 1152, 6100),                                         # 64 x 64
+    (50, 640, 1000), (100, 3200, 3000), (120, 1152, 5000),    # 32 x 64 (fewer tiles than CUs)
 ])
 def test_gemm_tilings_ragged_edges(pkg, hipdev, oracle_fast, op, rows, k, n):
     """Shapes that select each multi-row tiling, with a partial last row tile, a last
