@@ -1,7 +1,7 @@
 // Multi-row jobs (GEMM, GEMM_F32, DOT_GROUPS with rows >= kMfmaMinRows) on the
 // gfx950 matrix cores (v_mfma_i32_16x16x64_i8), fed from the matrix's resident
 // 1.125-bit layout: the sign bits of each 128-weight group are unpacked to +1/-1
-// bytes in LDS, per workgroup tile and group, right before the MFMAs use them.
+// bytes in LDS, per workgroup tile and group, two groups before the MFMAs use them.
 //
 // Numeric contract (reference bnn-accelerator.h:133-149, soft-bnn-accelerator.c:219-276),
 // per 128-weight group g:
@@ -18,18 +18,24 @@
 //     becomes -0 (x + -x == +0 in round-to-nearest), so the sums agree bit for bit.
 // DOT_GROUPS restarts the accumulator at 0 and stores D itself as int16.
 //
-// k_gemm_bits<TM, TN>: workgroup tile TM x TN, 4 waves (2 x 2) of (TM/2) x (TN/2).
-// Everything a group needs reaches LDS by DMA (global_load_lds, 16 bytes per lane,
-// no registers): the TM rows' 128 quantised bytes, the TN features' 16-byte sign-bit
-// chunks (1 KiB per 64-feature tile of the matrix layout) and each wave's column
-// scales.  Iteration g, after one wait and one barrier:
-//   * issue the DMAs of group g+1's rows, group g+3's bits and group g+2's scales;
-//   * unpack group g+1's bits into its +1/-1 tile: every thread turns 4 or 8 bytes
-//     of bits into 32 or 64 bytes with one 8-byte lookup per byte in a 256-entry
-//     table (2 KiB, built at start), i.e. ~0.25 VALU op per weight;
-//   * group g's MFMAs, interleaved subtile by subtile with group g-1's epilogue.
-// The bits run three groups ahead of the MFMAs (they come from HBM), the rows one
-// (they are shared by every column tile and come from the L2).
+// k_gemm_bits<TM, TN, WGM, WGN>: workgroup tile TM x TN, WGM x WGN waves of
+// (TM/WGM) x (TN/WGN).  Everything a group needs reaches LDS by DMA
+// (global_load_lds, 16 bytes per lane, no registers): the TM rows' 128 quantised
+// bytes, the TN features' 16-byte sign-bit chunks (1 KiB per 64-feature tile of the
+// matrix layout) and their column scales.  One barrier per group; iteration g:
+//   * issue the DMAs of group g+3's rows, group g+5's bits and group g+2's scales
+//     (each has two iterations to land);
+//   * look up group g+2's bits (read into registers one iteration ago) in a
+//     256-entry table (2 KiB, built at start): one 8-byte lookup turns a byte of
+//     bits into 8 bytes of +1/-1;
+//   * read group g+3's bits, and group g+1's MFMA operands into the second
+//     register set (the loop is unrolled by two, so the two sets alternate without
+//     copies);
+//   * group g's first-half MFMAs (operands read one iteration ago), each subtile
+//     interleaved with group g-1's epilogue on it;
+//   * store group g+2's +1/-1 tile; group g's second-half MFMAs.
+// At the end every wave writes its accumulators into LDS and the workgroup stores
+// the tile row by row, 16 bytes per lane.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -41,16 +47,10 @@ namespace bnnhip {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kMagicBits = 0x4B400000;  // bit pattern of 12582912.0f = 1.5 * 2^23
 constexpr float kMagicValue = 12582912.0f;
-
-// Output elements as nontemporal stores: written once, not kept dirty in the L2s for
-// the end-of-kernel release to write back.
-__device__ __forceinline__ void store_out(float* p, float v) {
-    __builtin_nontemporal_store(v, (__attribute__((address_space(1))) float*)p);
-}
 
 // 4 sign bits -> 4 bytes of +1 (bit 1) or -1 (bit 0): the multiply places copies of
 // the nibble at bit offsets 0, 7, 14, 21 (disjoint), the mask keeps bit i in byte i,
@@ -80,6 +80,30 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_addr) : "memory");
 }
 
+// The same for the lanes of a constant mask only: the mask goes into exec inside the
+// assembly (and exec is restored there), so that the caller needs no branch around
+// the load -- a branch would split the loop body into blocks across which the
+// compiler moves the arithmetic of one group into the next.
+template <uint64_t LANES>
+__device__ __forceinline__ void dma16_lanes(const void* gptr, uint32_t lds_addr) {
+    if constexpr (LANES == ~0ull) {
+        dma16(gptr, lds_addr);
+    } else {
+        uint64_t saved;
+        asm volatile(
+            "s_mov_b64 %0, exec\n\ts_mov_b64 exec, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+            "s_mov_b64 exec, %0"
+            : "=&s"(saved)
+            : "v"(gptr), "{m0}"(lds_addr), "s"(LANES)
+            : "memory");
+    }
+}
+
+template <uint32_t N>
+constexpr uint64_t lane_mask() {
+    return N >= 64 ? ~0ull : (1ull << N) - 1ull;
+}
+
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
@@ -92,84 +116,162 @@ __device__ __forceinline__ void wait_dma() {
     __builtin_amdgcn_s_waitcnt(0x0070 | N);
 }
 
-template <int TM, int TN, bool DOT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_bits(
-    GemmJob j, uint32_t mtiles, uint64_t seq, const uint64_t* __restrict__ flag) {
-    constexpr int MS = TM / 32, NS = TN / 32;  // 16 x 16 subtiles per wave
-    constexpr uint32_t A_INS = TM / 32;        // row DMAs per wave and group
-    constexpr uint32_t BIT_LANES = TN / 4;     // lanes of a wave carrying bits (TN * 16 B per group)
-    constexpr uint32_t SC_LANES = TN / 16;     // lanes carrying a wave's TN/2 column scales
-    constexpr uint32_t BPT = TN / 16;          // bytes of bits each thread unpacks per group
-    static_assert(MS >= 1 && (TN == 64 || TN == 128), "tile shape");
-    __shared__ __attribute__((aligned(1024))) unsigned char lds_a[2][TM * 128];
-    __shared__ __attribute__((aligned(1024))) unsigned char lds_b[2][TN * 128];
-    __shared__ __attribute__((aligned(16))) unsigned char lds_bits[4][TN * 16];
-    __shared__ __attribute__((aligned(16))) unsigned char lds_sc[4][4][TN];  // [slot][wave][TN/2 fp16]
-    __shared__ uint2 lut[256];
+__device__ __forceinline__ void barrier() {
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");  // no LDS access moves across it
+}
+
+template <int TM, int TN, int WGM, int WGN>
+struct Tiling {
+    static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
+    static constexpr int WTM = TM / WGM, WTN = TN / WGN, MS = WTM / 16, NS = WTN / 16;
+    // DMA work per wave and group: every wave issues exactly A_INS + 2 DMAs, each
+    // with at least one active lane, so that the vmcnt bookkeeping is uniform
+    static constexpr uint32_t A_CHUNKS = TM * 8 / WAVES;  // 16-byte row chunks
+    static constexpr uint32_t A_INS = A_CHUNKS >= 64 ? A_CHUNKS / 64 : 1;
+    static constexpr uint32_t A_LANES = A_CHUNKS >= 64 ? 64 : A_CHUNKS;
+    static constexpr uint32_t BIT_LANES = TN / WAVES;     // one 16-byte chunk per feature
+    static constexpr uint32_t SC_CHUNKS = TN / 8;         // 8 fp16 scales per chunk
+    static constexpr uint32_t SC_CPW = SC_CHUNKS >= (uint32_t)WAVES ? SC_CHUNKS / WAVES : 1;
+    // LDS carve-up (bytes)
+    static constexpr uint32_t A_SLOT = TM * 128, B_SLOT = TN * 128, BITS_SLOT = TN * 16, SC_SLOT = TN * 2;
+    static constexpr uint32_t OFF_B = 4 * A_SLOT, OFF_BITS = OFF_B + 2 * B_SLOT, OFF_SC = OFF_BITS + 4 * BITS_SLOT,
+                              OFF_LUT = (OFF_SC + 4 * SC_SLOT + 15u) & ~15u, LOOP_BYTES = OFF_LUT + 2048;
+    static constexpr uint32_t OUT_STRIDE = TN + 16;  // floats per staged output row
+    static constexpr uint32_t OUT_BYTES = TM * OUT_STRIDE * 4;
+    static constexpr uint32_t SMEM = LOOP_BYTES > OUT_BYTES ? LOOP_BYTES : OUT_BYTES;
+    static_assert(TM % (16 * WGM) == 0 && TN % (16 * WGN) == 0, "wave tiles of 16 x 16 subtiles");
+    static_assert(A_CHUNKS % 64 == 0 || A_CHUNKS < 64, "row DMA split");
+    static_assert(TN % WAVES == 0 && BIT_LANES <= 64, "bits DMA split");
+    static_assert(SC_CHUNKS < (uint32_t)WAVES || SC_CHUNKS % WAVES == 0, "scales DMA split");
+    static_assert(SMEM <= 160 * 1024, "LDS");
+    static_assert(TM * TN / 4 % THREADS == 0, "output chunks per thread");
+};
+
+template <int TM, int TN, int WGM, int WGN, bool DOT>
+__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_bits(GemmJob j, uint32_t mtiles, uint64_t seq,
+                                                              const uint64_t* __restrict__ flag) {
+    using T = Tiling<TM, TN, WGM, WGN>;
+    constexpr int MS = T::MS, NS = T::NS, WAVES = T::WAVES, THREADS = T::THREADS;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
     if (*flag == seq)
         return;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t wm = wave >> 1, wn = wave & 1u;
+    const uint32_t wm = wave / WGN, wn = wave % WGN;
     const uint32_t tile = gemm_tile_of_block(blockIdx.x, gridDim.x);
     const uint32_t mt = tile % mtiles, nt = tile / mtiles;
     const uint32_t m0 = mt * TM, n0 = nt * TN;
     const uint32_t groups = j.groups;
+    unsigned char* const lds_a = smem;
+    unsigned char* const lds_b = smem + T::OFF_B;
+    unsigned char* const lds_bits = smem + T::OFF_BITS;
+    unsigned char* const lds_sc = smem + T::OFF_SC;
+    uint2* const lut = reinterpret_cast<uint2*>(smem + T::OFF_LUT);
 
     // byte b of sign bits -> 8 bytes of +1/-1 (bit i -> byte i)
-    lut[tid] = make_uint2(pm1_nibble(tid & 15u), pm1_nibble(tid >> 4));
+    if (tid < 256u)
+        lut[tid] = make_uint2(pm1_nibble(tid & 15u), pm1_nibble(tid >> 4));
 
     // this lane's DMA sources (without the group offset)
-    const uint8_t* a_src[A_INS];
+    const uint8_t* a_src[T::A_INS];
 #pragma unroll
-    for (uint32_t i = 0; i < A_INS; ++i) {
-        const uint32_t p = (wave * A_INS + i) * 64u + lane, r = p >> 3;
+    for (uint32_t i = 0; i < T::A_INS; ++i) {
+        const uint32_t p = wave * T::A_CHUNKS + i * 64u + lane, r = p >> 3;
         const uint32_t c = (p & 7u) ^ ((r >> 1) & 7u);
-        a_src[i] = reinterpret_cast<const uint8_t*>(j.q) + (size_t)min(m0 + r, j.rows - 1u) * j.k + 16u * c;
+        a_src[i] = reinterpret_cast<const uint8_t*>(j.q) + (size_t)min(m0 + min(r, TM - 1u), j.rows - 1u) * j.k +
+                   16u * c;
     }
-    // bits: feature f = BIT_LANES * wave + lane of the tile; its 64-feature matrix tile
-    // is clamped into the array (features past the last tile are never stored)
-    const uint32_t f = BIT_LANES * wave + lane;
-    const uint32_t bit_tile = min((n0 + f) >> 6, j.tiles - 1u);
-    const uint8_t* bit_src = reinterpret_cast<const uint8_t*>(j.wbits) + ((size_t)bit_tile * groups * kTile + (f & 63u)) * 16u;
-    // scales of this wave's TN/2 columns: part of one 64-feature tile
-    const uint32_t col0 = n0 + wn * (TN / 2u);
-    const uint32_t sc_tile = min(col0 >> 6, j.tiles - 1u);
+    // bits: feature f of the tile; its 64-feature matrix tile is clamped into the
+    // array (features past the last tile are never stored)
+    const uint32_t f = T::BIT_LANES * wave + min(lane, T::BIT_LANES - 1u);
+    const uint8_t* bit_src = reinterpret_cast<const uint8_t*>(j.wbits) +
+                             ((size_t)min((n0 + f) >> 6, j.tiles - 1u) * groups * kTile + ((n0 + f) & 63u)) * 16u;
+    // scales: chunks of 8 columns, SC_CPW consecutive ones per wave (with fewer
+    // chunks than waves, the waves past the last chunk repeat one, writing the same
+    // bytes)
+    const uint32_t sc_first = (wave * T::SC_CPW) % T::SC_CHUNKS;
+    const uint32_t sc_col = n0 + 8u * (sc_first + min(lane, T::SC_CPW - 1u));
     const uint8_t* sc_src = reinterpret_cast<const uint8_t*>(j.wscale) +
-                            ((size_t)sc_tile * groups * kTile + (col0 & 63u)) * 2u + 16u * lane;
+                            ((size_t)min(sc_col >> 6, j.tiles - 1u) * groups * kTile + (sc_col & 63u)) * 2u;
     const uint32_t la0 = lds_offset(lds_a), lbits0 = lds_offset(lds_bits), lsc0 = lds_offset(lds_sc);
     const size_t bit_step = (size_t)kTile * 16u, sc_step = (size_t)kTile * 2u;  // bytes per group
     auto issue_rows = [&](uint32_t g) {
         const uint32_t gg = min(g, groups - 1u);
 #pragma unroll
-        for (uint32_t i = 0; i < A_INS; ++i)
-            dma16(a_src[i] + (size_t)gg * kGroup, la0 + (g & 1u) * (TM * 128u) + (wave * A_INS + i) * 1024u);
+        for (uint32_t i = 0; i < T::A_INS; ++i)
+            dma16_lanes<lane_mask<T::A_LANES>()>(a_src[i] + (size_t)gg * kGroup,
+                                                 la0 + (g & 3u) * T::A_SLOT + (wave * T::A_CHUNKS + i * 64u) * 16u);
     };
     auto issue_bits = [&](uint32_t g) {
         const uint32_t gg = min(g, groups - 1u);
-        if (lane < BIT_LANES)
-            dma16(bit_src + gg * bit_step, lbits0 + (g & 3u) * (TN * 16u) + wave * (BIT_LANES * 16u));
+        dma16_lanes<lane_mask<T::BIT_LANES>()>(bit_src + gg * bit_step,
+                                               lbits0 + (g & 3u) * T::BITS_SLOT + wave * (T::BIT_LANES * 16u));
     };
     auto issue_scales = [&](uint32_t g) {
         const uint32_t gg = min(g, groups - 1u);
-        if (lane < SC_LANES)
-            dma16(sc_src + gg * sc_step, lsc0 + (g & 3u) * (4u * TN) + wave * TN);
+        dma16_lanes<lane_mask<T::SC_CPW>()>(sc_src + gg * sc_step, lsc0 + (g & 3u) * T::SC_SLOT + 16u * sc_first);
     };
-    // unpacks group g's bits (slot g % 4) into the +1/-1 tile lds_b[g % 2]
+    // unpacks group g's bits (slot g % 4) into the +1/-1 tile lds_b[g % 2], in two
+    // parts so that the read of the bits can be issued long before its use: unit u =
+    // feature u / 4, bytes 4 * (u % 4) .. +3 of its 16 bytes of bits -> chunks
+    // 2 * (u % 4) and 2 * (u % 4) + 1 of its 128-byte row
+    constexpr uint32_t UNITS = TN * 4u, UPT = (UNITS + THREADS - 1u) / THREADS;  // units per thread
+    // a thread's i-th unit; past the last unit a thread repeats one (same bytes to the
+    // same place), so that no branch splits the loop body
+    auto unit = [&](uint32_t i) {
+        const uint32_t u = i * THREADS + tid;
+        return UNITS % THREADS == 0 || u < UNITS ? u : u - THREADS;
+    };
+    auto unpack_read = [&](uint32_t (&w)[UPT], uint32_t g) {
+        const unsigned char* bits = lds_bits + (g & 3u) * T::BITS_SLOT;
+#pragma unroll
+        for (uint32_t i = 0; i < UPT; ++i) {
+            const uint32_t u = unit(i);
+            w[i] = *reinterpret_cast<const uint32_t*>(bits + (u >> 2) * 16u + (u & 3u) * 4u);
+        }
+    };
+    auto unpack_lut = [&](uint2 (&e)[UPT][4], const uint32_t (&w)[UPT]) {
+#pragma unroll
+        for (uint32_t i = 0; i < UPT; ++i) {
+#pragma unroll
+            for (uint32_t b = 0; b < 4; ++b)
+                e[i][b] = lut[(w[i] >> (8u * b)) & 0xffu];
+        }
+    };
+    auto unpack_store = [&](const uint2 (&e)[UPT][4], uint32_t g) {
+        unsigned char* dst = lds_b + (g & 1u) * T::B_SLOT;
+#pragma unroll
+        for (uint32_t i = 0; i < UPT; ++i) {
+            const uint32_t u = unit(i), row = u >> 2, part = u & 3u;
+            *reinterpret_cast<uint4*>(dst + swz128(row, 2u * part)) =
+                make_uint4(e[i][0].x, e[i][0].y, e[i][1].x, e[i][1].y);
+            *reinterpret_cast<uint4*>(dst + swz128(row, 2u * part + 1u)) =
+                make_uint4(e[i][2].x, e[i][2].y, e[i][3].x, e[i][3].y);
+        }
+    };
     auto unpack = [&](uint32_t g) {
-        constexpr uint32_t PER_ROW = 16u / BPT;  // threads per feature
-        const uint32_t row = tid / PER_ROW, part = tid % PER_ROW;
-        const unsigned char* src = lds_bits[g & 3u] + row * 16u + part * BPT;
-        uint32_t w[BPT / 4];
+        uint32_t w[UPT];
+        uint2 e[UPT][4];
+        unpack_read(w, g);
+        unpack_lut(e, w);
+        unpack_store(e, g);
+    };
+
+    const uint32_t arow0 = wm * T::WTM + (lane & 15u), brow0 = wn * T::WTN + (lane & 15u);
+    const uint32_t chunk = lane >> 4;
+    // MFMA operands of group g: [half][subtile]
+    auto load_frags = [&](v4i (&a)[2][MS], v4i (&b)[2][NS], uint32_t g) {
+        const unsigned char* la = lds_a + (g & 3u) * T::A_SLOT;
+        const unsigned char* lb = lds_b + (g & 1u) * T::B_SLOT;
 #pragma unroll
-        for (uint32_t i = 0; i < BPT / 4; ++i)
-            w[i] = reinterpret_cast<const uint32_t*>(src)[i];
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (uint32_t c = 0; c < BPT / 2; ++c) {  // 16 expanded bytes = 2 bytes of bits per chunk
-            const uint32_t word = w[c / 2], sh = 16u * (c & 1u);
-            const uint2 lo = lut[(word >> sh) & 0xffu], hi = lut[(word >> (sh + 8u)) & 0xffu];
-            *reinterpret_cast<uint4*>(lds_b[g & 1u] + swz128(row, part * (BPT / 2) + c)) =
-                make_uint4(lo.x, lo.y, hi.x, hi.y);
+            for (int mi = 0; mi < MS; ++mi)
+                a[h][mi] = *reinterpret_cast<const v4i*>(la + swz128(arow0 + 16u * mi, 4u * h + chunk));
+#pragma unroll
+            for (int ni = 0; ni < NS; ++ni)
+                b[h][ni] = *reinterpret_cast<const v4i*>(lb + swz128(brow0 + 16u * ni, 4u * h + chunk));
         }
     };
 
@@ -185,52 +287,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int r = 0; r < 4; ++r)
                 acc[mi][ni][r] = 0.0f;
         }
-
-    issue_bits(0);
-    issue_scales(0);
-    issue_bits(1);
-    issue_scales(1);
-    issue_bits(2);
-    issue_rows(0);
-    wait_dma<0>();
-    __builtin_amdgcn_s_barrier();  // the table and group 0's bits are in LDS
-    asm volatile("" ::: "memory");
-    unpack(0);
-
-    const uint32_t arow0 = wm * (TM / 2u) + (lane & 15u), brow0 = wn * (TN / 2u) + (lane & 15u);
-    const uint32_t chunk = lane >> 4;
-    const uint32_t row_base = m0 + wm * (TM / 2u) + 4u * (lane >> 4);
-    const uint32_t col_base = n0 + wn * (TN / 2u) + (lane & 15u);
+    const uint32_t row_base = m0 + wm * T::WTM + 4u * (lane >> 4);
+    const uint32_t col_base = n0 + wn * T::WTN + (lane & 15u);
     float sc_prev[NS];
 #pragma unroll
     for (int ni = 0; ni < NS; ++ni)
         sc_prev[ni] = 0.0f;
-    for (uint32_t g = 0; g < groups; ++g) {
-        // group g's rows have landed (only the bits and scales issued one iteration ago
-        // may be in flight), every wave's unpacked tile of group g is written, and every
-        // wave has finished reading the buffers of group g-1
-        wait_dma<2>();
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        issue_rows(g + 1u);
-        issue_bits(g + 3u);
+
+    // One group: see the header.  At entry (after the barrier) LDS holds group g+1's
+    // rows and +1/-1 tile, group g+3's bits and group g's scales (the DMAs of the
+    // previous step may still be landing); ubits holds group g+2's bits, read in the
+    // previous step.
+    uint32_t ubits[UPT];
+    auto step = [&](uint32_t g, v4i (&ca)[2][MS], v4i (&cb)[2][NS], v4i (&na)[2][MS], v4i (&nb)[2][NS]) {
+        // this wave's DMAs but the previous step's have landed, its LDS accesses are
+        // done; after the barrier the same holds for every wave
+        wait_dma<T::A_INS + 2>();
+        barrier();
+        issue_rows(g + 3u);
+        issue_bits(g + 5u);
         issue_scales(g + 2u);
-        if (g + 1u < groups)
-            unpack(g + 1u);
-        const unsigned char* la = lds_a[g & 1u];
-        const unsigned char* lb = lds_b[g & 1u];
-        const uint16_t* scl = reinterpret_cast<const uint16_t*>(lds_sc[g & 3u][wave]);
+        // LDS reads in this order: the table lookups of group g+2 (first, so that the
+        // unpack does not queue behind the operand reads), group g+3's bits, group
+        // g+1's operands, group g's scales
+        uint2 ex[UPT][4];
+        unpack_lut(ex, ubits);
+        __builtin_amdgcn_sched_barrier(0);
+        unpack_read(ubits, g + 3u);
+        load_frags(na, nb, g + 1u);
         float sc_cur[NS];
+        const uint16_t* scl = reinterpret_cast<const uint16_t*>(lds_sc + (g & 3u) * T::SC_SLOT);
 #pragma unroll
         for (int ni = 0; ni < NS; ++ni)
-            sc_cur[ni] = DOT ? 0.0f : __half2float(__ushort_as_half(scl[16u * ni + (lane & 15u)]));
-        v4i a[MS], b[NS];
-#pragma unroll
-        for (int mi = 0; mi < MS; ++mi)
-            a[mi] = *reinterpret_cast<const v4i*>(la + swz128(arow0 + 16u * mi, chunk));
-#pragma unroll
-        for (int ni = 0; ni < NS; ++ni)
-            b[ni] = *reinterpret_cast<const v4i*>(lb + swz128(brow0 + 16u * ni, chunk));
+            sc_cur[ni] = DOT ? 0.0f : __half2float(__ushort_as_half(scl[wn * T::WTN + 16u * ni + (lane & 15u)]));
+        __builtin_amdgcn_sched_barrier(0);
         // first half: the epilogue of group g-1 on each subtile, then restart it
 #pragma unroll
         for (int ni = 0; ni < NS; ++ni) {
@@ -255,37 +345,61 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                     for (int r = 0; r < 4; ++r)
                         acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc, __int_as_float(d[mi][ni][r]), cneg);
                 }
-                d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], c_init, 0, 0, 0);
+                d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ca[0][mi], cb[0][ni], c_init, 0, 0, 0);
             }
         }
-#pragma unroll
-        for (int mi = 0; mi < MS; ++mi)
-            a[mi] = *reinterpret_cast<const v4i*>(la + swz128(arow0 + 16u * mi, 4u + chunk));
-#pragma unroll
-        for (int ni = 0; ni < NS; ++ni)
-            b[ni] = *reinterpret_cast<const v4i*>(lb + swz128(brow0 + 16u * ni, 4u + chunk));
-#pragma unroll
-        for (int ni = 0; ni < NS; ++ni)
-#pragma unroll
-            for (int mi = 0; mi < MS; ++mi)
-                d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi], b[ni], d[mi][ni], 0, 0, 0);
-#pragma unroll
-        for (int ni = 0; ni < NS; ++ni)
-            sc_prev[ni] = sc_cur[ni];
         if constexpr (!DOT) {
-            // issue order: the LDS reads of the scales and first half, then per subtile
-            // its 8 epilogue VALU ops and its restarting MFMA (the matrix pipe runs while
-            // the next subtile's VALU ops issue), then the second-half MFMAs
-            __builtin_amdgcn_sched_group_barrier(0x100, MS + 2 * NS, 0);
+            // per subtile its 8 epilogue VALU ops, then its restarting MFMA: the matrix
+            // pipe runs while the next subtile's VALU ops issue
 #pragma unroll
             for (int i = 0; i < MS * NS; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, MS * NS, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        unpack_store(ex, g + 2u);
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni)
+#pragma unroll
+            for (int mi = 0; mi < MS; ++mi)
+                d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ca[1][mi], cb[1][ni], d[mi][ni], 0, 0, 0);
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni)
+            sc_prev[ni] = sc_cur[ni];
+        __builtin_amdgcn_sched_barrier(0);  // nothing moves across steps
+    };
+
+    // prologue: groups 0..3's bits, 0..2's rows, 0..1's scales; groups 0 and 1 unpacked,
+    // group 2's bits in registers; group 4's bits issued once group 0's have been
+    // read (they share a slot); group 0's operands in registers
+#pragma unroll
+    for (uint32_t b = 0; b < 4; ++b)
+        issue_bits(b);
+    issue_scales(0);
+    issue_scales(1);
+    issue_rows(0);
+    issue_rows(1);
+    issue_rows(2);
+    wait_dma<0>();
+    barrier();  // the table and the first DMAs are in LDS
+    unpack(0);
+    unpack(1);
+    unpack_read(ubits, 2);
+    wait_dma<0>();
+    barrier();
+    issue_bits(4);
+    v4i xa[2][MS], xb[2][NS], ya[2][MS], yb[2][NS];
+    load_frags(xa, xb, 0);
+    uint32_t g = 0;
+    for (; g + 1u < groups; g += 2u) {
+        step(g, xa, xb, ya, yb);
+        step(g + 1u, ya, yb, xa, xb);
     }
-    // no DMA may still be writing this workgroup's LDS when it ends
+    if (g < groups)
+        step(g, xa, xb, ya, yb);
+
+    // no DMA may still be writing LDS when it is reused or the workgroup ends
     wait_dma<0>();
     if constexpr (DOT) {
         // D of the last group
@@ -306,7 +420,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         return;
     }
-    // epilogue of the last group, then store Z (or Z * s)
+    // epilogue of the last group
 #pragma unroll
     for (int ni = 0; ni < NS; ++ni) {
         const float sc = sc_prev[ni];
@@ -317,33 +431,250 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             for (int r = 0; r < 4; ++r)
                 acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc, __int_as_float(d[mi][ni][r]), cneg);
     }
+    // stage the tile in LDS, then store it row by row (16 bytes per lane where the
+    // output rows allow it); Z * s for GEMM_F32
+    barrier();
+    float* const so = reinterpret_cast<float*>(smem);
 #pragma unroll
-    for (int mi = 0; mi < MS; ++mi) {
+    for (int mi = 0; mi < MS; ++mi)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const uint32_t m = row_base + 16u * mi + r;
-            if (m >= j.rows)
-                continue;
-            const float s = j.mode == MODE_SUM_SCALED ? j.rscale[m] : 1.0f;
-            float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
+        for (int ni = 0; ni < NS; ++ni)
 #pragma unroll
-            for (int ni = 0; ni < NS; ++ni) {
-                const uint32_t n = col_base + 16u * ni;
-                if (n < j.n)
-                    store_out(orow + n, j.mode == MODE_SUM_SCALED ? acc[mi][ni][r] * s : acc[mi][ni][r]);
-            }
+            for (int r = 0; r < 4; ++r)
+                so[(wm * T::WTM + 16u * mi + 4u * (lane >> 4) + r) * T::OUT_STRIDE + wn * T::WTN + 16u * ni +
+                   (lane & 15u)] = acc[mi][ni][r];
+    wait_dma<0>();
+    barrier();
+    const bool vec = ((j.out_stride | (uint64_t)(uintptr_t)j.out) & 15u) == 0;
+    const bool scaled = j.mode == MODE_SUM_SCALED;
+#pragma unroll
+    for (uint32_t c0 = 0; c0 < TM * TN / 4u; c0 += THREADS) {
+        const uint32_t c = c0 + tid, row = c / (TN / 4u), col = 4u * (c % (TN / 4u));
+        const uint32_t m = m0 + row, n = n0 + col;
+        if (m >= j.rows || n >= j.n)
+            continue;
+        float4 v = *reinterpret_cast<const float4*>(so + row * T::OUT_STRIDE + col);
+        if (scaled) {
+            const float s = j.rscale[m];
+            v.x = v.x * s;
+            v.y = v.y * s;
+            v.z = v.z * s;
+            v.w = v.w * s;
+        }
+        float* dst = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride) + n;
+        if (vec && n + 4u <= j.n) {
+            const v4f w = {v.x, v.y, v.z, v.w};
+            __builtin_nontemporal_store(w, reinterpret_cast<v4f*>(dst));
+        } else {
+            dst[0] = v.x;
+            if (n + 1u < j.n)
+                dst[1] = v.y;
+            if (n + 2u < j.n)
+                dst[2] = v.z;
+            if (n + 3u < j.n)
+                dst[3] = v.w;
         }
     }
 }
 
-template <int TM, int TN>
+// k_gemm_ks: F32-accumulating jobs with too few tiles to give every CU a workgroup.
+// Workgroup tile (16*TMS) x (16*TNS); the W waves split K instead of the tile: wave w
+// computes groups w, w+W, w+2W, ... for the whole tile, its operands loaded from
+// global memory straight into registers DEPTH-1 rounds ahead.  The K order inside a
+// group is permuted so that a lane's share of a column's sign bits is 4 contiguous
+// bytes: lane chunk c (lane / 16) covers weights 32c .. 32c+31, MFMA half h the 16
+// starting at 32c + 16h, in the rows and the weights alike.  The bits of the next
+// round become +1/-1 operands through the byte table while this round's MFMAs run.
+// Per round each wave writes the exact products RN(scale * D) of its group to LDS;
+// then every thread adds the W products of its outputs to its FP32 accumulators in
+// group order -- the order of the sums is the reference's, only the integer work ran
+// in parallel.
+template <int TMS, int TNS>
+struct KsOps {
+    v4i a[TMS][2];
+    uint32_t bits[TNS];
+    uint16_t s[TNS];
+    v4i b[TNS][2];  // the +1/-1 operands, from bits
+};
+
+__device__ __forceinline__ v4i gload_v4i(const void* p) {
+    return *(const __attribute__((address_space(1))) v4i*)p;
+}
+
+template <int TMS, int TNS, int W, int DEPTH>
+__global__ __launch_bounds__(64 * W) void k_gemm_ks(GemmJob j, uint32_t mtiles, uint64_t seq,
+                                                   const uint64_t* __restrict__ flag) {
+    constexpr uint32_t TM = 16u * TMS, TN = 16u * TNS, SUBS = TMS * TNS, NT = 64u * W;
+    constexpr uint32_t BLOCKS = SUBS * 64u;  // 16-byte blocks of products per wave
+    constexpr uint32_t PER_THREAD = (BLOCKS + NT - 1u) / NT;
+    static_assert(DEPTH >= 3, "the next round's bits loaded a round before their expansion");
+    static_assert(TN <= 64, "a tile's columns lie in one 64-feature tile of the matrix layout");
+    __shared__ __attribute__((aligned(16))) float prod[W][BLOCKS * 4u];  // [wave][subtile][lane][4]
+    __shared__ uint2 lut[256];
+    if (*flag == seq)
+        return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t tile = gemm_tile_of_block(blockIdx.x, gridDim.x);
+    const uint32_t mt = tile % mtiles, nt = tile / mtiles;
+    const uint32_t m0 = mt * TM, n0 = nt * TN;
+    const uint32_t groups = j.groups;
+    for (uint32_t i = tid; i < 256u; i += NT)
+        lut[i] = make_uint2(pm1_nibble(i & 15u), pm1_nibble(i >> 4));
+
+    // rows past the end are clamped (never stored); so is the matrix tile of columns
+    // past the last tile
+    const uint32_t chunk = lane >> 4;
+    const uint8_t* a_ptr[TMS];
+    const uint8_t* b_ptr[TNS];
+    const uint16_t* s_ptr[TNS];
+#pragma unroll
+    for (int mi = 0; mi < TMS; ++mi) {
+        const uint32_t m = min(m0 + 16u * mi + (lane & 15u), j.rows - 1u);
+        a_ptr[mi] = reinterpret_cast<const uint8_t*>(j.q) + (size_t)m * j.k + 32u * chunk;
+    }
+#pragma unroll
+    for (int ni = 0; ni < TNS; ++ni) {
+        const uint32_t n = n0 + 16u * ni + (lane & 15u), st = min(n >> 6, j.tiles - 1u);
+        b_ptr[ni] = reinterpret_cast<const uint8_t*>(j.wbits) + ((size_t)st * groups * kTile + (n & 63u)) * 16u +
+                    4u * chunk;
+        s_ptr[ni] = j.wscale + (size_t)st * groups * kTile + (n & 63u);
+    }
+    // loads are unconditional (group clamped into range) so that every path has the
+    // same loads in flight
+    auto load = [&](KsOps<TMS, TNS>& o, uint32_t round) {
+        const uint32_t g = min(W * round + wave, groups - 1u);
+#pragma unroll
+        for (int mi = 0; mi < TMS; ++mi)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                o.a[mi][h] = gload_v4i(a_ptr[mi] + (size_t)g * kGroup + 16u * h);
+#pragma unroll
+        for (int ni = 0; ni < TNS; ++ni) {
+            o.bits[ni] = *reinterpret_cast<const uint32_t*>(b_ptr[ni] + (size_t)g * kTile * 16u);
+            o.s[ni] = s_ptr[ni][(size_t)g * kTile];
+        }
+    };
+    auto expand = [&](KsOps<TMS, TNS>& o) {
+#pragma unroll
+        for (int ni = 0; ni < TNS; ++ni)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint2 lo = lut[(o.bits[ni] >> (16u * h)) & 0xffu];
+                const uint2 hi = lut[(o.bits[ni] >> (16u * h + 8u)) & 0xffu];
+                o.b[ni][h] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+            }
+    };
+
+    float acc[PER_THREAD][4];
+#pragma unroll
+    for (int i = 0; i < (int)PER_THREAD; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            acc[i][r] = 0.0f;
+    const v4i c_init = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+    KsOps<TMS, TNS> o[DEPTH];
+
+    // round r with its operands in o[d] (d = r % DEPTH)
+    auto round = [&](int d, uint32_t r) {
+        KsOps<TMS, TNS>& cur = o[d];
+        load(o[(d + DEPTH - 1) % DEPTH], r + DEPTH - 1u);
+        const uint32_t g = W * r + wave;
+        float4 p[TMS][TNS];
+        if (g < groups) {
+#pragma unroll
+            for (int ni = 0; ni < TNS; ++ni) {
+                const float sc = __half2float(__ushort_as_half(cur.s[ni]));
+                const float cneg = sc * -kMagicValue;  // exact
+#pragma unroll
+                for (int mi = 0; mi < TMS; ++mi) {
+                    v4i dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[mi][0], cur.b[ni][0], c_init, 0, 0, 0);
+                    dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[mi][1], cur.b[ni][1], dd, 0, 0, 0);
+                    p[mi][ni].x = __builtin_fmaf(sc, __int_as_float(dd[0]), cneg);
+                    p[mi][ni].y = __builtin_fmaf(sc, __int_as_float(dd[1]), cneg);
+                    p[mi][ni].z = __builtin_fmaf(sc, __int_as_float(dd[2]), cneg);
+                    p[mi][ni].w = __builtin_fmaf(sc, __int_as_float(dd[3]), cneg);
+                }
+            }
+        }
+        expand(o[(d + 1) % DEPTH]);  // round r+1's operands, loaded one round ago
+        // the previous round's reads of prod are done (their sums consumed them)
+        barrier();
+        if (g < groups) {
+#pragma unroll
+            for (int mi = 0; mi < TMS; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < TNS; ++ni)
+                    *reinterpret_cast<float4*>(&prod[wave][((mi * TNS + ni) * 64u + lane) * 4u]) = p[mi][ni];
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+        barrier();
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            if (W * r + w < groups) {
+#pragma unroll
+                for (int i = 0; i < (int)PER_THREAD; ++i) {
+                    const uint32_t blk = NT * i + tid;
+                    if (BLOCKS % NT == 0 || blk < BLOCKS) {
+                        const float4 v = *reinterpret_cast<const float4*>(&prod[w][blk * 4u]);
+                        acc[i][0] = acc[i][0] + v.x;
+                        acc[i][1] = acc[i][1] + v.y;
+                        acc[i][2] = acc[i][2] + v.z;
+                        acc[i][3] = acc[i][3] + v.w;
+                    }
+                }
+            }
+        }
+    };
+
+#pragma unroll
+    for (int d = 0; d + 1 < DEPTH; ++d)
+        load(o[d], d);
+    barrier();  // the table is in LDS
+    expand(o[0]);
+    const uint32_t rounds = (groups + W - 1u) / W;
+    // the round count is padded to a multiple of DEPTH with rounds of no groups
+    for (uint32_t r = 0; r < rounds; r += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d)
+            round(d, r + d);
+    }
+    // block NT*i + tid is subtile W*i + wave, lane `lane`
+#pragma unroll
+    for (int i = 0; i < (int)PER_THREAD; ++i) {
+        const uint32_t sub = W * i + wave;
+        if (sub >= SUBS)
+            continue;
+        const uint32_t mi = sub / TNS, ni = sub % TNS;
+        const uint32_t n = n0 + 16u * ni + (lane & 15u);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + 16u * mi + 4u * (lane >> 4) + r;
+            if (m >= j.rows || n >= j.n)
+                continue;
+            float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
+            __builtin_nontemporal_store(j.mode == MODE_SUM_SCALED ? acc[i][r] * j.rscale[m] : acc[i][r], orow + n);
+        }
+    }
+}
+
+template <int TMS, int TNS, int W, int DEPTH>
+hipError_t launch_ks(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
+    const uint32_t mtiles = (job.rows + 16u * TMS - 1u) / (16u * TMS);
+    const uint32_t ntiles = (job.n + 16u * TNS - 1u) / (16u * TNS);
+    launch_kernel((k_gemm_ks<TMS, TNS, W, DEPTH>), dim3(mtiles * ntiles), dim3(64 * W), 0, stream, job, mtiles, seq,
+                  flag);
+    return hipGetLastError();
+}
+
+template <int TM, int TN, int WGM, int WGN>
 hipError_t launch_bits(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
     const uint32_t mtiles = (job.rows + TM - 1u) / TM, ntiles = (job.n + TN - 1u) / TN;
+    const dim3 grid(mtiles * ntiles), block(64 * WGM * WGN);
     if (job.mode == MODE_DOT_I16)
-        launch_kernel((k_gemm_bits<TM, TN, true>), dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq, flag);
+        launch_kernel((k_gemm_bits<TM, TN, WGM, WGN, true>), grid, block, 0, stream, job, mtiles, seq, flag);
     else
-        launch_kernel((k_gemm_bits<TM, TN, false>), dim3(mtiles * ntiles), dim3(256), 0, stream, job, mtiles, seq,
-                      flag);
+        launch_kernel((k_gemm_bits<TM, TN, WGM, WGN, false>), grid, block, 0, stream, job, mtiles, seq, flag);
     return hipGetLastError();
 }
 
@@ -358,12 +689,22 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
         return (uint64_t)((job.rows + tm - 1u) / tm) * ((job.n + tn - 1u) / tn);
     };
     if (blocks(128, 128) >= cus)
-        return launch_bits<128, 128>(stream, job, seq, flag);
+        return launch_bits<128, 128, 2, 4>(stream, job, seq, flag);
     if (blocks(64, 128) >= cus)
-        return launch_bits<64, 128>(stream, job, seq, flag);
+        return launch_bits<64, 128, 2, 4>(stream, job, seq, flag);
     if (blocks(64, 64) >= cus)
-        return launch_bits<64, 64>(stream, job, seq, flag);
-    return launch_bits<32, 64>(stream, job, seq, flag);
+        return launch_bits<64, 64, 2, 2>(stream, job, seq, flag);
+    const uint64_t enough = cus * 3u / 4u;
+    if (job.mode != MODE_DOT_I16 && blocks(32, 64) < enough) {
+        // too few tiles for the CUs: K split across the 8 waves of a workgroup, with the
+        // largest tile that still gives most CUs a workgroup
+        if (blocks(64, 32) >= enough)
+            return launch_ks<4, 2, 8, 3>(stream, job, seq, flag);
+        if (blocks(32, 32) >= enough)
+            return launch_ks<2, 2, 8, 3>(stream, job, seq, flag);
+        return launch_ks<2, 1, 8, 3>(stream, job, seq, flag);
+    }
+    return launch_bits<32, 64, 2, 2>(stream, job, seq, flag);
 }
 
 }  // namespace bnnhip

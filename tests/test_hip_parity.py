@@ -108,7 +108,8 @@ def test_quantiser_edge_rows(pkg, hipdev, oracle, i):
     (1000, 384, 4100), (2049, 128, 2000), (1152, 640, 8128),  # 128 x 128 workgroup tiles
     (1000, 640, 2000),                                         # 64 x 128
     (250, 1152, 6100),                                         # 64 x 64
-    (50, 640, 1000), (100, 3200, 3000), (120, 1152, 5000),    # 32 x 64 (fewer tiles than CUs)
+    (120, 1152, 5000),                                         # 32 x 64
+    (80, 1408, 3500), (100, 3200, 3000), (50, 640, 1000),     # K split over 8 waves: 64x32, 32x32, 32x16
 ])
 def test_gemm_tilings_ragged_edges(pkg, hipdev, oracle_fast, op, rows, k, n):
     """Shapes that select each multi-row tiling, with a partial last row tile, a last
