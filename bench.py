@@ -272,7 +272,10 @@ def gemm_leg(pkg, hip):
     return {"peak_TOPS": 5000.0, "best_TOPS": round(best, 1), "cases": out}
 
 
-def e2e_leg(pkg, hip):
+E2E_PATHS = {"device": 1, "prepared": 2, "host": 0}
+
+
+def e2e_leg(pkg, hip, paths=tuple(E2E_PATHS), new=128):
     """Config 5: Qwen3-1.7B-shape greedy decode through the engine (BNNE_* API)."""
     import tempfile
     fixture_path = ROOT / "tests" / "golden" / "e2e_qwen3_1p7b.json"
@@ -289,7 +292,8 @@ def e2e_leg(pkg, hip):
             t0 = time.perf_counter()
             model = pkg.engine.Model(eng, dev, path)
             load_s = time.perf_counter() - t0
-            for name, mode in (("device", 1), ("prepared", 2), ("host", 0)):
+            for name in paths:
+                mode = E2E_PATHS[name]
                 ctx = pkg.engine.Context(model, n_ctx=1024)
                 ctx.set_resident(mode)
                 assert ctx.resident() == mode, f"{name} path not available"
@@ -297,23 +301,24 @@ def e2e_leg(pkg, hip):
                 tokens = [int(np.argmax(ctx.decode(prompt)))]
                 t1 = time.perf_counter()
                 ctx.reset_stats()
-                for _ in range(127):
+                for _ in range(new - 1):
                     tokens.append(int(np.argmax(ctx.decode([tokens[-1]]))))
                 t2 = time.perf_counter()
                 st = ctx.stats()
                 ctx.free()
-                entry = {"prefill_tok_s": round(32 / (t1 - t0), 1), "decode_tok_s": round(127 / (t2 - t1), 1),
-                         "ms_per_token": round((t2 - t1) / 127 * 1e3, 3),
+                steps = new - 1
+                entry = {"prefill_tok_s": round(32 / (t1 - t0), 1), "decode_tok_s": round(steps / (t2 - t1), 1),
+                         "ms_per_token": round((t2 - t1) / steps * 1e3, 3),
                          "backend_share": round((st["transfer_ns"] + st["execute_ns"]) / max(st["total_ns"], 1), 4),
-                         "weight_GBps": round(info["weight_bytes"] * 127 / (t2 - t1) / 1e9, 1)}
+                         "weight_GBps": round(info["weight_bytes"] * steps / (t2 - t1) / 1e9, 1)}
                 if fixture:
-                    want = [row[1] for row in fixture["steps"]]
+                    want = [row[1] for row in fixture["steps"]][:new]
                     same = sum(a == b for a, b in zip(tokens, want))
                     entry["token_agreement"] = f"{same}/{len(want)}"
                 res[name] = entry
             model.free()
     out = {"model": "random-init Qwen3-1.7B shape (28 layers, 2048, 16/8 heads, FFN 6144, vocab 151669), Q1_0",
-           "tokens": "32 prompt + 128 greedy", "gguf_write_s": round(gen_s, 1), "load_s": round(load_s, 1),
+           "tokens": f"32 prompt + {new} greedy", "gguf_write_s": round(gen_s, 1), "load_s": round(load_s, 1),
            "weight_bytes_per_token": info["weight_bytes"], "paths": res}
     if fixture and fixture.get("soft_seconds"):
         # the fixture run: 32 prompt steps + 127 decode steps on one host core of the build container
@@ -367,6 +372,9 @@ def main():
                     help="only run one 256 MiB device-to-device copy (counter calibration)")
     ap.add_argument("--only", choices=("ops", "gemm", "e2e", "mlp"),
                     help="run one secondary leg alone and print its JSON (for profiling)")
+    ap.add_argument("--e2e-paths", default=",".join(E2E_PATHS),
+                    help="decode paths of the e2e leg (comma list of device, prepared, host)")
+    ap.add_argument("--e2e-new", type=int, default=128, help="greedy tokens per path in the e2e leg (2..128)")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration()
@@ -381,7 +389,11 @@ def main():
     pkg = load_pkg()
     hip = pkg.load_hip()
     if args.only:
-        legs = {"ops": ops_leg, "gemm": gemm_leg, "e2e": e2e_leg, "mlp": mlp_leg}
+        e2e_paths = tuple(p for p in args.e2e_paths.split(",") if p)
+        if not e2e_paths or any(p not in E2E_PATHS for p in e2e_paths) or not 2 <= args.e2e_new <= 128:
+            ap.error("--e2e-paths takes device, prepared, host; --e2e-new 2..128")
+        legs = {"ops": ops_leg, "gemm": gemm_leg, "mlp": mlp_leg,
+                "e2e": lambda pkg, hip: e2e_leg(pkg, hip, e2e_paths, args.e2e_new)}
         print(json.dumps({args.only: legs[args.only](pkg, hip)}), flush=True)
         return
     dev = pkg.Device(hip, 0)

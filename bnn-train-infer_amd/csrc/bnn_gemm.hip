@@ -37,6 +37,8 @@
 // At the end every wave writes its accumulators into LDS and the workgroup stores
 // the tile row by row, 16 bytes per lane.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <hip/hip_fp16.h>
 
 #include "bnn_internal.h"
@@ -64,11 +66,22 @@ __device__ __forceinline__ uint32_t pm1_nibble(uint32_t nib) {
 // one chunk) hit 16 distinct 16-byte bank groups.
 __device__ __forceinline__ uint32_t swz128(uint32_t r, uint32_t c) { return r * 128u + 16u * (c ^ ((r >> 1) & 7u)); }
 
-// The bijective workgroup remap that keeps consecutive tiles (the M tiles of one
-// N tile, which share the weights) on one XCD and its L2.
-__device__ __forceinline__ uint32_t gemm_tile_of_block(uint32_t b, uint32_t grid) {
+// Output tiles in bands of `band` M tiles, M tile fastest within a band (the last
+// band may be narrower), and workgroups remapped so that consecutive tiles run on one
+// XCD: each XCD's share of the grid is then a rectangle of about band M tiles by
+// (tiles / 8 / band) N tiles, whose rows and weights stay in that XCD's L2.  The host
+// picks `band` so that the rows (re-read once per XCD that covers an M tile) and the
+// weights (once per band) cost the least traffic.
+struct TileRC {
+    uint32_t mt, nt;
+};
+__device__ __forceinline__ TileRC gemm_tile_of_block(uint32_t b, uint32_t grid, uint32_t mtiles, uint32_t ntiles,
+                                                     uint32_t band) {
     const uint32_t x = b % 8u, i = b / 8u, q = grid / 8u, r = grid % 8u;
-    return (x < r ? x * (q + 1u) : r * (q + 1u) + (x - r) * q) + i;
+    const uint32_t t = (x < r ? x * (q + 1u) : r * (q + 1u) + (x - r) * q) + i;
+    const uint32_t bi = t / (band * ntiles), rest = t % (band * ntiles);
+    const uint32_t width = min(band, mtiles - bi * band);
+    return TileRC{bi * band + rest % width, rest / width};
 }
 
 // 16 bytes per active lane from global memory into LDS at lds_addr + 16 * lane (the
@@ -149,7 +162,8 @@ struct Tiling {
 };
 
 template <int TM, int TN, int WGM, int WGN, bool DOT>
-__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_bits(GemmJob j, uint32_t mtiles, uint64_t seq,
+__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_bits(GemmJob j, uint32_t mtiles, uint32_t ntiles, uint32_t band,
+    uint64_t seq,
                                                               const uint64_t* __restrict__ flag) {
     using T = Tiling<TM, TN, WGM, WGN>;
     constexpr int MS = T::MS, NS = T::NS, WAVES = T::WAVES, THREADS = T::THREADS;
@@ -159,8 +173,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_bits(GemmJob j, uint32_
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / WGN, wn = wave % WGN;
-    const uint32_t tile = gemm_tile_of_block(blockIdx.x, gridDim.x);
-    const uint32_t mt = tile % mtiles, nt = tile / mtiles;
+    const TileRC tile = gemm_tile_of_block(blockIdx.x, gridDim.x, mtiles, ntiles, band);
+    const uint32_t mt = tile.mt, nt = tile.nt;
     const uint32_t m0 = mt * TM, n0 = nt * TN;
     const uint32_t groups = j.groups;
     unsigned char* const lds_a = smem;
@@ -502,7 +516,8 @@ __device__ __forceinline__ v4i gload_v4i(const void* p) {
 }
 
 template <int TMS, int TNS, int W, int DEPTH>
-__global__ __launch_bounds__(64 * W) void k_gemm_ks(GemmJob j, uint32_t mtiles, uint64_t seq,
+__global__ __launch_bounds__(64 * W) void k_gemm_ks(GemmJob j, uint32_t mtiles, uint32_t ntiles, uint32_t band,
+    uint64_t seq,
                                                    const uint64_t* __restrict__ flag) {
     constexpr uint32_t TM = 16u * TMS, TN = 16u * TNS, SUBS = TMS * TNS, NT = 64u * W;
     constexpr uint32_t BLOCKS = SUBS * 64u;  // 16-byte blocks of products per wave
@@ -515,8 +530,8 @@ __global__ __launch_bounds__(64 * W) void k_gemm_ks(GemmJob j, uint32_t mtiles, 
         return;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t tile = gemm_tile_of_block(blockIdx.x, gridDim.x);
-    const uint32_t mt = tile % mtiles, nt = tile / mtiles;
+    const TileRC tile = gemm_tile_of_block(blockIdx.x, gridDim.x, mtiles, ntiles, band);
+    const uint32_t mt = tile.mt, nt = tile.nt;
     const uint32_t m0 = mt * TM, n0 = nt * TN;
     const uint32_t groups = j.groups;
     for (uint32_t i = tid; i < 256u; i += NT)
@@ -658,12 +673,29 @@ __global__ __launch_bounds__(64 * W) void k_gemm_ks(GemmJob j, uint32_t mtiles, 
     }
 }
 
+// The band width (in M tiles) of gemm_tile_of_block: an XCD covering band M tiles of
+// mtiles and (tiles / 8 / band) N tiles makes the rows (rows * k bytes) be fetched
+// into about 8 * band / mtiles L2s and the weights (1.125 bits each) into
+// mtiles / band of them; the band minimising the sum.
+uint32_t gemm_band(const GemmJob& job, uint32_t mtiles) {
+    const double a = (double)job.rows * job.k, b = (double)job.n * job.k * 0.140625;
+    uint32_t best = 1;
+    double best_cost = 0.0;
+    for (uint32_t band = 1; band <= mtiles; ++band) {
+        const double xcds_per_mtile = std::min(8.0, 8.0 * band / mtiles);
+        const double cost = a * std::max(1.0, xcds_per_mtile) + b * ((mtiles + band - 1u) / band);
+        if (band == 1 || cost < best_cost)
+            best = band, best_cost = cost;
+    }
+    return best;
+}
+
 template <int TMS, int TNS, int W, int DEPTH>
 hipError_t launch_ks(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
     const uint32_t mtiles = (job.rows + 16u * TMS - 1u) / (16u * TMS);
     const uint32_t ntiles = (job.n + 16u * TNS - 1u) / (16u * TNS);
-    launch_kernel((k_gemm_ks<TMS, TNS, W, DEPTH>), dim3(mtiles * ntiles), dim3(64 * W), 0, stream, job, mtiles, seq,
-                  flag);
+    launch_kernel((k_gemm_ks<TMS, TNS, W, DEPTH>), dim3(mtiles * ntiles), dim3(64 * W), 0, stream, job, mtiles, ntiles,
+                  gemm_band(job, mtiles), seq, flag);
     return hipGetLastError();
 }
 
@@ -671,10 +703,13 @@ template <int TM, int TN, int WGM, int WGN>
 hipError_t launch_bits(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
     const uint32_t mtiles = (job.rows + TM - 1u) / TM, ntiles = (job.n + TN - 1u) / TN;
     const dim3 grid(mtiles * ntiles), block(64 * WGM * WGN);
+    const uint32_t band = gemm_band(job, mtiles);
     if (job.mode == MODE_DOT_I16)
-        launch_kernel((k_gemm_bits<TM, TN, WGM, WGN, true>), grid, block, 0, stream, job, mtiles, seq, flag);
+        launch_kernel((k_gemm_bits<TM, TN, WGM, WGN, true>), grid, block, 0, stream, job, mtiles, ntiles, band, seq,
+                      flag);
     else
-        launch_kernel((k_gemm_bits<TM, TN, WGM, WGN, false>), grid, block, 0, stream, job, mtiles, seq, flag);
+        launch_kernel((k_gemm_bits<TM, TN, WGM, WGN, false>), grid, block, 0, stream, job, mtiles, ntiles, band, seq,
+                      flag);
     return hipGetLastError();
 }
 
