@@ -482,6 +482,196 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
     asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(lds_addr) : "memory");
 }
 
+// Attention of one query head in a single launch, for contexts of fewer than
+// kAttnOneMax positions (pos < kAttnOneMax): workgroup h, four waves, the same
+// operations in the same order as k_attn_scores + k_attn_pv.  Loads first, oldest
+// needed first (wave 0's head vectors, each thread's key row, then the V rows of
+// positions below pos into LDS by DMA); then
+//   wave 0: the head norms and RoPE of q and of the kv head's new key (the cache row
+//   at pos stored by the kv head's first query head);
+//   thread t <= pos: the score of position t (in-order dot over head_dim; position pos
+//   from the new key itself);
+//   wave 0: the maximum, expf, the in-order sum and the probabilities;
+//   thread i < head_dim: value[i] = sum over t in order of p[t] * V[t][i], row pos from
+//   the new value itself -- no workgroup reads a cache row that another is writing.
+constexpr uint32_t kAttnOneMax = 256;
+
+// Workgroup barrier for LDS data: waits for this wave's LDS accesses, not for its
+// outstanding global loads and DMAs.
+__device__ __forceinline__ void block_lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__global__ __launch_bounds__(256) void k_attn_one(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, uint32_t kv_mul, float eps,
+    const float* __restrict__ q_gain, const float* __restrict__ k_gain, const float* __restrict__ cosv,
+    const float* __restrict__ sinv, float* __restrict__ kc, float* __restrict__ vc, uint32_t pos, uint32_t kv_dim,
+    float scale, float* __restrict__ y, int* err, int code_base) {
+    constexpr uint32_t HD = kAttnHD, hd4 = HD / 4, half = HD / 2;
+    __shared__ float4 vs4[kAttnOneMax * HD / 4];  // V rows 0..pos-1 of the head
+    __shared__ float4 sq4[2][hd4];                 // the squares of q and k
+    __shared__ float4 qk4[2][hd4];                 // q and k normalised and rotated
+    __shared__ float4 p4[kAttnOneMax / 4];         // scores, then probabilities (+0 past pos)
+    __shared__ uint64_t exp_tab[32];
+    __shared__ int failed;
+    float* p = reinterpret_cast<float*>(p4);
+    const float* vs = reinterpret_cast<const float*>(vs4);
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t h = blockIdx.x, t = tid;
+    const size_t head_off = (size_t)(h / kv_mul) * HD;
+
+    float qa = 0.0f, qb = 0.0f, ka = 0.0f, kb = 0.0f, qga = 0.0f, qgb = 0.0f, kga = 0.0f, kgb = 0.0f, c = 0.0f, s = 0.0f;
+    if (wave == 0) {
+        qa = q[(size_t)h * HD + lane], qb = q[(size_t)h * HD + lane + half];
+        ka = k[head_off + lane], kb = k[head_off + lane + half];
+        qga = q_gain[lane], qgb = q_gain[lane + half], kga = k_gain[lane], kgb = k_gain[lane + half];
+        c = cosv[lane], s = sinv[lane];
+    }
+    float4 key[hd4];
+    if (t < pos) {
+        const float4* row = reinterpret_cast<const float4*>(kc + (size_t)t * kv_dim + head_off);
+#pragma unroll
+        for (uint32_t i = 0; i < hd4; ++i)
+            key[i] = row[i];
+    }
+    // V rows 0..pos-1: 16-byte piece ci = 32 * row + part at byte 16 * ci of vs4;
+    // wave w issues pieces w * 64 + 256 * i + lane (pieces past the last row load row
+    // pos - 1 again into unused space)
+    {
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
+        for (uint32_t c0 = wave * 64u; c0 < 32u * pos; c0 += 256u) {
+            const uint32_t ci = c0 + lane, row = min(ci >> 5, pos - 1u);
+            dma16(vc + (size_t)row * kv_dim + head_off + 4u * (ci & 31u), base + 16u * c0);
+        }
+    }
+    if (tid < 32u)
+        exp_tab[tid] = kExp2Table[tid];
+    if (wave == 0) {
+        // head norms: both in-order sums over head_dim, interleaved, in every lane
+        float* sq_q = reinterpret_cast<float*>(sq4[0]);
+        float* sq_k = reinterpret_cast<float*>(sq4[1]);
+        sq_q[lane] = qa * qa;
+        sq_q[lane + half] = qb * qb;
+        sq_k[lane] = ka * ka;
+        sq_k[lane + half] = kb * kb;
+        wave_lds_sync();
+        float sum_q = 0.0f, sum_k = 0.0f;
+#pragma unroll 8
+        for (uint32_t i = 0; i < hd4; ++i) {
+            const float4 a = sq4[0][i], b = sq4[1][i];
+            sum_q = sum_q + a.x;
+            sum_k = sum_k + b.x;
+            sum_q = sum_q + a.y;
+            sum_k = sum_k + b.y;
+            sum_q = sum_q + a.z;
+            sum_k = sum_k + b.z;
+            sum_q = sum_q + a.w;
+            sum_k = sum_k + b.w;
+        }
+        const float rq = sqrtf(sum_q / (float)HD + eps), rk = sqrtf(sum_k / (float)HD + eps);
+        const bool bad = !isfinite(rq) || rq == 0.0f || !isfinite(rk) || rk == 0.0f;
+        if (bad) {
+            if (lane == 0)
+                set_error_first(err, code_base + 2);
+        } else {
+            // x / rms * gain, then the rotation of pair (lane, lane + 64)
+            const float nqa = qa / rq * qga, nqb = qb / rq * qgb;
+            const float nka = ka / rk * kga, nkb = kb / rk * kgb;
+            float* qr = reinterpret_cast<float*>(qk4[0]);
+            float* kr = reinterpret_cast<float*>(qk4[1]);
+            qr[lane] = nqa * c - nqb * s;
+            qr[lane + half] = nqa * s + nqb * c;
+            const float rka = nka * c - nkb * s, rkb = nka * s + nkb * c;
+            kr[lane] = rka;
+            kr[lane + half] = rkb;
+            if (h % kv_mul == 0) {
+                kc[(size_t)pos * kv_dim + head_off + lane] = rka;
+                kc[(size_t)pos * kv_dim + head_off + lane + half] = rkb;
+                vc[(size_t)pos * kv_dim + head_off + lane] = v[head_off + lane];
+                vc[(size_t)pos * kv_dim + head_off + lane + half] = v[head_off + lane + half];
+            }
+        }
+        if (lane == 0)
+            failed = bad;
+    }
+    block_lds_barrier();
+    if (failed) {
+        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): no DMA still writing this workgroup's LDS
+        return;                              // the whole workgroup
+    }
+
+    // the score of position t: in-order dot over head_dim (row pos: the new key)
+    if (t <= pos) {
+        if (t == pos) {
+#pragma unroll
+            for (uint32_t i = 0; i < hd4; ++i)
+                key[i] = qk4[1][i];
+        }
+        float dot = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < hd4; ++i) {
+            const float4 qq = qk4[0][i];
+            dot = dot + qq.x * key[i].x;
+            dot = dot + qq.y * key[i].y;
+            dot = dot + qq.z * key[i].z;
+            dot = dot + qq.w * key[i].w;
+        }
+        const float score = dot * scale;
+        if (!isfinite(score))
+            set_error_first(err, code_base + 3 + 2 * (int)h);
+        p[t] = score;
+    }
+    block_lds_barrier();
+
+    // the maximum (order-free: finite or flagged), expf(score - max), their sum in
+    // position order over a multiple of 64 terms (+0 pads), the probabilities
+    if (wave == 0) {
+        float mx = -INFINITY;
+        for (uint32_t u = lane; u <= pos; u += 64u)
+            mx = p[u] > mx ? p[u] : mx;
+        const float maximum = __ockl_wfred_max_f32(mx);
+        const uint32_t padded = (pos + 64u) & ~63u;
+        for (uint32_t u = lane; u < padded; u += 64u)
+            p[u] = u <= pos ? bnne_expf_libc(p[u] - maximum, exp_tab) : 0.0f;
+        wave_lds_sync();
+        const float sum = sum_lds_in_order(p, padded);
+        if (!(sum > 0.0f) || !isfinite(sum)) {
+            if (lane == 0)
+                set_error_first(err, code_base + 4 + 2 * (int)h);
+        }
+        wave_lds_sync();
+        for (uint32_t u = lane; u <= pos; u += 64u)
+            p[u] = p[u] / sum;
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this wave's V rows are in LDS
+    block_lds_barrier();                 // ... and every wave's, with the probabilities
+
+    // value[i] in position order, 16 rows' LDS reads issued before their additions
+    if (tid < HD) {
+        const float* col = vs + tid;
+        float acc = 0.0f;
+        uint32_t u = 0;
+        for (; u + 16u <= pos; u += 16u) {
+            float vv[16], pp[16];
+#pragma unroll
+            for (uint32_t j = 0; j < 16; ++j) {
+                vv[j] = col[(u + j) * HD];
+                pp[j] = p[u + j];
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < 16; ++j)
+                acc = acc + pp[j] * vv[j];
+        }
+        for (; u < pos; ++u)
+            acc = acc + p[u] * col[u * HD];
+        acc = acc + p[pos] * v[head_off + tid];
+        y[(size_t)h * HD + tid] = acc;
+    }
+}
+
 constexpr uint32_t kPvRows = 1024;  // V slice rows in LDS per pass (128 KB)
 constexpr uint32_t kPvPad = 16;     // rows / probabilities read past the end by the pipelined loop
 
@@ -1053,14 +1243,22 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         for (uint32_t l = 0; l < r->L && st == BNNE_OK; ++l) {
             const size_t cache_layer = (size_t)l * r->n_ctx * r->kv_dim;
             launch(r->qkv[l]);
-            hipLaunchKernelGGL(k_attn_scores, dim3(r->H, pos / kScoreBlock + 1u), dim3(kScoreBlock), 0, r->stream,
-                               r->q, r->k, r->v, r->H / r->Hk, r->eps, q_norm + (size_t)l * HD,
-                               k_norm + (size_t)l * HD, r->rope_cos + (size_t)pos * half,
-                               r->rope_sin + (size_t)pos * half, r->kc + cache_layer, r->vc + cache_layer, pos,
-                               r->kv_dim, scale, r->scores, r->n_ctx, r->err, (int)l * code_span(r));
-            hipLaunchKernelGGL(k_attn_pv, dim3(r->H, HD / kPvSlice), dim3(128), 0, r->stream, r->scores,
-                               r->vc + cache_layer, r->H / r->Hk, pos, r->kv_dim, r->n_ctx, r->y, r->err,
-                               (int)l * code_span(r));
+            if (pos < kAttnOneMax) {
+                hipLaunchKernelGGL(k_attn_one, dim3(r->H), dim3(256), 0, r->stream, r->q, r->k, r->v, r->H / r->Hk,
+                                   r->eps, q_norm + (size_t)l * HD, k_norm + (size_t)l * HD,
+                                   r->rope_cos + (size_t)pos * half, r->rope_sin + (size_t)pos * half,
+                                   r->kc + cache_layer, r->vc + cache_layer, pos, r->kv_dim, scale, r->y, r->err,
+                                   (int)l * code_span(r));
+            } else {
+                hipLaunchKernelGGL(k_attn_scores, dim3(r->H, pos / kScoreBlock + 1u), dim3(kScoreBlock), 0,
+                                   r->stream, r->q, r->k, r->v, r->H / r->Hk, r->eps, q_norm + (size_t)l * HD,
+                                   k_norm + (size_t)l * HD, r->rope_cos + (size_t)pos * half,
+                                   r->rope_sin + (size_t)pos * half, r->kc + cache_layer, r->vc + cache_layer, pos,
+                                   r->kv_dim, scale, r->scores, r->n_ctx, r->err, (int)l * code_span(r));
+                hipLaunchKernelGGL(k_attn_pv, dim3(r->H, HD / kPvSlice), dim3(128), 0, r->stream, r->scores,
+                                   r->vc + cache_layer, r->H / r->Hk, pos, r->kv_dim, r->n_ctx, r->y, r->err,
+                                   (int)l * code_span(r));
+            }
             launch(r->attn_out[l]);
             launch(r->gate_up[l]);
             launch(r->down[l]);
