@@ -340,7 +340,9 @@ enum ItemMap : int { MAP_SINGLE = 0, MAP_UNIFORM = 1, MAP_TABLE = 2 };
 #define BNN_DOT_WAVE_WG_WAVES 4  // items (waves) per workgroup; one item per wave, no persistent loop
 #endif
 #ifndef BNN_DOT_WAVE_MIN_ITEMS_PER_CU
-#define BNN_DOT_WAVE_MIN_ITEMS_PER_CU 4
+// below this many items per CU the group-split kernel finishes sooner: the lm_head as 19
+// chunks (2370 items, ~9 per CU) 12.0 us against 13.6 us with one wave per item; 32 no better
+#define BNN_DOT_WAVE_MIN_ITEMS_PER_CU 16
 #endif
 #ifndef BNN_DOT_WAVE_XCDS
 #define BNN_DOT_WAVE_XCDS 0  // > 1: keep consecutive workgroups on one XCD
