@@ -134,7 +134,7 @@ __device__ __forceinline__ void barrier() {
     asm volatile("" ::: "memory");  // no LDS access moves across it
 }
 
-template <int TM, int TN, int WGM, int WGN>
+template <int TM, int TN, int WGM, int WGN, int ASLOTS = 4>
 struct Tiling {
     static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
     static constexpr int WTM = TM / WGM, WTN = TN / WGN, MS = WTM / 16, NS = WTN / 16;
@@ -148,7 +148,7 @@ struct Tiling {
     static constexpr uint32_t SC_CPW = SC_CHUNKS >= (uint32_t)WAVES ? SC_CHUNKS / WAVES : 1;
     // LDS carve-up (bytes)
     static constexpr uint32_t A_SLOT = TM * 128, B_SLOT = TN * 128, BITS_SLOT = TN * 16, SC_SLOT = TN * 2;
-    static constexpr uint32_t OFF_B = 4 * A_SLOT, OFF_BITS = OFF_B + 2 * B_SLOT, OFF_SC = OFF_BITS + 4 * BITS_SLOT,
+    static constexpr uint32_t OFF_B = ASLOTS * A_SLOT, OFF_BITS = OFF_B + 2 * B_SLOT, OFF_SC = OFF_BITS + 4 * BITS_SLOT,
                               OFF_LUT = (OFF_SC + 4 * SC_SLOT + 15u) & ~15u, LOOP_BYTES = OFF_LUT + 2048;
     static constexpr uint32_t OUT_STRIDE = TN + 16;  // floats per staged output row
     static constexpr uint32_t OUT_BYTES = TM * OUT_STRIDE * 4;
@@ -491,6 +491,265 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_bits(GemmJob j, uint32_
     }
 }
 
+// k_gemm_co<TM, TN, WGM, WGN>: GEMM / GEMM_F32 with two workgroups per CU.  The
+// same per-group work as k_gemm_bits with a shorter pipeline, so that a 128 x 128
+// tile fits in 75 KB of LDS and 4 waves of at most 256 VGPRs: the rows' DMA runs one
+// group ahead (two slots), the unpack one, and each group's MFMA operands are read
+// right after its barrier; the other workgroup on the CU covers the latency.
+// Iteration g, after one wait and one barrier:
+//   * issue the DMAs of group g+1's rows, group g+4's bits and group g+2's scales;
+//   * look up group g+1's bits (read one iteration ago), read group g+2's bits, group
+//     g's operands and scales;
+//   * group g's first-half MFMAs interleaved with group g-1's epilogue;
+//   * store group g+1's +1/-1 tile; group g's second-half MFMAs.
+template <int TM, int TN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(2))) void k_gemm_co(
+    GemmJob j, uint32_t mtiles, uint32_t ntiles, uint32_t band, uint64_t seq, const uint64_t* __restrict__ flag) {
+    using T = Tiling<TM, TN, WGM, WGN, 2>;
+    constexpr int MS = T::MS, NS = T::NS, THREADS = T::THREADS;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
+    if (*flag == seq)
+        return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave / WGN, wn = wave % WGN;
+    const TileRC tile = gemm_tile_of_block(blockIdx.x, gridDim.x, mtiles, ntiles, band);
+    const uint32_t m0 = tile.mt * TM, n0 = tile.nt * TN;
+    const uint32_t groups = j.groups;
+    unsigned char* const lds_a = smem;
+    unsigned char* const lds_b = smem + T::OFF_B;
+    unsigned char* const lds_bits = smem + T::OFF_BITS;
+    unsigned char* const lds_sc = smem + T::OFF_SC;
+    uint2* const lut = reinterpret_cast<uint2*>(smem + T::OFF_LUT);
+    if (tid < 256u)
+        lut[tid] = make_uint2(pm1_nibble(tid & 15u), pm1_nibble(tid >> 4));
+
+    const uint8_t* a_src[T::A_INS];
+#pragma unroll
+    for (uint32_t i = 0; i < T::A_INS; ++i) {
+        const uint32_t p = wave * T::A_CHUNKS + i * 64u + lane, r = min(p >> 3, TM - 1u);
+        const uint32_t c = (p & 7u) ^ ((r >> 1) & 7u);
+        a_src[i] = reinterpret_cast<const uint8_t*>(j.q) + (size_t)min(m0 + r, j.rows - 1u) * j.k + 16u * c;
+    }
+    const uint32_t f = T::BIT_LANES * wave + min(lane, T::BIT_LANES - 1u);
+    const uint8_t* bit_src = reinterpret_cast<const uint8_t*>(j.wbits) +
+                             ((size_t)min((n0 + f) >> 6, j.tiles - 1u) * groups * kTile + ((n0 + f) & 63u)) * 16u;
+    const uint32_t sc_first = (wave * T::SC_CPW) % T::SC_CHUNKS;
+    const uint32_t sc_col = n0 + 8u * (sc_first + min(lane, T::SC_CPW - 1u));
+    const uint8_t* sc_src = reinterpret_cast<const uint8_t*>(j.wscale) +
+                            ((size_t)min(sc_col >> 6, j.tiles - 1u) * groups * kTile + (sc_col & 63u)) * 2u;
+    const uint32_t la0 = lds_offset(lds_a), lbits0 = lds_offset(lds_bits), lsc0 = lds_offset(lds_sc);
+    const size_t bit_step = (size_t)kTile * 16u, sc_step = (size_t)kTile * 2u;
+    auto issue_rows = [&](uint32_t g) {
+        const uint32_t gg = min(g, groups - 1u);
+#pragma unroll
+        for (uint32_t i = 0; i < T::A_INS; ++i)
+            dma16_lanes<lane_mask<T::A_LANES>()>(a_src[i] + (size_t)gg * kGroup,
+                                                 la0 + (g & 1u) * T::A_SLOT + (wave * T::A_CHUNKS + i * 64u) * 16u);
+    };
+    auto issue_bits = [&](uint32_t g) {
+        const uint32_t gg = min(g, groups - 1u);
+        dma16_lanes<lane_mask<T::BIT_LANES>()>(bit_src + gg * bit_step,
+                                               lbits0 + (g & 3u) * T::BITS_SLOT + wave * (T::BIT_LANES * 16u));
+    };
+    auto issue_scales = [&](uint32_t g) {
+        const uint32_t gg = min(g, groups - 1u);
+        dma16_lanes<lane_mask<T::SC_CPW>()>(sc_src + gg * sc_step, lsc0 + (g & 3u) * T::SC_SLOT + 16u * sc_first);
+    };
+    constexpr uint32_t UNITS = TN * 4u, UPT = (UNITS + THREADS - 1u) / THREADS;
+    static_assert(UNITS % THREADS == 0, "whole units per thread");
+    auto unpack_read = [&](uint32_t (&w)[UPT], uint32_t g) {
+        const unsigned char* bits = lds_bits + (g & 3u) * T::BITS_SLOT;
+#pragma unroll
+        for (uint32_t i = 0; i < UPT; ++i) {
+            const uint32_t u = i * THREADS + tid;
+            w[i] = *reinterpret_cast<const uint32_t*>(bits + (u >> 2) * 16u + (u & 3u) * 4u);
+        }
+    };
+    auto unpack_lut = [&](uint2 (&e)[UPT][4], const uint32_t (&w)[UPT]) {
+#pragma unroll
+        for (uint32_t i = 0; i < UPT; ++i)
+#pragma unroll
+            for (uint32_t b = 0; b < 4; ++b)
+                e[i][b] = lut[(w[i] >> (8u * b)) & 0xffu];
+    };
+    auto unpack_store = [&](const uint2 (&e)[UPT][4], uint32_t g) {
+        unsigned char* dst = lds_b + (g & 1u) * T::B_SLOT;
+#pragma unroll
+        for (uint32_t i = 0; i < UPT; ++i) {
+            const uint32_t u = i * THREADS + tid, row = u >> 2, part = u & 3u;
+            *reinterpret_cast<uint4*>(dst + swz128(row, 2u * part)) =
+                make_uint4(e[i][0].x, e[i][0].y, e[i][1].x, e[i][1].y);
+            *reinterpret_cast<uint4*>(dst + swz128(row, 2u * part + 1u)) =
+                make_uint4(e[i][2].x, e[i][2].y, e[i][3].x, e[i][3].y);
+        }
+    };
+    const uint32_t arow0 = wm * T::WTM + (lane & 15u), brow0 = wn * T::WTN + (lane & 15u);
+    const uint32_t chunk = lane >> 4;
+    // half h of group g's MFMA operands (one register set, reused by the two halves)
+    auto load_half = [&](v4i (&a)[MS], v4i (&b)[NS], uint32_t g, uint32_t h) {
+        const unsigned char* la = lds_a + (g & 1u) * T::A_SLOT;
+        const unsigned char* lb = lds_b + (g & 1u) * T::B_SLOT;
+#pragma unroll
+        for (int mi = 0; mi < MS; ++mi)
+            a[mi] = *reinterpret_cast<const v4i*>(la + swz128(arow0 + 16u * mi, 4u * h + chunk));
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni)
+            b[ni] = *reinterpret_cast<const v4i*>(lb + swz128(brow0 + 16u * ni, 4u * h + chunk));
+    };
+
+    float acc[MS][NS][4];
+    v4i d[MS][NS];
+    const v4i c_init = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+#pragma unroll
+    for (int mi = 0; mi < MS; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni) {
+            d[mi][ni] = c_init;  // with scale 0 the first epilogue adds +0
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mi][ni][r] = 0.0f;
+        }
+    float sc_prev[NS];
+#pragma unroll
+    for (int ni = 0; ni < NS; ++ni)
+        sc_prev[ni] = 0.0f;
+
+    // prologue: groups 0..3's bits, 0..1's scales, group 0's rows; group 0 unpacked,
+    // group 1's bits in registers
+#pragma unroll
+    for (uint32_t b = 0; b < 4; ++b)
+        issue_bits(b);
+    issue_scales(0);
+    issue_scales(1);
+    issue_rows(0);
+    wait_dma<0>();
+    barrier();
+    uint32_t ubits[UPT];
+    {
+        uint2 e0[UPT][4];
+        unpack_read(ubits, 0);
+        unpack_lut(e0, ubits);
+        unpack_store(e0, 0);
+    }
+    unpack_read(ubits, 1);
+    wait_dma<0>();
+
+    for (uint32_t g = 0; g < groups; ++g) {
+        // this wave's DMAs but the last two have landed (group g's rows among them),
+        // its LDS accesses are done; after the barrier the same holds for every wave
+        wait_dma<2>();
+        barrier();
+        issue_rows(g + 1u);
+        issue_bits(g + 4u);
+        issue_scales(g + 2u);
+        uint2 ex[UPT][4];
+        unpack_lut(ex, ubits);
+        __builtin_amdgcn_sched_barrier(0);
+        unpack_read(ubits, g + 2u);
+        v4i ca[MS], cb[NS];
+        load_half(ca, cb, g, 0);
+        float sc_cur[NS];
+        const uint16_t* scl = reinterpret_cast<const uint16_t*>(lds_sc + (g & 3u) * T::SC_SLOT);
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni)
+            sc_cur[ni] = __half2float(__ushort_as_half(scl[wn * T::WTN + 16u * ni + (lane & 15u)]));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni) {
+            const float sc = sc_prev[ni];
+            const float cneg = sc * -kMagicValue;  // exact
+#pragma unroll
+            for (int mi = 0; mi < MS; ++mi) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc, __int_as_float(d[mi][ni][r]), cneg);
+                d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ca[mi], cb[ni], c_init, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MS * NS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        unpack_store(ex, g + 1u);
+        load_half(ca, cb, g, 1);
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni)
+#pragma unroll
+            for (int mi = 0; mi < MS; ++mi)
+                d[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ca[mi], cb[ni], d[mi][ni], 0, 0, 0);
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni)
+            sc_prev[ni] = sc_cur[ni];
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_dma<0>();
+#pragma unroll
+    for (int ni = 0; ni < NS; ++ni) {
+        const float sc = sc_prev[ni];
+        const float cneg = sc * -kMagicValue;
+#pragma unroll
+        for (int mi = 0; mi < MS; ++mi)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc, __int_as_float(d[mi][ni][r]), cneg);
+    }
+    barrier();
+    float* const so = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (int mi = 0; mi < MS; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                so[(wm * T::WTM + 16u * mi + 4u * (lane >> 4) + r) * T::OUT_STRIDE + wn * T::WTN + 16u * ni +
+                   (lane & 15u)] = acc[mi][ni][r];
+    wait_dma<0>();
+    barrier();
+    const bool vec = ((j.out_stride | (uint64_t)(uintptr_t)j.out) & 15u) == 0;
+    const bool scaled = j.mode == MODE_SUM_SCALED;
+#pragma unroll
+    for (uint32_t c0 = 0; c0 < TM * TN / 4u; c0 += THREADS) {
+        const uint32_t c = c0 + tid, row = c / (TN / 4u), col = 4u * (c % (TN / 4u));
+        const uint32_t m = m0 + row, n = n0 + col;
+        if (m >= j.rows || n >= j.n)
+            continue;
+        float4 v = *reinterpret_cast<const float4*>(so + row * T::OUT_STRIDE + col);
+        if (scaled) {
+            const float s = j.rscale[m];
+            v.x = v.x * s;
+            v.y = v.y * s;
+            v.z = v.z * s;
+            v.w = v.w * s;
+        }
+        float* dst = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride) + n;
+        if (vec && n + 4u <= j.n) {
+            const v4f w = {v.x, v.y, v.z, v.w};
+            __builtin_nontemporal_store(w, reinterpret_cast<v4f*>(dst));
+        } else {
+            dst[0] = v.x;
+            if (n + 1u < j.n)
+                dst[1] = v.y;
+            if (n + 2u < j.n)
+                dst[2] = v.z;
+            if (n + 3u < j.n)
+                dst[3] = v.w;
+        }
+    }
+}
+
+uint32_t gemm_band(const GemmJob& job, uint32_t mtiles);
+
+template <int TM, int TN, int WGM, int WGN>
+hipError_t launch_co(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
+    const uint32_t mtiles = (job.rows + TM - 1u) / TM, ntiles = (job.n + TN - 1u) / TN;
+    launch_kernel((k_gemm_co<TM, TN, WGM, WGN>), dim3(mtiles * ntiles), dim3(64 * WGM * WGN), 0, stream, job, mtiles,
+                  ntiles, gemm_band(job, mtiles), seq, flag);
+    return hipGetLastError();
+}
+
 // k_gemm_ks: F32-accumulating jobs with too few tiles to give every CU a workgroup.
 // Workgroup tile (16*TMS) x (16*TNS); the W waves split K instead of the tile: wave w
 // computes groups w, w+W, w+2W, ... for the whole tile, its operands loaded from
@@ -723,6 +982,11 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
     auto blocks = [&](uint32_t tm, uint32_t tn) {
         return (uint64_t)((job.rows + tm - 1u) / tm) * ((job.n + tn - 1u) / tn);
     };
+#ifndef BNN_GEMM_CO
+#define BNN_GEMM_CO 1  // F32-accumulating jobs with a 128 x 128 tile per CU: two workgroups per CU (k_gemm_co)
+#endif
+    if (BNN_GEMM_CO && job.mode != MODE_DOT_I16 && blocks(128, 128) >= cus)
+        return launch_co<128, 128, 2, 2>(stream, job, seq, flag);
     if (blocks(128, 128) >= cus)
         return launch_bits<128, 128, 2, 4>(stream, job, seq, flag);
     if (blocks(64, 128) >= cus)
