@@ -163,10 +163,9 @@ struct Tiling {
 
 template <int TM, int TN, int WGM, int WGN, bool DOT>
 __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_bits(GemmJob j, uint32_t mtiles, uint32_t ntiles, uint32_t band,
-    uint64_t seq,
-                                                              const uint64_t* __restrict__ flag) {
+                                                              uint64_t seq, const uint64_t* __restrict__ flag) {
     using T = Tiling<TM, TN, WGM, WGN>;
-    constexpr int MS = T::MS, NS = T::NS, WAVES = T::WAVES, THREADS = T::THREADS;
+    constexpr int MS = T::MS, NS = T::NS, THREADS = T::THREADS;
     __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
     if (*flag == seq)
         return;
