@@ -328,33 +328,42 @@ def e2e_leg(pkg, hip, paths=tuple(E2E_PATHS), new=128):
 
 
 def mlp_leg(pkg, hip):
-    """Config 1: bnn-mlp classifier through the engine."""
+    """Config 1: bnn-mlp classifier through the engine, 1000 samples in classify calls of
+    64.  The engine runs a call's samples through each block as one GEMM_F32 job (every
+    row of it is that sample's GEMV_F32); `per_sample` is the reference engine's call
+    pattern (bnn-mlp.c:173-198: one GEMV_F32 per sample and block), through contexts of
+    one sample per call (so it also carries one ctypes classify call per sample)."""
     import tempfile
     eng = pkg.engine.EngineLib()
+    fixture_path = ROOT / "tests" / "golden" / "e2e_bnn_mlp.json"
+    want = json.loads(fixture_path.read_text())["argmax"] if fixture_path.exists() else None
+
+    def run(model, x, batch):
+        ctx = pkg.engine.Context(model, n_batch=batch)
+        ctx.classify(x[:batch])
+        t0 = time.perf_counter()
+        preds = []
+        for s0 in range(0, len(x), batch):
+            preds.extend(ctx.classify(x[s0:s0 + batch]).argmax(axis=1).tolist())
+        dt = time.perf_counter() - t0
+        st = ctx.stats()
+        ctx.free()
+        agree = f"{sum(a == b for a, b in zip(preds, want))}/{len(want)}" if want else None
+        return {"samples_per_s": round(len(x) / dt, 1), "us_per_sample": round(dt / len(x) * 1e6, 1),
+                "device_calls_per_sample": round(st["device_calls"] / len(x), 4),
+                "backend_share": round((st["transfer_ns"] + st["execute_ns"]) / st["total_ns"], 4),
+                "argmax_agreement": agree}
+
     with tempfile.TemporaryDirectory() as d:
         path = Path(d) / "mlp.gguf"
         pkg.gguf.bnn_mlp_random(path)
         x = pkg.gguf.bnn_mlp_inputs(1000)
         with pkg.Device(hip, 0) as dev:
             model = pkg.engine.Model(eng, dev, path)
-            ctx = pkg.engine.Context(model, n_batch=64)
-            ctx.classify(x[:64])
-            t0 = time.perf_counter()
-            preds = []
-            for s0 in range(0, 1000, 64):
-                preds.extend(ctx.classify(x[s0:s0 + 64]).argmax(axis=1).tolist())
-            dt = time.perf_counter() - t0
-            st = ctx.stats()
-            ctx.free()
+            out = run(model, x, 64)
+            out["per_sample"] = run(model, x, 1)
             model.free()
-    fixture_path = ROOT / "tests" / "golden" / "e2e_bnn_mlp.json"
-    agree = None
-    if fixture_path.exists():
-        want = json.loads(fixture_path.read_text())["argmax"]
-        agree = f"{sum(a == b for a, b in zip(preds, want))}/{len(want)}"
-    return {"samples_per_s": round(1000 / dt, 1), "us_per_sample": round(dt / 1000 * 1e6, 1),
-            "gemv_calls_per_sample": 3, "backend_share": round((st["transfer_ns"] + st["execute_ns"]) / st["total_ns"], 4),
-            "argmax_agreement": agree}
+    return out
 
 
 def main():

@@ -111,8 +111,8 @@ bnne_context::~bnne_context() {
 }
 
 void bnne_context::allocate_staging() {
-    const size_t in_bytes = (size_t)(model->widest_in ? model->widest_in : 1u) * sizeof(float);
-    const size_t out_bytes = (size_t)(model->widest_shard ? model->widest_shard : 1u) * sizeof(float);
+    const size_t in_bytes = (size_t)stage_rows * (model->widest_in ? model->widest_in : 1u) * sizeof(float);
+    const size_t out_bytes = (size_t)stage_rows * (model->widest_shard ? model->widest_shard : 1u) * sizeof(float);
     bnne::require(BNN_BufferAlloc(model->device, in_bytes, &stage_in), "BNN_BufferAlloc (layer input)");
     bnne::require(BNN_BufferAlloc(model->device, out_bytes, &stage_out), "BNN_BufferAlloc (layer output)");
 }

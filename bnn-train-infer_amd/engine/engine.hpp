@@ -175,7 +175,10 @@ namespace bnne {
 // A linear layer y = W x resident on the accelerator as shards of at most the device's
 // max_out_features outputs.  apply() is the accelerator's call pattern: the input row
 // written once to the context's input buffer, then per shard one synchronous
-// BNN_Execute(GEMV_F32, rows = 1) and one BNN_BufferRead of its outputs.
+// BNN_Execute(GEMV_F32, rows = 1) and one BNN_BufferRead of its outputs.  apply_rows()
+// takes up to the context's stage_rows rows at once: one write of all of them, then per
+// shard one GEMM_F32 job over every row (the API computes each row of a GEMM_F32 exactly
+// as a GEMV_F32 of that row) and one read.
 class SignLinear {
 public:
     SignLinear() = default;
@@ -185,6 +188,8 @@ public:
 
     void upload(bnne_model& model, const SignWeights& w);
     void apply(bnne_context& ctx, const float* x, float* y) const;
+    // x: rows x in() floats, y: rows x out() floats, rows <= ctx.stage_rows
+    void apply_rows(bnne_context& ctx, const float* x, uint32_t rows, float* y) const;
 
     uint32_t in() const { return in_; }
     uint32_t out() const { return out_; }
@@ -246,8 +251,9 @@ struct bnne_context {
     BNNE_ContextParams params;
     uint32_t pos = 0;
     BNNE_Stats stats{};
-    BNN_Buffer stage_in = nullptr;   // widest_in floats: the input row of SignLinear::apply
-    BNN_Buffer stage_out = nullptr;  // widest_shard floats: one shard's outputs
+    uint32_t stage_rows = 1;         // rows the staging buffers hold (set before allocate_staging)
+    BNN_Buffer stage_in = nullptr;   // stage_rows x widest_in floats: the input rows of SignLinear
+    BNN_Buffer stage_out = nullptr;  // stage_rows x widest_shard floats: one shard's outputs
 
     bnne_context(bnne_model& m, const BNNE_ContextParams& p) : model(&m), params(p) {}
     virtual ~bnne_context();

@@ -35,15 +35,23 @@ public:
     uint32_t widest = 0;  // the widest activation row (input or block output)
 };
 
+// Samples run through the blocks in chunks of up to kChunkRows: one GEMM_F32 job per
+// block and chunk (each row of it is that sample's GEMV_F32), so a classify call of n
+// samples makes ceil(n / kChunkRows) accelerator calls per block instead of n.
+constexpr uint32_t kChunkRows = 256;
+
 class MlpContext final : public bnne_context {
 public:
-    MlpContext(MlpModel& net, const BNNE_ContextParams& p)
-        : bnne_context(net, p), net_(net), rows_{std::vector<float>(net.widest), std::vector<float>(net.widest)} {}
+    MlpContext(MlpModel& net, const BNNE_ContextParams& p) : bnne_context(net, p), net_(net) {
+        stage_rows = p.n_batch < kChunkRows ? (p.n_batch ? p.n_batch : 1u) : kChunkRows;
+        for (std::vector<float>& r : rows_)
+            r.resize((size_t)stage_rows * net.widest);
+    }
     void classify(const float* input, uint32_t n, float* logits) override;
 
 private:
     MlpModel& net_;
-    std::vector<float> rows_[2];  // the hidden activations alternate between these
+    std::vector<float> rows_[2];  // the hidden activations of a chunk alternate between these
 };
 
 std::string block_key(uint32_t i, const char* what) {
@@ -103,16 +111,21 @@ bnne_context* MlpModel::new_context(const BNNE_ContextParams& p) { return new Ml
 
 void MlpContext::classify(const float* input, uint32_t n, float* logits) {
     const size_t count = net_.blocks.size();
-    for (uint32_t s = 0; s < n; ++s) {
-        const float* x = input + (size_t)s * net_.inputs;
+    for (uint32_t s0 = 0; s0 < n; s0 += stage_rows) {
+        const uint32_t rows = n - s0 < stage_rows ? n - s0 : stage_rows;
+        const float* x = input + (size_t)s0 * net_.inputs;
         for (size_t i = 0; i < count; ++i) {
             const MlpBlock& b = *net_.blocks[i];
-            float* y = i + 1 == count ? logits + (size_t)s * net_.classes : rows_[i % 2].data();
-            b.weight.apply(*this, x, y);
-            for (uint32_t o = 0; o < b.weight.out(); ++o) {
-                const float scaled = b.post_scale[o] * y[o];
-                const float v = scaled + b.post_bias[o];
-                y[o] = b.relu && v < 0.0f ? 0.0f : v;
+            const uint32_t out = b.weight.out();
+            float* y = i + 1 == count ? logits + (size_t)s0 * net_.classes : rows_[i % 2].data();
+            b.weight.apply_rows(*this, x, rows, y);
+            for (uint32_t r = 0; r < rows; ++r) {
+                float* yr = y + (size_t)r * out;
+                for (uint32_t o = 0; o < out; ++o) {
+                    const float scaled = b.post_scale[o] * yr[o];
+                    const float v = scaled + b.post_bias[o];
+                    yr[o] = b.relu && v < 0.0f ? 0.0f : v;
+                }
             }
             x = y;
         }

@@ -11,10 +11,12 @@
 // that many outputs (linear.c:104-125), each its own BNN_Matrix.  apply() is the call
 // sequence of the reference engine's linear layer (linear.c:161-216) with the same
 // statistics: the input row written once, then per shard one BNN_Execute of
-// GEMV_F32 at rows = 1 and one read of its outputs.
+// GEMV_F32 at rows = 1 and one read of its outputs.  apply_rows() is the same sequence
+// for a block of rows, with GEMM_F32 over all of them in place of one GEMV_F32 per row.
 #include "engine.hpp"
 
 #include <cstring>
+#include <vector>
 
 namespace bnne {
 
@@ -112,6 +114,54 @@ void SignLinear::apply(bnne_context& ctx, const float* x, float* y) const {
         require(st, "BNN_BufferRead");
     }
     const uint64_t macs = (uint64_t)in_ * out_;
+    ctx.count(&BNNE_Stats::logical_macs, macs);
+    ctx.count(&BNNE_Stats::executed_macs, macs);
+}
+
+void SignLinear::apply_rows(bnne_context& ctx, const float* x, uint32_t rows, float* y) const {
+    if (rows > ctx.stage_rows)
+        raise(BNNE_EINVAL, "%u rows at once; the context stages %u", rows, ctx.stage_rows);
+    if (rows <= 1 || !(ctx.model->caps.supported_ops & BNN_CAP_GEMM_F32)) {
+        for (uint32_t r = 0; r < rows; ++r)
+            apply(ctx, x + (size_t)r * in_, y + (size_t)r * out_);
+        return;
+    }
+    const size_t in_bytes = (size_t)rows * in_ * sizeof(float);
+    {
+        Span busy(ctx.counter(&BNNE_Stats::transfer_ns));
+        const BNN_Status st = BNN_BufferWrite(ctx.stage_in, 0, x, in_bytes);
+        ctx.count(&BNNE_Stats::bytes_written, in_bytes);
+        require(st, "BNN_BufferWrite");
+    }
+    // a layer of one shard reads its rows straight into y; a sharded one reads each
+    // shard's block of rows and places it at the shard's columns
+    std::vector<float> block(shards_.size() > 1 ? (size_t)rows * shards_.front().count : 0);
+    for (const Shard& s : shards_) {
+        BNN_Job job{};
+        job.operation = BNN_OP_GEMM_F32;
+        job.matrix = s.matrix;
+        job.input = BNN_BufferView{ctx.stage_in, BNN_TYPE_F32, 0, 0};
+        job.output = BNN_BufferView{ctx.stage_out, BNN_TYPE_F32, 0, 0};
+        job.rows = rows;
+        {
+            Span busy(ctx.counter(&BNNE_Stats::execute_ns));
+            require(BNN_Execute(ctx.model->device, &job), "BNN_Execute");
+        }
+        const size_t out_bytes = (size_t)rows * s.count * sizeof(float);
+        float* dst = shards_.size() > 1 ? block.data() : y;
+        {
+            Span busy(ctx.counter(&BNNE_Stats::transfer_ns));
+            const BNN_Status st = BNN_BufferRead(ctx.stage_out, 0, dst, out_bytes);
+            ctx.count(&BNNE_Stats::device_calls, 1);
+            ctx.count(&BNNE_Stats::bytes_read, out_bytes);
+            require(st, "BNN_BufferRead");
+        }
+        if (shards_.size() > 1)
+            for (uint32_t r = 0; r < rows; ++r)
+                std::memcpy(y + (size_t)r * out_ + s.first, block.data() + (size_t)r * s.count,
+                            s.count * sizeof(float));
+    }
+    const uint64_t macs = (uint64_t)rows * in_ * out_;
     ctx.count(&BNNE_Stats::logical_macs, macs);
     ctx.count(&BNNE_Stats::executed_macs, macs);
 }

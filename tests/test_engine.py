@@ -239,6 +239,36 @@ def test_engine_host_step_on_cpu_oracle(pkg, tmp_path, exe):
     check_mlp_output(out.stdout)
 
 
+def _classify(exe, model, inp, samples, batch, env=None):
+    out = subprocess.run([str(exe), "classify", str(model), str(inp), str(samples), str(batch)],
+                         capture_output=True, text=True, timeout=300, env=env)
+    assert out.returncode == 0, out.stderr[-2000:]
+    return out.stdout
+
+
+def write_wide_mlp(pkg, tmp_path, samples):
+    """One block of 256 -> 8320 outputs: two accelerator shards (8192 + 128 outputs)."""
+    model, inp = tmp_path / "wide.gguf", tmp_path / "wide.f32"
+    pkg.gguf.bnn_mlp_random(model, dims=(256, 8320), seed=5, input_pixels=200)
+    pkg.gguf.bnn_mlp_inputs(samples, features=256, pixels=200, seed=5).tofile(inp)
+    return model, inp
+
+
+@pytest.mark.parametrize("exe", [ENGINE_RUN_CPU, ENGINE_RUN_ASAN], ids=["plain", "sanitized"])
+def test_engine_classify_rows_match_per_sample_on_cpu_oracle(pkg, tmp_path, exe):
+    """A classify call's samples go through each block as one GEMM_F32 job per shard, in
+    chunks of at most 256 rows; the logits are bit-identical to one sample per call (one
+    GEMV_F32 per sample, the reference's pattern), including a layer split into two
+    shards and a last chunk of 44 rows (300 samples per call)."""
+    import os
+    env = dict(os.environ, **ASAN_ENV)
+    model, inp = write_wide_mlp(pkg, tmp_path, 300)
+    rows = _classify(exe, model, inp, 300, 300, env)
+    single = _classify(exe, model, inp, 300, 1, env)
+    assert len(rows.splitlines()) == 300
+    assert rows == single
+
+
 def _run_sanitized(args, env):
     out = subprocess.run([str(ENGINE_RUN_ASAN), *args], capture_output=True, text=True, timeout=60, env=env)
     report = "AddressSanitizer" in out.stderr or "runtime error" in out.stderr or "LeakSanitizer" in out.stderr
@@ -375,6 +405,15 @@ def test_engine_bnn_mlp_bit_exact(pkg, tmp_path, runner):
     out = subprocess.run([str(exe), "classify", str(model), str(inp), str(MLP["samples"]), str(MLP["batch"])],
                          capture_output=True, text=True, timeout=120, check=True).stdout
     check_mlp_output(out)
+
+
+@pytest.mark.gpu
+def test_engine_classify_rows_match_per_sample(pkg, tmp_path):
+    """On the HIP backend: the multi-row classify path (GEMM_F32 on the matrix cores,
+    two shards, chunks of 256 + 44 rows) equals one GEMV_F32 per sample, bit for bit."""
+    model, inp = write_wide_mlp(pkg, tmp_path, 300)
+    print("engine classify 256->8320, 300 samples, rows vs per sample", flush=True)
+    assert _classify(ENGINE_RUN_OWN, model, inp, 300, 300) == _classify(ENGINE_RUN_OWN, model, inp, 300, 1)
 
 
 @pytest.mark.gpu
