@@ -34,6 +34,24 @@ namespace {
 
 __constant__ uint64_t kFusedExp2Table[32] = BNNE_EXP2_TABLE;
 
+// The expf table into LDS for per-lane lookups (called by one whole wave): scalar loads,
+// whose wait (lgkmcnt) leaves the wave's vector loads in flight -- a vector load of the
+// table would complete in order behind the row operands and the weights already requested
+template <int I>
+__device__ __forceinline__ void fused_exp_table_fill_lanes(uint32_t& lo, uint32_t& hi) {
+    const uint64_t e = kFusedExp2Table[I];  // uniform address: a scalar load
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(lo) : "s"((uint32_t)e), "n"(I));
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(hi) : "s"((uint32_t)(e >> 32)), "n"(I));
+    if constexpr (I < 31)
+        fused_exp_table_fill_lanes<I + 1>(lo, hi);
+}
+__device__ __forceinline__ void fused_exp_table_fill(uint64_t* tab, uint32_t lane) {
+    uint32_t lo = 0, hi = 0;
+    fused_exp_table_fill_lanes<0>(lo, hi);
+    if (lane < 32u)
+        tab[lane] = (uint64_t)hi << 32 | lo;
+}
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 fload(const uint4* p) {
     const u32x4 v = *(const __attribute__((address_space(1))) u32x4*)p;
@@ -360,8 +378,10 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     TileRegs<GPW> cur, nxt;
     LaneRow lr = lane_row(job, job2, paired, tile - job.first_tile, G, lane);
     load_tile<GPW>(lr, G, wave, cur);
-    if (paired && tid < 32u)  // the expf table of the SiLU (read after the first product barrier)
-        exp_tab[tid] = kFusedExp2Table[tid];
+    // the expf table of a SiLU (the post-operation's, read after the first product
+    // barrier, or the pre-operation's, published by the barrier below), by the last wave
+    if ((paired || fa.kind == PRE_SILU_MUL) && wave == kFusedWaves - 1u)
+        fused_exp_table_fill(exp_tab, lane);
 
     // 2. the input row
     if (fa.kind == PRE_RMSNORM) {
@@ -469,10 +489,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
         for (int i = 0; i < EPT; ++i)
             xv[i] = xv[i] / rms * gv[i];
     } else if (fa.kind == PRE_SILU_MUL) {
-        // the expf table in LDS: its lookups are per-lane gathers
-        if (tid < 32u)
-            exp_tab[tid] = kFusedExp2Table[tid];
-        lds_barrier();
+        lds_barrier();  // the expf table in LDS (its lookups are per-lane gathers)
 #pragma unroll
         for (int i = 0; i < EPT; ++i) {
             const float silu = xv[i] / (1.0f + bnne_expf_libc(-xv[i], exp_tab));

@@ -34,6 +34,24 @@ __constant__ uint64_t kExp2Table[32] = BNNE_EXP2_TABLE;
 
 __device__ __forceinline__ float expf_libc(float x) { return bnne_expf_libc(x, kExp2Table); }
 
+// The table into LDS for per-lane lookups (called by one whole wave): scalar loads, whose
+// wait (lgkmcnt) leaves the wave's vector loads in flight -- a vector load of the table
+// would complete in order behind every key row and V row the wave has requested
+template <int I>
+__device__ __forceinline__ void exp_table_fill_lanes(uint32_t& lo, uint32_t& hi) {
+    const uint64_t e = kExp2Table[I];  // uniform address: a scalar load
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(lo) : "s"((uint32_t)e), "n"(I));
+    asm("v_writelane_b32 %0, %1, %2" : "+v"(hi) : "s"((uint32_t)(e >> 32)), "n"(I));
+    if constexpr (I < 31)
+        exp_table_fill_lanes<I + 1>(lo, hi);
+}
+__device__ __forceinline__ void exp_table_fill(uint64_t* tab, uint32_t lane) {
+    uint32_t lo = 0, hi = 0;
+    exp_table_fill_lanes<0>(lo, hi);
+    if (lane < 32u)
+        tab[lane] = (uint64_t)hi << 32 | lo;
+}
+
 // Sequential sums with latency hiding: the values of a chunk are loaded into
 // registers first (independent loads, issued back to back), then added one after
 // another in index order -- the same roundings as a plain loop.
@@ -484,13 +502,16 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
 
 // Attention of one query head in a single launch, for contexts of fewer than
 // kAttnOneMax positions (pos < kAttnOneMax): workgroup h, four waves, the same
-// operations in the same order as k_attn_scores + k_attn_pv.  Loads first, oldest
-// needed first (wave 0's head vectors, each thread's key row, then the V rows of
-// positions below pos into LDS by DMA); then
+// operations in the same order as k_attn_scores + k_attn_pv.  Position t belongs to
+// thread (t + 64) % 256: waves 1..3 hold positions 0..191 and wave 0 the rest, and wave 0
+// requests its key rows only after its norms (loads complete in order: a wait for the
+// head vectors would also wait for every row requested after them).  Then
 //   wave 0: the head norms and RoPE of q and of the kv head's new key (the cache row
-//   at pos stored by the kv head's first query head);
-//   thread t <= pos: the score of position t (in-order dot over head_dim; position pos
-//   from the new key itself);
+//   at pos stored by the kv head's first query head), while waves 1..3 load their
+//   key rows;
+//   the thread of position t <= pos: its score (in-order dot over head_dim; position
+//   pos from the new key itself); then waves 1..3 request the V rows of positions
+//   below pos into LDS by DMA, which arrive during
 //   wave 0: the maximum, expf, the in-order sum and the probabilities;
 //   thread i < head_dim: value[i] = sum over t in order of p[t] * V[t][i], row pos from
 //   the new value itself -- no workgroup reads a cache row that another is writing.
@@ -520,7 +541,7 @@ __global__ __launch_bounds__(256) void k_attn_one(
     float* p = reinterpret_cast<float*>(p4);
     const float* vs = reinterpret_cast<const float*>(vs4);
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t h = blockIdx.x, t = tid;
+    const uint32_t h = blockIdx.x, t = (tid + 192u) & 255u;  // this thread's position
     const size_t head_off = (size_t)(h / kv_mul) * HD;
 
     float qa = 0.0f, qb = 0.0f, ka = 0.0f, kb = 0.0f, qga = 0.0f, qgb = 0.0f, kga = 0.0f, kgb = 0.0f, c = 0.0f, s = 0.0f;
@@ -530,25 +551,20 @@ __global__ __launch_bounds__(256) void k_attn_one(
         qga = q_gain[lane], qgb = q_gain[lane + half], kga = k_gain[lane], kgb = k_gain[lane + half];
         c = cosv[lane], s = sinv[lane];
     }
+    // this thread's key row (past position 192, wave 0 requests it after its norms)
     float4 key[hd4];
-    if (t < pos) {
-        const float4* row = reinterpret_cast<const float4*>(kc + (size_t)t * kv_dim + head_off);
+    const auto load_key = [&] {
+        if (t < pos) {
+            const float4* row = reinterpret_cast<const float4*>(kc + (size_t)t * kv_dim + head_off);
 #pragma unroll
-        for (uint32_t i = 0; i < hd4; ++i)
-            key[i] = row[i];
-    }
-    // V rows 0..pos-1: 16-byte piece ci = 32 * row + part at byte 16 * ci of vs4;
-    // wave w issues pieces w * 64 + 256 * i + lane (pieces past the last row load row
-    // pos - 1 again into unused space)
-    {
-        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
-        for (uint32_t c0 = wave * 64u; c0 < 32u * pos; c0 += 256u) {
-            const uint32_t ci = c0 + lane, row = min(ci >> 5, pos - 1u);
-            dma16(vc + (size_t)row * kv_dim + head_off + 4u * (ci & 31u), base + 16u * c0);
+            for (uint32_t i = 0; i < hd4; ++i)
+                key[i] = row[i];
         }
-    }
-    if (tid < 32u)
-        exp_tab[tid] = kExp2Table[tid];
+    };
+    if (wave != 0)
+        load_key();
+    if (wave == 1)  // not on the norms' path
+        exp_table_fill(exp_tab, lane);
     if (wave == 0) {
         // head norms: both in-order sums over head_dim, interleaved, in every lane
         float* sq_q = reinterpret_cast<float*>(sq4[0]);
@@ -596,6 +612,7 @@ __global__ __launch_bounds__(256) void k_attn_one(
         }
         if (lane == 0)
             failed = bad;
+        load_key();
     }
     block_lds_barrier();
     if (failed) {
@@ -624,6 +641,16 @@ __global__ __launch_bounds__(256) void k_attn_one(
             set_error_first(err, code_base + 3 + 2 * (int)h);
         p[t] = score;
     }
+    // V rows 0..pos-1: 16-byte piece ci = 32 * row + part at byte 16 * ci of vs4; wave
+    // w > 0 issues pieces (w - 1) * 64 + 192 * i + lane (pieces past the last row load
+    // row pos - 1 again into unused space)
+    if (wave != 0) {
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
+        for (uint32_t c0 = (wave - 1u) * 64u; c0 < 32u * pos; c0 += 192u) {
+            const uint32_t ci = c0 + lane, row = min(ci >> 5, pos - 1u);
+            dma16(vc + (size_t)row * kv_dim + head_off + 4u * (ci & 31u), base + 16u * c0);
+        }
+    }
     block_lds_barrier();
 
     // the maximum (order-free: finite or flagged), expf(score - max), their sum in
@@ -649,21 +676,37 @@ __global__ __launch_bounds__(256) void k_attn_one(
     __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this wave's V rows are in LDS
     block_lds_barrier();                 // ... and every wave's, with the probabilities
 
-    // value[i] in position order, 16 rows' LDS reads issued before their additions
+    // value[i] in position order: the LDS reads of the next 16 rows are issued before
+    // the additions of the current 16
     if (tid < HD) {
         const float* col = vs + tid;
         float acc = 0.0f;
-        uint32_t u = 0;
-        for (; u + 16u <= pos; u += 16u) {
-            float vv[16], pp[16];
+        float vv[2][16], pp[2][16];
+        const auto fetch = [&](float(&v)[16], float(&pr)[16], uint32_t u) {
 #pragma unroll
             for (uint32_t j = 0; j < 16; ++j) {
-                vv[j] = col[(u + j) * HD];
-                pp[j] = p[u + j];
+                v[j] = col[(u + j) * HD];
+                pr[j] = p[u + j];
             }
+        };
+        const auto add = [&](const float(&v)[16], const float(&pr)[16]) {
 #pragma unroll
             for (uint32_t j = 0; j < 16; ++j)
-                acc = acc + pp[j] * vv[j];
+                acc = acc + pr[j] * v[j];
+        };
+        uint32_t u = 0;
+        if (pos >= 16u)
+            fetch(vv[0], pp[0], 0);
+        for (; u + 32u <= pos; u += 32u) {
+            fetch(vv[1], pp[1], u + 16u);
+            add(vv[0], pp[0]);
+            if (u + 48u <= pos)
+                fetch(vv[0], pp[0], u + 32u);
+            add(vv[1], pp[1]);
+        }
+        if (u + 16u <= pos) {
+            add(vv[0], pp[0]);
+            u += 16u;
         }
         for (; u < pos; ++u)
             acc = acc + p[u] * col[u * HD];
