@@ -852,8 +852,10 @@ BNN_Status run_single_row(BNN_Device device, const BNN_Job* job, const JobPlan& 
     const bool mirror =
         allow_mirror && !p.dot_out && !job->output.buffer->exposed && ensure_mirror(device) == BNN_OK;
     fa.mirror = mirror ? device->mirror : nullptr;
+    // one workgroup per tile up to one per CU (a CU holds one 1024-thread workgroup of
+    // the kernel at a time); beyond that workgroups loop over tiles
     const uint32_t cus = device->cu_count ? device->cu_count : 256u;
-    const uint32_t grid = p.m->tiles < 2u * cus ? p.m->tiles : 2u * cus;
+    const uint32_t grid = p.m->tiles < cus ? p.m->tiles : cus;
     const uint64_t seq = ++device->seq;
     fa.done_count = device->flag_dev + 1;
     fa.done_target = device->done_base + grid;
@@ -1409,6 +1411,18 @@ EXPORT BNN_Status BNNX_BatchCreateFusedPost(BNN_Device device, const BNN_Job* jo
             b->mem = static_cast<unsigned char*>(mem);
         }
     }
+    // the job of a tile in one step when the jobs (pairs) start at multiples of a power of two
+    uint32_t walk_shift = 32;
+    if (st == BNN_OK) {
+        const uint32_t nwalk = paired ? count / 2u : count;
+        for (uint32_t sh = 0; sh < 31u && walk_shift == 32u; ++sh) {
+            bool fits = true;
+            for (uint32_t i = 0; fits && i < nwalk; ++i)
+                fits = (uint64_t)table[i].first_tile == ((uint64_t)i << sh);
+            if (fits)
+                walk_shift = sh;
+        }
+    }
     free(table);
     if (st != BNN_OK) {
         free(b);
@@ -1419,10 +1433,11 @@ EXPORT BNN_Status BNNX_BatchCreateFusedPost(BNN_Device device, const BNN_Job* jo
     b->needs_nearest = true;
     b->fused = true;
     b->fused_tiles = tiles;
-    // one workgroup per tile up to two per CU; beyond that workgroups loop over tiles
-    // (each produces the row once)
+    // one workgroup per tile up to one per CU (a CU holds one 1024-thread workgroup of the
+    // kernel at a time: a second one per CU would start only as the first ends); beyond
+    // that workgroups loop over tiles (each produces the row once)
     const uint32_t cus = device->cu_count ? device->cu_count : 256u;
-    b->fused_grid = tiles < 2u * cus ? tiles : 2u * cus;
+    b->fused_grid = tiles < cus ? tiles : cus;
     FusedArgs& fa = b->fused_args;
     fa.jobs = reinterpret_cast<const FusedJob*>(b->mem);
     fa.njobs = count;
@@ -1438,6 +1453,7 @@ EXPORT BNN_Status BNNX_BatchCreateFusedPost(BNN_Device device, const BNN_Job* jo
     fa.err_code = pre->err_code;
     fa.post = paired ? POST_SILU_MUL : POST_NONE;
     fa.post_out = paired ? post->out : nullptr;
+    fa.walk_shift = walk_shift;
     device->live_batches++;
     *out_batch = b;
     return BNN_OK;

@@ -14,7 +14,8 @@
 //      bit planes and group sums), each wave the groups of its own dots;
 //   4. per tile computes D per group (bit-plane dots), the rounded products
 //      F32(scale)*D, and adds them in group order (one lane per feature), times
-//      the row scale, with the next tile's weights already loading.
+//      the row scale, with the next tiles' weights already loading (a register ring
+//      of three tiles for K <= 2048, two above).
 // Every workgroup produces the same row from the same inputs, so all of them take
 // the same decisions; workgroup 0 alone stores the pre-operation's residual sum.
 // With the post-operation SILU_MUL the tiles are half-tiles of job pairs (32 features
@@ -309,7 +310,9 @@ __device__ __forceinline__ void load_tile(const LaneRow& lr, uint32_t G, uint32_
 // next tile's weights loading while the current one is computed.
 // SINGLE: one job in the kernel arguments (BNN_Execute): its row may be int8, its output
 // DOT_GROUPS' D or mirrored into host memory.  Batches compile without those branches.
-template <int GPW, int EPT, bool PAIRED, bool SINGLE>
+// RING: tiles of weights in flight per workgroup -- 1 when every workgroup has one tile
+// (no prefetch), 2 or 3 when workgroups walk several tiles.
+template <int GPW, int EPT, bool PAIRED, bool SINGLE, int RING>
 __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_total, uint64_t seq, uint64_t* flag,
                                            uint64_t* host_status) {
     static_assert(EPT == 2 * GPW, "a wave quantises exactly the groups of its dots");
@@ -346,9 +349,16 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     const JobTable<SINGLE> jobs{fa.jobs, fa.single};
     constexpr bool paired = PAIRED;  // fa.post == POST_SILU_MUL
     const uint32_t nwalk = paired ? fa.njobs / 2u : fa.njobs, pair_step = paired ? nwalk : 0u;
-    uint32_t tile = blockIdx.x, ji = 0;
-    while (ji + 1u < nwalk && jobs.first_tile(ji + 1u) <= tile)
-        ++ji;
+    // the job (or pair) of tile t: first tiles at multiples of 2^walk_shift give it in one
+    // step, else a walk from a job at or before it
+    const auto job_of = [&](uint32_t t, uint32_t from) -> uint32_t {
+        if (fa.walk_shift < 32u)
+            return min(t >> fa.walk_shift, nwalk - 1u);
+        while (from + 1u < nwalk && jobs.first_tile(from + 1u) <= t)
+            ++from;
+        return from;
+    };
+    uint32_t tile = blockIdx.x, ji = job_of(tile, 0);
     FusedJob job = jobs[ji], job2 = jobs[ji + pair_step];
     const float* src_a = fa.kind == PRE_ROW ? fa.row : fa.a;
     const bool int_row = SINGLE && fa.kind == PRE_ROW_I8;
@@ -375,9 +385,29 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
         for (int i = 0; i < EPT; ++i)
             gv[i] = fload(fa.gain + min(elem(i), K - 1u));
     }
-    TileRegs<GPW> cur, nxt;
+    // a ring of RING tiles' weights in flight: a workgroup that walks several tiles (the
+    // lm_head's 2370 over one workgroup per CU) would otherwise wait one memory latency per tile
+    constexpr int kRing = RING;
+    TileRegs<GPW> ring[kRing];
     LaneRow lr = lane_row(job, job2, paired, tile - job.first_tile, G, lane);
-    load_tile<GPW>(lr, G, wave, cur);
+    load_tile<GPW>(lr, G, wave, ring[0]);
+    // the prefetch cursor: the last tile whose weights were requested, and its job.  Past
+    // the workgroup's last tile the cursor's tile is loaded again (an L2 hit, never used):
+    // with the same number of loads on every path the compiler's wait for a slot leaves
+    // the later slots' loads in flight (a skipped load would make it wait for all)
+    uint32_t pf_tile = tile, pf_ji = ji;
+    const auto prefetch = [&](TileRegs<GPW>& r) {
+        const uint32_t t = pf_tile + gridDim.x;
+        if (t < tiles_total) {
+            pf_tile = t;
+            pf_ji = job_of(t, pf_ji);
+        }
+        const FusedJob pj = jobs[pf_ji], pj2 = jobs[pf_ji + pair_step];
+        load_tile<GPW>(lane_row(pj, pj2, paired, pf_tile - pj.first_tile, G, lane), G, wave, r);
+    };
+#pragma unroll
+    for (int r = 1; r < kRing; ++r)
+        prefetch(ring[r]);
     // the expf table of a SiLU (the post-operation's, read after the first product
     // barrier, or the pre-operation's, published by the barrier below), by the last wave
     if ((paired || fa.kind == PRE_SILU_MUL) && wave == kFusedWaves - 1u)
@@ -572,17 +602,9 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     // and applies the row scale.  One barrier per tile: a buffer is rewritten only
     // two tiles later, after wave 0 has passed the barrier that follows its sums.
     uint32_t buf = 0;
-    for (;;) {
-        const uint32_t next = tile + gridDim.x;
-        uint32_t nji = ji;
-        LaneRow nlr = lr;
-        if (next < tiles_total) {
-            while (nji + 1u < nwalk && jobs.first_tile(nji + 1u) <= next)
-                ++nji;
-            const FusedJob nj = jobs[nji], nj2 = jobs[nji + pair_step];
-            nlr = lane_row(nj, nj2, paired, next - nj.first_tile, G, lane);
-            load_tile<GPW>(nlr, G, wave, nxt);
-        }
+    // one tile: its dots from ring slot `cur`, the slot refilled kRing tiles ahead (with a
+    // ring), the in-order sums, then (`more`: another tile follows) the cursor on the next tile
+    const auto step = [&](TileRegs<GPW>& cur, bool more) {
         float* prod = scratch + buf * (kFusedMaxGroups * 64u);
 #pragma unroll
         for (int i = 0; i < GPW; ++i) {
@@ -599,6 +621,8 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
                                                   : __half2float(__ushort_as_half((uint16_t)cur.s[i])) * (float)d;
             }
         }
+        if constexpr (kRing > 1)
+            prefetch(cur);
         lds_barrier();
         if (wave == 0 && dot_out) {
             // int16 D[n][g]: a lane's groups are contiguous, 16-byte stores of 8 when aligned
@@ -649,22 +673,47 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
                     fstore(fa.post_out + job.post_off + n, acc / (1.0f + bnne_expf_libc(-acc, exp_tab)) * second);
             }
         }
-        if (next >= tiles_total)
-            break;
-        tile = next;
-        ji = nji;
-        job = jobs[ji];
-        job2 = jobs[ji + pair_step];
-        lr = nlr;
-        cur = nxt;
-        buf ^= 1u;
+        if (more) {
+            tile += gridDim.x;
+            ji = job_of(tile, ji);
+            job = jobs[ji];
+            job2 = jobs[ji + pair_step];
+            lr = lane_row(job, job2, paired, tile - job.first_tile, G, lane);
+            buf ^= 1u;
+        }
+    };
+    static_assert(kRing >= 1 && kRing <= 3, "ring slots are named statically");
+    if constexpr (kRing == 1) {
+        // one tile per workgroup (the host's choice); more would each load their own
+        for (;;) {
+            const bool more = tile + gridDim.x < tiles_total;
+            step(ring[0], more);
+            if (!more)
+                break;
+            load_tile<GPW>(lr, G, wave, ring[0]);
+        }
+    } else {
+        // whole rounds of the ring, then the rest: the loop has one exit, so the compiler's
+        // waits see the ring's loads in flight on every path into the loop
+        const uint32_t mine = (tiles_total - blockIdx.x + gridDim.x - 1u) / gridDim.x;  // grid <= tiles
+        uint32_t done = 0;
+        for (; done + kRing <= mine; done += kRing) {
+            step(ring[0], true);
+            step(ring[1], kRing > 2 || done + 2u < mine);
+            if constexpr (kRing == 3)
+                step(ring[kRing - 1], done + 3u < mine);
+        }
+        if (done < mine)
+            step(ring[0], done + 1u < mine);
+        if (done + 1u < mine)
+            step(ring[1], false);
     }
 }
 
-template <int GPW, int EPT, bool PAIRED, bool SINGLE>
+template <int GPW, int EPT, bool PAIRED, bool SINGLE, int RING>
 __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t tiles_total, uint64_t seq,
                                                          uint64_t* flag, uint64_t* host_status) {
-    fused_body<GPW, EPT, PAIRED, SINGLE>(fa, tiles_total, seq, flag, host_status);
+    fused_body<GPW, EPT, PAIRED, SINGLE, RING>(fa, tiles_total, seq, flag, host_status);
     // Completion signal of a single job, so that the host need not wait for the end of the
     // kernel: in this form every global store (outputs, host mirror, error words) comes from
     // wave 0, which makes them visible system-wide before its workgroup counts itself; the
@@ -682,28 +731,38 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
 
 }  // namespace
 
+namespace {
+// one tile per workgroup: no weight ring; several: a ring of three tiles (two for K > 2048)
+template <int GPW, int EPT, bool PAIRED, bool SINGLE>
+void launch_fused_ring(hipStream_t stream, const FusedArgs& args, uint32_t tiles, uint32_t grid, uint64_t seq,
+                       uint64_t* flag, uint64_t* host_status) {
+    const dim3 g(grid), b(kFusedThreads);
+    if (tiles <= grid)
+        launch_kernel((k_fused<GPW, EPT, PAIRED, SINGLE, 1>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+    else
+        launch_kernel((k_fused<GPW, EPT, PAIRED, SINGLE, GPW == 1 ? 3 : 2>), g, b, 0, stream, args, tiles, seq, flag,
+                      host_status);
+}
+}  // namespace
+
 hipError_t launch_fused(hipStream_t stream, const FusedArgs& args, uint32_t tiles, uint32_t grid, uint64_t seq,
                         uint64_t* flag, uint64_t* host_status) {
     static_assert(kFusedMaxGroups * 64u * 2u <= kFusedMaxWidth, "two product buffers fit the scratch");
     constexpr int kWideGpw = kFusedMaxGroups / kFusedWaves, kWideEpt = kFusedMaxWidth / kFusedThreads;
     const bool paired = args.post == POST_SILU_MUL;
-    const dim3 g(grid), b(kFusedThreads);
     if (args.jobs == nullptr) {  // a single job in the kernel arguments
         if (args.width <= 2048u)
-            launch_kernel((k_fused<1, 2, false, true>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+            launch_fused_ring<1, 2, false, true>(stream, args, tiles, grid, seq, flag, host_status);
         else
-            launch_kernel((k_fused<kWideGpw, kWideEpt, false, true>), g, b, 0, stream, args, tiles, seq, flag,
-                               host_status);
+            launch_fused_ring<kWideGpw, kWideEpt, false, true>(stream, args, tiles, grid, seq, flag, host_status);
     } else if (args.width <= 2048u && !paired) {
-        launch_kernel((k_fused<1, 2, false, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+        launch_fused_ring<1, 2, false, false>(stream, args, tiles, grid, seq, flag, host_status);
     } else if (args.width <= 2048u) {
-        launch_kernel((k_fused<1, 2, true, false>), g, b, 0, stream, args, tiles, seq, flag, host_status);
+        launch_fused_ring<1, 2, true, false>(stream, args, tiles, grid, seq, flag, host_status);
     } else if (!paired) {
-        launch_kernel((k_fused<kWideGpw, kWideEpt, false, false>), g, b, 0, stream, args, tiles, seq, flag,
-                           host_status);
+        launch_fused_ring<kWideGpw, kWideEpt, false, false>(stream, args, tiles, grid, seq, flag, host_status);
     } else {
-        launch_kernel((k_fused<kWideGpw, kWideEpt, true, false>), g, b, 0, stream, args, tiles, seq, flag,
-                           host_status);
+        launch_fused_ring<kWideGpw, kWideEpt, true, false>(stream, args, tiles, grid, seq, flag, host_status);
     }
     return hipGetLastError();
 }

@@ -142,6 +142,9 @@ struct FusedArgs {
     int32_t post;          // PostKind
     float* post_out;       // POST_SILU_MUL
     FusedJob single;       // jobs == null (njobs == 1): the job, passed in the kernel arguments
+    // when every walked job (or pair) j starts at tile j << walk_shift, the job of tile t is
+    // min(t >> walk_shift, last); 32: none does, the kernel walks the table
+    uint32_t walk_shift;
     float* mirror;         // single F32 job: host memory that also receives the output row (may be null)
     int32_t dot_out;       // DOT_GROUPS: out receives int16 D[n][group] instead of the sums
     // single job: completion signal (may be null).  Every workgroup adds 1 to *done_count
