@@ -483,14 +483,29 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
             // branch-free lookups (a scalar branch per step costs more than the
             // step); a miss anywhere is noted and the walk repeated below
             uint32_t v = 0, miss = 0;
+            if (nseg == 2u * kPairs) {
+                // a full-width row: every step live, and one test of all the offsets at the end
+                // (an offset outside the window sets a bit above the window's) -- a chain of
+                // three scalar and vector instructions per step
+                uint32_t any = 0;
 #pragma unroll
-            for (uint32_t j = 0; j < 2u * kPairs; ++j) {
-                const uint32_t idx = v - (uint32_t)__builtin_amdgcn_readlane(bases, j);
-                const uint32_t nv = (uint32_t)__builtin_amdgcn_readlane(__float_as_int(ends[j / 2u]),
-                                                                        (int)((j & 1u) * 32u + (idx & (kWindow - 1u))));
-                const bool live = j < nseg;
-                miss |= live ? idx & ~(kWindow - 1u) : 0u;
-                v = live ? nv : v;
+                for (uint32_t j = 0; j < 2u * kPairs; ++j) {
+                    const uint32_t idx = v - (uint32_t)__builtin_amdgcn_readlane(bases, j);
+                    any |= idx;
+                    v = (uint32_t)__builtin_amdgcn_readlane(__float_as_int(ends[j / 2u]),
+                                                            (int)((j & 1u) * 32u + (idx & (kWindow - 1u))));
+                }
+                miss = any & ~(kWindow - 1u);
+            } else {
+#pragma unroll
+                for (uint32_t j = 0; j < 2u * kPairs; ++j) {
+                    const uint32_t idx = v - (uint32_t)__builtin_amdgcn_readlane(bases, j);
+                    const uint32_t nv = (uint32_t)__builtin_amdgcn_readlane(
+                        __float_as_int(ends[j / 2u]), (int)((j & 1u) * 32u + (idx & (kWindow - 1u))));
+                    const bool live = j < nseg;
+                    miss |= live ? idx & ~(kWindow - 1u) : 0u;
+                    v = live ? nv : v;
+                }
             }
             if (miss) {  // the walk with term-by-term additions where the running sum is no candidate
                 v = 0;
