@@ -153,6 +153,39 @@ def test_fused_rmsnorm(pkg, hipdev, oracle, k, ns, with_b, with_out):
         f.free()
 
 
+@pytest.mark.parametrize("ns,kind", [
+    ([8192, 8192, 8192], "rms"),          # 384 tiles: workgroups walk tiles, jobs at multiples of 128 tiles
+    ([8192, 3000, 8192, 4213], "row"),    # 394 tiles: jobs at irregular tiles (the table walk)
+    ([6144] * 4 + [4096], "rms"),         # 448 tiles
+])
+def test_fused_many_tiles(pkg, hipdev, oracle, ns, kind):
+    """Batches with more tiles than workgroups (one per CU): each workgroup walks several
+    tiles with a ring of weights in flight, finding each tile's job in one step when the
+    jobs start at multiples of a power of two and by walking the table otherwise."""
+    k = 2048
+    rng = np.random.default_rng(len(ns))
+    f = Fused(pkg, hipdev, k, ns, seed=17)
+    try:
+        print(f"fused batch: {len(ns)} jobs, {sum((n + 63) // 64 for n in ns)} tiles, pre {kind}", flush=True)
+        if kind == "rms":
+            a, b = f32(rng, k, 2.0), f32(rng, k, 0.5)
+            gain = (1.0 + 0.02 * rng.standard_normal(k)).astype(np.float32)
+            f.ops["a"].write(a)
+            f.ops["b"].write(b)
+            f.ops["gain"].write(gain)
+            assert f.create(f.pre(pkg.api.PreOp.RMSNORM, True, False, eps=1e-6)) == 0
+            _, row, _ = host_rmsnorm(a, b, gain, 1e-6)
+        else:
+            row = f32(rng, k)
+            f.row.write(row)
+            assert f.create(f.pre(pkg.api.PreOp.ROW)) == 0
+        for _ in range(2):
+            assert f.run() == 0
+            check(f.outputs(), expected(pkg, oracle, f.chunks, row))
+    finally:
+        f.free()
+
+
 def sum_pattern(name, k, rng):
     """Rows chosen for the sum of squares: rounding that drifts far from the exact
     prefix sums, terms across many binades, subnormal terms, long zero runs."""
