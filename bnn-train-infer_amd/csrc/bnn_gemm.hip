@@ -931,6 +931,166 @@ __global__ __launch_bounds__(64 * W) void k_gemm_ks(GemmJob j, uint32_t mtiles, 
     }
 }
 
+// k_gemm_wv: F32-accumulating jobs with few rows.  Every wave computes a (16*MS) x
+// (16*NS) block of the output over the whole K on its own: its rows' quantised bytes,
+// its columns' sign bits and scales come from global memory straight into a ring of
+// DEPTH groups of registers; the bits become +1/-1 operands through the byte table
+// (LDS, written once before the loop); no barrier or LDS exchange sits in the loop, so
+// the waves of a CU run their chains independently and the latency of one group's
+// loads is covered by the DEPTH-1 groups ahead of it.  The K order inside a group is
+// that of k_gemm_ks (lane chunk c: weights 32c .. 32c+31, MFMA half h the 16 from
+// 32c + 16h), so a lane's operands are 32 contiguous row bytes and 4 contiguous bytes
+// of bits.  Group g's MFMAs write one of two D sets while group g-1's epilogue reads
+// the other; each output element's products are added in group order by one thread.
+// The group count is padded to a multiple of DEPTH with groups of scale 0 (the
+// clamped last group's operands), whose products are +0 and leave the sums unchanged.
+template <int MS, int NS>
+struct WvOps {
+    v4i a[MS][2];
+    uint32_t bits[NS];
+    uint32_t s[NS];
+};
+
+template <int MS, int NS, int WM, int WN, int DEPTH>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm_wv(GemmJob j, uint32_t mtiles, uint32_t ntiles, uint32_t band,
+                                                         uint64_t seq, const uint64_t* __restrict__ flag) {
+    constexpr uint32_t TM = 16u * MS * WM, TN = 16u * NS * WN, NT = 64u * WM * WN;
+    static_assert(DEPTH >= 2 && DEPTH % 2 == 0, "two D sets alternate with the ring slots");
+    static_assert(16 * NS <= 64 && 64 % (16 * NS) == 0, "a wave's columns lie in one 64-feature tile");
+    __shared__ uint2 lut[256];
+    if (*flag == seq)
+        return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave / WN, wn = wave % WN;
+    const TileRC tile = gemm_tile_of_block(blockIdx.x, gridDim.x, mtiles, ntiles, band);
+    const uint32_t m0 = tile.mt * TM + 16u * MS * wm, n0 = tile.nt * TN + 16u * NS * wn;
+    const uint32_t groups = j.groups;
+    for (uint32_t i = tid; i < 256u; i += NT)
+        lut[i] = make_uint2(pm1_nibble(i & 15u), pm1_nibble(i >> 4));
+
+    // rows past the end are clamped (never stored); so is the matrix tile of columns
+    // past the last tile
+    const uint32_t chunk = lane >> 4;
+    const uint8_t* a_ptr[MS];
+    const uint8_t* b_ptr[NS];
+    const uint16_t* s_ptr[NS];
+#pragma unroll
+    for (int mi = 0; mi < MS; ++mi) {
+        const uint32_t m = min(m0 + 16u * mi + (lane & 15u), j.rows - 1u);
+        a_ptr[mi] = reinterpret_cast<const uint8_t*>(j.q) + (size_t)m * j.k + 32u * chunk;
+    }
+#pragma unroll
+    for (int ni = 0; ni < NS; ++ni) {
+        const uint32_t n = n0 + 16u * ni + (lane & 15u), st = min(n >> 6, j.tiles - 1u);
+        b_ptr[ni] = reinterpret_cast<const uint8_t*>(j.wbits) + ((size_t)st * groups * kTile + (n & 63u)) * 16u +
+                    4u * chunk;
+        s_ptr[ni] = j.wscale + (size_t)st * groups * kTile + (n & 63u);
+    }
+    // every load is unconditional (group clamped into range): the same loads are in
+    // flight on every path
+    auto load = [&](WvOps<MS, NS>& o, uint32_t g) {
+        const uint32_t gc = min(g, groups - 1u);
+#pragma unroll
+        for (int mi = 0; mi < MS; ++mi)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                o.a[mi][h] = gload_v4i(a_ptr[mi] + (size_t)gc * kGroup + 16u * h);
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni) {
+            o.bits[ni] = *reinterpret_cast<const uint32_t*>(b_ptr[ni] + (size_t)gc * kTile * 16u);
+            o.s[ni] = s_ptr[ni][(size_t)gc * kTile];
+        }
+    };
+
+    float acc[MS][NS][4];
+    v4i dd[2][MS][NS];
+    const v4i c_init = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+    float sc_prev[NS];
+#pragma unroll
+    for (int ni = 0; ni < NS; ++ni)
+        sc_prev[ni] = 0.0f;  // the epilogue before group 0 adds +0
+#pragma unroll
+    for (int mi = 0; mi < MS; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni) {
+            dd[1][mi][ni] = c_init;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mi][ni][r] = 0.0f;
+        }
+    auto epilogue = [&](const v4i (&d)[MS][NS]) {
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni) {
+            const float sc = sc_prev[ni];
+            const float cneg = sc * -kMagicValue;  // exact
+#pragma unroll
+            for (int mi = 0; mi < MS; ++mi)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc, __int_as_float(d[mi][ni][r]), cneg);
+        }
+    };
+
+    WvOps<MS, NS> o[DEPTH];
+#pragma unroll
+    for (int d = 0; d + 1 < DEPTH; ++d)
+        load(o[d], d);
+    barrier();  // the table is in LDS
+
+    // group g = g0 + d from ring slot d: refill the slot emptied one group ago, expand
+    // the bits, group g's MFMAs into D set d % 2, group g-1's epilogue from the other
+    auto step = [&](int d, uint32_t g) {
+        load(o[(d + DEPTH - 1) % DEPTH], g + DEPTH - 1u);
+        const WvOps<MS, NS>& cur = o[d];
+        v4i b[NS][2];
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint2 lo = lut[(cur.bits[ni] >> (16u * h)) & 0xffu];
+                const uint2 hi = lut[(cur.bits[ni] >> (16u * h + 8u)) & 0xffu];
+                b[ni][h] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+            }
+        v4i (&dn)[MS][NS] = dd[d & 1];
+#pragma unroll
+        for (int mi = 0; mi < MS; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < NS; ++ni) {
+                v4i x = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[mi][0], b[ni][0], c_init, 0, 0, 0);
+                dn[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur.a[mi][1], b[ni][1], x, 0, 0, 0);
+            }
+        epilogue(dd[(d & 1) ^ 1]);
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni)
+            sc_prev[ni] = g < groups ? __half2float(__ushort_as_half((uint16_t)cur.s[ni])) : 0.0f;
+    };
+    for (uint32_t g0 = 0; g0 < groups; g0 += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d)
+            step(d, g0 + d);
+    }
+    epilogue(dd[(DEPTH - 1) & 1]);  // the last step's group
+
+#pragma unroll
+    for (int mi = 0; mi < MS; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NS; ++ni) {
+            const uint32_t n = n0 + 16u * ni + (lane & 15u);
+            if (n >= j.n)
+                continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t m = m0 + 16u * mi + 4u * (lane >> 4) + r;
+                if (m >= j.rows)
+                    continue;
+                float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
+                __builtin_nontemporal_store(j.mode == MODE_SUM_SCALED ? acc[mi][ni][r] * j.rscale[m] : acc[mi][ni][r],
+                                            orow + n);
+            }
+        }
+}
+
 // The band width (in M tiles) of gemm_tile_of_block: an XCD covering band M tiles of
 // mtiles and (tiles / 8 / band) N tiles makes the rows (rows * k bytes) be fetched
 // into about 8 * band / mtiles L2s and the weights (1.125 bits each) into
@@ -954,6 +1114,15 @@ hipError_t launch_ks(hipStream_t stream, const GemmJob& job, uint64_t seq, const
     const uint32_t ntiles = (job.n + 16u * TNS - 1u) / (16u * TNS);
     launch_kernel((k_gemm_ks<TMS, TNS, W, DEPTH>), dim3(mtiles * ntiles), dim3(64 * W), 0, stream, job, mtiles, ntiles,
                   gemm_band(job, mtiles), seq, flag);
+    return hipGetLastError();
+}
+
+template <int MS, int NS, int WM, int WN, int DEPTH>
+hipError_t launch_wv(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
+    constexpr uint32_t TM = 16u * MS * WM, TN = 16u * NS * WN;
+    const uint32_t mtiles = (job.rows + TM - 1u) / TM, ntiles = (job.n + TN - 1u) / TN;
+    launch_kernel((k_gemm_wv<MS, NS, WM, WN, DEPTH>), dim3(mtiles * ntiles), dim3(64 * WM * WN), 0, stream, job,
+                  mtiles, ntiles, gemm_band(job, mtiles), seq, flag);
     return hipGetLastError();
 }
 
@@ -984,6 +1153,13 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
 #ifndef BNN_GEMM_CO
 #define BNN_GEMM_CO 1  // F32-accumulating jobs with a 128 x 128 tile per CU: two workgroups per CU (k_gemm_co)
 #endif
+    // few rows: one wave per 16 x 16 output block with its operands straight in
+    // registers, while that makes at most three waves per CU (the blocks of 16 columns
+    // each load their rows, and more of them outrun the loads a CU keeps in flight);
+    // with 33..64 rows only for K <= 2048 (a longer K favours splitting it, below)
+    if (job.mode != MODE_DOT_I16 && job.rows <= 64u && (job.rows <= 32u || job.groups <= 16u) &&
+        blocks(16, 16) <= 3u * cus)
+        return launch_wv<1, 1, 1, 1, 8>(stream, job, seq, flag);
     if (BNN_GEMM_CO && job.mode != MODE_DOT_I16 && blocks(128, 128) >= cus)
         return launch_co<128, 128, 2, 2>(stream, job, seq, flag);
     if (blocks(128, 128) >= cus)
@@ -994,13 +1170,13 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
         return launch_bits<64, 64, 2, 2>(stream, job, seq, flag);
     const uint64_t enough = cus * 3u / 4u;
     if (job.mode != MODE_DOT_I16 && blocks(32, 64) < enough) {
-        // too few tiles for the CUs: K split across the 8 waves of a workgroup, with the
-        // largest tile that still gives most CUs a workgroup
+        // too few tiles for the CUs: K split across the waves of a workgroup (8, or 4 for
+        // the smallest tile), with the largest tile that still gives most CUs a workgroup
         if (blocks(64, 32) >= enough)
             return launch_ks<4, 2, 8, 3>(stream, job, seq, flag);
         if (blocks(32, 32) >= enough)
             return launch_ks<2, 2, 8, 3>(stream, job, seq, flag);
-        return launch_ks<2, 1, 8, 3>(stream, job, seq, flag);
+        return launch_ks<2, 1, 4, 3>(stream, job, seq, flag);
     }
     return launch_bits<32, 64, 2, 2>(stream, job, seq, flag);
 }

@@ -109,7 +109,10 @@ def test_quantiser_edge_rows(pkg, hipdev, oracle, i):
     (1000, 640, 2000),                                         # 64 x 128
     (250, 1152, 6100),                                         # 64 x 64
     (120, 1152, 5000),                                         # 32 x 64
-    (80, 1408, 3500), (100, 3200, 3000), (50, 640, 1000),     # K split over 8 waves: 64x32, 32x32, 32x16
+    (80, 1408, 3500), (100, 3200, 3000),                      # K split over 8 waves: 64x32, 32x32
+    (40, 2304, 1500),                                          # K split over 4 waves: 32x16
+    (8, 2048, 6144), (17, 640, 1000), (24, 6144, 2048),       # a wave per 16 x 16 block, operands in registers
+    (32, 1408, 2050), (50, 640, 1000),
 ])
 def test_gemm_tilings_ragged_edges(pkg, hipdev, oracle_fast, op, rows, k, n):
     """Shapes that select each multi-row tiling, with a partial last row tile, a last
