@@ -321,3 +321,46 @@ def test_read_after_single_row_execute(pkg, hipdev, oracle):
         bi.free()
         bo.free()
         m.destroy()
+
+
+def test_batches_drop_the_host_copy(pkg, hipdev, oracle):
+    """A single-row F32 output read from its host copy must not outlive a batch that
+    rewrites the same bytes: BNNX_ExecuteBatch, and a prepared BNNX_BatchLaunch read
+    after BNNX_DeviceSynchronize."""
+    k, n = 2048, 300
+    bits, scales = pkg.synth.matrix(n, k, seed=12)
+    x = pkg.synth.normal_f32(3, k, seed=12)
+    with pkg.Device(oracle, 0) as odev:
+        mo = odev.matrix(bits, scales)
+        want = [odev.run(pkg.Op.GEMV_F32, mo, x[r:r + 1])[0].view(np.uint32) for r in range(3)]
+        mo.destroy()
+    assert not np.array_equal(want[0], want[1]) and not np.array_equal(want[0], want[2])
+    api = hipdev.api
+    m = hipdev.matrix(bits, scales)
+    bi, bo = hipdev.buffer(x.nbytes), hipdev.buffer(4 * n)
+    batch = ctypes.c_void_p()
+    try:
+        bi.write(x)
+        job = lambda r: pkg.Job(int(pkg.Op.GEMV_F32), m.handle.value, bi.view(pkg.Type.F32, r * 4 * k),
+                                bo.view(pkg.Type.F32, 0), 1)
+        out = lambda: bo.read().view(np.uint32)
+        prepared = (pkg.Job * 1)(job(2))
+        assert api.BNNX_BatchCreate(hipdev.handle, prepared, 1, ctypes.byref(batch)) == pkg.Status.OK
+        # row 0 through BNN_Execute (host copy), then row 1 through BNNX_ExecuteBatch
+        assert hipdev.execute(job(0)) == pkg.Status.OK
+        assert np.array_equal(out(), want[0])
+        assert api.BNNX_ExecuteBatch(hipdev.handle, (pkg.Job * 1)(job(1)), 1) == pkg.Status.OK
+        assert np.array_equal(out(), want[1])
+        # row 0 again, then the prepared batch (row 2) and the synchronisation
+        assert hipdev.execute(job(0)) == pkg.Status.OK
+        assert np.array_equal(out(), want[0])
+        assert api.BNNX_BatchCheck(batch) == pkg.Status.OK
+        assert api.BNNX_BatchLaunch(batch) == pkg.Status.OK
+        assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.OK
+        assert np.array_equal(out(), want[2])
+    finally:
+        if batch.value:
+            api.BNNX_BatchDestroy(batch)
+        bi.free()
+        bo.free()
+        m.destroy()
