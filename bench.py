@@ -28,8 +28,8 @@ Secondary legs (the other benchmark configurations; --no-extra skips them):
   ops              configs 2/3: DOT_GROUPS, GEMV_I8 and the GEMV_F32 Qwen3 shapes,
                    per call (BNN_Execute) and sustained over >= 1 GiB of distinct
                    resident matrices in one BNNX_ExecuteBatch per step
-  gemm             config 4: GEMM_F32 / GEMM_I8 at rows 64/256/1024 on the matrix
-                   cores: TOPS and utilisation of the 5.0 POPS dense int8 peak
+  gemm             config 4: GEMM_F32 / GEMM_I8 at rows 64/256/1024 (and 8/32, prefill-sized)
+                   on the matrix cores: TOPS and utilisation of the 5.0 POPS dense int8 peak
   e2e              config 5: Qwen3-1.7B-shape greedy decode (random-init Q1_0 model,
                    32 prompt + 128 new tokens) through the engine: the device path
                    (fused batches), the device path with prepared batches, and the
@@ -251,7 +251,7 @@ def gemm_leg(pkg, hip):
             for k, n in ((2048, 6144), (6144, 2048)):
                 bits, scales = pkg.synth.matrix(n, k, seed=4)
                 m = dev.matrix(bits, scales)
-                for rows in (64, 256, 1024):
+                for rows in (8, 32, 64, 256, 1024):
                     f32 = op.endswith("F32")
                     x = pkg.synth.normal_f32(rows, k, seed=4) if f32 else pkg.synth.int8_uniform(rows, k, seed=4)
                     in_t, out_t = pkg.api.OP_TYPES[pkg.Op[op]]
