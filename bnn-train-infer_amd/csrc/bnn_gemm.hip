@@ -1160,6 +1160,10 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
     if (job.mode != MODE_DOT_I16 && job.rows <= 64u && (job.rows <= 32u || job.groups <= 16u) &&
         blocks(16, 16) <= 3u * cus)
         return launch_wv<1, 1, 1, 1, 8>(stream, job, seq, flag);
+    // a long K (>= 32 groups) with two to three 32 x 32 blocks per CU: a wave per block
+    // beats the tiled kernels, whose per-group steps serialise over the long K
+    if (job.mode != MODE_DOT_I16 && job.groups >= 32u && blocks(32, 32) >= 2u * cus && blocks(32, 32) <= 3u * cus)
+        return launch_wv<2, 2, 1, 1, 4>(stream, job, seq, flag);
     if (BNN_GEMM_CO && job.mode != MODE_DOT_I16 && blocks(128, 128) >= cus)
         return launch_co<128, 128, 2, 2>(stream, job, seq, flag);
     if (blocks(128, 128) >= cus)
