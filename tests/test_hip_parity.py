@@ -106,6 +106,7 @@ def test_quantiser_edge_rows(pkg, hipdev, oracle, i):
 @pytest.mark.parametrize("op", ["GEMM", "GEMM_F32"])
 @pytest.mark.parametrize("rows,k,n", [
     (1000, 384, 4100), (2049, 128, 2000), (1152, 640, 8128),  # 128 x 128 workgroup tiles
+    (400, 640, 6100),                                          # 128 x 128, one workgroup per CU
     (1000, 640, 2000),                                         # 64 x 128
     (250, 1152, 6100),                                         # 64 x 64
     (120, 1152, 5000),                                         # 32 x 64
