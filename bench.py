@@ -297,12 +297,13 @@ def e2e_leg(pkg, hip, paths=tuple(E2E_PATHS), new=128):
                 ctx = pkg.engine.Context(model, n_ctx=1024)
                 ctx.set_resident(mode)
                 assert ctx.resident() == mode, f"{name} path not available"
+                logits = np.empty(info["vocab"], np.float32)  # one buffer for every step, as bnn-infer-v2.c
                 t0 = time.perf_counter()
-                tokens = [int(np.argmax(ctx.decode(prompt)))]
+                tokens = [int(np.argmax(ctx.decode(prompt, out=logits)))]
                 t1 = time.perf_counter()
                 ctx.reset_stats()
                 for _ in range(new - 1):
-                    tokens.append(int(np.argmax(ctx.decode([tokens[-1]]))))
+                    tokens.append(int(np.argmax(ctx.decode([tokens[-1]], out=logits))))
                 t2 = time.perf_counter()
                 st = ctx.stats()
                 ctx.free()

@@ -110,9 +110,17 @@ class Context:
                        "BNNE_ContextCreate")
         self.handle = h
 
-    def decode(self, tokens, want_logits: bool = True) -> np.ndarray | None:
+    def decode(self, tokens, want_logits: bool = True, out: np.ndarray | None = None) -> np.ndarray | None:
+        """BNNE_Decode; the logits go into `out` when given (a caller's buffer reused across
+        steps, as bnn-infer-v2.c:246-279 reuses one), else into a new array."""
         ids = np.ascontiguousarray(tokens, dtype=np.int32)
-        out = np.empty(self.model.info.n_vocab, np.float32) if want_logits else None
+        if want_logits and out is not None:
+            if out.dtype != np.float32 or out.shape != (self.model.info.n_vocab,) or not out.flags.c_contiguous:
+                raise ValueError("out: a contiguous float32 array of n_vocab elements")
+        elif want_logits:
+            out = np.empty(self.model.info.n_vocab, np.float32)
+        else:
+            out = None
         self.eng.check(self.eng.BNNE_Decode(self.handle, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
                                             ids.size,
                                             out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if want_logits

@@ -199,10 +199,11 @@ BNNE_EXPORT BNNE_Status BNNE_Decode(BNNE_Context ctx, const int32_t* tokens, uin
         if (tokens[i] < 0 || (uint32_t)tokens[i] >= info.n_vocab)
             return complain(BNNE_ERANGE, "token %d is not in the vocabulary", tokens[i]);
     CallStats call(*ctx);
+    ctx->logits_checked = false;
     const BNNE_Status st = guarded([&] { ctx->decode(tokens, n_tokens, logits); });
     if (st != BNNE_OK)
         return st;
-    if (logits && !all_finite(logits, info.n_vocab))
+    if (logits && !ctx->logits_checked && !all_finite(logits, info.n_vocab))
         return complain(BNNE_ECOMPUTE, "the logits hold a NaN or infinity");
     ctx->pos += n_tokens;
     call.done(n_tokens);

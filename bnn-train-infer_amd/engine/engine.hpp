@@ -254,6 +254,7 @@ struct bnne_context {
     uint32_t stage_rows = 1;         // rows the staging buffers hold (set before allocate_staging)
     BNN_Buffer stage_in = nullptr;   // stage_rows x widest_in floats: the input rows of SignLinear
     BNN_Buffer stage_out = nullptr;  // stage_rows x widest_shard floats: one shard's outputs
+    bool logits_checked = false;     // set by a decode that verified its logits are finite
 
     bnne_context(bnne_model& m, const BNNE_ContextParams& p) : model(&m), params(p) {}
     virtual ~bnne_context();

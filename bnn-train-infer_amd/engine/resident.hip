@@ -883,6 +883,10 @@ struct Resident {
     uint8_t* emb_bits;
     uint16_t* emb_scales;
     int* err;
+    float* logits_dev;  // the lm_head's output (b_logits)
+    // pinned host memory: V floats of logits, then the error word; both are copied back
+    // on the stream behind a step's last launch, so the host waits once per step
+    float* pinned;
     // fused: every linear layer is a fused batch (its input row produced and
     // quantised inside its one launch), else prepared batches plus this engine's
     // norm and SiLU kernels (models wider than a fused batch takes)
@@ -1153,9 +1157,8 @@ BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, bool fused,
         st = alloc_buffer(r, m.FF, &r->b_up, &r->up);
     if (st == BNNE_OK)
         st = alloc_buffer(r, m.FF, &r->b_h, &r->h);
-    float* logits_dev = nullptr;
     if (st == BNNE_OK)
-        st = alloc_buffer(r, m.V, &r->b_logits, &logits_dev);
+        st = alloc_buffer(r, m.V, &r->b_logits, &r->logits_dev);
     const size_t cache = (size_t)m.L * m.n_ctx * m.kv_dim * sizeof(float);
     if (st == BNNE_OK)
         st = upload(&r->x, nullptr, (size_t)m.C * sizeof(float));
@@ -1201,6 +1204,11 @@ BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, bool fused,
         if (st == BNNE_OK && (e = hipMemset(r->err, 0, sizeof(int))) != hipSuccess)
             st = hip_error(e, "hipMemset");
     }
+    if (st == BNNE_OK &&
+        (e = hipHostMalloc(reinterpret_cast<void**>(&r->pinned), ((size_t)m.V + 1u) * sizeof(float))) != hipSuccess) {
+        r->pinned = nullptr;
+        st = hip_error(e, "hipHostMalloc");
+    }
     if (st == BNNE_OK) {
         r->qkv = static_cast<BNNX_Batch*>(std::calloc(m.L, sizeof(BNNX_Batch)));
         r->attn_out = static_cast<BNNX_Batch*>(std::calloc(m.L, sizeof(BNNX_Batch)));
@@ -1244,6 +1252,8 @@ void resident_free(Resident* r) {
                     (void*)r->rope_sin, (void*)r->emb_bits, (void*)r->emb_scales, (void*)r->err})
         if (p)
             (void)hipFree(p);
+    if (r->pinned)
+        (void)hipHostFree(r->pinned);
     std::free(r);
 }
 
@@ -1340,6 +1350,12 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         }
     }
     e = hipGetLastError();
+    // the error word and the logits come back behind the last launch, into pinned memory
+    int* const err_host = reinterpret_cast<int*>(r->pinned + r->V);
+    if (st == BNNE_OK && e == hipSuccess)
+        e = hipMemcpyAsync(err_host, r->err, sizeof(int), hipMemcpyDeviceToHost, r->stream);
+    if (st == BNNE_OK && e == hipSuccess && logits)
+        e = hipMemcpyAsync(r->pinned, r->logits_dev, (size_t)r->V * sizeof(float), hipMemcpyDeviceToHost, r->stream);
     const uint64_t t1 = stats ? clock_ns() : 0;
     const BNN_Status sync = BNNX_DeviceSynchronize(r->dev);
     const uint64_t t2 = stats ? clock_ns() : 0;
@@ -1347,11 +1363,10 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         return st;
     if (e != hipSuccess)
         return hip_error(e, "kernel launch");
-    int err = 0;
-    e = hipMemcpy(&err, r->err, sizeof err, hipMemcpyDeviceToHost);
-    if (e == hipSuccess && err != kErrNone)
-        e = hipMemset(r->err, 0, sizeof(int));
-    if (e != hipSuccess)
+    if (sync == BNN_EIO)
+        return accel_status(sync, "BNN_Execute");
+    const int err = *static_cast<volatile int*>(err_host);
+    if (err != kErrNone && (e = hipMemset(r->err, 0, sizeof(int))) != hipSuccess)
         return hip_error(e, "error word");
     int kind = err;
     if (r->fused && err != kErrNone) {
@@ -1368,9 +1383,19 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
     if (st != BNNE_OK)
         return st;
     if (logits) {
-        st = accel_status(BNN_BufferRead(r->b_logits, 0, logits, (size_t)r->V * sizeof(float)), "BNN_BufferRead");
-        if (st != BNNE_OK)
-            return st;
+        // to the caller's buffer, checking on the way that every logit is finite
+        // (BNNE_Decode's own check, made here in the same pass)
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(r->pinned);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(logits);
+        uint32_t bad = 0;
+        for (uint32_t i = 0; i < r->V; ++i) {
+            const uint32_t u = src[i];
+            dst[i] = u;
+            bad |= (uint32_t)((u & 0x7F800000u) == 0x7F800000u);
+        }
+        if (bad)
+            return complain(BNNE_ECOMPUTE, "the logits hold a NaN or infinity");
+        c->logits_checked = true;
     }
     if (stats) {
         const uint64_t t3 = clock_ns();
