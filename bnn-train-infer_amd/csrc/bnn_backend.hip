@@ -846,7 +846,8 @@ BNN_Status run_single_row(BNN_Device device, const BNN_Job* job, const JobPlan& 
     fa.width = p.m->k;
     fa.row = reinterpret_cast<const float*>(p.in_base);
     fa.post = POST_NONE;
-    fa.single = FusedJob{p.m->wbits, p.m->wscale, reinterpret_cast<float*>(p.out_base), p.m->n, p.m->tiles, 0, 0};
+    fa.inl[0] = FusedJob{p.m->wbits, p.m->wscale, reinterpret_cast<float*>(p.out_base), p.m->n, p.m->tiles, 0, 0};
+    fa.inline_jobs = 1;
     // F32 outputs of buffers whose device address was never handed out are mirrored
     // into pinned host memory by the same kernel
     const bool mirror =
@@ -1423,6 +1424,10 @@ EXPORT BNN_Status BNNX_BatchCreateFusedPost(BNN_Device device, const BNN_Job* jo
                 walk_shift = sh;
         }
     }
+    FusedJob inl[kFusedInline] = {};
+    const bool inline_jobs = count <= kFusedInline;
+    for (uint32_t i = 0; st == BNN_OK && inline_jobs && i < count; ++i)
+        inl[i] = table[i];
     free(table);
     if (st != BNN_OK) {
         free(b);
@@ -1454,6 +1459,9 @@ EXPORT BNN_Status BNNX_BatchCreateFusedPost(BNN_Device device, const BNN_Job* jo
     fa.post = paired ? POST_SILU_MUL : POST_NONE;
     fa.post_out = paired ? post->out : nullptr;
     fa.walk_shift = walk_shift;
+    for (uint32_t i = 0; i < kFusedInline; ++i)
+        fa.inl[i] = inl[i];
+    fa.inline_jobs = inline_jobs ? 1u : 0u;
     device->live_batches++;
     *out_batch = b;
     return BNN_OK;

@@ -229,23 +229,50 @@ struct TileRegs {
 };
 
 // The job table, written by the host only: read through the constant address space
-// (scalar loads through the scalar cache).  A single job (BNN_Execute, SINGLE) comes in
-// the kernel arguments instead, with no table in device memory.
+// (scalar loads through the scalar cache).  Up to kFusedInline jobs (a single job of
+// BNN_Execute, SINGLE, or a decode step's small batches) also come in the kernel
+// arguments, loaded with them at the start: the first tile's job is taken from there, so
+// its weights are requested without first waiting for a table read (or the dependent
+// reads of a walk); later tiles (prefetches) read the table.
 template <bool SINGLE>
 struct JobTable {
-    const FusedJob* t;
-    const FusedJob& single;
+    const FusedArgs& fa;
     typedef const __attribute__((address_space(4))) FusedJob* Ptr;
+    static_assert(kFusedInline == 3, "the inline selections name three slots");
     __device__ __forceinline__ uint32_t first_tile(uint32_t i) const {
         if constexpr (SINGLE)
-            return single.first_tile;
+            return fa.inl[0].first_tile;
         else
-            return ((Ptr)t)[i].first_tile;
+            return ((Ptr)fa.jobs)[i].first_tile;
+    }
+    // the job (or pair) of a workgroup's first tile t, and that job
+    __device__ __forceinline__ uint32_t first_job_of(uint32_t t, uint32_t nwalk) const {
+        if (SINGLE || nwalk == 1u)
+            return 0;
+        if (fa.inline_jobs)
+            return t >= fa.inl[2].first_tile && nwalk > 2u ? 2u : t >= fa.inl[1].first_tile ? 1u : 0u;
+        if (fa.walk_shift < 32u)
+            return min(t >> fa.walk_shift, nwalk - 1u);
+        uint32_t from = 0;
+        while (from + 1u < nwalk && first_tile(from + 1u) <= t)
+            ++from;
+        return from;
+    }
+    __device__ __forceinline__ FusedJob first(uint32_t i) const {
+        if (SINGLE || fa.inline_jobs) {
+            FusedJob j = fa.inl[0];
+            if (i == 1u)
+                j = fa.inl[1];
+            if (i == 2u)
+                j = fa.inl[2];
+            return j;
+        }
+        return (*this)[i];
     }
     __device__ __forceinline__ FusedJob operator[](uint32_t i) const {
         if constexpr (SINGLE)
-            return single;
-        const Ptr c = (Ptr)t;
+            return fa.inl[0];
+        const Ptr c = (Ptr)fa.jobs;
         FusedJob j;
         j.wbits = c[i].wbits;
         j.wscale = c[i].wscale;
@@ -346,7 +373,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     // load counter completes in order: the row is needed first), arriving while the
     // row is produced
     // tiles are walked over the jobs, or over the pairs (the first half of the table)
-    const JobTable<SINGLE> jobs{fa.jobs, fa.single};
+    const JobTable<SINGLE> jobs{fa};
     constexpr bool paired = PAIRED;  // fa.post == POST_SILU_MUL
     const uint32_t nwalk = paired ? fa.njobs / 2u : fa.njobs, pair_step = paired ? nwalk : 0u;
     // the job (or pair) of tile t: first tiles at multiples of 2^walk_shift give it in one
@@ -358,8 +385,8 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
             ++from;
         return from;
     };
-    uint32_t tile = blockIdx.x, ji = job_of(tile, 0);
-    FusedJob job = jobs[ji], job2 = jobs[ji + pair_step];
+    uint32_t tile = blockIdx.x, ji = jobs.first_job_of(tile, nwalk);
+    FusedJob job = jobs.first(ji), job2 = jobs.first(ji + pair_step);
     const float* src_a = fa.kind == PRE_ROW ? fa.row : fa.a;
     const bool int_row = SINGLE && fa.kind == PRE_ROW_I8;
     const bool dot_out = SINGLE && fa.dot_out;
@@ -573,8 +600,9 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
         s = quant_row_scale(amax);
 
     // 4. quantise the wave's own groups; their bit planes are ballots (wave-uniform
-    // masks: kept in scalar registers for one group per wave, else in LDS), and
-    // -sum(Q) per group from the same masks; no exchange between waves
+    // masks: kept in scalar registers for one group per wave or, with one tile per
+    // workgroup, formed group by group next to that group's dots; else in LDS), and
+    // -sum(Q) per group; no exchange between waves
     const float rcp = 1.0f / s;
     const bool exact = quant_exact(s);  // 1 / s may overflow
     int q[EPT];
@@ -592,6 +620,24 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
 #pragma unroll
             for (int b = 0; b < 8; ++b)
                 masks[h][b] = __ballot((q[h] >> b) & 1);
+    } else if constexpr (RING == 1) {
+        // the tile's dots form each group's masks themselves (no planes in LDS: the 16 waves'
+        // plane words would queue on the CU's one scalar unit); -sum(Q) of two groups per
+        // wave reduction, packed: each lane's pair sum lies in [-254, 254], a group's in
+        // [-16256, 16256], so S0 + 65536 S1 neither overflows nor mixes the halves
+#pragma unroll
+        for (int gi = 0; gi < GPW; gi += 2) {
+            const int v0 = q[2 * gi] + q[2 * gi + 1];
+            if (gi + 1 < GPW) {
+                const int v1 = q[2 * gi + 2] + q[2 * gi + 3];
+                const int total = __ockl_wfred_add_i32(v0 + v1 * 65536);
+                const int s0 = (int)(int16_t)(uint16_t)((uint32_t)total & 0xffffu);
+                neg_sum[gi] = -s0;
+                neg_sum[gi + 1] = -((total - s0) / 65536);
+            } else {
+                neg_sum[gi] = -__ockl_wfred_add_i32(v0);
+            }
+        }
     } else {
 #pragma unroll
         for (int gi = 0; gi < GPW; ++gi) {
@@ -628,6 +674,17 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
                 int d;
                 if constexpr (GPW == 1) {
                     d = f_group_dot_s(cur.w[i], masks, neg_sum[i]);
+                } else if constexpr (RING == 1) {
+                    uint64_t m[2][8];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+#pragma unroll
+                        for (int b = 0; b < 8; ++b)
+                            m[h][b] = __ballot((q[2 * i + h] >> b) & 1);
+                    d = f_group_dot_s(cur.w[i], m, neg_sum[i]);
+                    // one group's 32 mask registers at a time (scheduled together, the
+                    // groups' masks would not fit the scalar register file)
+                    __builtin_amdgcn_sched_barrier(0);
                 } else {
                     d = f_group_dot(cur.w[i], planes + g * (kPlaneWords / 4u), neg_sum[i]);
                 }
@@ -699,14 +756,8 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     };
     static_assert(kRing >= 1 && kRing <= 3, "ring slots are named statically");
     if constexpr (kRing == 1) {
-        // one tile per workgroup (the host's choice); more would each load their own
-        for (;;) {
-            const bool more = tile + gridDim.x < tiles_total;
-            step(ring[0], more);
-            if (!more)
-                break;
-            load_tile<GPW>(lr, G, wave, ring[0]);
-        }
+        // one tile per workgroup: the host launches this form only with a workgroup per tile
+        step(ring[0], false);
     } else {
         // whole rounds of the ring, then the rest: the loop has one exit, so the compiler's
         // waits see the ring's loads in flight on every path into the loop

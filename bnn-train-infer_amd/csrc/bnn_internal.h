@@ -113,6 +113,7 @@ constexpr uint32_t kMfmaMinRows = BNN_MFMA_MIN_ROWS;
 // with row scale 1; single jobs only)
 enum PreKind : int32_t { PRE_ROW = 0, PRE_RMSNORM = 1, PRE_SILU_MUL = 2, PRE_ROW_I8 = 3 };
 constexpr uint32_t kFusedMaxWidth = 6144;  // K of a fused batch (LDS holds the whole row)
+constexpr uint32_t kFusedInline = 3;       // jobs passed in the kernel arguments
 
 struct FusedJob {
     const uint4* wbits;
@@ -141,7 +142,11 @@ struct FusedArgs {
     int32_t err_code;
     int32_t post;          // PostKind
     float* post_out;       // POST_SILU_MUL
-    FusedJob single;       // jobs == null (njobs == 1): the job, passed in the kernel arguments
+    // the jobs themselves, in the kernel arguments, when there are at most kFusedInline
+    // (inline_jobs != 0; a single job: jobs == null): the first tile's weight loads then
+    // wait for no table read
+    FusedJob inl[kFusedInline];
+    uint32_t inline_jobs;
     // when every walked job (or pair) j starts at tile j << walk_shift, the job of tile t is
     // min(t >> walk_shift, last); 32: none does, the kernel walks the table
     uint32_t walk_shift;
