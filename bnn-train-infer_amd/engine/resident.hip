@@ -526,6 +526,11 @@ __device__ __forceinline__ void block_lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Keeps the LDS reads issued before it ahead of the arithmetic written after it: the
+// in-order sums below read their operands one stage ahead, so that each stage's reads
+// are in flight while the previous stage's additions run.
+__device__ __forceinline__ void lds_reads_issued() { asm volatile("" ::: "memory"); }
+
 __global__ __launch_bounds__(256) void k_attn_one(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, uint32_t kv_mul, float eps,
     const float* __restrict__ q_gain, const float* __restrict__ k_gain, const float* __restrict__ cosv,
@@ -574,18 +579,37 @@ __global__ __launch_bounds__(256) void k_attn_one(
         sq_k[lane] = ka * ka;
         sq_k[lane + half] = kb * kb;
         wave_lds_sync();
+        // stages of 4 float4 per sum, the next stage's reads in flight during the additions
         float sum_q = 0.0f, sum_k = 0.0f;
-#pragma unroll 8
-        for (uint32_t i = 0; i < hd4; ++i) {
-            const float4 a = sq4[0][i], b = sq4[1][i];
-            sum_q = sum_q + a.x;
-            sum_k = sum_k + b.x;
-            sum_q = sum_q + a.y;
-            sum_k = sum_k + b.y;
-            sum_q = sum_q + a.z;
-            sum_k = sum_k + b.z;
-            sum_q = sum_q + a.w;
-            sum_k = sum_k + b.w;
+        float4 ra[2][4], rb[2][4];
+#pragma unroll
+        for (uint32_t c = 0; c < 4u; ++c) {
+            ra[0][c] = sq4[0][c];
+            rb[0][c] = sq4[1][c];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < hd4; i += 4u) {
+            const uint32_t cur = (i / 4u) & 1u;
+            if (i + 4u < hd4) {
+#pragma unroll
+                for (uint32_t c = 0; c < 4u; ++c) {
+                    ra[cur ^ 1u][c] = sq4[0][i + 4u + c];
+                    rb[cur ^ 1u][c] = sq4[1][i + 4u + c];
+                }
+            }
+            lds_reads_issued();
+#pragma unroll
+            for (uint32_t c = 0; c < 4u; ++c) {
+                const float4 a = ra[cur][c], b = rb[cur][c];
+                sum_q = sum_q + a.x;
+                sum_k = sum_k + b.x;
+                sum_q = sum_q + a.y;
+                sum_k = sum_k + b.y;
+                sum_q = sum_q + a.z;
+                sum_k = sum_k + b.z;
+                sum_q = sum_q + a.w;
+                sum_k = sum_k + b.w;
+            }
         }
         const float rq = sqrtf(sum_q / (float)HD + eps), rk = sqrtf(sum_k / (float)HD + eps);
         const bool bad = !isfinite(rq) || rq == 0.0f || !isfinite(rk) || rk == 0.0f;
@@ -627,14 +651,29 @@ __global__ __launch_bounds__(256) void k_attn_one(
             for (uint32_t i = 0; i < hd4; ++i)
                 key[i] = qk4[1][i];
         }
+        // q in stages of 4 float4, the next stage's reads in flight during the additions
         float dot = 0.0f;
+        float4 qs[2][4];
 #pragma unroll
-        for (uint32_t i = 0; i < hd4; ++i) {
-            const float4 qq = qk4[0][i];
-            dot = dot + qq.x * key[i].x;
-            dot = dot + qq.y * key[i].y;
-            dot = dot + qq.z * key[i].z;
-            dot = dot + qq.w * key[i].w;
+        for (uint32_t c = 0; c < 4u; ++c)
+            qs[0][c] = qk4[0][c];
+#pragma unroll
+        for (uint32_t i = 0; i < hd4; i += 4u) {
+            const uint32_t cur = (i / 4u) & 1u;
+            if (i + 4u < hd4) {
+#pragma unroll
+                for (uint32_t c = 0; c < 4u; ++c)
+                    qs[cur ^ 1u][c] = qk4[0][i + 4u + c];
+            }
+            lds_reads_issued();
+#pragma unroll
+            for (uint32_t c = 0; c < 4u; ++c) {
+                const float4 qq = qs[cur][c];
+                dot = dot + qq.x * key[i + c].x;
+                dot = dot + qq.y * key[i + c].y;
+                dot = dot + qq.z * key[i + c].z;
+                dot = dot + qq.w * key[i + c].w;
+            }
         }
         const float score = dot * scale;
         if (!isfinite(score))
@@ -676,40 +715,55 @@ __global__ __launch_bounds__(256) void k_attn_one(
     __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this wave's V rows are in LDS
     block_lds_barrier();                 // ... and every wave's, with the probabilities
 
-    // value[i] in position order: the LDS reads of the next 16 rows are issued before
-    // the additions of the current 16
+    // the products p[t] * V[t][i] of rows t < pos, in place (each rounded once, as the
+    // in-order loop forms them), by all four waves
+    for (uint32_t ci = tid; ci < 32u * pos; ci += 256u) {
+        const float pt = p[ci >> 5];
+        float4 v4 = vs4[ci];
+        v4.x = v4.x * pt;
+        v4.y = v4.y * pt;
+        v4.z = v4.z * pt;
+        v4.w = v4.w * pt;
+        vs4[ci] = v4;
+    }
+    block_lds_barrier();
+
+    // value[i] = sum over t in position order of the products: stages of 16 rows, the next
+    // stage's reads in flight during the current stage's additions (rows past pos - 1 are read
+    // and not added)
     if (tid < HD) {
         const float* col = vs + tid;
         float acc = 0.0f;
-        float vv[2][16], pp[2][16];
-        const auto fetch = [&](float(&v)[16], float(&pr)[16], uint32_t u) {
+        float ra[16], rb[16];
+        const auto fetch = [&](float(&r)[16], uint32_t u) {
 #pragma unroll
-            for (uint32_t j = 0; j < 16; ++j) {
-                v[j] = col[(u + j) * HD];
-                pr[j] = p[u + j];
-            }
+            for (uint32_t j = 0; j < 16u; ++j)
+                r[j] = col[min(u + j, kAttnOneMax - 1u) * HD];
         };
-        const auto add = [&](const float(&v)[16], const float(&pr)[16]) {
+        const auto add = [&](const float(&r)[16], uint32_t n) {
 #pragma unroll
-            for (uint32_t j = 0; j < 16; ++j)
-                acc = acc + pr[j] * v[j];
+            for (uint32_t j = 0; j < 16u; ++j)
+                if (j < n)
+                    acc = acc + r[j];
         };
         uint32_t u = 0;
-        if (pos >= 16u)
-            fetch(vv[0], pp[0], 0);
+        fetch(ra, 0);
         for (; u + 32u <= pos; u += 32u) {
-            fetch(vv[1], pp[1], u + 16u);
-            add(vv[0], pp[0]);
-            if (u + 48u <= pos)
-                fetch(vv[0], pp[0], u + 32u);
-            add(vv[1], pp[1]);
+            fetch(rb, u + 16u);
+            lds_reads_issued();
+            add(ra, 16u);
+            fetch(ra, u + 32u);
+            lds_reads_issued();
+            add(rb, 16u);
         }
         if (u + 16u <= pos) {
-            add(vv[0], pp[0]);
-            u += 16u;
+            fetch(rb, u + 16u);
+            lds_reads_issued();
+            add(ra, 16u);
+            add(rb, pos - u - 16u);
+        } else {
+            add(ra, pos - u);
         }
-        for (; u < pos; ++u)
-            acc = acc + p[u] * col[u * HD];
         acc = acc + p[pos] * v[head_off + tid];
         y[(size_t)h * HD + tid] = acc;
     }
