@@ -526,10 +526,25 @@ __device__ __forceinline__ void block_lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// Keeps the LDS reads issued before it ahead of the arithmetic written after it: the
-// in-order sums below read their operands one stage ahead, so that each stage's reads
-// are in flight while the previous stage's additions run.
-__device__ __forceinline__ void lds_reads_issued() { asm volatile("" ::: "memory"); }
+// The in-order sums below read their LDS operands in stages: a stage's reads are
+// issued, then the previous stage's operands are declared ready (the compiler waits for
+// those reads only, and the stage's additions cannot move above the declaration), and the
+// additions run while the new stage's reads are in flight.  The memory clobber keeps the
+// next stage's reads from being issued before the declaration.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void lds_stage_ready(f32x4 (&r)[8]) {
+    asm volatile("" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
+                 :
+                 : "memory");
+}
+__device__ __forceinline__ void lds_stage_ready(float (&r)[16]) {
+    asm volatile(""
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+                   "+v"(r[8]), "+v"(r[9]), "+v"(r[10]), "+v"(r[11]), "+v"(r[12]), "+v"(r[13]), "+v"(r[14]),
+                   "+v"(r[15])
+                 :
+                 : "memory");
+}
 
 __global__ __launch_bounds__(256) void k_attn_one(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, uint32_t kv_mul, float eps,
@@ -537,7 +552,9 @@ __global__ __launch_bounds__(256) void k_attn_one(
     const float* __restrict__ sinv, float* __restrict__ kc, float* __restrict__ vc, uint32_t pos, uint32_t kv_dim,
     float scale, float* __restrict__ y, int* err, int code_base) {
     constexpr uint32_t HD = kAttnHD, hd4 = HD / 4, half = HD / 2;
-    __shared__ float4 vs4[kAttnOneMax * HD / 4];  // V rows 0..pos-1 of the head
+    // V rows 0..pos-1 of the head (then their products), and 16 rows that the value sums'
+    // last stage may read past row 255 (never added)
+    __shared__ float4 vs4[(kAttnOneMax + 16u) * HD / 4];
     __shared__ float4 sq4[2][hd4];                 // the squares of q and k
     __shared__ float4 qk4[2][hd4];                 // q and k normalised and rotated
     __shared__ float4 p4[kAttnOneMax / 4];         // scores, then probabilities (+0 past pos)
@@ -579,13 +596,15 @@ __global__ __launch_bounds__(256) void k_attn_one(
         sq_k[lane] = ka * ka;
         sq_k[lane + half] = kb * kb;
         wave_lds_sync();
-        // stages of 4 float4 per sum, the next stage's reads in flight during the additions
+        // stages of 4 float4 of each sum, the next stage's reads in flight during the additions
         float sum_q = 0.0f, sum_k = 0.0f;
-        float4 ra[2][4], rb[2][4];
+        const f32x4* sq_q4 = reinterpret_cast<const f32x4*>(sq4[0]);
+        const f32x4* sq_k4 = reinterpret_cast<const f32x4*>(sq4[1]);
+        f32x4 r[2][8];
 #pragma unroll
         for (uint32_t c = 0; c < 4u; ++c) {
-            ra[0][c] = sq4[0][c];
-            rb[0][c] = sq4[1][c];
+            r[0][c] = sq_q4[c];
+            r[0][4u + c] = sq_k4[c];
         }
 #pragma unroll
         for (uint32_t i = 0; i < hd4; i += 4u) {
@@ -593,14 +612,14 @@ __global__ __launch_bounds__(256) void k_attn_one(
             if (i + 4u < hd4) {
 #pragma unroll
                 for (uint32_t c = 0; c < 4u; ++c) {
-                    ra[cur ^ 1u][c] = sq4[0][i + 4u + c];
-                    rb[cur ^ 1u][c] = sq4[1][i + 4u + c];
+                    r[cur ^ 1u][c] = sq_q4[i + 4u + c];
+                    r[cur ^ 1u][4u + c] = sq_k4[i + 4u + c];
                 }
             }
-            lds_reads_issued();
+            lds_stage_ready(r[cur]);
 #pragma unroll
             for (uint32_t c = 0; c < 4u; ++c) {
-                const float4 a = ra[cur][c], b = rb[cur][c];
+                const f32x4 a = r[cur][c], b = r[cur][4u + c];
                 sum_q = sum_q + a.x;
                 sum_k = sum_k + b.x;
                 sum_q = sum_q + a.y;
@@ -651,24 +670,25 @@ __global__ __launch_bounds__(256) void k_attn_one(
             for (uint32_t i = 0; i < hd4; ++i)
                 key[i] = qk4[1][i];
         }
-        // q in stages of 4 float4, the next stage's reads in flight during the additions
+        // q in stages of 8 float4, the next stage's reads in flight during the additions
         float dot = 0.0f;
-        float4 qs[2][4];
+        const f32x4* q4 = reinterpret_cast<const f32x4*>(qk4[0]);
+        f32x4 qs[2][8];
 #pragma unroll
-        for (uint32_t c = 0; c < 4u; ++c)
-            qs[0][c] = qk4[0][c];
+        for (uint32_t c = 0; c < 8u; ++c)
+            qs[0][c] = q4[c];
 #pragma unroll
-        for (uint32_t i = 0; i < hd4; i += 4u) {
-            const uint32_t cur = (i / 4u) & 1u;
-            if (i + 4u < hd4) {
+        for (uint32_t i = 0; i < hd4; i += 8u) {
+            const uint32_t cur = (i / 8u) & 1u;
+            if (i + 8u < hd4) {
 #pragma unroll
-                for (uint32_t c = 0; c < 4u; ++c)
-                    qs[cur ^ 1u][c] = qk4[0][i + 4u + c];
+                for (uint32_t c = 0; c < 8u; ++c)
+                    qs[cur ^ 1u][c] = q4[i + 8u + c];
             }
-            lds_reads_issued();
+            lds_stage_ready(qs[cur]);
 #pragma unroll
-            for (uint32_t c = 0; c < 4u; ++c) {
-                const float4 qq = qs[cur][c];
+            for (uint32_t c = 0; c < 8u; ++c) {
+                const f32x4 qq = qs[cur][c];
                 dot = dot + qq.x * key[i + c].x;
                 dot = dot + qq.y * key[i + c].y;
                 dot = dot + qq.z * key[i + c].z;
@@ -729,8 +749,8 @@ __global__ __launch_bounds__(256) void k_attn_one(
     block_lds_barrier();
 
     // value[i] = sum over t in position order of the products: stages of 16 rows, the next
-    // stage's reads in flight during the current stage's additions (rows past pos - 1 are read
-    // and not added)
+    // stage's reads in flight during the current stage's additions (rows past pos - 1, at most
+    // row 255 + 16, are read and not added)
     if (tid < HD) {
         const float* col = vs + tid;
         float acc = 0.0f;
@@ -738,7 +758,7 @@ __global__ __launch_bounds__(256) void k_attn_one(
         const auto fetch = [&](float(&r)[16], uint32_t u) {
 #pragma unroll
             for (uint32_t j = 0; j < 16u; ++j)
-                r[j] = col[min(u + j, kAttnOneMax - 1u) * HD];
+                r[j] = col[(u + j) * HD];
         };
         const auto add = [&](const float(&r)[16], uint32_t n) {
 #pragma unroll
@@ -750,18 +770,20 @@ __global__ __launch_bounds__(256) void k_attn_one(
         fetch(ra, 0);
         for (; u + 32u <= pos; u += 32u) {
             fetch(rb, u + 16u);
-            lds_reads_issued();
+            lds_stage_ready(ra);
             add(ra, 16u);
             fetch(ra, u + 32u);
-            lds_reads_issued();
+            lds_stage_ready(rb);
             add(rb, 16u);
         }
         if (u + 16u <= pos) {
             fetch(rb, u + 16u);
-            lds_reads_issued();
+            lds_stage_ready(ra);
             add(ra, 16u);
+            lds_stage_ready(rb);
             add(rb, pos - u - 16u);
         } else {
+            lds_stage_ready(ra);
             add(ra, pos - u);
         }
         acc = acc + p[pos] * v[head_off + tid];
