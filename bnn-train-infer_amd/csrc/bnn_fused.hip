@@ -357,6 +357,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     constexpr uint32_t kPairs = kRowMax / kSegment / 2u;
     __shared__ double chunk_sum[kRowMax / kChunk];
     __shared__ float seg_end[kPairs * 64u];
+    __shared__ float seg_comp[kPairs * 32u];  // pair p's two segments composed, per candidate of segment 2p
     __shared__ int seg_base[kPairs * 2u];
     float* scratch = reinterpret_cast<float*>(scratch4);
 
@@ -467,6 +468,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
         const uint32_t half = lane >> 5, cand = lane & (kWindow - 1u);
         constexpr int kPairsPerWave = (kPairs + kFusedWaves - 1) / kFusedWaves;
         float c[kPairsPerWave];
+        int bs[kPairsPerWave];
         const float4* src[kPairsPerWave];
 #pragma unroll
         for (int r = 0; r < kPairsPerWave; ++r) {
@@ -481,6 +483,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
             if (half)
                 e = e + chunk_sum[4u * p] + chunk_sum[4u * p + 1u];
             const int base = __float_as_int((float)e) - (int)(kWindow / 2u);
+            bs[r] = base;
             c[r] = __int_as_float(base + (int)cand);
             const uint32_t j = min(2u * p + half, nseg - 1u);
             src[r] = reinterpret_cast<const float4*>(scratch + kSegment * j);
@@ -495,45 +498,54 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
             run_chains<1>(c1, s1);
             c[0] = c1[0];
         }
+        // each pair's two segments composed in its own wave: candidate c of segment 2p ends at
+        // a value whose offset in segment 2p + 1's window names the lane that continued from
+        // it; an offset outside that window leaves the marker 0xffffffff (no candidate)
 #pragma unroll
-        for (int r = 0; r < kPairsPerWave; ++r)
-            if (wave + kFusedWaves * r < npairs)
-                seg_end[(wave + kFusedWaves * r) * 64u + lane] = c[r];
+        for (int r = 0; r < kPairsPerWave; ++r) {
+            const uint32_t pr = wave + kFusedWaves * r;
+            const uint32_t idx = (uint32_t)__float_as_int(c[r]) - (uint32_t)__builtin_amdgcn_readlane(bs[r], 32);
+            const float nxt = __shfl(c[r], (int)(32u + (idx & (kWindow - 1u))));
+            const float comp = 2u * pr + 1u >= nseg ? c[r] : idx < kWindow ? nxt : __int_as_float(-1);
+            if (pr < npairs) {
+                seg_end[pr * 64u + lane] = c[r];
+                if (lane < kWindow)
+                    seg_comp[pr * kWindow + lane] = comp;
+            }
+        }
         lds_barrier();
-        // the walk (wave 0): bits of the running sum, uniform across the wave
+        // the walk (wave 0) over the composed pairs: bits of the running sum, uniform across
+        // the wave
         if (wave == 0) {
-            float ends[kPairs];
+            float comps[kPairs];
 #pragma unroll
             for (uint32_t m = 0; m < kPairs; ++m)
-                ends[m] = seg_end[min(m, npairs - 1u) * 64u + lane];
+                comps[m] = seg_comp[min(m, npairs - 1u) * kWindow + (lane & (kWindow - 1u))];
             const int bases = seg_base[min(lane, nseg - 1u)];
-            // branch-free lookups (a scalar branch per step costs more than the
-            // step); a miss anywhere is noted and the walk repeated below
-            uint32_t v = 0, miss = 0;
-            if (nseg == 2u * kPairs) {
-                // a full-width row: every step live, and one test of all the offsets at the end
-                // (an offset outside the window sets a bit above the window's) -- a chain of
-                // three scalar and vector instructions per step
-                uint32_t any = 0;
+            // branch-free lookups (a scalar branch per step costs more than the step); an
+            // offset outside a window sets a bit above the window's in `any`, a composed miss
+            // leaves the marker (caught by the next offset, or at the end), and either repeats
+            // the walk below
+            uint32_t v = 0, any = 0;
+            if (npairs == kPairs) {
 #pragma unroll
-                for (uint32_t j = 0; j < 2u * kPairs; ++j) {
-                    const uint32_t idx = v - (uint32_t)__builtin_amdgcn_readlane(bases, j);
+                for (uint32_t m = 0; m < kPairs; ++m) {
+                    const uint32_t idx = v - (uint32_t)__builtin_amdgcn_readlane(bases, 2u * m);
                     any |= idx;
-                    v = (uint32_t)__builtin_amdgcn_readlane(__float_as_int(ends[j / 2u]),
-                                                            (int)((j & 1u) * 32u + (idx & (kWindow - 1u))));
+                    v = (uint32_t)__builtin_amdgcn_readlane(__float_as_int(comps[m]), (int)(idx & (kWindow - 1u)));
                 }
-                miss = any & ~(kWindow - 1u);
             } else {
 #pragma unroll
-                for (uint32_t j = 0; j < 2u * kPairs; ++j) {
-                    const uint32_t idx = v - (uint32_t)__builtin_amdgcn_readlane(bases, j);
-                    const uint32_t nv = (uint32_t)__builtin_amdgcn_readlane(
-                        __float_as_int(ends[j / 2u]), (int)((j & 1u) * 32u + (idx & (kWindow - 1u))));
-                    const bool live = j < nseg;
-                    miss |= live ? idx & ~(kWindow - 1u) : 0u;
+                for (uint32_t m = 0; m < kPairs; ++m) {
+                    const uint32_t idx = v - (uint32_t)__builtin_amdgcn_readlane(bases, 2u * m);
+                    const uint32_t nv =
+                        (uint32_t)__builtin_amdgcn_readlane(__float_as_int(comps[m]), (int)(idx & (kWindow - 1u)));
+                    const bool live = m < npairs;
+                    any |= live ? idx : 0u;
                     v = live ? nv : v;
                 }
             }
+            const uint32_t miss = (any & ~(kWindow - 1u)) | (uint32_t)(v == 0xffffffffu);
             if (miss) {  // the walk with term-by-term additions where the running sum is no candidate
                 v = 0;
                 for (uint32_t j = 0; j < nseg; ++j) {
