@@ -26,6 +26,8 @@
 
 #pragma clang fp contract(off)
 
+extern "C" __device__ int __ockl_wfred_add_i32(int);
+
 namespace bnnhip {
 namespace {
 
@@ -192,20 +194,18 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
                 gstore_stream(j.q + (size_t)m * k_total + base + tid, (int8_t)q);
             if (!planes)  // matrix-core rows: Q only
                 continue;
-            // bit planes of these 64 values; the wave's sum follows from the same
-            // masks: sum q = sum_{b<7} 2^b popc(M_b) - 2^7 popc(M_7)  (scalar ops)
+            // bit planes of these 64 values, and their sum as a wave reduction (vector
+            // ops: popcounts of the masks would queue the CU's waves on its one scalar unit)
             uint32_t word = 0;
-            int part = 0;
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
                 const unsigned long long mask = __ballot((q >> b) & 1);
-                const int cnt = __popcll(mask);
-                part += b == 7 ? -(cnt << 7) : (cnt << b);
                 if (lane == 2u * b)
                     word = (uint32_t)mask;
                 if (lane == 2u * b + 1u)
                     word = (uint32_t)(mask >> 32);
             }
+            const int part = __ockl_wfred_add_i32(q);
             const uint32_t g = (uint32_t)kPrepGroupsPerIter * i + (wave >> 1), half = wave & 1u;
             if (lane < 16u)
                 gstore_stream(planes + g * kPlaneWords + (lane >> 1) * 4u + half * 2u + (lane & 1u), word);

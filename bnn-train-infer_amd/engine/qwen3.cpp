@@ -302,16 +302,38 @@ void Qwen3Context::attend(uint32_t layer, uint32_t pos) {
     for (uint32_t h = 0; h < s_.heads; ++h) {
         const float* q = q_.data() + (size_t)h * HD;
         const size_t kv_head = (size_t)(h / group) * HD;
-        float top = -INFINITY;
-        for (uint32_t t = 0; t <= pos; ++t) {
+        // q.k for four positions at a time: four independent in-order sums, so that their
+        // dependent additions overlap (each dot still adds its terms in index order)
+        uint32_t t = 0;
+        for (; t + 4u <= pos + 1u; t += 4u) {
+            const float* k0 = keys + (size_t)t * s_.kv_width + kv_head;
+            const float* k1 = k0 + s_.kv_width;
+            const float* k2 = k1 + s_.kv_width;
+            const float* k3 = k2 + s_.kv_width;
+            float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
+            for (uint32_t i = 0; i < HD; ++i) {
+                d0 += q[i] * k0[i];
+                d1 += q[i] * k1[i];
+                d2 += q[i] * k2[i];
+                d3 += q[i] * k3[i];
+            }
+            scores_[t] = d0 * scale;
+            scores_[t + 1u] = d1 * scale;
+            scores_[t + 2u] = d2 * scale;
+            scores_[t + 3u] = d3 * scale;
+        }
+        for (; t <= pos; ++t) {
             const float* key = keys + (size_t)t * s_.kv_width + kv_head;
             float dot = 0.0f;
             for (uint32_t i = 0; i < HD; ++i)
                 dot += q[i] * key[i];
-            const float score = dot * scale;
+            scores_[t] = dot * scale;
+        }
+        float top = -INFINITY;
+        for (t = 0; t <= pos; ++t) {
+            const float score = scores_[t];
             if (!std::isfinite(score))
                 raise(BNNE_ECOMPUTE, "non-finite attention score");
-            scores_[t] = score;
             if (score > top)
                 top = score;
         }
@@ -324,12 +346,17 @@ void Qwen3Context::attend(uint32_t layer, uint32_t pos) {
             raise(BNNE_ECOMPUTE, "softmax normaliser is zero or not finite");
         for (uint32_t t = 0; t <= pos; ++t)
             probs_[t] /= total;
+        // out[i] = sum over t in position order of probs[t] * value[t][i]: the positions in
+        // the outer loop, so that each cache row is read once and in order (every out[i]
+        // still receives its terms in the same order, one rounding each)
         float* out = y_.data() + (size_t)h * HD;
-        for (uint32_t i = 0; i < HD; ++i) {
-            float acc = 0.0f;
-            for (uint32_t t = 0; t <= pos; ++t)
-                acc += probs_[t] * values[(size_t)t * s_.kv_width + kv_head + i];
-            out[i] = acc;
+        for (uint32_t i = 0; i < HD; ++i)
+            out[i] = 0.0f;
+        for (uint32_t t = 0; t <= pos; ++t) {
+            const float p = probs_[t];
+            const float* value = values + (size_t)t * s_.kv_width + kv_head;
+            for (uint32_t i = 0; i < HD; ++i)
+                out[i] += p * value[i];
         }
     }
 }
