@@ -508,12 +508,12 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_addr) {
 // head vectors would also wait for every row requested after them).  Then
 //   wave 0: the head norms and RoPE of q and of the kv head's new key (the cache row
 //   at pos stored by the kv head's first query head), while waves 1..3 load their
-//   key rows;
+//   key rows and request the V rows of positions below pos into LDS by DMA;
 //   the thread of position t <= pos: its score (in-order dot over head_dim; position
-//   pos from the new key itself); then waves 1..3 request the V rows of positions
-//   below pos into LDS by DMA, which arrive during
+//   pos from the new key itself);
 //   wave 0: the maximum, expf, the in-order sum and the probabilities;
-//   thread i < head_dim: value[i] = sum over t in order of p[t] * V[t][i], row pos from
+//   all waves: the products p[t] * V[t][i] in place;
+//   thread i < head_dim: value[i] = sum over t in order of the products, row pos from
 //   the new value itself -- no workgroup reads a cache row that another is writing.
 constexpr uint32_t kAttnOneMax = 256;
 
@@ -583,8 +583,18 @@ __global__ __launch_bounds__(256) void k_attn_one(
                 key[i] = row[i];
         }
     };
-    if (wave != 0)
+    if (wave != 0) {
         load_key();
+        // V rows 0..pos-1 (cache rows of earlier tokens) into LDS by DMA, behind the key
+        // rows: 16-byte piece ci = 32 * row + part at byte 16 * ci of vs4; wave w > 0 issues
+        // pieces (w - 1) * 64 + 192 * i + lane (pieces past the last row load row pos - 1
+        // again into unused space).  They land during the head norms and the scores.
+        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
+        for (uint32_t c0 = (wave - 1u) * 64u; c0 < 32u * pos; c0 += 192u) {
+            const uint32_t ci = c0 + lane, row = min(ci >> 5, pos - 1u);
+            dma16(vc + (size_t)row * kv_dim + head_off + 4u * (ci & 31u), base + 16u * c0);
+        }
+    }
     if (wave == 1)  // not on the norms' path
         exp_table_fill(exp_tab, lane);
     if (wave == 0) {
@@ -699,16 +709,6 @@ __global__ __launch_bounds__(256) void k_attn_one(
         if (!isfinite(score))
             set_error_first(err, code_base + 3 + 2 * (int)h);
         p[t] = score;
-    }
-    // V rows 0..pos-1: 16-byte piece ci = 32 * row + part at byte 16 * ci of vs4; wave
-    // w > 0 issues pieces (w - 1) * 64 + 192 * i + lane (pieces past the last row load
-    // row pos - 1 again into unused space)
-    if (wave != 0) {
-        const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)vs4;
-        for (uint32_t c0 = (wave - 1u) * 64u; c0 < 32u * pos; c0 += 192u) {
-            const uint32_t ci = c0 + lane, row = min(ci >> 5, pos - 1u);
-            dma16(vc + (size_t)row * kv_dim + head_off + 4u * (ci & 31u), base + 16u * c0);
-        }
     }
     block_lds_barrier();
 
