@@ -1461,10 +1461,14 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
     if (logits) {
         // to the caller's buffer, checking on the way that every logit is finite
         // (BNNE_Decode's own check, made here in the same pass)
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(r->pinned);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(logits);
+        // (the count and pointers in locals, restrict-qualified: the stores then cannot alias
+        // them and the loop runs as vector copies -- a per-element reload of the count had kept
+        // it scalar, tens of microseconds per token)
+        const uint32_t V = r->V;
+        const uint32_t* __restrict__ src = reinterpret_cast<const uint32_t*>(r->pinned);
+        uint32_t* __restrict__ dst = reinterpret_cast<uint32_t*>(logits);
         uint32_t bad = 0;
-        for (uint32_t i = 0; i < r->V; ++i) {
+        for (uint32_t i = 0; i < V; ++i) {
             const uint32_t u = src[i];
             dst[i] = u;
             bad |= (uint32_t)((u & 0x7F800000u) == 0x7F800000u);
