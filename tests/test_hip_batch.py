@@ -283,3 +283,58 @@ def test_device_index_contract(pkg, hip):
     caps = pkg.Caps()
     assert hip.BNN_DeviceGetCaps(h, ctypes.byref(caps)) == pkg.Status.OK and caps.max_in_features == 8192
     assert hip.BNN_DeviceClose(h) == pkg.Status.OK
+
+
+@pytest.mark.parametrize("specs", [
+    [("GEMV_F32", 2048, 6144, 1)] * 45,                                   # uniform, 45 rows (not a multiple of 8)
+    [("GEMV_F32", 2048, 6144, 1)] * 24 + [("GEMV", 1024, 8192, 1)] * 12 + [("DOT_GROUPS", 2048, 4096, 1)] * 6
+    + [("GEMV_F32", 640, 1000, 1)] * 3,                                   # mixed one-row jobs, table-mapped
+], ids=["uniform45", "mixed"])
+def test_full_chip_one_row_batch(pkg, hipdev, specs):
+    """Batches of one-row jobs with K <= 2048 and a full chip of 64-feature items (the
+    headline's form, on the one-wave-per-item kernel): the same results as single jobs,
+    through BNNX_ExecuteBatch and through repeated prepared launches, and an illegal row
+    writes nothing while the next launch works again."""
+    import ctypes
+    api = hipdev.api
+    mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs, seed=11)
+    items = sum(-(-n // 64) for _, _, n, _ in specs)
+    assert items >= 256 * 16  # enough items for the one-wave-per-item kernel
+    want = [hipdev.run(pkg.Op[op], mats[i], xs[i]) for i, (op, k, n, rows) in enumerate(specs)]
+    for rep in range(2):
+        assert api.BNNX_ExecuteBatch(hipdev.handle, jobs, len(specs)) == pkg.Status.OK
+        got = _outputs(bo, out_off, layouts)
+        for i, (op, k, n, rows) in enumerate(specs):
+            assert np.array_equal(got[i].view(np.uint8), want[i].view(np.uint8)), (rep, i, op, first_mismatch(got[i], want[i]))
+    b = ctypes.c_void_p()
+    assert api.BNNX_BatchCreate(hipdev.handle, jobs, len(specs), ctypes.byref(b)) == pkg.Status.OK
+    bo.write(np.zeros(bo.nbytes, np.uint8))
+    for rep in range(5):
+        assert api.BNNX_BatchLaunch(b) == pkg.Status.OK
+    assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.OK
+    got = _outputs(bo, out_off, layouts)
+    for i, (op, k, n, rows) in enumerate(specs):
+        assert np.array_equal(got[i].view(np.uint8), want[i].view(np.uint8)), ("prepared", i, op)
+    # one illegal value in the last job's row: no output of the launch is written
+    raw = bi.read()
+    o = jobs[len(specs) - 1].input.offset
+    bad = np.frombuffer(np.float32(np.inf).tobytes(), np.uint8) if specs[-1][0].endswith("F32") else np.array([0x80], np.uint8)
+    raw[o:o + bad.size] = bad
+    bi.write(raw)
+    sentinel = np.full(bo.nbytes, 0x5A, np.uint8)
+    bo.write(sentinel)
+    assert api.BNNX_BatchLaunch(b) == pkg.Status.OK
+    assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.ERANGE
+    assert np.array_equal(bo.read(), sentinel)
+    assert api.BNNX_ExecuteBatch(hipdev.handle, jobs, len(specs)) == pkg.Status.ERANGE
+    assert np.array_equal(bo.read(), sentinel)
+    # the row made legal again: the next launches compute everything
+    raw[o:o + bad.size] = np.frombuffer(xs[-1].view(np.uint8).reshape(-1)[:bad.size].tobytes(), np.uint8)
+    bi.write(raw)
+    assert api.BNNX_BatchLaunch(b) == pkg.Status.OK
+    assert api.BNNX_DeviceSynchronize(hipdev.handle) == pkg.Status.OK
+    got = _outputs(bo, out_off, layouts)
+    for i, (op, k, n, rows) in enumerate(specs):
+        assert np.array_equal(got[i].view(np.uint8), want[i].view(np.uint8)), ("after error", i, op)
+    api.BNNX_BatchDestroy(b)
+    _free(mats, bi, bo)
