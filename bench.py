@@ -272,7 +272,9 @@ def gemm_leg(pkg, hip):
     return {"peak_TOPS": 5000.0, "best_TOPS": round(best, 1), "cases": out}
 
 
-E2E_PATHS = {"device": 1, "prepared": 2, "host": 0}
+# device_greedy: the device path with the greedy loop on the device (BNNEX_DecodeGreedy,
+# one host wait for all the steps); the others return logits to the host every step
+E2E_PATHS = {"device": 1, "device_greedy": 1, "prepared": 2, "host": 0}
 
 
 def e2e_leg(pkg, hip, paths=tuple(E2E_PATHS), new=128):
@@ -302,8 +304,11 @@ def e2e_leg(pkg, hip, paths=tuple(E2E_PATHS), new=128):
                 tokens = [int(np.argmax(ctx.decode(prompt, out=logits)))]
                 t1 = time.perf_counter()
                 ctx.reset_stats()
-                for _ in range(new - 1):
-                    tokens.append(int(np.argmax(ctx.decode([tokens[-1]], out=logits))))
+                if name == "device_greedy":
+                    tokens += ctx.decode_greedy(tokens[-1], new - 1)
+                else:
+                    for _ in range(new - 1):
+                        tokens.append(int(np.argmax(ctx.decode([tokens[-1]], out=logits))))
                 t2 = time.perf_counter()
                 st = ctx.stats()
                 ctx.free()
@@ -401,7 +406,7 @@ def main():
     if args.only:
         e2e_paths = tuple(p for p in args.e2e_paths.split(",") if p)
         if not e2e_paths or any(p not in E2E_PATHS for p in e2e_paths) or not 2 <= args.e2e_new <= 128:
-            ap.error("--e2e-paths takes device, prepared, host; --e2e-new 2..128")
+            ap.error("--e2e-paths takes " + ", ".join(E2E_PATHS) + "; --e2e-new 2..128")
         legs = {"ops": ops_leg, "gemm": gemm_leg, "mlp": mlp_leg,
                 "e2e": lambda pkg, hip: e2e_leg(pkg, hip, e2e_paths, args.e2e_new)}
         print(json.dumps({args.only: legs[args.only](pkg, hip)}), flush=True)

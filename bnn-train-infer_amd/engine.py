@@ -74,6 +74,7 @@ class EngineLib:
             "BNNE_LastError": (ctypes.c_char_p, []),
             "BNNEX_ContextSetResident": (ctypes.c_int, [vp, ctypes.c_int]),
             "BNNEX_ContextIsResident": (ctypes.c_int, [vp]),
+            "BNNEX_DecodeGreedy": (ctypes.c_int, [vp, i32, u32, ctypes.POINTER(i32)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(lib, name)
@@ -126,6 +127,15 @@ class Context:
                                             out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) if want_logits
                                             else None), "BNNE_Decode")
         return out
+
+    def decode_greedy(self, token: int, steps: int) -> list[int]:
+        """BNNEX_DecodeGreedy: `steps` one-token decode steps from `token`, each next token
+        the argmax of the previous logits; the argmax after every step."""
+        out = np.empty(steps, np.int32)
+        self.eng.check(self.eng.BNNEX_DecodeGreedy(self.handle, int(token), int(steps),
+                                                   out.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))),
+                       "BNNEX_DecodeGreedy")
+        return out.tolist()
 
     def classify(self, x: np.ndarray) -> np.ndarray:
         x = np.ascontiguousarray(x, dtype=np.float32)

@@ -285,3 +285,24 @@ BNNE_EXPORT BNNE_Status BNNEX_ContextSetResident(BNNE_Context ctx, int path) {
 }
 
 BNNE_EXPORT int BNNEX_ContextIsResident(BNNE_Context ctx) { return ctx ? qwen3_path(ctx) : 0; }
+
+BNNE_EXPORT BNNE_Status BNNEX_DecodeGreedy(BNNE_Context ctx, int32_t token, uint32_t n_steps, int32_t* out_tokens) {
+    forget_message();
+    if (!ctx || !out_tokens || n_steps == 0)
+        return BNNE_EINVAL;
+    const BNNE_ModelInfo& info = ctx->model->info;
+    if (info.task != BNNE_TASK_LLM)
+        return complain(BNNE_ENOTSUP, "the model is not a language model");
+    if (ctx->pos > ctx->params.n_ctx || n_steps > ctx->params.n_ctx - ctx->pos)
+        return complain(BNNE_ERANGE, "%u steps do not fit the remaining context", n_steps);
+    if (token < 0 || (uint32_t)token >= info.n_vocab)
+        return complain(BNNE_ERANGE, "token %d is not in the vocabulary", token);
+    CallStats call(*ctx);
+    const uint32_t pos0 = ctx->pos;
+    const BNNE_Status st = guarded([&] { ctx->decode_greedy(token, n_steps, out_tokens); });
+    if (st != BNNE_OK)
+        return st;
+    ctx->pos = pos0 + n_steps;
+    call.done(n_steps);
+    return BNNE_OK;
+}

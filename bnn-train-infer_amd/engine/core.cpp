@@ -125,4 +125,28 @@ void bnne_context::decode(const int32_t*, uint32_t, float*) {
     bnne::raise(BNNE_ENOTSUP, "this model does not decode tokens");
 }
 
+void bnne_context::decode_greedy(int32_t token, uint32_t n, int32_t* out) {
+    std::vector<float> logits(model->info.n_vocab);
+    const uint32_t pos0 = pos;
+    struct Restore {
+        bnne_context& c;
+        uint32_t pos0;
+        ~Restore() { c.pos = pos0; }
+    } restore{*this, pos0};
+    for (uint32_t i = 0; i < n; ++i) {
+        logits_checked = false;
+        decode(&token, 1, logits.data());
+        uint32_t best = 0;
+        for (uint32_t v = 0; v < (uint32_t)logits.size(); ++v) {
+            if (!std::isfinite(logits[v]))
+                bnne::raise(BNNE_ECOMPUTE, "the logits hold a NaN or infinity");
+            if (logits[v] > logits[best])
+                best = v;
+        }
+        token = (int32_t)best;
+        out[i] = token;
+        ++pos;
+    }
+}
+
 void bnne_context::rewind(uint32_t) {}

@@ -263,6 +263,9 @@ struct bnne_context {
 
     virtual void classify(const float* input, uint32_t n, float* logits);
     virtual void decode(const int32_t* tokens, uint32_t n, float* logits);
+    // n decode steps from `token` at pos, each next token the previous step's argmax
+    // (bnn-infer-v2.c:48-54), out[i] the argmax after step i; leaves pos as it found it
+    virtual void decode_greedy(int32_t token, uint32_t n, int32_t* out);
     virtual void rewind(uint32_t pos);
 
     // The statistics counter `field`, or null when statistics are off.

@@ -171,6 +171,7 @@ public:
     Qwen3Context(Qwen3Model& m, const BNNE_ContextParams& p);
     ~Qwen3Context() override { resident_free(device_); }
     void decode(const int32_t* tokens, uint32_t n, float* logits) override;
+    void decode_greedy(int32_t token, uint32_t n, int32_t* out) override;
 
     // 0 host step, 1 device path with fused batches, 2 device path with prepared batches
     int path() const { return device_ ? (resident_fused(device_) ? 1 : 2) : 0; }
@@ -420,6 +421,16 @@ void Qwen3Context::decode(const int32_t* tokens, uint32_t n, float* logits) {
     }
     for (uint32_t i = 0; i < n; ++i)
         step((uint32_t)tokens[i], pos + i, i + 1 == n ? logits : nullptr);
+}
+
+void Qwen3Context::decode_greedy(int32_t token, uint32_t n, int32_t* out) {
+    if (!device_) {
+        bnne_context::decode_greedy(token, n, out);
+        return;
+    }
+    const BNNE_Status st = resident_greedy(this, device_, token, n, pos, out);
+    if (st != BNNE_OK)
+        throw Failure{st};
 }
 
 bnne_context* Qwen3Model::new_context(const BNNE_ContextParams& p) { return new Qwen3Context(*this, p); }

@@ -51,6 +51,12 @@ bool resident_fused(const Resident* r);
 // non-null.  Enqueues everything, waits once.
 BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, uint32_t n, uint32_t pos0,
                           float* logits);
+// Greedy decoding of n tokens on the device, as n calls of resident_step with logits,
+// each followed by the caller's argmax (bnn-infer-v2.c:48-54) fed back as the next
+// token: `token` at pos0, then each argmax; out_tokens[i] the argmax after step i.  The
+// host waits once, after the last step.
+BNNE_Status resident_greedy(bnne_context* c, Resident* r, int32_t token, uint32_t n, uint32_t pos0,
+                            int32_t* out_tokens);
 void resident_free(Resident* r);
 
 }  // namespace bnne

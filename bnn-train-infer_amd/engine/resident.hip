@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <algorithm>
 
 #include "bnn-accelerator-hip.h"
 #include "resident.h"
@@ -111,16 +112,78 @@ __device__ void set_error(int* err, int code) { atomicCAS(err, kErrNone, code); 
 
 extern "C" __device__ float __ockl_wfred_max_f32(float);
 
-// x[i] = +scale or -scale of the token's Q1_0 embedding row (qwen3.c:355-366).
-__global__ __launch_bounds__(256) void k_embed(uint32_t token, const uint8_t* __restrict__ bits,
+// Greedy decoding on the device takes the caller's argmax (bnn-infer-v2.c:48-54: the
+// first index of the largest logit) as the largest of 64-bit keys: the order-preserving
+// image of the value's bits above the complement of the index, so that equal values
+// order by the smaller index.  -0 is made +0 first (the reference compares values, and
+// -0 == +0).  Every key is nonzero, and the index it carries is one of the logits'.
+__device__ __forceinline__ unsigned long long logit_key(float v, uint32_t i) {
+    const uint32_t b = __float_as_uint(v + 0.0f);
+    const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)ord << 32) | (0xffffffffu - i);
+}
+__device__ __forceinline__ uint32_t key_token(unsigned long long key) { return 0xffffffffu - (uint32_t)key; }
+
+// x[i] = +scale or -scale of the token's Q1_0 embedding row (qwen3.c:355-366).  In a
+// greedy run the token is the one the previous step's argmax left in *key_in; the first
+// workgroup records it in *tok_out and clears *key_reset for this step's argmax.
+__global__ __launch_bounds__(256) void k_embed(uint32_t token, const unsigned long long* __restrict__ key_in,
+                                               int32_t* __restrict__ tok_out, unsigned long long* __restrict__ key_reset,
+                                               const uint8_t* __restrict__ bits,
                                                const uint16_t* __restrict__ scales, uint32_t C,
                                                float* __restrict__ x) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (key_in)
+        token = key_token(*key_in);
+    if (i == 0) {
+        if (tok_out)
+            *tok_out = (int32_t)token;
+        if (key_reset)
+            *key_reset = 0;
+    }
     if (i >= C)
         return;
     const float s = __half2float(__ushort_as_half(scales[(size_t)token * (C / 128u) + i / 128u]));
     const bool bit = (bits[(size_t)token * (C / 8u) + i / 8u] >> (i & 7u)) & 1u;
     x[i] = bit ? s : -s;
+}
+
+// The argmax of the logits as the largest key (above), merged into *key, which the
+// step's embedding launch cleared; a non-finite logit sets *bad (the engine's check of
+// the logits).
+constexpr uint32_t kArgmaxThreads = 256;
+__global__ __launch_bounds__(kArgmaxThreads) void k_argmax(const float* __restrict__ logits, uint32_t V,
+                                                           unsigned long long* __restrict__ key, int* __restrict__ bad) {
+    __shared__ unsigned long long wave_best[kArgmaxThreads / 64u];
+    unsigned long long best = 0;
+    bool nonfinite = false;
+    for (uint32_t i = blockIdx.x * kArgmaxThreads + threadIdx.x; i < V; i += gridDim.x * kArgmaxThreads) {
+        const float v = logits[i];
+        nonfinite |= !__builtin_isfinite(v);
+        best = max(best, logit_key(v, i));
+    }
+    if (nonfinite)
+        *bad = 1;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)best, off), hi = __shfl_xor((uint32_t)(best >> 32), off);
+        best = max(best, ((unsigned long long)hi << 32) | lo);
+    }
+    if ((threadIdx.x & 63u) == 0)
+        wave_best[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (uint32_t w = 1; w < kArgmaxThreads / 64u; ++w)
+            best = max(best, wave_best[w]);
+        atomicMax(key, best);
+    }
+}
+
+// The last greedy step's token, which no later embedding launch records.
+__global__ __launch_bounds__(64) void k_key_token(const unsigned long long* __restrict__ key, int32_t* __restrict__ out) {
+    if (threadIdx.x == 0)
+        *out = (int32_t)key_token(*key);
 }
 
 // [x += add] then out = x / rms * gain, rms = sqrt(sum x^2 / n + eps) with the sum
@@ -963,6 +1026,13 @@ struct Resident {
     // pinned host memory: V floats of logits, then the error word; both are copied back
     // on the stream behind a step's last launch, so the host waits once per step
     float* pinned;
+    // greedy runs: two argmax keys (steps alternate), the logits-check flag, then the
+    // tokens [n_ctx] (device); the tokens and the flag come back into pinned_tokens
+    // [n_ctx + 1]
+    unsigned long long* keys;
+    int* logit_bad;
+    int32_t* tokens_dev;
+    int32_t* pinned_tokens;
     // fused: every linear layer is a fused batch (its input row produced and
     // quantised inside its one launch), else prepared batches plus this engine's
     // norm and SiLU kernels (models wider than a fused batch takes)
@@ -1286,6 +1356,20 @@ BNNE_Status resident_create(bnne_context* c, const ResidentModel& m, bool fused,
         st = hip_error(e, "hipHostMalloc");
     }
     if (st == BNNE_OK) {
+        st = upload(&r->keys, nullptr, 2 * sizeof(unsigned long long) + sizeof(int) * (2u + (size_t)m.n_ctx));
+        if (st == BNNE_OK) {
+            r->logit_bad = reinterpret_cast<int*>(r->keys + 2);
+            r->tokens_dev = reinterpret_cast<int32_t*>(r->logit_bad + 2);
+            if ((e = hipMemset(r->logit_bad, 0, sizeof(int))) != hipSuccess)
+                st = hip_error(e, "hipMemset");
+        }
+    }
+    if (st == BNNE_OK && (e = hipHostMalloc(reinterpret_cast<void**>(&r->pinned_tokens),
+                                            ((size_t)m.n_ctx + 1u) * sizeof(int32_t))) != hipSuccess) {
+        r->pinned_tokens = nullptr;
+        st = hip_error(e, "hipHostMalloc");
+    }
+    if (st == BNNE_OK) {
         r->qkv = static_cast<BNNX_Batch*>(std::calloc(m.L, sizeof(BNNX_Batch)));
         r->attn_out = static_cast<BNNX_Batch*>(std::calloc(m.L, sizeof(BNNX_Batch)));
         r->gate_up = static_cast<BNNX_Batch*>(std::calloc(m.L, sizeof(BNNX_Batch)));
@@ -1325,21 +1409,35 @@ void resident_free(Resident* r) {
     for (BNN_Buffer b : {r->b_norm, r->b_q, r->b_k, r->b_v, r->b_y, r->b_o, r->b_gate, r->b_up, r->b_h, r->b_logits})
         BNN_BufferFree(b);
     for (void* p : {(void*)r->x, (void*)r->x2, (void*)r->kc, (void*)r->vc, (void*)r->scores, (void*)r->gains, (void*)r->rope_cos,
-                    (void*)r->rope_sin, (void*)r->emb_bits, (void*)r->emb_scales, (void*)r->err})
+                    (void*)r->rope_sin, (void*)r->emb_bits, (void*)r->emb_scales, (void*)r->err, (void*)r->keys})
         if (p)
             (void)hipFree(p);
     if (r->pinned)
         (void)hipHostFree(r->pinned);
+    if (r->pinned_tokens)
+        (void)hipHostFree(r->pinned_tokens);
     std::free(r);
 }
 
-BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, uint32_t n, uint32_t pos0,
-                          float* logits) {
-    const bool stats = c->params.enable_stats != 0;
-    const uint64_t t0 = stats ? clock_ns() : 0;
-    hipError_t e = hipSetDevice(r->ordinal);
-    if (e != hipSuccess)
-        return hip_error(e, "hipSetDevice");
+namespace {
+
+// Stale prepared batches (any matrix or buffer of the device destroyed since: another
+// context, another model) are rebuilt; nothing can be destroyed during a step, so
+// checking one batch decides for all of them.
+BNNE_Status ready_batches(Resident* r) {
+    const BNN_Status valid = BNNX_BatchCheck(r->qkv[0]);
+    if (valid == BNN_EINVAL) {
+        destroy_batches(r);
+        return build_batches(r);
+    }
+    return valid == BNN_OK ? BNNE_OK : accel_status(valid, "BNNX_BatchCheck");
+}
+
+// The launches of one token at position pos: its embedding row (of `token`, or of the
+// token a greedy step's argmax left in *key_in, recorded in *tok_out, with *key_reset
+// cleared), the layers, and the lm_head when `head`.
+BNNE_Status enqueue_token(Resident* r, uint32_t pos, uint32_t token, const unsigned long long* key_in,
+                          int32_t* tok_out, unsigned long long* key_reset, bool head) {
     const uint32_t C = r->C, HD = r->HD, half = HD / 2u;
     const float scale = 1.0f / sqrtf((float)HD);
     const float* attn_norm = r->gains;
@@ -1349,82 +1447,94 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
     const float* final_norm = k_norm + (size_t)r->L * HD;
     const size_t norm_lds = (size_t)C * sizeof(float);
     BNNE_Status st = BNNE_OK;
-    // Prepared batches go stale when any matrix or buffer of the device is destroyed
-    // (another context, another model); nothing can be destroyed during a step, so
-    // checking one batch decides for all of them.
-    const BNN_Status valid = BNNX_BatchCheck(r->qkv[0]);
-    if (valid == BNN_EINVAL) {
-        destroy_batches(r);
-        st = build_batches(r);
-        if (st != BNNE_OK)
-            return st;
-    } else if (valid != BNN_OK) {
-        return accel_status(valid, "BNNX_BatchCheck");
-    }
     auto launch = [&](BNNX_Batch b) {
         if (st == BNNE_OK)
             st = accel_status(BNNX_BatchLaunch(b), "BNNX_BatchLaunch");
     };
-    for (uint32_t i = 0; i < n && st == BNNE_OK && r->fused; ++i) {
-        const uint32_t pos = pos0 + i;
-        hipLaunchKernelGGL(k_embed, dim3((C + 255u) / 256u), dim3(256), 0, r->stream, (uint32_t)tokens[i],
-                           r->emb_bits, r->emb_scales, C, r->x);
-        for (uint32_t l = 0; l < r->L && st == BNNE_OK; ++l) {
-            const size_t cache_layer = (size_t)l * r->n_ctx * r->kv_dim;
-            launch(r->qkv[l]);
-            if (pos < kAttnOneMax) {
-                hipLaunchKernelGGL(k_attn_one, dim3(r->H), dim3(256), 0, r->stream, r->q, r->k, r->v, r->H / r->Hk,
-                                   r->eps, q_norm + (size_t)l * HD, k_norm + (size_t)l * HD,
-                                   r->rope_cos + (size_t)pos * half, r->rope_sin + (size_t)pos * half,
-                                   r->kc + cache_layer, r->vc + cache_layer, pos, r->kv_dim, scale, r->y, r->err,
-                                   (int)l * code_span(r));
-            } else {
-                hipLaunchKernelGGL(k_attn_scores, dim3(r->H, pos / kScoreBlock + 1u), dim3(kScoreBlock), 0,
-                                   r->stream, r->q, r->k, r->v, r->H / r->Hk, r->eps, q_norm + (size_t)l * HD,
-                                   k_norm + (size_t)l * HD, r->rope_cos + (size_t)pos * half,
-                                   r->rope_sin + (size_t)pos * half, r->kc + cache_layer, r->vc + cache_layer, pos,
-                                   r->kv_dim, scale, r->scores, r->n_ctx, r->err, (int)l * code_span(r));
-                hipLaunchKernelGGL(k_attn_pv, dim3(r->H, HD / kPvSlice), dim3(128), 0, r->stream, r->scores,
-                                   r->vc + cache_layer, r->H / r->Hk, pos, r->kv_dim, r->n_ctx, r->y, r->err,
-                                   (int)l * code_span(r));
-            }
-            launch(r->attn_out[l]);
-            launch(r->gate_up[l]);
-            launch(r->down[l]);
-        }
-        if (logits && i + 1 == n)
-            launch(r->lm_head);
-    }
-    for (uint32_t i = 0; i < n && st == BNNE_OK && !r->fused; ++i) {
-        const uint32_t pos = pos0 + i;
-        hipLaunchKernelGGL(k_embed, dim3((C + 255u) / 256u), dim3(256), 0, r->stream, (uint32_t)tokens[i],
-                           r->emb_bits, r->emb_scales, C, r->x);
-        for (uint32_t l = 0; l < r->L && st == BNNE_OK; ++l) {
-            const size_t cache_layer = (size_t)l * r->n_ctx * r->kv_dim;
-            hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kNormThreads), norm_lds, r->stream, r->x, l ? r->o : nullptr, C,
-                               r->eps, attn_norm + (size_t)l * C, r->norm, r->err);
-            launch(r->qkv[l]);
-            hipLaunchKernelGGL(k_head_norm_rope, dim3(r->H + r->Hk), dim3(64), 0, r->stream, r->q, r->k, r->v, r->H,
-                               HD, r->eps, q_norm + (size_t)l * HD, k_norm + (size_t)l * HD,
+    hipLaunchKernelGGL(k_embed, dim3((C + 255u) / 256u), dim3(256), 0, r->stream, token, key_in, tok_out, key_reset,
+                       r->emb_bits, r->emb_scales, C, r->x);
+    for (uint32_t l = 0; l < r->L && st == BNNE_OK && r->fused; ++l) {
+        const size_t cache_layer = (size_t)l * r->n_ctx * r->kv_dim;
+        launch(r->qkv[l]);
+        if (pos < kAttnOneMax) {
+            hipLaunchKernelGGL(k_attn_one, dim3(r->H), dim3(256), 0, r->stream, r->q, r->k, r->v, r->H / r->Hk,
+                               r->eps, q_norm + (size_t)l * HD, k_norm + (size_t)l * HD,
                                r->rope_cos + (size_t)pos * half, r->rope_sin + (size_t)pos * half,
-                               r->kc + cache_layer + (size_t)pos * r->kv_dim,
-                               r->vc + cache_layer + (size_t)pos * r->kv_dim, r->err);
-            hipLaunchKernelGGL(k_attention, dim3(r->H), dim3(256), 0, r->stream, r->q, r->kc + cache_layer,
-                               r->vc + cache_layer, pos, r->kv_dim, HD, r->H / r->Hk, scale, r->scores, r->n_ctx,
-                               r->y, r->err);
-            launch(r->attn_out[l]);
-            hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kNormThreads), norm_lds, r->stream, r->x, r->o, C, r->eps,
-                               ffn_norm + (size_t)l * C, r->norm, r->err);
-            launch(r->gate_up[l]);
-            hipLaunchKernelGGL(k_silu_mul, dim3((r->FF + 255u) / 256u), dim3(256), 0, r->stream, r->gate, r->up, r->FF);
-            launch(r->down[l]);
+                               r->kc + cache_layer, r->vc + cache_layer, pos, r->kv_dim, scale, r->y, r->err,
+                               (int)l * code_span(r));
+        } else {
+            hipLaunchKernelGGL(k_attn_scores, dim3(r->H, pos / kScoreBlock + 1u), dim3(kScoreBlock), 0,
+                               r->stream, r->q, r->k, r->v, r->H / r->Hk, r->eps, q_norm + (size_t)l * HD,
+                               k_norm + (size_t)l * HD, r->rope_cos + (size_t)pos * half,
+                               r->rope_sin + (size_t)pos * half, r->kc + cache_layer, r->vc + cache_layer, pos,
+                               r->kv_dim, scale, r->scores, r->n_ctx, r->err, (int)l * code_span(r));
+            hipLaunchKernelGGL(k_attn_pv, dim3(r->H, HD / kPvSlice), dim3(128), 0, r->stream, r->scores,
+                               r->vc + cache_layer, r->H / r->Hk, pos, r->kv_dim, r->n_ctx, r->y, r->err,
+                               (int)l * code_span(r));
         }
-        if (logits && i + 1 == n) {
-            hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kNormThreads), norm_lds, r->stream, r->x, r->o, C, r->eps, final_norm,
-                               r->norm, r->err);
-            launch(r->lm_head);
-        }
+        launch(r->attn_out[l]);
+        launch(r->gate_up[l]);
+        launch(r->down[l]);
     }
+    for (uint32_t l = 0; l < r->L && st == BNNE_OK && !r->fused; ++l) {
+        const size_t cache_layer = (size_t)l * r->n_ctx * r->kv_dim;
+        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kNormThreads), norm_lds, r->stream, r->x, l ? r->o : nullptr, C,
+                           r->eps, attn_norm + (size_t)l * C, r->norm, r->err);
+        launch(r->qkv[l]);
+        hipLaunchKernelGGL(k_head_norm_rope, dim3(r->H + r->Hk), dim3(64), 0, r->stream, r->q, r->k, r->v, r->H,
+                           HD, r->eps, q_norm + (size_t)l * HD, k_norm + (size_t)l * HD,
+                           r->rope_cos + (size_t)pos * half, r->rope_sin + (size_t)pos * half,
+                           r->kc + cache_layer + (size_t)pos * r->kv_dim,
+                           r->vc + cache_layer + (size_t)pos * r->kv_dim, r->err);
+        hipLaunchKernelGGL(k_attention, dim3(r->H), dim3(256), 0, r->stream, r->q, r->kc + cache_layer,
+                           r->vc + cache_layer, pos, r->kv_dim, HD, r->H / r->Hk, scale, r->scores, r->n_ctx,
+                           r->y, r->err);
+        launch(r->attn_out[l]);
+        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kNormThreads), norm_lds, r->stream, r->x, r->o, C, r->eps,
+                           ffn_norm + (size_t)l * C, r->norm, r->err);
+        launch(r->gate_up[l]);
+        hipLaunchKernelGGL(k_silu_mul, dim3((r->FF + 255u) / 256u), dim3(256), 0, r->stream, r->gate, r->up, r->FF);
+        launch(r->down[l]);
+    }
+    if (head && st == BNNE_OK && !r->fused)
+        hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kNormThreads), norm_lds, r->stream, r->x, r->o, C, r->eps,
+                           final_norm, r->norm, r->err);
+    if (head)
+        launch(r->lm_head);
+    return st;
+}
+
+// The step's error word (read back into pinned memory), cleared on the device when set,
+// as the engine's status.
+BNNE_Status step_error(Resident* r, int err) {
+    hipError_t e;
+    if (err != kErrNone && (e = hipMemset(r->err, 0, sizeof(int))) != hipSuccess)
+        return hip_error(e, "error word");
+    int kind = err;
+    if (r->fused && err != kErrNone) {
+        const int p = err % code_span(r);  // 1: attention norm, 2: head norms, 3 + 2H: FFN norm
+        kind = p == 1 || p == 2 || p == code_span(r) - 1 ? kErrNorm : ((p - 3) % 2 == 0 ? kErrScore : kErrSoftmax);
+    }
+    if (kind == kErrNorm)
+        return complain(BNNE_ECOMPUTE, "RMSNorm divisor is zero or not finite");
+    if (kind == kErrScore)
+        return complain(BNNE_ECOMPUTE, "non-finite attention score");
+    if (kind == kErrSoftmax)
+        return complain(BNNE_ECOMPUTE, "softmax normaliser is zero or not finite");
+    return BNNE_OK;
+}
+
+}  // namespace
+
+BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, uint32_t n, uint32_t pos0,
+                          float* logits) {
+    const bool stats = c->params.enable_stats != 0;
+    hipError_t e = hipSetDevice(r->ordinal);
+    if (e != hipSuccess)
+        return hip_error(e, "hipSetDevice");
+    BNNE_Status st = ready_batches(r);
+    for (uint32_t i = 0; i < n && st == BNNE_OK; ++i)
+        st = enqueue_token(r, pos0 + i, (uint32_t)tokens[i], nullptr, nullptr, nullptr, logits && i + 1 == n);
     e = hipGetLastError();
     // the error word and the logits come back behind the last launch, into pinned memory
     int* const err_host = reinterpret_cast<int*>(r->pinned + r->V);
@@ -1441,20 +1551,9 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         return hip_error(e, "kernel launch");
     if (sync == BNN_EIO)
         return accel_status(sync, "BNN_Execute");
-    const int err = *static_cast<volatile int*>(err_host);
-    if (err != kErrNone && (e = hipMemset(r->err, 0, sizeof(int))) != hipSuccess)
-        return hip_error(e, "error word");
-    int kind = err;
-    if (r->fused && err != kErrNone) {
-        const int p = err % code_span(r);  // 1: attention norm, 2: head norms, 3 + 2H: FFN norm
-        kind = p == 1 || p == 2 || p == code_span(r) - 1 ? kErrNorm : ((p - 3) % 2 == 0 ? kErrScore : kErrSoftmax);
-    }
-    if (kind == kErrNorm)
-        return complain(BNNE_ECOMPUTE, "RMSNorm divisor is zero or not finite");
-    if (kind == kErrScore)
-        return complain(BNNE_ECOMPUTE, "non-finite attention score");
-    if (kind == kErrSoftmax)
-        return complain(BNNE_ECOMPUTE, "softmax normaliser is zero or not finite");
+    st = step_error(r, *static_cast<volatile int*>(err_host));
+    if (st != BNNE_OK)
+        return st;
     st = accel_status(sync, "BNN_Execute");
     if (st != BNNE_OK)
         return st;
@@ -1486,7 +1585,68 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         c->stats.bytes_read += lm * r->V * sizeof(float);
         c->stats.logical_macs += n * r->macs_per_token + lm * r->lm_macs;
         c->stats.executed_macs += n * r->macs_per_token + lm * r->lm_macs;
-        (void)t0;
+    }
+    return BNNE_OK;
+}
+
+BNNE_Status resident_greedy(bnne_context* c, Resident* r, int32_t token, uint32_t n, uint32_t pos0,
+                            int32_t* out_tokens) {
+    const bool stats = c->params.enable_stats != 0;
+    hipError_t e = hipSetDevice(r->ordinal);
+    if (e != hipSuccess)
+        return hip_error(e, "hipSetDevice");
+    BNNE_Status st = ready_batches(r);
+    // step i embeds the token step i - 1's argmax left in keys[(i - 1) % 2] and clears
+    // keys[i % 2] for its own argmax; nothing returns to the host until the last step
+    const uint32_t argmax_grid = std::min<uint32_t>((r->V + 4u * kArgmaxThreads - 1u) / (4u * kArgmaxThreads), 1024u);
+    for (uint32_t i = 0; i < n && st == BNNE_OK; ++i) {
+        st = enqueue_token(r, pos0 + i, (uint32_t)token, i ? r->keys + ((i - 1u) & 1u) : nullptr,
+                           i ? r->tokens_dev + (i - 1u) : nullptr, r->keys + (i & 1u), true);
+        if (st == BNNE_OK)
+            hipLaunchKernelGGL(k_argmax, dim3(argmax_grid), dim3(kArgmaxThreads), 0, r->stream, r->logits_dev, r->V,
+                               r->keys + (i & 1u), r->logit_bad);
+    }
+    if (st == BNNE_OK)
+        hipLaunchKernelGGL(k_key_token, dim3(1), dim3(64), 0, r->stream, r->keys + ((n - 1u) & 1u),
+                           r->tokens_dev + (n - 1u));
+    e = hipGetLastError();
+    // the error word, the logits flag and the tokens come back behind the last launch
+    int* const err_host = reinterpret_cast<int*>(r->pinned + r->V);
+    if (st == BNNE_OK && e == hipSuccess)
+        e = hipMemcpyAsync(err_host, r->err, sizeof(int), hipMemcpyDeviceToHost, r->stream);
+    if (st == BNNE_OK && e == hipSuccess)
+        e = hipMemcpyAsync(r->pinned_tokens + n, r->logit_bad, sizeof(int), hipMemcpyDeviceToHost, r->stream);
+    if (st == BNNE_OK && e == hipSuccess)
+        e = hipMemcpyAsync(r->pinned_tokens, r->tokens_dev, (size_t)n * sizeof(int32_t), hipMemcpyDeviceToHost,
+                           r->stream);
+    const uint64_t t1 = stats ? clock_ns() : 0;
+    const BNN_Status sync = BNNX_DeviceSynchronize(r->dev);
+    const uint64_t t2 = stats ? clock_ns() : 0;
+    if (st != BNNE_OK)
+        return st;
+    if (e != hipSuccess)
+        return hip_error(e, "kernel launch");
+    if (sync == BNN_EIO)
+        return accel_status(sync, "BNN_Execute");
+    st = step_error(r, *static_cast<volatile int*>(err_host));
+    if (st != BNNE_OK)
+        return st;
+    st = accel_status(sync, "BNN_Execute");
+    if (st != BNNE_OK)
+        return st;
+    if (*static_cast<volatile int32_t*>(r->pinned_tokens + n) != 0) {
+        if ((e = hipMemset(r->logit_bad, 0, sizeof(int))) != hipSuccess)
+            return hip_error(e, "logits flag");
+        return complain(BNNE_ECOMPUTE, "the logits hold a NaN or infinity");
+    }
+    std::memcpy(out_tokens, r->pinned_tokens, (size_t)n * sizeof(int32_t));
+    if (stats) {
+        c->stats.execute_ns += t2 - t1;
+        c->stats.transfer_ns += clock_ns() - t2;
+        c->stats.device_calls += n * (r->jobs_per_token + r->lm_jobs);
+        c->stats.bytes_read += n * sizeof(int32_t);
+        c->stats.logical_macs += n * (r->macs_per_token + r->lm_macs);
+        c->stats.executed_macs += n * (r->macs_per_token + r->lm_macs);
     }
     return BNNE_OK;
 }

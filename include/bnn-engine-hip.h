@@ -34,6 +34,16 @@ BNNE_Status BNNEX_ContextSetResident(BNNE_Context ctx, int enable);
  * prepared batches. */
 int BNNEX_ContextIsResident(BNNE_Context ctx);
 
+/* Greedy decoding: n_steps BNNE_Decode calls of one token each, the first of `token`,
+ * every later one of the argmax of the previous logits (the first index of the largest
+ * value, as bnn-infer-v2.c:48-54 picks it); out_tokens[i] receives the argmax after
+ * step i.  The same tokens as that loop; on the device path every step, its argmax
+ * included, stays on the device and the host waits once.  No EOG test: the caller
+ * truncates at the first end-of-generation token (BNNE_ContextTruncate).  On success
+ * the position advances by n_steps; on an error (BNNE_ECOMPUTE for non-finite logits
+ * or norms, as BNNE_Decode) it is left where it was and out_tokens is undefined. */
+BNNE_Status BNNEX_DecodeGreedy(BNNE_Context ctx, int32_t token, uint32_t n_steps, int32_t* out_tokens);
+
 #ifdef __cplusplus
 }
 #endif

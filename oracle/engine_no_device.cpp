@@ -20,6 +20,10 @@ BNNE_Status resident_step(bnne_context*, Resident*, const int32_t*, uint32_t, ui
     return complain(BNNE_ENOTSUP, "this build of the engine has no device path");
 }
 
+BNNE_Status resident_greedy(bnne_context*, Resident*, int32_t, uint32_t, uint32_t, int32_t*) {
+    return complain(BNNE_ENOTSUP, "this build of the engine has no device path");
+}
+
 void resident_free(Resident*) {}
 
 }  // namespace bnne

@@ -494,6 +494,91 @@ def test_engine_qwen3_1p7b_matches_reference(pkg, tmp_path, path):
     assert parse_llm(out) == full["steps"]
 
 
+def _prefill(ctx, prompt, n_batch):
+    logits = None
+    for i in range(0, len(prompt), n_batch):
+        logits = ctx.decode(prompt[i:i + n_batch])
+    return int(np.argmax(logits))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("resident", [1, 2, 0], ids=["device", "prepared", "host"])
+def test_engine_greedy_decode(pkg, hip, tmp_path, resident):
+    """BNNEX_DecodeGreedy: the tokens of the reference loop (bnn-infer-v2.c:246-279, its
+    argmax at :48-54) over the tiny model, the position advanced by the steps taken, and
+    its argument checks leaving the position alone."""
+    model_path, _ = write_tiny(pkg, tmp_path)
+    eng = _engine_lib(pkg)
+    want = [row[1] for row in TINY["steps"]]
+    with pkg.Device(hip, 0) as dev:
+        m = pkg.engine.Model(eng, dev, model_path)
+        c = pkg.engine.Context(m, n_ctx=TINY["ctx"])
+        c.set_resident(resident)
+        print(f"greedy decode, tiny model, path {resident}", flush=True)
+        first = _prefill(c, TINY["prompt"], len(TINY["prompt"]))
+        assert first == want[0]
+        got = c.decode_greedy(first, len(want) - 1)
+        assert [first] + got == want
+        pos = len(TINY["prompt"]) + len(want) - 1
+        assert c.pos() == pos
+        s = c.stats()
+        assert s["items"] == len(TINY["prompt"]) + len(want) - 1
+        for token, steps in ((TINY["model"]["vocab"], 1), (-1, 1), (0, TINY["ctx"] - pos + 1)):
+            with pytest.raises(pkg.engine.EngineError) as e:
+                c.decode_greedy(token, steps)
+            assert e.value.status == -4 and c.pos() == pos
+        out = (ctypes.c_int32 * 1)()
+        assert eng.BNNEX_DecodeGreedy(c.handle, 0, 0, out) == -1
+        assert eng.BNNEX_DecodeGreedy(c.handle, 0, 1, None) == -1
+        # the same steps again from a truncated context
+        assert eng.BNNE_ContextTruncate(c.handle, len(TINY["prompt"]) + 3) == 0
+        assert c.decode_greedy(want[3], len(want) - 4) == want[4:]
+        c.free()
+        m.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("resident", [1, 2], ids=["device", "prepared"])
+def test_engine_greedy_decode_long_context(pkg, hip, tmp_path, resident):
+    """Greedy steps past position 4160 (the device attention's multi-block form), against
+    the reference engine + soft backend's tokens."""
+    model_path = tmp_path / "long.gguf"
+    pkg.gguf.qwen3_random(model_path, **LONG["model"])
+    prompt = pkg.gguf.prompt_ids(LONG["prompt_count"], LONG["model"]["vocab"], seed=LONG["prompt_seed"])
+    want = [row[1] for row in LONG["steps"]]
+    eng = _engine_lib(pkg)
+    with pkg.Device(hip, 0) as dev:
+        m = pkg.engine.Model(eng, dev, model_path)
+        c = pkg.engine.Context(m, n_ctx=LONG["ctx"], n_batch=512)
+        c.set_resident(resident)
+        print(f"greedy decode, long context, path {resident}", flush=True)
+        first = _prefill(c, prompt, 512)
+        assert first == want[0]
+        assert [first] + c.decode_greedy(first, len(want) - 1) == want
+        c.free()
+        m.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not FULL_FIXTURE.exists(), reason="full-size fixture not generated")
+def test_engine_greedy_decode_1p7b(pkg, hip, tmp_path):
+    """Benchmark configuration 5 as one greedy call on the device path: the 128 tokens of
+    the reference engine's run."""
+    full = json.loads(FULL_FIXTURE.read_text())
+    model_path = tmp_path / "q.gguf"
+    pkg.gguf.qwen3_random(model_path)
+    want = [row[1] for row in full["steps"]]
+    eng = _engine_lib(pkg)
+    with pkg.Device(hip, 0) as dev:
+        m = pkg.engine.Model(eng, dev, model_path)
+        c = pkg.engine.Context(m, n_ctx=full["ctx"])
+        print("greedy decode, 1.7B shape, 32 + 128 tokens, device path", flush=True)
+        first = _prefill(c, full["prompt"], len(full["prompt"]))
+        assert [first] + c.decode_greedy(first, len(want) - 1) == want
+        c.free()
+        m.free()
+
+
 def test_device_expf_restatement_matches_host_libm():
     """The device expf (csrc/libc_expf.h, shared by the backend and engine kernels) returns what the
     host C library's expf returns: every 13th float bit pattern here (the full 2^32
