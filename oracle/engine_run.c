@@ -88,6 +88,7 @@ static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint3
         goto done;
     }
     int32_t next = (int32_t)argmax(logits, info.n_vocab);
+    const int32_t first = next;
     printf("step 0 %d %016" PRIx64 "\n", next, fnv64(logits, (size_t)info.n_vocab * 4));
     for (uint32_t s = 1; s <= steps; s++) {
         st = BNNE_Decode(c, &next, 1, logits);
@@ -105,6 +106,27 @@ static int run_llm(BNNE_Model model, const char* ids_path, uint32_t steps, uint3
            " execute_ns=%" PRIu64 " host_ns=%" PRIu64 " device_calls=%" PRIu64 "\n",
            stats.calls, stats.items, stats.total_ns, stats.transfer_ns, stats.execute_ns, stats.host_ns,
            stats.device_calls);
+#ifdef OWN_ENGINE
+    /* the same steps again, as one BNNEX_DecodeGreedy call from the first generated token */
+    if (steps > 0) {
+        int32_t* greedy = malloc(steps * sizeof *greedy);
+        if (!greedy)
+            goto done;
+        if ((st = BNNE_ContextTruncate(c, count)) != BNNE_OK ||
+            (st = BNNEX_DecodeGreedy(c, first, steps, greedy)) != BNNE_OK) {
+            free(greedy);
+            rc = fail("BNNEX_DecodeGreedy", st);
+            goto done;
+        }
+        printf("greedy");
+        for (uint32_t s = 0; s < steps; s++)
+            printf(" %d", greedy[s]);
+        printf("\n");
+        free(greedy);
+    }
+#else
+    (void)first;
+#endif
     rc = 0;
 done:
     if (f)

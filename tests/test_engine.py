@@ -46,6 +46,14 @@ def parse_llm(text: str) -> list[list]:
     return [[int(f[1]), int(f[2]), f[3]] for f in (ln.split() for ln in text.splitlines()) if f and f[0] == "step"]
 
 
+def parse_greedy(text: str) -> list[int] | None:
+    """The tokens of engine_run's BNNEX_DecodeGreedy pass (this engine's builds only)."""
+    for f in (ln.split() for ln in text.splitlines()):
+        if f and f[0] == "greedy":
+            return [int(t) for t in f[1:]]
+    return None
+
+
 def write_tiny(pkg, tmp_path):
     model, ids = tmp_path / "tiny.gguf", tmp_path / "ids.txt"
     pkg.gguf.qwen3_random(model, **TINY["model"])
@@ -232,6 +240,7 @@ def test_engine_host_step_on_cpu_oracle(pkg, tmp_path, exe):
     assert out.returncode == 0, out.stderr[-2000:]
     assert parse_path(out.stdout) == "host"
     assert parse_llm(out.stdout) == TINY["steps"]
+    assert parse_greedy(out.stdout) == [row[1] for row in TINY["steps"][1:]]
     model, inp = write_mlp(pkg, tmp_path)
     out = subprocess.run([str(exe), "classify", str(model), str(inp), str(MLP["samples"]), str(MLP["batch"])],
                          capture_output=True, text=True, timeout=300, env=env)
@@ -359,6 +368,7 @@ def test_engine_qwen3_tiny_bit_exact(pkg, tmp_path, runner):
                          text=True, timeout=120, check=True).stdout
     if runner != "refhip":
         assert parse_path(out) == runner.split("-")[1]
+        assert parse_greedy(out) == [row[1] for row in TINY["steps"][1:]]
     assert parse_llm(out) == TINY["steps"]
 
 
