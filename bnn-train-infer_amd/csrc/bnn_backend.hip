@@ -17,6 +17,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "bnn-accelerator-hip.h"
 #include "bnn-accelerator.h"
@@ -241,6 +242,9 @@ namespace {
 constexpr int kMaxOrdinals = 64;
 pthread_mutex_t g_static_lock = PTHREAD_MUTEX_INITIALIZER;
 unsigned char* g_static_scratch[kMaxOrdinals];  // per HIP ordinal, null until resolved
+// Held by BNNX_ExecuteNoAlloc while it uses its GPU's `scratch` (the call is synchronous):
+// devices are independent (bnn-accelerator.h:166-168) even when several handles share a GPU.
+std::mutex g_static_use[kMaxOrdinals];
 
 // The current device's copy of `scratch` (the caller has made `ordinal` current).
 hipError_t resolve_static_scratch(int ordinal, unsigned char** out) {
@@ -964,6 +968,8 @@ EXPORT BNN_Status BNNX_ExecuteNoAlloc(BNN_Device device, const BNN_Job* job) {
         return BNN_ENOMEM;  // one row's quantised form and staging exceed the fixed scratch
     if (hipSetDevice(device->ordinal) != hipSuccess)
         return BNN_EIO;
+    // every handle on this GPU shares the array: one call at a time uses it
+    const std::lock_guard<std::mutex> hold(g_static_use[device->ordinal]);
     return run_rows(device, job, p, false, device->static_scratch, chunk, rows_bytes, hipSuccess);
 }
 
@@ -1118,7 +1124,7 @@ void fill_batch_tables(const BatchPlan& bp, const BNN_Job* jobs, unsigned char* 
 // The two launches of a batch whose tables start at 'tables' on the device.
 hipError_t launch_batch(BNN_Device device, const unsigned char* tables, size_t prep_tab, size_t dot_tab,
                         size_t prep_map, uint32_t prep_blocks, uint32_t items, uint32_t uniform_items,
-                        uint32_t max_groups, uint64_t seq, uint64_t* status) {
+                        uint32_t max_groups, bool scales, uint64_t seq, uint64_t* status) {
     const PrepJob* dp = reinterpret_cast<const PrepJob*>(tables);
     const DotJob* dd = reinterpret_cast<const DotJob*>(tables + prep_tab);
     // no map (prep_map == 0) when every job has one row: prep block b is job b
@@ -1130,8 +1136,8 @@ hipError_t launch_batch(BNN_Device device, const unsigned char* tables, size_t p
     });
     if (e == hipSuccess)
         e = timed(device, KK_DOT, [&] {
-            return launch_dot_batch(device->stream, dd, ddm, items, uniform_items, max_groups, device->cu_count, seq,
-                                    device->flag_dev);
+            return launch_dot_batch(device->stream, dd, ddm, items, uniform_items, max_groups, scales,
+                                    device->cu_count, seq, device->flag_dev);
         });
     return e;
 }
@@ -1215,8 +1221,8 @@ static BNN_Status run_cached_batch(BNN_Device device) {
     const uint64_t seq = ++device->seq;
     const hipError_t e = launch_batch(device, device->table_dev, device->batch_prep_tab, device->batch_dot_tab,
                                       device->batch_prep_map, device->batch_prep_blocks, device->batch_items,
-                                      device->batch_uniform_items, device->batch_max_groups, seq,
-                                      device->status_host);
+                                      device->batch_uniform_items, device->batch_max_groups,
+                                      device->batch_needs_nearest, seq, device->status_host);
     if (e != hipSuccess)
         device->batch_count = 0;
     return finish(device, e, seq);
@@ -1499,8 +1505,8 @@ EXPORT BNN_Status BNNX_BatchLaunch(BNNX_Batch batch) {
                                                      device->status_host + 1);
                              })
                      : launch_batch(device, batch->mem, batch->prep_tab, batch->dot_tab, batch->prep_map,
-                                    batch->prep_blocks, batch->items, batch->uniform_items, batch->max_groups, seq,
-                                    device->status_host + 1);
+                                    batch->prep_blocks, batch->items, batch->uniform_items, batch->max_groups,
+                                    batch->needs_nearest, seq, device->status_host + 1);
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return BNN_EIO;

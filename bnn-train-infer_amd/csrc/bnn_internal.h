@@ -195,9 +195,11 @@ uint32_t dot_items(uint32_t tiles, uint32_t rows, uint32_t max_groups);
 hipError_t launch_prep_batch(hipStream_t stream, const PrepJob* jobs, const uint32_t* block_job,
                              uint32_t blocks, uint32_t max_groups, uint64_t seq, uint64_t* flag,
                              uint64_t* host_status);
+// `scales`: some job sums scaled products; false for batches of DOT_GROUPS jobs only,
+// which then read no scales.
 hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32_t* item_job, uint32_t items,
-                            uint32_t uniform_items, uint32_t max_groups, uint32_t cu_count, uint64_t seq,
-                            const uint64_t* flag);
+                            uint32_t uniform_items, uint32_t max_groups, bool scales, uint32_t cu_count,
+                            uint64_t seq, const uint64_t* flag);
 hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count, uint64_t seq,
                        const uint64_t* flag);
 // One launch of a fused batch of `tiles` 64-feature tiles on `grid` workgroups

@@ -563,7 +563,10 @@ __device__ __forceinline__ uint32_t xcd_local_block(uint32_t b, uint32_t grid) {
     return (x < r ? x * (q + 1u) : r * (q + 1u) + (x - r) * q) + i;
 }
 
-template <int MAP>
+// SCALES: some job of the batch sums scaled products (GEMV, GEMV_F32, GEMM*).  A batch of
+// DOT_GROUPS jobs only (SCALES = false) issues no scale loads: DOT stores D alone
+// (soft-bnn-accelerator.c:260-262), so its bytes per job are bits + row + D.
+template <int MAP, bool SCALES>
 __global__ __launch_bounds__(64 * BNN_DOT_WAVE_WG_WAVES) __attribute__((amdgpu_waves_per_eu(BNN_DOT_WAVE_OCC)))
 void k_dot_wave(const DotJob* __restrict__ jobs, const uint32_t* __restrict__ item_job, uint32_t items,
                 uint32_t uniform_items, uint64_t seq, const uint64_t* __restrict__ flag) {
@@ -598,7 +601,7 @@ void k_dot_wave(const DotJob* __restrict__ jobs, const uint32_t* __restrict__ it
     for (int g = 0; g < kWaveMaxGroups; ++g) {
         const size_t at = first + (size_t)min((uint32_t)g, groups - 1u) * kTile;
         w[g] = gload_stream(it.j.wbits + at);
-        sc[g] = gload_stream(it.j.wscale + at);
+        sc[g] = SCALES ? gload_stream(it.j.wscale + at) : 0u;
     }
     lds_planes[wave][lane] = p0;
     lds_planes[wave][lane + 64u] = p1;
@@ -607,7 +610,7 @@ void k_dot_wave(const DotJob* __restrict__ jobs, const uint32_t* __restrict__ it
     const uint32_t n0 = it.t0 * kTile;
     const bool live = n0 + lane < it.j.n;
     unsigned char* orow = it.j.out + (size_t)it.row * it.j.out_stride;
-    if (it.j.mode != MODE_DOT_I16) {
+    if (SCALES && it.j.mode != MODE_DOT_I16) {
         float acc = 0.0f;
 #pragma unroll
         for (int g = 0; g < kWaveMaxGroups; ++g) {
@@ -657,7 +660,7 @@ constexpr int kLongBlock = 8;
 constexpr int kLongMaxGroups = 64;
 constexpr int kLongWaves = 4;
 
-template <int MAP, int NB>
+template <int MAP, int NB, bool SCALES>
 __global__ __launch_bounds__(64 * kLongWaves) __attribute__((amdgpu_waves_per_eu(4)))
 void k_dot_wave_long(const DotJob* __restrict__ jobs, const uint32_t* __restrict__ item_job, uint32_t items,
                      uint32_t uniform_items, uint64_t seq, const uint64_t* __restrict__ flag) {
@@ -689,7 +692,7 @@ void k_dot_wave_long(const DotJob* __restrict__ jobs, const uint32_t* __restrict
         for (int i = 0; i < kLongBlock; ++i) {
             const size_t at = first + (size_t)min((uint32_t)(blk * kLongBlock + i), groups - 1u) * kTile;
             w[buf][i] = gload_stream(it.j.wbits + at);
-            sc[buf][i] = gload_stream(it.j.wscale + at);
+            sc[buf][i] = SCALES ? gload_stream(it.j.wscale + at) : 0u;  // see k_dot_wave
         }
     };
     load_block(0, 0);
@@ -701,7 +704,7 @@ void k_dot_wave_long(const DotJob* __restrict__ jobs, const uint32_t* __restrict
     const uint32_t n0 = it.t0 * kTile;
     const bool live = n0 + lane < it.j.n;
     unsigned char* orow = it.j.out + (size_t)it.row * it.j.out_stride;
-    const bool sum_mode = it.j.mode != MODE_DOT_I16;
+    const bool sum_mode = SCALES && it.j.mode != MODE_DOT_I16;
     const bool store = live && !failed;
     int16_t* od = reinterpret_cast<int16_t*>(orow) + (size_t)(n0 + lane) * groups;
     float acc = 0.0f;
@@ -736,20 +739,28 @@ void k_dot_wave_long(const DotJob* __restrict__ jobs, const uint32_t* __restrict
     }
 }
 
-template <int MAP>
+template <int MAP, bool SCALES>
 hipError_t launch_dot_long(hipStream_t stream, const DotJob* jobs, const uint32_t* item_job, uint32_t items,
                            uint32_t uniform_items, uint32_t max_groups, uint64_t seq, const uint64_t* flag) {
     const uint32_t grid = (items + kLongWaves - 1u) / kLongWaves;
     const dim3 block(64 * kLongWaves);
     switch ((max_groups + kLongBlock - 1u) / kLongBlock) {
-    case 3: launch_kernel((k_dot_wave_long<MAP, 3>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
-    case 4: launch_kernel((k_dot_wave_long<MAP, 4>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
-    case 5: launch_kernel((k_dot_wave_long<MAP, 5>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
-    case 6: launch_kernel((k_dot_wave_long<MAP, 6>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
-    case 7: launch_kernel((k_dot_wave_long<MAP, 7>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
-    default: launch_kernel((k_dot_wave_long<MAP, 8>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 3: launch_kernel((k_dot_wave_long<MAP, 3, SCALES>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 4: launch_kernel((k_dot_wave_long<MAP, 4, SCALES>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 5: launch_kernel((k_dot_wave_long<MAP, 5, SCALES>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 6: launch_kernel((k_dot_wave_long<MAP, 6, SCALES>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    case 7: launch_kernel((k_dot_wave_long<MAP, 7, SCALES>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
+    default: launch_kernel((k_dot_wave_long<MAP, 8, SCALES>), dim3(grid), block, 0, stream, jobs, item_job, items, uniform_items, seq, flag); break;
     }
     return hipGetLastError();
+}
+
+template <int MAP, bool SCALES>
+void launch_dot_wave(hipStream_t stream, const DotJob* jobs, const uint32_t* item_job, uint32_t items,
+                     uint32_t uniform_items, uint64_t seq, const uint64_t* flag) {
+    const uint32_t grid = (items + BNN_DOT_WAVE_WG_WAVES - 1u) / BNN_DOT_WAVE_WG_WAVES;
+    launch_kernel((k_dot_wave<MAP, SCALES>), dim3(grid), dim3(64 * BNN_DOT_WAVE_WG_WAVES), 0, stream, jobs,
+                  item_job, items, uniform_items, seq, flag);
 }
 
 template <int MAXG, int MAP, int TPI>
@@ -839,7 +850,7 @@ hipError_t launch_dot(hipStream_t stream, const DotJob& job, uint32_t cu_count, 
 }
 
 hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32_t* item_job, uint32_t items,
-                            uint32_t uniform_items, uint32_t max_groups, uint32_t cu_count, uint64_t seq,
+                            uint32_t uniform_items, uint32_t max_groups, bool scales, uint32_t cu_count, uint64_t seq,
                             const uint64_t* flag) {
     DotJob none = {};
     // One wave per item streams best when the items fill the chip several times;
@@ -847,21 +858,26 @@ hipError_t launch_dot_batch(hipStream_t stream, const DotJob* jobs, const uint32
     // finishes each item sooner.
     const bool many = (uint64_t)items >= (uint64_t)(cu_count ? cu_count : 256u) * BNN_DOT_WAVE_MIN_ITEMS_PER_CU;
     if (BNN_DOT_WAVE_ITEMS && max_groups <= (uint32_t)kWaveMaxGroups && many) {
-        const uint32_t grid = (items + BNN_DOT_WAVE_WG_WAVES - 1u) / BNN_DOT_WAVE_WG_WAVES;
-        const dim3 block(64 * BNN_DOT_WAVE_WG_WAVES);
-        if (uniform_items)
-            launch_kernel(k_dot_wave<MAP_UNIFORM>, dim3(grid), block, 0, stream, jobs, item_job, items,
-                               uniform_items, seq, flag);
+        if (uniform_items && scales)
+            launch_dot_wave<MAP_UNIFORM, true>(stream, jobs, item_job, items, uniform_items, seq, flag);
+        else if (uniform_items)
+            launch_dot_wave<MAP_UNIFORM, false>(stream, jobs, item_job, items, uniform_items, seq, flag);
+        else if (scales)
+            launch_dot_wave<MAP_TABLE, true>(stream, jobs, item_job, items, 0u, seq, flag);
         else
-            launch_kernel(k_dot_wave<MAP_TABLE>, dim3(grid), block, 0, stream, jobs, item_job, items, 0u, seq,
-                               flag);
+            launch_dot_wave<MAP_TABLE, false>(stream, jobs, item_job, items, 0u, seq, flag);
         return hipGetLastError();
     }
 #if BNN_DOT_WAVE_LONG
-    if (BNN_DOT_WAVE_ITEMS && max_groups <= (uint32_t)kLongMaxGroups && many)
-        return uniform_items ? launch_dot_long<MAP_UNIFORM>(stream, jobs, item_job, items, uniform_items, max_groups,
-                                                            seq, flag)
-                             : launch_dot_long<MAP_TABLE>(stream, jobs, item_job, items, 0u, max_groups, seq, flag);
+    if (BNN_DOT_WAVE_ITEMS && max_groups <= (uint32_t)kLongMaxGroups && many) {
+        if (uniform_items)
+            return scales ? launch_dot_long<MAP_UNIFORM, true>(stream, jobs, item_job, items, uniform_items,
+                                                               max_groups, seq, flag)
+                          : launch_dot_long<MAP_UNIFORM, false>(stream, jobs, item_job, items, uniform_items,
+                                                                max_groups, seq, flag);
+        return scales ? launch_dot_long<MAP_TABLE, true>(stream, jobs, item_job, items, 0u, max_groups, seq, flag)
+                      : launch_dot_long<MAP_TABLE, false>(stream, jobs, item_job, items, 0u, max_groups, seq, flag);
+    }
 #endif
     const uint32_t grid = dot_grid(items, max_groups, cu_count);
     if (max_groups <= 16u)
