@@ -121,3 +121,44 @@ def test_no_alloc_errors_and_device_memory(pkg, hip):
             bi.free()
             bo.free()
             m.destroy()
+
+
+def test_no_alloc_two_handles_two_threads(pkg, hip):
+    """Devices are independent (bnn-accelerator.h:166-168) although every handle on a GPU
+    shares that GPU's one scratch array: two threads, each with its own handle on GPU 0,
+    run multi-row NoAlloc jobs (which stage their quantised rows in the array) at the
+    same time; every result equals BNN_Execute's."""
+    import threading
+    fn = hip.lib.BNNX_ExecuteNoAlloc
+    specs = [("GEMM_F32", 2048, 2048, 700, 1), ("GEMM", 6144, 1024, 400, 2)]  # rows staged in the array
+    results = {}
+
+    def worker(t, op, k, n, rows, seed):
+        try:
+            with pkg.Device(hip, 0) as dev:
+                m = dev.matrix(*pkg.synth.matrix(n, k, seed=seed))
+                try:
+                    xs = [_inputs(pkg, op, rows, k, seed=seed * 10 + i) for i in range(2)]
+                    want = [_run(pkg, dev, hip.BNN_Execute, op, m, k, n, rows, x, 0, 0, 0) for x in xs]
+                    barrier.wait(timeout=60)
+                    for it in range(6):
+                        i = it % 2
+                        st, got = _run(pkg, dev, fn, op, m, k, n, rows, xs[i], 0, 0, 0)
+                        assert want[i][0] == pkg.Status.OK and st == pkg.Status.OK, (t, it, st)
+                        assert got.tobytes() == want[i][1].tobytes(), (t, it, op)
+                finally:
+                    m.destroy()
+            results[t] = "ok"
+        except BaseException as e:  # reported by the main thread
+            results[t] = e
+
+    barrier = threading.Barrier(len(specs))
+    threads = [threading.Thread(target=worker, args=(t, *spec)) for t, spec in enumerate(specs)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=300)
+    assert not any(th.is_alive() for th in threads), "a NoAlloc thread did not finish"
+    for t in range(len(specs)):
+        if results.get(t) != "ok":
+            raise AssertionError(f"thread {t}: {results.get(t)!r}")
