@@ -1,11 +1,12 @@
-"""BNNX_ExecuteBatch (HIP-backend extension): same results as BNN_Execute per job,
-all-or-nothing input checks, concurrency rules, and table-cache invalidation."""
+"""BNNX_ExecuteBatch (HIP-backend extension): every job's output equals the CPU
+oracle's (bit for bit), all-or-nothing input checks, concurrency rules, and
+table-cache invalidation."""
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
-from bnn_cases import first_mismatch
+from bnn_cases import fast_oracle, first_mismatch
 
 pytestmark = pytest.mark.gpu
 
@@ -15,7 +16,9 @@ def _mk_batch(pkg, dev, specs, seed=0):
     mats, xs, in_off, out_off, layouts = [], [], [], [], []
     ioff = ooff = 0
     for i, (op, k, n, rows) in enumerate(specs):
-        mats.append(dev.matrix(*pkg.synth.matrix(n, k, seed=seed * 100 + i)))
+        host = pkg.synth.matrix(n, k, seed=seed * 100 + i)
+        mats.append(dev.matrix(*host))
+        mats[-1].host = host  # the oracle's copy
         f32 = op.endswith("F32")
         x = pkg.synth.normal_f32(rows, k, seed=seed + i) if f32 else pkg.synth.int8_uniform(rows, k, seed=seed + i)
         xs.append(x)
@@ -38,6 +41,11 @@ def _mk_batch(pkg, dev, specs, seed=0):
         jobs[i] = pkg.Job(int(pkg.Op[op]), mats[i].handle.value, bi.view(in_t, in_off[i]), bo.view(out_t, out_off[i]),
                           rows)
     return mats, xs, bi, bo, jobs, out_off, layouts
+
+
+def _oracle(pkg, oracle_fast, specs, mats, xs):
+    """Every job's expected output from the CPU oracle (never from another HIP path)."""
+    return [fast_oracle(pkg, oracle_fast, op, *mats[i].host, xs[i]) for i, (op, k, n, rows) in enumerate(specs)]
 
 
 def _outputs(bo, out_off, layouts):
@@ -66,12 +74,13 @@ def _free(mats, bi, bo):
     [("GEMV_F32", 6144, 2048, 1)] * 16 + [("GEMV", 2176, 4100, 1)] * 8 + [("DOT_GROUPS", 8192, 640, 1)] * 4
     + [("GEMV_F32", 3072, 1000, 1)] * 8,                                  # long K, table-mapped: 17..64 groups
 ], ids=["uniform", "mixed", "mixed_small", "long_k", "long_k_mixed"])
-def test_batch_equals_single_jobs(pkg, hipdev, specs):
+def test_batch_equals_oracle(pkg, hipdev, oracle_fast, specs):
     mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs)
     assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, len(specs)) == pkg.Status.OK
     got = _outputs(bo, out_off, layouts)
+    wants = _oracle(pkg, oracle_fast, specs, mats, xs)
     for i, (op, k, n, rows) in enumerate(specs):
-        want = hipdev.run(pkg.Op[op], mats[i], xs[i])
+        want = wants[i]
         assert np.array_equal(got[i].view(np.uint8), want.view(np.uint8)), (i, op, first_mismatch(got[i], want))
     # a second, cached call on new input data
     xs2 = [(-x if x.dtype == np.float32 else np.negative(x)) for x in xs]
@@ -81,23 +90,24 @@ def test_batch_equals_single_jobs(pkg, hipdev, specs):
     bi.write(raw)
     assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, len(specs)) == pkg.Status.OK
     got = _outputs(bo, out_off, layouts)
+    wants = _oracle(pkg, oracle_fast, specs, mats, xs2)
     for i, (op, k, n, rows) in enumerate(specs):
-        want = hipdev.run(pkg.Op[op], mats[i], xs2[i])
-        assert np.array_equal(got[i].view(np.uint8), want.view(np.uint8)), (i, op)
+        assert np.array_equal(got[i].view(np.uint8), wants[i].view(np.uint8)), (i, op)
     _free(mats, bi, bo)
 
 
-def test_batch_cache_follows_resource_changes(pkg, hipdev):
+def test_batch_cache_follows_resource_changes(pkg, hipdev, oracle_fast):
     specs = [("GEMV_F32", 256, 100, 1)] * 3
     mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs, seed=5)
     assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, 3) == pkg.Status.OK
     # replace matrix 1 by a different one; the job array may even hold the same handle value
     mats[1].destroy()
-    mats[1] = hipdev.matrix(*pkg.synth.matrix(100, 256, seed=999))
+    host = pkg.synth.matrix(100, 256, seed=999)
+    mats[1] = hipdev.matrix(*host)
     jobs[1].matrix = mats[1].handle.value
     assert hipdev.api.BNNX_ExecuteBatch(hipdev.handle, jobs, 3) == pkg.Status.OK
     got = _outputs(bo, out_off, layouts)
-    want = hipdev.run(pkg.Op.GEMV_F32, mats[1], xs[1])
+    want = fast_oracle(pkg, oracle_fast, "GEMV_F32", *host, xs[1])
     assert np.array_equal(got[1].view(np.uint32), want.view(np.uint32))
     _free(mats, bi, bo)
 
@@ -149,16 +159,14 @@ def test_batch_rejections(pkg, hipdev):
     _free(mats, bi, bo)
 
 
-def test_prepared_batch_launches(pkg, hipdev):
+def test_prepared_batch_launches(pkg, hipdev, oracle_fast):
     """BNNX_BatchCreate/Launch/DeviceSynchronize: same results as single jobs, input
     errors reported at the synchronisation, batches invalidated by destroys."""
     api = hipdev.api
     specs = [("GEMV_F32", 2048, 1024, 1), ("GEMV", 1024, 100, 1), ("DOT_GROUPS", 384, 70, 3), ("GEMM_F32", 256, 129, 5)]
     mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs, seed=7)
     import ctypes
-    # expected results first: single jobs allocate and free buffers, which makes
-    # prepared batches stale
-    want = [hipdev.run(pkg.Op[op], mats[i], xs[i]) for i, (op, k, n, rows) in enumerate(specs)]
+    want = _oracle(pkg, oracle_fast, specs, mats, xs)
     b = ctypes.c_void_p()
     assert api.BNNX_BatchCreate(hipdev.handle, jobs, len(specs), ctypes.byref(b)) == pkg.Status.OK
     for rep in range(3):  # launched repeatedly without waiting in between
@@ -290,7 +298,7 @@ def test_device_index_contract(pkg, hip):
     [("GEMV_F32", 2048, 6144, 1)] * 24 + [("GEMV", 1024, 8192, 1)] * 12 + [("DOT_GROUPS", 2048, 4096, 1)] * 6
     + [("GEMV_F32", 640, 1000, 1)] * 3,                                   # mixed one-row jobs, table-mapped
 ], ids=["uniform45", "mixed"])
-def test_full_chip_one_row_batch(pkg, hipdev, specs):
+def test_full_chip_one_row_batch(pkg, hipdev, oracle_fast, specs):
     """Batches of one-row jobs with K <= 2048 and a full chip of 64-feature items (the
     headline's form, on the one-wave-per-item kernel): the same results as single jobs,
     through BNNX_ExecuteBatch and through repeated prepared launches, and an illegal row
@@ -300,7 +308,7 @@ def test_full_chip_one_row_batch(pkg, hipdev, specs):
     mats, xs, bi, bo, jobs, out_off, layouts = _mk_batch(pkg, hipdev, specs, seed=11)
     items = sum(-(-n // 64) for _, _, n, _ in specs)
     assert items >= 256 * 16  # enough items for the one-wave-per-item kernel
-    want = [hipdev.run(pkg.Op[op], mats[i], xs[i]) for i, (op, k, n, rows) in enumerate(specs)]
+    want = _oracle(pkg, oracle_fast, specs, mats, xs)
     for rep in range(2):
         assert api.BNNX_ExecuteBatch(hipdev.handle, jobs, len(specs)) == pkg.Status.OK
         got = _outputs(bo, out_off, layouts)
