@@ -126,9 +126,13 @@ __device__ __forceinline__ uint32_t key_token(unsigned long long key) { return 0
 
 // x[i] = +scale or -scale of the token's Q1_0 embedding row (qwen3.c:355-366).  In a
 // greedy run the token is the one the previous step's argmax left in *key_in; the first
-// workgroup records it in *tok_out and clears *key_reset for this step's argmax.
+// workgroup records it in *tok_out and clears *key_reset for this step's argmax.  The
+// first token of a call also clears the step error word and the logits flag (err_reset,
+// bad_reset; null otherwise), so that nothing a failed earlier call left behind is
+// reported by this one.
 __global__ __launch_bounds__(256) void k_embed(uint32_t token, const unsigned long long* __restrict__ key_in,
                                                int32_t* __restrict__ tok_out, unsigned long long* __restrict__ key_reset,
+                                               int* __restrict__ err_reset, int* __restrict__ bad_reset,
                                                const uint8_t* __restrict__ bits,
                                                const uint16_t* __restrict__ scales, uint32_t C,
                                                float* __restrict__ x) {
@@ -140,6 +144,10 @@ __global__ __launch_bounds__(256) void k_embed(uint32_t token, const unsigned lo
             *tok_out = (int32_t)token;
         if (key_reset)
             *key_reset = 0;
+        if (err_reset)
+            *err_reset = kErrNone;
+        if (bad_reset)
+            *bad_reset = 0;
     }
     if (i >= C)
         return;
@@ -1435,9 +1443,10 @@ BNNE_Status ready_batches(Resident* r) {
 
 // The launches of one token at position pos: its embedding row (of `token`, or of the
 // token a greedy step's argmax left in *key_in, recorded in *tok_out, with *key_reset
-// cleared), the layers, and the lm_head when `head`.
+// cleared), the layers, and the lm_head when `head`.  `first`: the call's first token,
+// whose embedding launch clears the error word and the logits flag.
 BNNE_Status enqueue_token(Resident* r, uint32_t pos, uint32_t token, const unsigned long long* key_in,
-                          int32_t* tok_out, unsigned long long* key_reset, bool head) {
+                          int32_t* tok_out, unsigned long long* key_reset, bool head, bool first) {
     const uint32_t C = r->C, HD = r->HD, half = HD / 2u;
     const float scale = 1.0f / sqrtf((float)HD);
     const float* attn_norm = r->gains;
@@ -1452,7 +1461,7 @@ BNNE_Status enqueue_token(Resident* r, uint32_t pos, uint32_t token, const unsig
             st = accel_status(BNNX_BatchLaunch(b), "BNNX_BatchLaunch");
     };
     hipLaunchKernelGGL(k_embed, dim3((C + 255u) / 256u), dim3(256), 0, r->stream, token, key_in, tok_out, key_reset,
-                       r->emb_bits, r->emb_scales, C, r->x);
+                       first ? r->err : nullptr, first ? r->logit_bad : nullptr, r->emb_bits, r->emb_scales, C, r->x);
     for (uint32_t l = 0; l < r->L && st == BNNE_OK && r->fused; ++l) {
         const size_t cache_layer = (size_t)l * r->n_ctx * r->kv_dim;
         launch(r->qkv[l]);
@@ -1534,7 +1543,7 @@ BNNE_Status resident_step(bnne_context* c, Resident* r, const int32_t* tokens, u
         return hip_error(e, "hipSetDevice");
     BNNE_Status st = ready_batches(r);
     for (uint32_t i = 0; i < n && st == BNNE_OK; ++i)
-        st = enqueue_token(r, pos0 + i, (uint32_t)tokens[i], nullptr, nullptr, nullptr, logits && i + 1 == n);
+        st = enqueue_token(r, pos0 + i, (uint32_t)tokens[i], nullptr, nullptr, nullptr, logits && i + 1 == n, i == 0);
     e = hipGetLastError();
     // the error word and the logits come back behind the last launch, into pinned memory
     int* const err_host = reinterpret_cast<int*>(r->pinned + r->V);
@@ -1601,7 +1610,7 @@ BNNE_Status resident_greedy(bnne_context* c, Resident* r, int32_t token, uint32_
     const uint32_t argmax_grid = std::min<uint32_t>((r->V + 4u * kArgmaxThreads - 1u) / (4u * kArgmaxThreads), 1024u);
     for (uint32_t i = 0; i < n && st == BNNE_OK; ++i) {
         st = enqueue_token(r, pos0 + i, (uint32_t)token, i ? r->keys + ((i - 1u) & 1u) : nullptr,
-                           i ? r->tokens_dev + (i - 1u) : nullptr, r->keys + (i & 1u), true);
+                           i ? r->tokens_dev + (i - 1u) : nullptr, r->keys + (i & 1u), true, i == 0);
         if (st == BNNE_OK)
             hipLaunchKernelGGL(k_argmax, dim3(argmax_grid), dim3(kArgmaxThreads), 0, r->stream, r->logits_dev, r->V,
                                r->keys + (i & 1u), r->logit_bad);
@@ -1634,11 +1643,8 @@ BNNE_Status resident_greedy(bnne_context* c, Resident* r, int32_t token, uint32_
     st = accel_status(sync, "BNN_Execute");
     if (st != BNNE_OK)
         return st;
-    if (*static_cast<volatile int32_t*>(r->pinned_tokens + n) != 0) {
-        if ((e = hipMemset(r->logit_bad, 0, sizeof(int))) != hipSuccess)
-            return hip_error(e, "logits flag");
+    if (*static_cast<volatile int32_t*>(r->pinned_tokens + n) != 0)  // cleared by the next call's first launch
         return complain(BNNE_ECOMPUTE, "the logits hold a NaN or infinity");
-    }
     std::memcpy(out_tokens, r->pinned_tokens, (size_t)n * sizeof(int32_t));
     if (stats) {
         c->stats.execute_ns += t2 - t1;
