@@ -15,6 +15,7 @@
 // for a block of rows, with GEMM_F32 over all of them in place of one GEMV_F32 per row.
 #include "engine.hpp"
 
+#include <algorithm>
 #include <cstring>
 #include <vector>
 
@@ -134,25 +135,28 @@ void SignLinear::apply_rows(bnne_context& ctx, const float* x, uint32_t rows, fl
         require(st, "BNN_BufferWrite");
     }
     // a layer of one shard reads its rows straight into y; a sharded one reads each
-    // shard's block of rows and places it at the shard's columns
+    // shard's block of rows and places it at the shard's columns.  A job holds at most
+    // the backend's max_rows rows (the remote backend's limit is 128): larger blocks run
+    // as several jobs over consecutive rows of the staged input and output.
+    const uint32_t job_rows = std::max(1u, std::min(rows, ctx.model->caps.max_rows));
     std::vector<float> block(shards_.size() > 1 ? (size_t)rows * shards_.front().count : 0);
     for (const Shard& s : shards_) {
-        BNN_Job job{};
-        job.operation = BNN_OP_GEMM_F32;
-        job.matrix = s.matrix;
-        job.input = BNN_BufferView{ctx.stage_in, BNN_TYPE_F32, 0, 0};
-        job.output = BNN_BufferView{ctx.stage_out, BNN_TYPE_F32, 0, 0};
-        job.rows = rows;
-        {
+        for (uint32_t r0 = 0; r0 < rows; r0 += job_rows) {
+            BNN_Job job{};
+            job.operation = BNN_OP_GEMM_F32;
+            job.matrix = s.matrix;
+            job.input = BNN_BufferView{ctx.stage_in, BNN_TYPE_F32, (size_t)r0 * in_ * sizeof(float), 0};
+            job.output = BNN_BufferView{ctx.stage_out, BNN_TYPE_F32, (size_t)r0 * s.count * sizeof(float), 0};
+            job.rows = std::min(job_rows, rows - r0);
             Span busy(ctx.counter(&BNNE_Stats::execute_ns));
             require(BNN_Execute(ctx.model->device, &job), "BNN_Execute");
+            ctx.count(&BNNE_Stats::device_calls, 1);
         }
         const size_t out_bytes = (size_t)rows * s.count * sizeof(float);
         float* dst = shards_.size() > 1 ? block.data() : y;
         {
             Span busy(ctx.counter(&BNNE_Stats::transfer_ns));
             const BNN_Status st = BNN_BufferRead(ctx.stage_out, 0, dst, out_bytes);
-            ctx.count(&BNNE_Stats::device_calls, 1);
             ctx.count(&BNNE_Stats::bytes_read, out_bytes);
             require(st, "BNN_BufferRead");
         }

@@ -299,6 +299,15 @@ EXPORT BNN_Status BNN_DeviceClose(BNN_Device device) {
     return BNN_OK;
 }
 
+/* Test hook: ORACLE_MAX_ROWS=n makes this backend report max_rows = n and reject jobs
+ * with more rows (as the reference's remote backend does with its 128-row limit,
+ * remote-bnn-accelerator.c:39,432,624), so that callers' row splitting can be tested. */
+static uint32_t max_rows_limit(void) {
+    const char* v = getenv("ORACLE_MAX_ROWS");
+    const long n = v ? strtol(v, NULL, 10) : 0;
+    return n > 0 && n < (long)UINT32_MAX ? (uint32_t)n : UINT32_MAX;
+}
+
 EXPORT BNN_Status BNN_DeviceGetCaps(BNN_Device device, BNN_Caps* out_caps) {
     if (device == NULL || out_caps == NULL)
         return BNN_EINVAL;
@@ -306,7 +315,7 @@ EXPORT BNN_Status BNN_DeviceGetCaps(BNN_Device device, BNN_Caps* out_caps) {
     out_caps->api_version = BNN_API_VERSION;
     out_caps->max_in_features = CPU_MAX_FEATURES;
     out_caps->max_out_features = CPU_MAX_FEATURES;
-    out_caps->max_rows = UINT32_MAX;
+    out_caps->max_rows = max_rows_limit();
     out_caps->group_size = CPU_GROUP;
     out_caps->supported_ops = BNN_CAP_GEMV | BNN_CAP_GEMM | BNN_CAP_DOT_GROUPS | BNN_CAP_GEMV_F32 |
                               BNN_CAP_GEMM_F32;
@@ -441,6 +450,8 @@ EXPORT BNN_Status BNN_Execute(BNN_Device device, const BNN_Job* job) {
     if (st != BNN_OK)
         return st;
     if ((job->operation == BNN_OP_GEMV || job->operation == BNN_OP_GEMV_F32) && job->rows != 1u)
+        return BNN_EINVAL;
+    if (job->rows > max_rows_limit())
         return BNN_EINVAL;
     if (job->input.type != in_type || job->output.type != out_type)
         return BNN_EINVAL;
