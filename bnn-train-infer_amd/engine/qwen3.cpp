@@ -103,8 +103,9 @@ void Qwen3Model::read_shape() {
         raise(BNNE_ENOTSUP, "Qwen3 layers need an accelerator with 128-weight groups and GEMV_F32");
 
     // RoPE scaling (YaRN when qwen3.rope.scaling.type is "yarn")
+    // a factor <= 0 (or none) means 1; a NaN factor stays NaN and is rejected below (gguf.c:483-484)
     const float factor = f.real("qwen3.rope.scaling.factor").value_or(0.0f);
-    s.freq_scale = 1.0f / (factor > 0.0f ? factor : 1.0f);
+    s.freq_scale = 1.0f / (factor <= 0.0f ? 1.0f : factor);
     s.yarn = f.text("qwen3.rope.scaling.type").value_or("") == "yarn";
     s.ramp_lo = 0;
     s.ramp_hi = (int32_t)s.head_dim - 1;

@@ -143,7 +143,7 @@ def byte_vocabulary() -> list[str]:
 
 
 def qwen3_random(path, *, layers=28, hidden=2048, heads=16, kv_heads=8, head_dim=128, ffn=6144, vocab=151669,
-                 context=40960, seed=5) -> dict:
+                 context=40960, seed=5, rope_scaling=None, tweak=None) -> dict:
     """Random-init Qwen3-architecture Q1_0 model (benchmark configuration 5).
 
     Sign bits uniform; every Q1_0 scale of a tensor with input width `in` is
@@ -151,6 +151,13 @@ def qwen3_random(path, *, layers=28, hidden=2048, heads=16, kv_heads=8, head_dim
     N(1, 0.02); eps 1e-6; rope base 1e6, no rope scaling.  The vocabulary table holds
     the 256 byte tokens and placeholders, enough for a BPE tokenizer to load; there is
     no EOS token, so generation never stops early.
+
+    rope_scaling: None, or {"type": "yarn" | "linear" | ..., "factor": f,
+    "original_context_length": n (optional)} written as the qwen3.rope.scaling.* keys
+    the reference reads (bnn-sw-v2/gguf.c:272-280).
+    tweak: None, or a function (tensor name, data) -> data applied before a tensor is
+    written; data is (bits [out][in/8] u8, scales [out][in/128] u16) for Q1_0 tensors
+    and a float32 array for gains (tests build models with chosen values this way).
     """
     w = Writer()
     w.string("general.architecture", "qwen3")
@@ -165,8 +172,14 @@ def qwen3_random(path, *, layers=28, hidden=2048, heads=16, kv_heads=8, head_dim
     w.u32("qwen3.attention.value_length", head_dim)
     w.f32("qwen3.attention.layer_norm_rms_epsilon", 1e-6)
     w.f32("qwen3.rope.freq_base", 1e6)
-    w.string("qwen3.rope.scaling.type", "none")
-    w.f32("qwen3.rope.scaling.factor", 1.0)
+    if rope_scaling is None:
+        w.string("qwen3.rope.scaling.type", "none")
+        w.f32("qwen3.rope.scaling.factor", 1.0)
+    else:
+        w.string("qwen3.rope.scaling.type", rope_scaling["type"])
+        w.f32("qwen3.rope.scaling.factor", rope_scaling["factor"])
+        if "original_context_length" in rope_scaling:
+            w.u32("qwen3.rope.scaling.original_context_length", rope_scaling["original_context_length"])
     w.string("tokenizer.ggml.model", "gpt2")
     toks = byte_vocabulary() + [f"<t{i}>" for i in range(256, vocab)]
     w.strings("tokenizer.ggml.tokens", toks[:vocab])
@@ -178,11 +191,16 @@ def qwen3_random(path, *, layers=28, hidden=2048, heads=16, kv_heads=8, head_dim
         bits = synth.sign_bits(out_f, in_f, seed, stream=stream[0])
         scale = np.float16(1.0 / np.sqrt(in_f)).view(np.uint16)
         scales = np.full((out_f, in_f // GROUP), scale, np.uint16)
+        if tweak is not None:
+            bits, scales = tweak(name, (bits, scales))
         w.tensor(name, (in_f, out_f), TYPE_Q1_0, q1_0_blocks(bits, scales))
 
     def gains(name, n):
         stream[0] += 1
-        w.tensor(name, (n,), TYPE_F32, _normal(seed, 7000 + stream[0], n, 1.0, 0.02).astype("<f4").tobytes())
+        g = _normal(seed, 7000 + stream[0], n, 1.0, 0.02).astype("<f4")
+        if tweak is not None:
+            g = np.asarray(tweak(name, g), "<f4")
+        w.tensor(name, (n,), TYPE_F32, g.tobytes())
 
     q1("token_embd.weight", hidden, vocab)
     gains("output_norm.weight", hidden)
@@ -204,6 +222,37 @@ def qwen3_random(path, *, layers=28, hidden=2048, heads=16, kv_heads=8, head_dim
     return {"layers": layers, "hidden": hidden, "heads": heads, "kv_heads": kv_heads, "head_dim": head_dim,
             "ffn": ffn, "vocab": vocab, "context": context, "seed": seed, "weights": weights,
             "weight_bytes": weights // 8 + weights // 64}
+
+
+def qwen3_overflow_tweak(token: int, gain: float = 2.19e19):
+    """A `tweak` for qwen3_random: the model decodes every token normally except `token`,
+    whose step fails with a non-finite head RMSNorm divisor (BNNE_ECOMPUTE) in layer 0.
+
+    Layer 0's attention RMSNorm gain of feature 0 is `gain`, so that the normalised row's
+    absmax -- and with it every q/k value of the layer (its other quantised values round
+    to 0) -- is `gain` times feature 0's normalised value.  That value is ~1 for a token
+    whose two embedding groups have equal scales, and sqrt(2) for `token`, whose second
+    group's scale is the smallest fp16 subnormal; the head norm's sum of squares
+    (128 * (absmax / 16)^2 for hidden 256) then stays below FLT_MAX for every other token
+    and overflows for `token`.  Layer 0's value weights get the smallest fp16 scale, so
+    that the residual stream stays far from overflow.  Meant for the tiny shape
+    (hidden 256, head_dim 128).
+    """
+    def tweak(name, data):
+        if name == "token_embd.weight":
+            bits, scales = data
+            scales = scales.copy()
+            scales[token, 1:] = 0x0001
+            return bits, scales
+        if name == "blk.0.attn_v.weight":
+            bits, scales = data
+            return bits, np.full_like(scales, 0x0001)
+        if name == "blk.0.attn_norm.weight":
+            g = np.array(data, np.float32)
+            g[0] = np.float32(gain)
+            return g
+        return data
+    return tweak
 
 
 def prompt_ids(count: int, vocab: int, seed: int = 5) -> list[int]:

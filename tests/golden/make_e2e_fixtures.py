@@ -7,7 +7,7 @@ them, and stores its outputs (per decode step: greedy token and an FNV-1a-64 has
 of the logits bytes; for classification: every logit's float32 bits, hashed) as
 JSON fixtures under tests/golden/.  Run from the repository root:
 
-    python tests/golden/make_e2e_fixtures.py [tiny] [mlp] [long] [full FULL_OUTPUT.txt]
+    python tests/golden/make_e2e_fixtures.py [tiny] [mlp] [long] [rope] [error] [full FULL_OUTPUT.txt]
 
 'full' converts the output of a full-size run made beforehand (it takes ~15 min on
 one core):  oracle/_ref/engine_run_soft llm MODEL.gguf PROMPT.txt 127 1024
@@ -35,6 +35,14 @@ FULL_PROMPT, FULL_STEPS, FULL_CTX = 32, 127, 1024
 # a one-layer model decoding past 4096 positions (attention over long contexts)
 LONG = dict(layers=1, hidden=256, heads=2, kv_heads=1, head_dim=128, ffn=256, vocab=256, context=4608, seed=23)
 LONG_PROMPT, LONG_STEPS, LONG_CTX = 4160, 6, 4400
+# the tiny model with RoPE scaling (qwen3.c:116-142 parameters, :298-319 tables): YaRN with a
+# ramp over pairs 13..31 (original context 4096, base 1e6, head_dim 128), YaRN with the
+# original context taken from the trained context (gguf.c:485-486), and linear scaling
+ROPE = {
+    "yarn": dict(TINY, context=16384, rope_scaling={"type": "yarn", "factor": 4.0, "original_context_length": 4096}),
+    "yarn_default_original": dict(TINY, context=8192, rope_scaling={"type": "yarn", "factor": 2.5}),
+    "linear": dict(TINY, rope_scaling={"type": "linear", "factor": 4.0}),
+}
 
 
 def package():
@@ -85,6 +93,43 @@ def long(pkg):
     (GOLDEN / "e2e_qwen3_long.json").write_text(json.dumps(res, indent=1) + "\n")
 
 
+def rope(pkg):
+    res = {}
+    for name, params in ROPE.items():
+        with tempfile.TemporaryDirectory() as d:
+            model, ids = Path(d) / "rope.gguf", Path(d) / "ids.txt"
+            pkg.gguf.qwen3_random(model, **params)
+            prompt = pkg.gguf.prompt_ids(TINY_PROMPT, params["vocab"], seed=params["seed"])
+            ids.write_text(" ".join(map(str, prompt)) + "\n")
+            out = subprocess.run([str(RUN), "llm", str(model), str(ids), str(TINY_STEPS), str(TINY_CTX)], check=True,
+                                 capture_output=True, text=True).stdout
+        res[name] = {"model": params, "prompt": prompt, "steps_arg": TINY_STEPS, "ctx": TINY_CTX, **parse_llm(out)}
+    (GOLDEN / "e2e_qwen3_rope.json").write_text(json.dumps(res, indent=1) + "\n")
+
+
+ERROR_TOKEN = 7
+
+
+def error(pkg):
+    """The tiny model with qwen3_overflow_tweak(ERROR_TOKEN): the reference's tokens for
+    the tiny prompt, and its failure (BNNE_ECOMPUTE) when ERROR_TOKEN is decoded."""
+    with tempfile.TemporaryDirectory() as d:
+        model, ids, bad = Path(d) / "err.gguf", Path(d) / "ids.txt", Path(d) / "bad.txt"
+        pkg.gguf.qwen3_random(model, **TINY, tweak=pkg.gguf.qwen3_overflow_tweak(ERROR_TOKEN))
+        prompt = pkg.gguf.prompt_ids(TINY_PROMPT, TINY["vocab"], seed=TINY["seed"])
+        ids.write_text(" ".join(map(str, prompt)) + "\n")
+        bad.write_text(" ".join(map(str, prompt + [ERROR_TOKEN])) + "\n")
+        out = subprocess.run([str(RUN), "llm", str(model), str(ids), str(TINY_STEPS), str(TINY_CTX)], check=True,
+                             capture_output=True, text=True).stdout
+        failed = subprocess.run([str(RUN), "llm", str(model), str(bad), "1", str(TINY_CTX)], capture_output=True,
+                                text=True)
+    assert failed.returncode != 0 and "computation failed" in failed.stderr, failed.stderr
+    res = {"model": TINY, "error_token": ERROR_TOKEN, "prompt": prompt, "steps_arg": TINY_STEPS, "ctx": TINY_CTX,
+           **parse_llm(out), "error_stderr": failed.stderr.strip()}
+    assert ERROR_TOKEN not in [row[1] for row in res["steps"]]
+    (GOLDEN / "e2e_qwen3_error.json").write_text(json.dumps(res, indent=1) + "\n")
+
+
 def mlp(pkg):
     with tempfile.TemporaryDirectory() as d:
         model, inp = Path(d) / "mlp.gguf", Path(d) / "in.f32"
@@ -120,6 +165,10 @@ if __name__ == "__main__":
         mlp(pkg)
     if "long" in args:
         long(pkg)
+    if "rope" in args:
+        rope(pkg)
+    if "error" in args:
+        error(pkg)
     if "full" in args:
         i = args.index("full")
         full(pkg, Path(args[i + 1]), float(args[i + 2]) if len(args) > i + 2 else None)

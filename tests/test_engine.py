@@ -27,6 +27,8 @@ ENGINE_RUN_REFHIP = REF_DIR / "engine_run_refhip"
 TINY = json.loads((GOLDEN / "e2e_qwen3_tiny.json").read_text())
 MLP = json.loads((GOLDEN / "e2e_bnn_mlp.json").read_text())
 LONG = json.loads((GOLDEN / "e2e_qwen3_long.json").read_text())
+ROPE = json.loads((GOLDEN / "e2e_qwen3_rope.json").read_text())
+ERR = json.loads((GOLDEN / "e2e_qwen3_error.json").read_text())
 FULL_FIXTURE = GOLDEN / "e2e_qwen3_1p7b.json"
 
 
@@ -59,6 +61,25 @@ def write_tiny(pkg, tmp_path):
     pkg.gguf.qwen3_random(model, **TINY["model"])
     ids.write_text(" ".join(map(str, TINY["prompt"])) + "\n")
     return model, ids
+
+
+def write_rope(pkg, tmp_path, name):
+    """The tiny model with one of the fixtures' RoPE scalings (YaRN or linear)."""
+    rec = ROPE[name]
+    model, ids = tmp_path / f"rope_{name}.gguf", tmp_path / f"rope_{name}.txt"
+    pkg.gguf.qwen3_random(model, **rec["model"])
+    ids.write_text(" ".join(map(str, rec["prompt"])) + "\n")
+    return rec, model, ids
+
+
+def write_error_model(pkg, tmp_path):
+    """The tiny model on which decoding ERR["error_token"] fails (BNNE_ECOMPUTE) and
+    every other token decodes normally; ids files of the prompt with and without it."""
+    model, ids, bad = tmp_path / "err.gguf", tmp_path / "ids.txt", tmp_path / "bad.txt"
+    pkg.gguf.qwen3_random(model, **ERR["model"], tweak=pkg.gguf.qwen3_overflow_tweak(ERR["error_token"]))
+    ids.write_text(" ".join(map(str, ERR["prompt"])) + "\n")
+    bad.write_text(" ".join(map(str, ERR["prompt"] + [ERR["error_token"]])) + "\n")
+    return model, ids, bad
 
 
 def write_mlp(pkg, tmp_path):
@@ -221,6 +242,27 @@ def test_reference_engine_reproduces_fixtures(pkg, tmp_path):
     check_mlp_output(out)
 
 
+@pytest.mark.skipif(not ENGINE_RUN_SOFT.exists(), reason="reference engine not built (no reference tree)")
+@pytest.mark.parametrize("name", sorted(ROPE))
+def test_reference_engine_reproduces_rope_fixtures(pkg, tmp_path, name):
+    """The RoPE-scaling fixtures (YaRN ramp and mscale, qwen3.c:116-142 and :298-319;
+    original context defaulting to the trained one, gguf.c:483-486; linear scaling) are
+    what the reference engine + soft backend compute on the models written here."""
+    rec, model, ids = write_rope(pkg, tmp_path, name)
+    out = subprocess.run([str(ENGINE_RUN_SOFT), "llm", str(model), str(ids), str(rec["steps_arg"]),
+                          str(rec["ctx"])], capture_output=True, text=True, check=True).stdout
+    assert parse_llm(out) == rec["steps"]
+
+
+def test_rope_fixtures_differ_from_unscaled():
+    """Each scaling changes the logits (the fixtures would otherwise pin nothing of it)."""
+    plain = [row[2] for row in TINY["steps"]]
+    hashes = {name: [row[2] for row in rec["steps"]] for name, rec in ROPE.items()}
+    for name, h in hashes.items():
+        assert all(a != b for a, b in zip(h, plain)), name
+    assert hashes["yarn"][1:] != hashes["yarn_default_original"][1:]
+
+
 ENGINE_RUN_CPU = ROOT / "oracle" / "lib" / "engine_run_cpu"
 ENGINE_RUN_ASAN = ROOT / "oracle" / "lib" / "engine_run_asan"
 ASAN_ENV = {"ASAN_OPTIONS": "detect_leaks=1:abort_on_error=0:exitcode=99", "UBSAN_OPTIONS": "print_stacktrace=1"}
@@ -246,6 +288,36 @@ def test_engine_host_step_on_cpu_oracle(pkg, tmp_path, exe):
                          capture_output=True, text=True, timeout=300, env=env)
     assert out.returncode == 0, out.stderr[-2000:]
     check_mlp_output(out.stdout)
+
+
+@pytest.mark.parametrize("name", sorted(ROPE))
+def test_engine_rope_scaling_host_step_on_cpu_oracle(pkg, tmp_path, name):
+    """This engine's RoPE tables (YaRN / linear scaling) in its host step, on the CPU
+    oracle backend: every step's token and logits hash equal the reference's."""
+    rec, model, ids = write_rope(pkg, tmp_path, name)
+    out = subprocess.run([str(ENGINE_RUN_CPU), "llm", str(model), str(ids), str(rec["steps_arg"]), str(rec["ctx"]),
+                          "host"], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr[-2000:]
+    assert parse_llm(out.stdout) == rec["steps"]
+    assert parse_greedy(out.stdout) == [row[1] for row in rec["steps"][1:]]
+
+
+@pytest.mark.parametrize("exe", [ENGINE_RUN_SOFT, ENGINE_RUN_CPU], ids=["reference", "own-host"])
+def test_engine_error_model_on_cpu(pkg, tmp_path, exe):
+    """The error-path model: the prompt decodes to the fixture's tokens and hashes, and a
+    prompt ending in the error token fails with BNNE_ECOMPUTE, for the reference engine
+    (soft backend) and this engine's host step (CPU oracle backend)."""
+    if not exe.exists():
+        pytest.skip(f"{exe.name} not built")
+    model, ids, bad = write_error_model(pkg, tmp_path)
+    mode = ["host"] if exe == ENGINE_RUN_CPU else []
+    out = subprocess.run([str(exe), "llm", str(model), str(ids), str(ERR["steps_arg"]), str(ERR["ctx"])] + mode,
+                         capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr[-2000:]
+    assert parse_llm(out.stdout) == ERR["steps"]
+    out = subprocess.run([str(exe), "llm", str(model), str(bad), "1", str(ERR["ctx"])] + mode, capture_output=True,
+                         text=True, timeout=120)
+    assert out.returncode == 2 and "computation failed or produced non-finite values" in out.stderr
 
 
 def _classify(exe, model, inp, samples, batch, env=None):
@@ -274,6 +346,21 @@ def test_engine_classify_rows_match_per_sample_on_cpu_oracle(pkg, tmp_path, exe)
     model, inp = write_wide_mlp(pkg, tmp_path, 300)
     rows = _classify(exe, model, inp, 300, 300, env)
     single = _classify(exe, model, inp, 300, 1, env)
+    assert len(rows.splitlines()) == 300
+    assert rows == single
+
+
+@pytest.mark.parametrize("exe", [ENGINE_RUN_CPU, ENGINE_RUN_ASAN], ids=["plain", "sanitized"])
+def test_engine_classify_respects_backend_max_rows(pkg, tmp_path, exe):
+    """A backend that takes at most 100 rows per job (as the reference's remote backend
+    takes 128: remote-bnn-accelerator.c:39,624; the CPU oracle's ORACLE_MAX_ROWS hook
+    reports and enforces such a limit): chunks of 256 rows run as jobs of <= 100 rows,
+    with the same logits as one sample per call."""
+    import os
+    env = dict(os.environ, **ASAN_ENV, ORACLE_MAX_ROWS="100")
+    model, inp = write_wide_mlp(pkg, tmp_path, 300)
+    rows = _classify(exe, model, inp, 300, 300, env)
+    single = _classify(exe, model, inp, 300, 1, dict(os.environ, **ASAN_ENV))
     assert len(rows.splitlines()) == 300
     assert rows == single
 
@@ -370,6 +457,22 @@ def test_engine_qwen3_tiny_bit_exact(pkg, tmp_path, runner):
         assert parse_path(out) == runner.split("-")[1]
         assert parse_greedy(out) == [row[1] for row in TINY["steps"][1:]]
     assert parse_llm(out) == TINY["steps"]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["device", "prepared", "host"])
+@pytest.mark.parametrize("name", sorted(ROPE))
+def test_engine_rope_scaling_bit_exact(pkg, tmp_path, name, path):
+    """YaRN and linear RoPE scaling on every decode path (the device paths read the
+    host-computed tables): every step's token and logits hash, and the greedy loop's
+    tokens, equal the reference engine + soft backend's."""
+    rec, model, ids = write_rope(pkg, tmp_path, name)
+    print(f"engine qwen3 rope {name}, {path} path", flush=True)
+    out = subprocess.run([str(ENGINE_RUN_OWN), "llm", str(model), str(ids), str(rec["steps_arg"]), str(rec["ctx"]),
+                          path], capture_output=True, text=True, timeout=120, check=True).stdout
+    assert parse_path(out) == path
+    assert parse_llm(out) == rec["steps"]
+    assert parse_greedy(out) == [row[1] for row in rec["steps"][1:]]
 
 
 @pytest.mark.gpu
@@ -543,6 +646,41 @@ def test_engine_greedy_decode(pkg, hip, tmp_path, resident):
         # the same steps again from a truncated context
         assert eng.BNNE_ContextTruncate(c.handle, len(TINY["prompt"]) + 3) == 0
         assert c.decode_greedy(want[3], len(want) - 4) == want[4:]
+        c.free()
+        m.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("resident", [1, 2, 0], ids=["device", "prepared", "host"])
+def test_engine_greedy_recovers_after_compute_error(pkg, hip, tmp_path, resident):
+    """A greedy call that fails with BNNE_ECOMPUTE (its first token overflows a head
+    RMSNorm, so the logits come out NaN too) leaves nothing behind: after truncating,
+    the next greedy calls return the reference's tokens (the error word and the logits
+    flag are cleared by each call's first launch)."""
+    model_path, _, _ = write_error_model(pkg, tmp_path)
+    eng = _engine_lib(pkg)
+    want = [row[1] for row in ERR["steps"]]
+    prompt = ERR["prompt"]
+    with pkg.Device(hip, 0) as dev:
+        m = pkg.engine.Model(eng, dev, model_path)
+        c = pkg.engine.Context(m, n_ctx=ERR["ctx"])
+        c.set_resident(resident)
+        print(f"greedy after a compute error, path {resident}", flush=True)
+        first = _prefill(c, prompt, len(prompt))
+        assert first == want[0]
+        for rep in range(2):  # twice in a row: each failure is reported once
+            with pytest.raises(pkg.engine.EngineError) as e:
+                c.decode_greedy(ERR["error_token"], 3)
+            assert e.value.status == -7
+            assert eng.BNNE_ContextTruncate(c.handle, len(prompt)) == 0
+        assert [first] + c.decode_greedy(first, 5) == want[:6]
+        assert c.decode_greedy(want[5], len(want) - 6) == want[6:]
+        # a failed per-token decode, then greedy again
+        with pytest.raises(pkg.engine.EngineError) as e:
+            c.decode([ERR["error_token"]])
+        assert e.value.status == -7
+        assert eng.BNNE_ContextTruncate(c.handle, len(prompt)) == 0
+        assert c.decode_greedy(first, 4) == want[1:5]
         c.free()
         m.free()
 
