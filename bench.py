@@ -22,7 +22,9 @@ back and closed by one BNNX_DeviceSynchronize.
                    BNN_Execute, one job per call (latency-bound at this size)
   cpu_baseline     the reference soft backend (compiled from its source into
                    oracle/_ref) or else this project's C restatement of it, one
-                   host core, on a bounded sample of the same jobs
+                   host core, on a bounded sample of the same jobs; `configs` holds
+                   the same for every benchmark configuration (per-shape samples
+                   composed into samples/s, GB/s, TOPS and tok/s)
 
 Secondary legs (the other benchmark configurations; --no-extra skips them):
   ops              configs 2/3: DOT_GROUPS, GEMV_I8 and the GEMV_F32 Qwen3 shapes,
@@ -98,8 +100,28 @@ def copy_calibration(mib: int = 256) -> None:
     print(f"copy calibration: {mib} MiB device-to-device", flush=True)
 
 
-def cpu_baseline(pkg, seconds: float = 12.0):
-    """Bounded single-core sample of the same jobs on the host (checker-side code)."""
+def alg_bytes(op: str, k: int, n: int, rows: int = 1) -> int:
+    """Algorithmic bytes of one job: sign bits + fp16 scales (not read by DOT_GROUPS) +
+    input rows + output rows."""
+    weights = n * k // 8 + (0 if op == "DOT_GROUPS" else n * (k // 128) * 2)
+    in_row = 4 * k if op.endswith("F32") else k
+    out_row = n * (k // 128) * 2 if op == "DOT_GROUPS" else 4 * n
+    return weights + rows * (in_row + out_row)
+
+
+# Per decode token at the Qwen3-1.7B shape, the reference caller's BNN_Execute calls by
+# shape (bnne_linear_forward, linear.c:161-216): per layer q, k, v, o, gate, up, down; the
+# lm_head as 18 chunks of 8192 outputs and one of 4213 (bnne_linear_init, linear.c:104-125).
+DECODE_CALLS = [((2048, 2048), 56), ((2048, 1024), 56), ((2048, 6144), 56), ((6144, 2048), 28),
+                ((2048, 8192), 18), ((2048, 4213), 1)]
+MLP_SHAPES = [(896, 512), (512, 512), (512, 10)]  # bnn-mlp blocks, one GEMV_F32 each per sample
+
+
+def cpu_baseline(pkg, seconds: float = 6.0, per_shape: float = 0.8):
+    """Bounded single-core samples on the host (checker-side code): the headline job for
+    `seconds`, then every benchmark configuration -- each distinct job shape timed for
+    about `per_shape` seconds (at least one call) and composed into the configuration's
+    unit (samples/s, GB/s, TOPS, tok/s)."""
     ref = ROOT / "oracle" / "_ref" / "libbnn_soft_ref.so"
     port = ROOT / "oracle" / "lib" / "liboracle_cpu.so"
     path, kind = (ref, "reference") if ref.exists() else (port, "port")
@@ -108,21 +130,69 @@ def cpu_baseline(pkg, seconds: float = 12.0):
     core = sorted(os.sched_getaffinity(0))[0]
     os.sched_setaffinity(0, {core})
     api = pkg.Api(path)
-    bits, scales = pkg.synth.matrix(N_OUT, K_IN, seed=3)
-    x = pkg.synth.normal_f32(1, K_IN, seed=3)
-    with pkg.Device(api, 0) as dev:
+    t_all = time.perf_counter()
+
+    def per_call(dev, op, k, n, rows, seed, budget):
+        """Seconds per BNN_Execute of one job of this shape, over `budget` seconds."""
+        bits, scales = pkg.synth.matrix(n, k, seed=seed)
+        f32 = op.endswith("F32")
+        x = pkg.synth.normal_f32(rows, k, seed=seed) if f32 else pkg.synth.int8_uniform(rows, k, seed=seed)
+        in_t, out_t = pkg.api.OP_TYPES[pkg.Op[op]]
+        out_row = n * (k // 128) * 2 if op == "DOT_GROUPS" else 4 * n
         m = dev.matrix(bits, scales)
-        bi, bo = dev.buffer(x.nbytes), dev.buffer(4 * N_OUT)
+        bi, bo = dev.buffer(x.nbytes), dev.buffer(rows * out_row)
         bi.write(x)
-        job = pkg.Job(int(pkg.Op.GEMV_F32), m.handle.value, bi.view(pkg.Type.F32), bo.view(pkg.Type.F32), 1)
+        job = pkg.Job(int(pkg.Op[op]), m.handle.value, bi.view(in_t), bo.view(out_t), rows)
         calls, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < seconds:
+        while calls == 0 or time.perf_counter() - t0 < budget:
             assert dev.execute(job) == 0
             calls += 1
         dt = time.perf_counter() - t0
         bi.free()
         bo.free()
         m.destroy()
+        return dt / calls, calls
+
+    configs = {}
+    with pkg.Device(api, 0) as dev:
+        head, calls = per_call(dev, "GEMV_F32", K_IN, N_OUT, 1, 3, seconds)
+        shape_s = {}
+
+        def gemv_f32(k, n):
+            if (k, n) not in shape_s:
+                shape_s[(k, n)] = per_call(dev, "GEMV_F32", k, n, 1, 3, per_shape)[0]
+            return shape_s[(k, n)]
+
+        shape_s[(K_IN, N_OUT)] = head
+        # config 1: bnn-mlp, the reference engine's pattern (one GEMV_F32 per block and sample)
+        per_sample = sum(gemv_f32(k, n) for k, n in MLP_SHAPES)
+        configs["1 bnn-mlp 896->512->512->10, one GEMV_F32 per block and sample"] = {
+            "samples_per_s": round(1.0 / per_sample, 2), "ms_per_sample": round(per_sample * 1e3, 3),
+            "bytes_per_sample": sum(alg_bytes("GEMV_F32", k, n) for k, n in MLP_SHAPES)}
+        # config 2: single-op microbench at one row
+        for op in ("DOT_GROUPS", "GEMV"):
+            t, c = per_call(dev, op, 2048, 6144, 1, 2, per_shape)
+            configs[f"2 {op} 2048->6144"] = {"ms_per_call": round(t * 1e3, 3),
+                                             "GBps": round(alg_bytes(op, 2048, 6144) / t / 1e9, 5), "calls": c}
+        # config 3: the GEMV_F32 sweep; the lm_head as its 19 chunks
+        for k, n in ((2048, 2048), (2048, 1024), (2048, 6144), (6144, 2048)):
+            t = gemv_f32(k, n)
+            configs[f"3 GEMV_F32 {k}->{n}"] = {"ms_per_call": round(t * 1e3, 3),
+                                               "GBps": round(alg_bytes("GEMV_F32", k, n) / t / 1e9, 5)}
+        lm = 18 * gemv_f32(2048, 8192) + gemv_f32(2048, 4213)
+        lm_bytes = 18 * alg_bytes("GEMV_F32", 2048, 8192) + alg_bytes("GEMV_F32", 2048, 4213)
+        configs["3 GEMV_F32 2048->151669 (19 chunks)"] = {"ms_per_call": round(lm * 1e3, 2),
+                                                          "GBps": round(lm_bytes / lm / 1e9, 5)}
+        # config 4: one multi-row job per op at 64 rows
+        for op in ("GEMM", "GEMM_F32"):
+            t, c = per_call(dev, op, 2048, 6144, 64, 4, 0.0)
+            configs[f"4 {op} 2048->6144 rows=64"] = {"ms_per_call": round(t * 1e3, 1),
+                                                     "TOPS": round(2.0 * 64 * 2048 * 6144 / t / 1e12, 6)}
+        # config 5: one decode token's 215 calls, composed from the per-shape times
+        token = sum(gemv_f32(k, n) * count for (k, n), count in DECODE_CALLS)
+        configs["5 Qwen3-1.7B-shape decode, 215 GEMV_F32 calls per token"] = {
+            "tok_per_s": round(1.0 / token, 4), "s_per_token": round(token, 2),
+            "calls_per_token": sum(c for _, c in DECODE_CALLS)}
     cpu_name = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -131,10 +201,12 @@ def cpu_baseline(pkg, seconds: float = 12.0):
                 break
     except OSError:
         pass
-    return {"value": round(calls * BYTES_PER_JOB / dt / 1e9, 5), "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{calls} GEMV_F32 {K_IN}->{N_OUT} rows=1 calls in {dt:.1f} s on core {core} "
-                      f"({cpu_name}, nproc {os.cpu_count()}), {dt / calls * 1e3:.1f} ms/call",
-            "library": str(path.relative_to(ROOT))}
+    return {"value": round(BYTES_PER_JOB / head / 1e9, 5), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{calls} GEMV_F32 {K_IN}->{N_OUT} rows=1 calls in {head * calls:.1f} s on core {core} "
+                      f"({cpu_name}, nproc {os.cpu_count()}), {head * 1e3:.1f} ms/call; per config below, each "
+                      f"job shape timed for ~{per_shape} s (one call at least); {time.perf_counter() - t_all:.0f} s "
+                      f"in all",
+            "library": str(path.relative_to(ROOT)), "configs": configs}
 
 
 def _timed_calls(dev, job, reps):
