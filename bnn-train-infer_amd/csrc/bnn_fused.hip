@@ -23,6 +23,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
+#include "bnn_bitplane.h"
 #include "bnn_internal.h"
 
 #define BNNE_EXPF_QUALIFIER static __device__ __forceinline__
@@ -53,78 +54,9 @@ __device__ __forceinline__ void fused_exp_table_fill(uint64_t* tab, uint32_t lan
         tab[lane] = (uint64_t)hi << 32 | lo;
 }
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 fload(const uint4* p) {
-    const u32x4 v = *(const __attribute__((address_space(1))) u32x4*)p;
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint32_t fload(const uint16_t* p) {
-    return *(const __attribute__((address_space(1))) uint16_t*)p;
-}
-__device__ __forceinline__ float fload(const float* p) { return *(const __attribute__((address_space(1))) float*)p; }
-__device__ __forceinline__ void fstore(float* p, float v) { *(__attribute__((address_space(1))) float*)p = v; }
-
 extern "C" __device__ uint32_t __ockl_wfred_max_u32(uint32_t);
 extern "C" __device__ double __ockl_wfred_add_f64(double);
 extern "C" __device__ int __ockl_wfred_add_i32(int);
-
-// popc(x) + acc and (c << SHIFT) + acc as single instructions (the compiler would
-// otherwise re-associate the chains)
-__device__ __forceinline__ uint32_t f_bcnt_acc(uint32_t x, uint32_t acc) {
-    uint32_t r;
-    asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));
-    return r;
-}
-template <int SHIFT>
-__device__ __forceinline__ uint32_t f_lshl_add(uint32_t c, uint32_t acc) {
-    uint32_t r;
-    asm("v_lshl_add_u32 %0, %1, %2, %3" : "=v"(r) : "v"(c), "i"(SHIFT), "v"(acc));
-    return r;
-}
-template <int B>
-__device__ __forceinline__ uint32_t f_plane_count(uint4 w, const uint4* p) {
-    const uint4 pb = p[B];
-    uint32_t c = (uint32_t)__builtin_popcount(w.x & pb.x);
-    c = f_bcnt_acc(w.y & pb.y, c);
-    c = f_bcnt_acc(w.z & pb.z, c);
-    return f_bcnt_acc(w.w & pb.w, c);
-}
-// (planes in LDS) D = sum_{b<7} 2^(b+1) popc(w & P_b) - 2^8 popc(w & P_7) - sum(Q)  (exact)
-__device__ __forceinline__ int f_group_dot(uint4 w, const uint4* p, int neg_sum) {
-    uint32_t d = (uint32_t)neg_sum;
-    d = f_lshl_add<1>(f_plane_count<0>(w, p), d);
-    d = f_lshl_add<2>(f_plane_count<1>(w, p), d);
-    d = f_lshl_add<3>(f_plane_count<2>(w, p), d);
-    d = f_lshl_add<4>(f_plane_count<3>(w, p), d);
-    d = f_lshl_add<5>(f_plane_count<4>(w, p), d);
-    d = f_lshl_add<6>(f_plane_count<5>(w, p), d);
-    d = f_lshl_add<7>(f_plane_count<6>(w, p), d);
-    d -= f_plane_count<7>(w, p) << 8;
-    return (int)d;
-}
-
-// popc(w & P_B) of a group's sign bits w and plane B of the quantised row, the plane
-// as wave-uniform ballot masks: bit l of m[h][B] is bit B of element 64 h + l
-template <int B>
-__device__ __forceinline__ uint32_t f_plane_count_s(uint4 w, const uint64_t (&m)[2][8]) {
-    uint32_t c = (uint32_t)__builtin_popcount(w.x & (uint32_t)m[0][B]);
-    c = f_bcnt_acc(w.y & (uint32_t)(m[0][B] >> 32), c);
-    c = f_bcnt_acc(w.z & (uint32_t)m[1][B], c);
-    return f_bcnt_acc(w.w & (uint32_t)(m[1][B] >> 32), c);
-}
-// D = sum_{b<7} 2^(b+1) popc(w & P_b) - 2^8 popc(w & P_7) - sum(Q)  (exact)
-__device__ __forceinline__ int f_group_dot_s(uint4 w, const uint64_t (&m)[2][8], int neg_sum) {
-    uint32_t d = (uint32_t)neg_sum;
-    d = f_lshl_add<1>(f_plane_count_s<0>(w, m), d);
-    d = f_lshl_add<2>(f_plane_count_s<1>(w, m), d);
-    d = f_lshl_add<3>(f_plane_count_s<2>(w, m), d);
-    d = f_lshl_add<4>(f_plane_count_s<3>(w, m), d);
-    d = f_lshl_add<5>(f_plane_count_s<4>(w, m), d);
-    d = f_lshl_add<6>(f_plane_count_s<5>(w, m), d);
-    d = f_lshl_add<7>(f_plane_count_s<6>(w, m), d);
-    d -= f_plane_count_s<7>(w, m) << 8;
-    return (int)d;
-}
 
 // Bit planes B..7 of the wave's 64 quantised values q: lane 2b of `word` receives
 // the low and lane 2b + 1 the high half of plane b's mask (v_writelane_b32 with the
@@ -327,8 +259,8 @@ __device__ __forceinline__ void load_tile(const LaneRow& lr, uint32_t G, uint32_
 #pragma unroll
     for (int i = 0; i < GPW; ++i) {
         const uint32_t g = min(wave + kFusedWaves * i, G - 1u);
-        r.w[i] = fload(lr.wbits + lr.base + (size_t)g * kTile);
-        r.s[i] = fload(lr.wscale + lr.base + (size_t)g * kTile);
+        r.w[i] = gload(lr.wbits + lr.base + (size_t)g * kTile);
+        r.s[i] = gload(lr.wscale + lr.base + (size_t)g * kTile);
     }
 }
 
@@ -401,17 +333,17 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     } else {
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
-            xv[i] = fload(src_a + min(elem(i), K - 1u));
+            xv[i] = gload(src_a + min(elem(i), K - 1u));
     }
     if (fa.b) {
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
-            bv[i] = fload(fa.b + min(elem(i), K - 1u));
+            bv[i] = gload(fa.b + min(elem(i), K - 1u));
     }
     if (fa.kind == PRE_RMSNORM) {
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
-            gv[i] = fload(fa.gain + min(elem(i), K - 1u));
+            gv[i] = gload(fa.gain + min(elem(i), K - 1u));
     }
     // a ring of RING tiles' weights in flight: a workgroup that walks several tiles (the
     // lm_head's 2370 over one workgroup per CU) would otherwise wait one memory latency per tile
@@ -456,7 +388,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
             if (live(i)) {
                 scratch[k] = sq;
                 if (fa.a_out && blockIdx.x == 0)
-                    fstore(fa.a_out + k, xv[i]);
+                    gstore(fa.a_out + k, xv[i]);
                 const double h = __ockl_wfred_add_f64((double)sq);
                 if (lane == 0)
                     chunk_sum[k / kChunk] = h;
@@ -685,7 +617,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
             if (g < G) {
                 int d;
                 if constexpr (GPW == 1) {
-                    d = f_group_dot_s(cur.w[i], masks, neg_sum[i]);
+                    d = group_dot_s(cur.w[i], masks, neg_sum[i]);
                 } else if constexpr (RING == 1) {
                     uint64_t m[2][8];
 #pragma unroll
@@ -693,12 +625,12 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
 #pragma unroll
                         for (int b = 0; b < 8; ++b)
                             m[h][b] = __ballot((q[2 * i + h] >> b) & 1);
-                    d = f_group_dot_s(cur.w[i], m, neg_sum[i]);
+                    d = group_dot_s(cur.w[i], m, neg_sum[i]);
                     // one group's 32 mask registers at a time (scheduled together, the
                     // groups' masks would not fit the scalar register file)
                     __builtin_amdgcn_sched_barrier(0);
                 } else {
-                    d = f_group_dot(cur.w[i], planes + g * (kPlaneWords / 4u), neg_sum[i]);
+                    d = group_dot_v(cur.w[i], planes + g * (kPlaneWords / 4u), neg_sum[i]);
                 }
                 // DOT_GROUPS: D itself goes through the exchange
                 prod[g * 64u + lane] = dot_out ? __int_as_float(d)
@@ -746,7 +678,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
                 acc = acc + prod[g * 64u + lane];
             acc = acc * s;
             if (n < job.n) {
-                fstore(lane_pick(paired && lane >= 32u, job.out, job2.out) + n, acc);
+                gstore(lane_pick(paired && lane >= 32u, job.out, job2.out) + n, acc);
                 if (mirror)
                     mirror[n] = acc;
             }
@@ -754,7 +686,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
                 // y_p / (1 + expf(-y_p)) * y_(m+p) (qwen3.c:491-495), y_(m+p) from lane + 32
                 const float second = __shfl(acc, (int)(lane | 32u));
                 if (lane < 32u && n < job.n)
-                    fstore(fa.post_out + job.post_off + n, acc / (1.0f + bnne_expf_libc(-acc, exp_tab)) * second);
+                    gstore(fa.post_out + job.post_off + n, acc / (1.0f + bnne_expf_libc(-acc, exp_tab)) * second);
             }
         }
         if (more) {

@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
+#include "bnn_bitplane.h"
 #include "bnn_internal.h"
 
 #pragma clang fp contract(off)
@@ -34,44 +35,12 @@ namespace {
 constexpr int kLdsPitch = 65;                     // words per group row of the D/term exchange
 
 
-// Pointers taken from job descriptors are generic; loading through these
-// global-address-space views makes the compiler emit global_load, not flat_load.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint4 gload(const uint4* p) {
-    const u32x4 v = *(const __attribute__((address_space(1))) u32x4*)p;
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint32_t gload(const uint16_t* p) {
-    return *(const __attribute__((address_space(1))) uint16_t*)p;
-}
-// Nontemporal loads for the weight stream of the batched kernels: each byte is read
-// once per launch, and marking the loads as streaming (not kept in the caches)
-// measured 6.28 vs 5.69 TB/s for the 608-job GEMV_F32 2048->6144 batch.
-__device__ __forceinline__ uint4 gload_stream(const uint4* p) {
-    const u32x4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4*)p);
-    return make_uint4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ uint32_t gload_stream(const uint16_t* p) {
-    return __builtin_nontemporal_load((const __attribute__((address_space(1))) uint16_t*)p);
-}
-__device__ __forceinline__ int gload(const int32_t* p) {
-    return *(const __attribute__((address_space(1))) int32_t*)p;
-}
-__device__ __forceinline__ float gload(const float* p) {
-    return *(const __attribute__((address_space(1))) float*)p;
-}
-// Global (not flat) stores: a flat store is counted by both the vector-memory and
-// the LDS counters, which makes every later LDS wait also wait for the store.
-__device__ __forceinline__ void gstore(float* p, float v) { *(__attribute__((address_space(1))) float*)p = v; }
 // Nontemporal (streaming) stores for results written once per launch: they are not
 // kept dirty in the L2s, which the end-of-kernel release would otherwise write back
 // (GEMV_F32 2048->6144 x 608: 182 -> 177 us per dot launch).
 template <class T>
 __device__ __forceinline__ void gstore_stream(T* p, T v) {
     __builtin_nontemporal_store(v, (__attribute__((address_space(1))) T*)p);
-}
-__device__ __forceinline__ void gstore(int16_t* p, int16_t v) {
-    *(__attribute__((address_space(1))) int16_t*)p = v;
 }
 // 16 bytes at a 16-byte aligned address
 __device__ __forceinline__ void gstore16(int16_t* p, u32x4 v) { *(__attribute__((address_space(1))) u32x4*)p = v; }
@@ -246,71 +215,6 @@ __global__ __launch_bounds__(NT) void k_prep(PrepJob single, const PrepJob* __re
         prep_row<NT, PER>(single, blockIdx.x, validate_only != 0, seq, flag, host_status);
     }
 }
-
-// D of one group from its weights w (128 bits) and activation planes p[32]:
-//   D = 2*pos - sum = sum_{b<7} 2^(b+1) c_b - 2^8 c_7 - sum,  c_b = popc(w & P_b)
-// Each c_b is one accumulating BCNT chain, so a group costs 32 AND + 32 BCNT +
-// 8 shift-adds.
-// popc(x) + acc in one VALU op.  Written as asm because the compiler otherwise
-// re-associates the chain into ADD3 trees (11 instead of 9 ops per plane).
-__device__ __forceinline__ uint32_t bcnt_acc(uint32_t x, uint32_t acc) {
-    uint32_t r;
-    asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));
-    return r;
-}
-
-// (c << SHIFT) + acc in one VALU op, kept fused for the same reason.
-template <int SHIFT>
-__device__ __forceinline__ uint32_t lshl_add(uint32_t c, uint32_t acc) {
-    uint32_t r;
-    asm("v_lshl_add_u32 %0, %1, %2, %3" : "=v"(r) : "v"(c), "i"(SHIFT), "v"(acc));
-    return r;
-}
-
-template <int B>
-__device__ __forceinline__ uint32_t plane_count(uint4 w, const uint32_t* p) {
-    uint32_t c = (uint32_t)__builtin_popcount(w.x & p[4 * B + 0]);
-    c = bcnt_acc(w.y & p[4 * B + 1], c);
-    c = bcnt_acc(w.z & p[4 * B + 2], c);
-    return bcnt_acc(w.w & p[4 * B + 3], c);
-}
-
-__device__ __forceinline__ int group_dot(uint4 w, const uint32_t* p, int neg_sum) {
-    uint32_t d = (uint32_t)neg_sum;  // two's complement arithmetic, exact result in [-16256, 16256]
-    d = lshl_add<1>(plane_count<0>(w, p), d);
-    d = lshl_add<2>(plane_count<1>(w, p), d);
-    d = lshl_add<3>(plane_count<2>(w, p), d);
-    d = lshl_add<4>(plane_count<3>(w, p), d);
-    d = lshl_add<5>(plane_count<4>(w, p), d);
-    d = lshl_add<6>(plane_count<5>(w, p), d);
-    d = lshl_add<7>(plane_count<6>(w, p), d);
-    d -= plane_count<7>(w, p) << 8;  // the sign plane weighs -2^7, doubled
-    return (int)d;
-}
-
-// The same with the planes read as one 16-byte word each (P_b = p[b]).
-template <int B>
-__device__ __forceinline__ uint32_t plane_count_v(uint4 w, const uint4* p) {
-    const uint4 pb = p[B];
-    uint32_t c = (uint32_t)__builtin_popcount(w.x & pb.x);
-    c = bcnt_acc(w.y & pb.y, c);
-    c = bcnt_acc(w.z & pb.z, c);
-    return bcnt_acc(w.w & pb.w, c);
-}
-
-__device__ __forceinline__ int group_dot_v(uint4 w, const uint4* p, int neg_sum) {
-    uint32_t d = (uint32_t)neg_sum;
-    d = lshl_add<1>(plane_count_v<0>(w, p), d);
-    d = lshl_add<2>(plane_count_v<1>(w, p), d);
-    d = lshl_add<3>(plane_count_v<2>(w, p), d);
-    d = lshl_add<4>(plane_count_v<3>(w, p), d);
-    d = lshl_add<5>(plane_count_v<4>(w, p), d);
-    d = lshl_add<6>(plane_count_v<5>(w, p), d);
-    d = lshl_add<7>(plane_count_v<6>(w, p), d);
-    d -= plane_count_v<7>(w, p) << 8;
-    return (int)d;
-}
-
 
 // ---------------------------------------------------------------------------
 // dot: persistent workgroups of 4 waves; one work item = (job, row, TPI tiles of
