@@ -112,6 +112,12 @@ __device__ __forceinline__ void dma16_lanes(const void* gptr, uint32_t lds_addr)
     }
 }
 
+// The same with the address as a wave-uniform base (SGPRs) plus a 32-bit per-lane
+// offset: no 64-bit per-lane address arithmetic per DMA.
+__device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32_t lds_addr) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_addr) : "memory");
+}
+
 template <uint32_t N>
 constexpr uint64_t lane_mask() {
     return N >= 64 ? ~0ull : (1ull << N) - 1ull;
@@ -1091,6 +1097,281 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_wv(GemmJob j, uint32_t mt
         }
 }
 
+// k_gemm_mx<TM, TN, WGM, WGN>: GEMM / GEMM_F32 with a chip's worth of TM x TN tiles,
+// one workgroup of WGM x WGN waves per CU (two waves per SIMD for 8 waves).  Per
+// 128-weight group g:
+//   * the TM rows' quantised bytes and the TN columns' sign bits and scales reach LDS by
+//     DMA, DEPTH groups ahead, in a ring of DEPTH + 1 slots: A_INS + 1 DMA instructions
+//     per wave and group (one barrier per group: every wave has read slot g-1 before the
+//     DMAs of group g+DEPTH reuse it);
+//   * every wave expands its own columns' sign bits (4 bytes per lane) straight into
+//     +1/-1 MFMA operands through the byte table -- no +1/-1 tile in LDS;
+//   * group g-1's exact epilogue on each 16 x 16 subtile (the other D set) comes before
+//     group g's first-half MFMA on it; the second halves follow, each accumulating onto
+//     a first half issued MS * NS MFMAs earlier.
+// The K order inside a group is that of k_gemm_ks / k_gemm_wv (lane chunk c: weights
+// 32c .. 32c+31, MFMA half h the 16 from 32c + 16h).  The tile leaves through LDS as
+// 16-byte row-contiguous stores where the output view allows.
+template <int TM, int TN, int WGM, int WGN>
+struct MxTiling {
+    static constexpr uint32_t WAVES = WGM * WGN, THREADS = 64u * WAVES;
+    static constexpr uint32_t WTM = TM / WGM, WTN = TN / WGN, MS = WTM / 16u, NS = WTN / 16u;
+    static constexpr uint32_t DEPTH = 3, SLOTS = DEPTH + 1;
+    static constexpr uint32_t A_INS = TM * 8u / THREADS;  // 16-byte row chunks per thread and group
+    // a slot: rows [TM][128] (chunks swizzled), then the columns' 16-byte sign-bit chunks
+    // [TN][16], then their fp16 scales [TN]; the column part as TN + TN / 8 chunks of 16
+    // bytes, CPW per wave
+    static constexpr uint32_t A_BYTES = TM * 128u, COL_CHUNKS = TN + TN / 8u, CPW = COL_CHUNKS / WAVES;
+    static constexpr uint32_t SLOT_BYTES = A_BYTES + 16u * COL_CHUNKS;
+    // vector-memory operations a wave issues per group (row DMAs, one column DMA)
+    static constexpr uint32_t VM_PER_GROUP = A_INS + 1u;
+    // the byte table in 32 copies, entry e of copy c at (32 e + c) * 8 bytes: lane l reads
+    // copy l % 32, i.e. only its own pair of the 64 banks, so that the lanes' lookups of
+    // arbitrary entries never conflict
+    static constexpr uint32_t LUT_COPIES = 32;
+    static constexpr uint32_t OFF_LUT = SLOTS * SLOT_BYTES, LOOP_BYTES = OFF_LUT + 256u * LUT_COPIES * 8u;
+    static constexpr uint32_t OUT_STRIDE = TN + 4u;  // floats per staged output row
+    static constexpr uint32_t OUT_BYTES = TM * OUT_STRIDE * 4u;
+    static constexpr uint32_t SMEM = LOOP_BYTES > OUT_BYTES ? LOOP_BYTES : OUT_BYTES;
+    static_assert(TM % (16 * WGM) == 0 && TN % (16 * WGN) == 0, "wave tiles of 16 x 16 subtiles");
+    static_assert(TN % 64 == 0, "whole 64-feature tiles of the matrix layout");
+    static_assert(TM * 8u % THREADS == 0 && A_INS >= 1u, "whole row DMAs per thread");
+    static_assert(COL_CHUNKS % WAVES == 0 && CPW <= 64u, "column DMA chunks per wave");
+    static_assert(SLOT_BYTES % 16u == 0 && OFF_LUT % 16u == 0, "16-byte DMA destinations");
+    static_assert((DEPTH - 1u) * VM_PER_GROUP < 64u, "vmcnt range");
+    static_assert(SMEM <= 160u * 1024u, "LDS");
+    static_assert(TM * TN / 4u % THREADS == 0, "output chunks per thread");
+};
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) for N < 64 (the gfx9 encoding splits vmcnt into bits
+// 3:0 and 15:14)
+template <uint32_t N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N < 64u, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((int)((N & 15u) | 0x0070u | ((N >> 4) << 14)));
+}
+
+template <int TM, int TN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_mx(GemmJob j, uint32_t mtiles, uint32_t ntiles,
+                                                            uint32_t band, uint64_t seq,
+                                                            const uint64_t* __restrict__ flag) {
+    using T = MxTiling<TM, TN, WGM, WGN>;
+    constexpr uint32_t MS = T::MS, NS = T::NS, THREADS = T::THREADS, DEPTH = T::DEPTH;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
+    if (*flag == seq)
+        return;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, chunk = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave / WGN, wn = wave % WGN;
+    const TileRC tile = gemm_tile_of_block(blockIdx.x, gridDim.x, mtiles, ntiles, band);
+    const uint32_t m0 = tile.mt * TM, n0 = tile.nt * TN;
+    const uint32_t groups = j.groups;
+    uint2* const lut_all = reinterpret_cast<uint2*>(smem + T::OFF_LUT);
+    for (uint32_t i = tid; i < 256u * T::LUT_COPIES; i += THREADS) {
+        const uint32_t e = i / T::LUT_COPIES;
+        lut_all[i] = make_uint2(pm1_nibble(e & 15u), pm1_nibble(e >> 4));
+    }
+    const uint2* const lut = lut_all + (lane % T::LUT_COPIES);  // entry e at lut[32 e]
+
+    // the rows' DMA: instruction i of wave w fills LDS chunks p = 64 (A_INS w + i) + lane
+    // of a slot's rows, as a wave-uniform base plus a 32-bit per-lane offset (the rows of
+    // one launch chunk are far below 4 GiB); rows past the end are clamped (never stored)
+    uint32_t a_src[T::A_INS];
+#pragma unroll
+    for (uint32_t i = 0; i < T::A_INS; ++i) {
+        const uint32_t p = 64u * (T::A_INS * wave + i) + lane, r = p >> 3;
+        const uint32_t c = (p & 7u) ^ ((r >> 1) & 7u);
+        a_src[i] = min(m0 + r, j.rows - 1u) * j.k + 16u * c;
+    }
+    // the columns' DMA: chunk k = CPW w + lane of wave w (lanes past CPW inactive): chunk
+    // k < TN is the 16 bytes of sign bits of column n0 + k, chunk TN + c the scales of
+    // columns n0 + 8c .. +7; per group the bits advance 1 KiB (one 64-feature tile) and
+    // the scales 128 bytes.  The matrix tile of columns past the last one is clamped
+    // (never stored).
+    const unsigned char* col_src;
+    uint32_t col_step;
+    {
+        const uint32_t k = T::CPW * wave + min(lane, T::CPW - 1u);
+        const uint32_t col = k < (uint32_t)TN ? k : 8u * (k - TN);
+        const size_t t = min((n0 + col) >> 6, j.tiles - 1u);
+        if (k < (uint32_t)TN) {
+            col_src = reinterpret_cast<const unsigned char*>(j.wbits) + (t * groups * kTile + (col & 63u)) * 16u;
+            col_step = kTile * 16u;
+        } else {
+            col_src = reinterpret_cast<const unsigned char*>(j.wscale) + (t * groups * kTile + (col & 63u)) * 2u;
+            col_step = kTile * 2u;
+        }
+    }
+    const uint32_t la0 = lds_offset(smem);
+    auto issue_group = [&](uint32_t g) {
+        const uint32_t gg = min(g, groups - 1u);
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(j.q) + (size_t)gg * kGroup;
+        const uint32_t slot = la0 + (g % T::SLOTS) * T::SLOT_BYTES;
+#pragma unroll
+        for (uint32_t i = 0; i < T::A_INS; ++i)
+            dma16_s(a_src[i], base, slot + 1024u * (T::A_INS * wave + i));
+        dma16_lanes<lane_mask<T::CPW>()>(col_src + (size_t)gg * col_step, slot + T::A_BYTES + 16u * T::CPW * wave);
+    };
+    // A operand rows of this wave in a slot: row r = wm * WTM + 16 mi + (lane & 15)
+    uint32_t a_off[MS][2];
+#pragma unroll
+    for (uint32_t mi = 0; mi < MS; ++mi)
+#pragma unroll
+        for (uint32_t h = 0; h < 2; ++h)
+            a_off[mi][h] = swz128(wm * T::WTM + 16u * mi + (lane & 15u), 2u * chunk + h);
+    // this lane's columns in a slot: 4 bytes of sign bits (chunk c of the 16) and the scale
+    const uint32_t col0 = wn * T::WTN + (lane & 15u);
+
+    v4i dd[2][MS][NS];
+    float acc[MS][NS][4];
+#pragma unroll
+    for (uint32_t mi = 0; mi < MS; ++mi)
+#pragma unroll
+        for (uint32_t ni = 0; ni < NS; ++ni)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mi][ni][r] = 0.0f;
+    float sc_prev[NS], cneg_prev[NS];
+    const v4i c_init = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+
+    // group g (D set e = g % 2): its MFMAs into dd[e]; with `epi`, group g-1's epilogue
+    // from dd[e ^ 1] (scales sc_prev)
+    auto step = [&](uint32_t g, uint32_t e, bool epi) {
+        // this wave's DMAs of group g have landed (those of groups g+1 .. g+DEPTH-1 are
+        // newer); then every wave's have, and every wave has read the slot that group
+        // g+DEPTH takes
+        wait_vm_lgkm0<(DEPTH - 1u) * T::VM_PER_GROUP>();
+        barrier();
+        const unsigned char* slot = smem + (g % T::SLOTS) * T::SLOT_BYTES;
+        uint32_t bits[NS];
+        uint16_t sraw[NS];
+#pragma unroll
+        for (uint32_t ni = 0; ni < NS; ++ni) {
+            bits[ni] = *reinterpret_cast<const uint32_t*>(slot + T::A_BYTES + (col0 + 16u * ni) * 16u + 4u * chunk);
+            sraw[ni] = *reinterpret_cast<const uint16_t*>(slot + T::A_BYTES + 16u * TN + (col0 + 16u * ni) * 2u);
+        }
+        v4i a[MS][2], b[NS][2];
+#pragma unroll
+        for (uint32_t mi = 0; mi < MS; ++mi)
+#pragma unroll
+            for (uint32_t h = 0; h < 2; ++h)
+                a[mi][h] = *reinterpret_cast<const v4i*>(slot + a_off[mi][h]);
+#pragma unroll
+        for (uint32_t ni = 0; ni < NS; ++ni)
+#pragma unroll
+            for (uint32_t h = 0; h < 2; ++h) {
+                const uint2 lo = lut[T::LUT_COPIES * ((bits[ni] >> (16u * h)) & 0xffu)];
+                const uint2 hi = lut[T::LUT_COPIES * ((bits[ni] >> (16u * h + 8u)) & 0xffu)];
+                b[ni][h] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+            }
+        float sc[NS], cneg[NS];
+#pragma unroll
+        for (uint32_t ni = 0; ni < NS; ++ni) {
+            sc[ni] = __half2float(__ushort_as_half(sraw[ni]));
+            // the converted scale as a register operand of the epilogue's FMAs (folded into
+            // them, the conversion would make each a mixed-precision FMA)
+            asm volatile("" : "+v"(sc[ni]));
+            cneg[ni] = sc[ni] * -kMagicValue;  // exact
+        }
+        issue_group(g + DEPTH);
+        // the first halves of all subtiles (independent MFMAs, each after group g-1's
+        // epilogue on that subtile), then the second halves, each accumulating onto a first
+        // half issued MS * NS MFMAs earlier (a dependent MFMA right behind its source waits
+        // for that one's result)
+#pragma unroll
+        for (uint32_t mi = 0; mi < MS; ++mi)
+#pragma unroll
+            for (uint32_t ni = 0; ni < NS; ++ni) {
+                if (epi) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc_prev[ni],
+                                                                         __int_as_float(dd[e ^ 1u][mi][ni][r]),
+                                                                         cneg_prev[ni]);
+                }
+                dd[e][mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi][0], b[ni][0], c_init, 0, 0, 0);
+            }
+#pragma unroll
+        for (uint32_t mi = 0; mi < MS; ++mi)
+#pragma unroll
+            for (uint32_t ni = 0; ni < NS; ++ni)
+                dd[e][mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mi][1], b[ni][1], dd[e][mi][ni], 0, 0, 0);
+#pragma unroll
+        for (uint32_t ni = 0; ni < NS; ++ni) {
+            sc_prev[ni] = sc[ni];
+            cneg_prev[ni] = cneg[ni];
+        }
+    };
+
+    // prologue: groups 0 .. DEPTH-1 (the order the waits of step() count on)
+#pragma unroll
+    for (uint32_t g = 0; g < DEPTH; ++g)
+        issue_group(g);
+    step(0, 0, false);
+    uint32_t g = 1;
+    for (; g + 1u < groups; g += 2u) {
+        step(g, 1, true);
+        step(g + 1u, 0, true);
+    }
+    const bool last_in_d1 = g < groups;
+    if (last_in_d1)
+        step(g, 1, true);
+    // epilogue of the last group
+#pragma unroll
+    for (uint32_t mi = 0; mi < MS; ++mi)
+#pragma unroll
+        for (uint32_t ni = 0; ni < NS; ++ni)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[mi][ni][r] = acc[mi][ni][r] + __builtin_fmaf(sc_prev[ni],
+                                                                 __int_as_float(last_in_d1 ? dd[1][mi][ni][r]
+                                                                                           : dd[0][mi][ni][r]),
+                                                                 cneg_prev[ni]);
+    // no DMA may still be writing LDS when it is reused for the staged tile
+    wait_dma<0>();
+    barrier();
+    float* const so = reinterpret_cast<float*>(smem);
+#pragma unroll
+    for (uint32_t mi = 0; mi < MS; ++mi)
+#pragma unroll
+        for (uint32_t ni = 0; ni < NS; ++ni)
+#pragma unroll
+            for (uint32_t r = 0; r < 4; ++r)
+                so[(wm * T::WTM + 16u * mi + 4u * chunk + r) * T::OUT_STRIDE + wn * T::WTN + 16u * ni + (lane & 15u)] =
+                    acc[mi][ni][r];
+    barrier();
+    const bool vec = ((j.out_stride | (uint64_t)(uintptr_t)j.out) & 15u) == 0;
+    const bool scaled = j.mode == MODE_SUM_SCALED;
+#pragma unroll
+    for (uint32_t c0 = 0; c0 < TM * TN / 4u; c0 += THREADS) {
+        const uint32_t c = c0 + tid, row = c / (TN / 4u), col = 4u * (c % (TN / 4u));
+        const uint32_t m = m0 + row, n = n0 + col;
+        if (m >= j.rows || n >= j.n)
+            continue;
+        float4 v = *reinterpret_cast<const float4*>(so + row * T::OUT_STRIDE + col);
+        if (scaled) {
+            const float s = j.rscale[m];
+            v.x = v.x * s;
+            v.y = v.y * s;
+            v.z = v.z * s;
+            v.w = v.w * s;
+        }
+        float* dst = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride) + n;
+        if (vec && n + 4u <= j.n) {
+            const v4f w = {v.x, v.y, v.z, v.w};
+            __builtin_nontemporal_store(w, reinterpret_cast<v4f*>(dst));
+        } else {
+            dst[0] = v.x;
+            if (n + 1u < j.n)
+                dst[1] = v.y;
+            if (n + 2u < j.n)
+                dst[2] = v.z;
+            if (n + 3u < j.n)
+                dst[3] = v.w;
+        }
+    }
+}
+
 // The band width (in M tiles) of gemm_tile_of_block: an XCD covering band M tiles of
 // mtiles and (tiles / 8 / band) N tiles makes the rows (rows * k bytes) be fetched
 // into about 8 * band / mtiles L2s and the weights (1.125 bits each) into
@@ -1114,6 +1395,14 @@ hipError_t launch_ks(hipStream_t stream, const GemmJob& job, uint64_t seq, const
     const uint32_t ntiles = (job.n + 16u * TNS - 1u) / (16u * TNS);
     launch_kernel((k_gemm_ks<TMS, TNS, W, DEPTH>), dim3(mtiles * ntiles), dim3(64 * W), 0, stream, job, mtiles, ntiles,
                   gemm_band(job, mtiles), seq, flag);
+    return hipGetLastError();
+}
+
+template <int TM, int TN, int WGM, int WGN>
+hipError_t launch_mx(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
+    const uint32_t mtiles = (job.rows + TM - 1u) / TM, ntiles = (job.n + TN - 1u) / TN;
+    launch_kernel((k_gemm_mx<TM, TN, WGM, WGN>), dim3(mtiles * ntiles), dim3(64 * WGM * WGN), 0, stream, job,
+                  mtiles, ntiles, gemm_band(job, mtiles), seq, flag);
     return hipGetLastError();
 }
 
@@ -1164,6 +1453,10 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
     // beats the tiled kernels, whose per-group steps serialise over the long K
     if (job.mode != MODE_DOT_I16 && job.groups >= 32u && blocks(32, 32) >= 2u * cus && blocks(32, 32) <= 3u * cus)
         return launch_wv<2, 2, 1, 1, 4>(stream, job, seq, flag);
+    if (job.mode != MODE_DOT_I16 && blocks(128, 192) >= cus)
+        return launch_mx<128, 192, 2, 4>(stream, job, seq, flag);
+    if (job.mode != MODE_DOT_I16 && blocks(64, 128) >= cus && job.groups >= 32u)
+        return launch_mx<64, 128, 2, 4>(stream, job, seq, flag);
     if (BNN_GEMM_CO && job.mode != MODE_DOT_I16 && blocks(128, 128) >= cus)
         return launch_co<128, 128, 2, 2>(stream, job, seq, flag);
     // 128 x 128 tiles also where 64 x 128 ones would need a second round of workgroups
