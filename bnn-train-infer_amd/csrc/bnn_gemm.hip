@@ -1110,9 +1110,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_wv(GemmJob j, uint32_t mt
 //     group g's first-half MFMA on it; the second halves follow, each accumulating onto
 //     a first half issued MS * NS MFMAs earlier.
 // The K order inside a group is that of k_gemm_ks / k_gemm_wv (lane chunk c: weights
-// 32c .. 32c+31, MFMA half h the 16 from 32c + 16h).  The results are stored from the
-// registers (through LDS as 16-byte row stores measured no faster: the 25 MB of a
-// 1024 x 6144 output are written at the write bandwidth either way).
+// 32c .. 32c+31, MFMA half h the 16 from 32c + 16h).  The tile leaves through LDS as
+// 16-byte row-contiguous stores where the output view allows (stored straight from the
+// registers, 64 bytes per row and instruction, it ran as fast but wrote 1.3-1.45x the
+// output's bytes).
 template <int TM, int TN, int WGM, int WGN>
 struct MxTiling {
     static constexpr uint32_t WAVES = WGM * WGN, THREADS = 64u * WAVES;
@@ -1130,7 +1131,10 @@ struct MxTiling {
     // copy l % 32, i.e. only its own pair of the 64 banks, so that the lanes' lookups of
     // arbitrary entries never conflict
     static constexpr uint32_t LUT_COPIES = 32;
-    static constexpr uint32_t OFF_LUT = SLOTS * SLOT_BYTES, SMEM = OFF_LUT + 256u * LUT_COPIES * 8u;
+    static constexpr uint32_t OFF_LUT = SLOTS * SLOT_BYTES, LOOP_BYTES = OFF_LUT + 256u * LUT_COPIES * 8u;
+    static constexpr uint32_t OUT_STRIDE = TN + 4u;  // floats per staged output row
+    static constexpr uint32_t OUT_BYTES = TM * OUT_STRIDE * 4u;
+    static constexpr uint32_t SMEM = LOOP_BYTES > OUT_BYTES ? LOOP_BYTES : OUT_BYTES;
     static_assert(TM % (16 * WGM) == 0 && TN % (16 * WGN) == 0, "wave tiles of 16 x 16 subtiles");
     static_assert(TN % 64 == 0, "whole 64-feature tiles of the matrix layout");
     static_assert(TM * 8u % THREADS == 0 && A_INS >= 1u, "whole row DMAs per thread");
@@ -1138,6 +1142,7 @@ struct MxTiling {
     static_assert(SLOT_BYTES % 16u == 0 && OFF_LUT % 16u == 0, "16-byte DMA destinations");
     static_assert((DEPTH - 1u) * VM_PER_GROUP < 64u, "vmcnt range");
     static_assert(SMEM <= 160u * 1024u, "LDS");
+    static_assert(TM * TN / 4u % THREADS == 0, "output chunks per thread");
 };
 
 // s_waitcnt vmcnt(N) lgkmcnt(0) for N < 64 (the gfx9 encoding splits vmcnt into bits
@@ -1324,26 +1329,49 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_mx(GemmJob j, uint32_t 
                                                                  __int_as_float(last_in_d1 ? dd[1][mi][ni][r]
                                                                                            : dd[0][mi][ni][r]),
                                                                  cneg_prev[ni]);
-    // no DMA may still be in flight when the workgroup ends; the results leave from the
-    // registers (each store of 16 lanes writes 64 contiguous bytes of one row)
+    // no DMA may still be writing LDS when it is reused for the staged tile
     wait_dma<0>();
-    const bool scaled = j.mode == MODE_SUM_SCALED;
+    barrier();
+    float* const so = reinterpret_cast<float*>(smem);
 #pragma unroll
     for (uint32_t mi = 0; mi < MS; ++mi)
 #pragma unroll
-        for (uint32_t r = 0; r < 4; ++r) {
-            const uint32_t m = m0 + wm * T::WTM + 16u * mi + 4u * chunk + r;
-            if (m >= j.rows)
-                continue;
-            const float s = scaled ? j.rscale[m] : 1.0f;
-            float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
+        for (uint32_t ni = 0; ni < NS; ++ni)
 #pragma unroll
-            for (uint32_t ni = 0; ni < NS; ++ni) {
-                const uint32_t n = n0 + wn * T::WTN + 16u * ni + (lane & 15u);
-                if (n < j.n)
-                    __builtin_nontemporal_store(scaled ? acc[mi][ni][r] * s : acc[mi][ni][r], orow + n);
-            }
+            for (uint32_t r = 0; r < 4; ++r)
+                so[(wm * T::WTM + 16u * mi + 4u * chunk + r) * T::OUT_STRIDE + wn * T::WTN + 16u * ni + (lane & 15u)] =
+                    acc[mi][ni][r];
+    barrier();
+    const bool vec = ((j.out_stride | (uint64_t)(uintptr_t)j.out) & 15u) == 0;
+    const bool scaled = j.mode == MODE_SUM_SCALED;
+#pragma unroll
+    for (uint32_t c0 = 0; c0 < TM * TN / 4u; c0 += THREADS) {
+        const uint32_t c = c0 + tid, row = c / (TN / 4u), col = 4u * (c % (TN / 4u));
+        const uint32_t m = m0 + row, n = n0 + col;
+        if (m >= j.rows || n >= j.n)
+            continue;
+        float4 v = *reinterpret_cast<const float4*>(so + row * T::OUT_STRIDE + col);
+        if (scaled) {
+            const float s = j.rscale[m];
+            v.x = v.x * s;
+            v.y = v.y * s;
+            v.z = v.z * s;
+            v.w = v.w * s;
         }
+        float* dst = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride) + n;
+        if (vec && n + 4u <= j.n) {
+            const v4f w = {v.x, v.y, v.z, v.w};
+            __builtin_nontemporal_store(w, reinterpret_cast<v4f*>(dst));
+        } else {
+            dst[0] = v.x;
+            if (n + 1u < j.n)
+                dst[1] = v.y;
+            if (n + 2u < j.n)
+                dst[2] = v.z;
+            if (n + 3u < j.n)
+                dst[3] = v.w;
+        }
+    }
 }
 
 // The band width (in M tiles) of gemm_tile_of_block: an XCD covering band M tiles of
