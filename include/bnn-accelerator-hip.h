@@ -68,11 +68,13 @@ BNN_Status BNNX_ExecuteBatch(BNN_Device device, const BNN_Job* jobs, uint32_t co
  * for an output view that is not naturally aligned, its staged output rows) in one
  * fixed 8 MiB device array per GPU, created with the library's code object and held
  * until the process ends; the rows run in chunks that fit it, on the bit-plane dot
- * kernels (never on the matrix cores, whose +1/-1 weight copy BNN_Execute allocates).
- * A job whose single row does not fit the array is rejected with BNN_ENOMEM (none
- * does within the 8192-feature limits of BNN_DeviceGetCaps).  Single-row outputs are
- * not mirrored in host memory.  Every call on one GPU, from any BNN_Device handle
- * opened on it, shares that array: calls that overlap in time on one GPU race.
+ * kernels.  A job whose single row does not fit the array is rejected with
+ * BNN_ENOMEM (none does within the 8192-feature limits of BNN_DeviceGetCaps).
+ * Single-row outputs are not mirrored in host memory.  Every call on one GPU, from
+ * any BNN_Device handle opened on it, shares that array; the call is synchronous and
+ * holds a per-GPU lock while it uses the array, so calls from several threads or
+ * handles on one GPU run one after another (devices stay independent, as
+ * bnn-accelerator.h requires of BNN_Device handles).
  */
 BNN_Status BNNX_ExecuteNoAlloc(BNN_Device device, const BNN_Job* job);
 
