@@ -166,14 +166,59 @@ struct TileRegs {
 // arguments, loaded with them at the start: the first tile's job is taken from there, so
 // its weights are requested without first waiting for a table read (or the dependent
 // reads of a walk); later tiles (prefetches) read the table.
+// A kernel-argument value as an opaque scalar register: the compiler then keeps it as a
+// value loaded with the other arguments at the start, and a uniform choice among such
+// values stays a choice of values (left to itself it turns a choice among argument
+// fields into a choice of address and loads the field afterwards, one dependent round
+// of scalar loads per choice).
+__device__ __forceinline__ uint32_t sreg(uint32_t v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+template <class T>
+__device__ __forceinline__ T* sreg(T* p) {
+    uint64_t x = (uint64_t)p;
+    asm volatile("" : "+s"(x));
+    return (T*)x;
+}
+
+// slot i of three, as a choice of values (uniform i)
+template <class T>
+__device__ __forceinline__ T pick3(uint32_t i, T a, T b, T c) {
+    a = sreg(a);
+    b = sreg(b);
+    c = sreg(c);
+    return i == 0u ? a : i == 1u ? b : c;
+}
+
 template <bool SINGLE>
 struct JobTable {
     const FusedArgs& fa;
     typedef const __attribute__((address_space(4))) FusedJob* Ptr;
     static_assert(kFusedInline == 3, "the inline selections name three slots");
+    // the inline slots, every field read at the start (SINGLE: the one job)
+    FusedJob slot[kFusedInline];
+    __device__ __forceinline__ static FusedJob held(const FusedJob& s) {
+        FusedJob j;
+        j.wbits = sreg(s.wbits);
+        j.wscale = sreg(s.wscale);
+        j.out = sreg(s.out);
+        j.n = sreg(s.n);
+        j.tiles = sreg(s.tiles);
+        j.first_tile = sreg(s.first_tile);
+        j.post_off = sreg(s.post_off);
+        return j;
+    }
+    __device__ __forceinline__ explicit JobTable(const FusedArgs& f) : fa(f) {
+        slot[0] = held(f.inl[0]);
+        if constexpr (!SINGLE) {
+            slot[1] = held(f.inl[1]);
+            slot[2] = held(f.inl[2]);
+        }
+    }
     __device__ __forceinline__ uint32_t first_tile(uint32_t i) const {
         if constexpr (SINGLE)
-            return fa.inl[0].first_tile;
+            return slot[0].first_tile;
         else
             return ((Ptr)fa.jobs)[i].first_tile;
     }
@@ -182,7 +227,7 @@ struct JobTable {
         if (SINGLE || nwalk == 1u)
             return 0;
         if (fa.inline_jobs)
-            return t >= fa.inl[2].first_tile && nwalk > 2u ? 2u : t >= fa.inl[1].first_tile ? 1u : 0u;
+            return t >= slot[2].first_tile && nwalk > 2u ? 2u : t >= slot[1].first_tile ? 1u : 0u;
         if (fa.walk_shift < 32u)
             return min(t >> fa.walk_shift, nwalk - 1u);
         uint32_t from = 0;
@@ -191,19 +236,24 @@ struct JobTable {
         return from;
     }
     __device__ __forceinline__ FusedJob first(uint32_t i) const {
-        if (SINGLE || fa.inline_jobs) {
-            FusedJob j = fa.inl[0];
-            if (i == 1u)
-                j = fa.inl[1];
-            if (i == 2u)
-                j = fa.inl[2];
+        if constexpr (SINGLE)
+            return slot[0];
+        if (fa.inline_jobs) {
+            FusedJob j;
+            j.wbits = pick3(i, slot[0].wbits, slot[1].wbits, slot[2].wbits);
+            j.wscale = pick3(i, slot[0].wscale, slot[1].wscale, slot[2].wscale);
+            j.out = pick3(i, slot[0].out, slot[1].out, slot[2].out);
+            j.n = pick3(i, slot[0].n, slot[1].n, slot[2].n);
+            j.tiles = pick3(i, slot[0].tiles, slot[1].tiles, slot[2].tiles);
+            j.first_tile = pick3(i, slot[0].first_tile, slot[1].first_tile, slot[2].first_tile);
+            j.post_off = pick3(i, slot[0].post_off, slot[1].post_off, slot[2].post_off);
             return j;
         }
         return (*this)[i];
     }
     __device__ __forceinline__ FusedJob operator[](uint32_t i) const {
         if constexpr (SINGLE)
-            return fa.inl[0];
+            return slot[0];
         const Ptr c = (Ptr)fa.jobs;
         FusedJob j;
         j.wbits = c[i].wbits;
@@ -296,6 +346,11 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t K = fa.width, G = K / kGroup;
+    // the row's operands, read with the job slots in the first round of argument loads
+    const int32_t kind = (int32_t)sreg((uint32_t)fa.kind);
+    const float* const row_a = sreg(fa.kind == PRE_ROW ? fa.row : fa.a);
+    const float* const row_b = sreg(fa.b);
+    const float* const row_gain = sreg(fa.gain);
 
     // row element i of a thread: half i % 2 of group w + 16 (i / 2), w its wave -- the
     // groups of the wave's dots (whole waves: K % 128 == 0)
@@ -306,7 +361,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     // load counter completes in order: the row is needed first), arriving while the
     // row is produced
     // tiles are walked over the jobs, or over the pairs (the first half of the table)
-    const JobTable<SINGLE> jobs{fa};
+    const JobTable<SINGLE> jobs(fa);
     constexpr bool paired = PAIRED;  // fa.post == POST_SILU_MUL
     const uint32_t nwalk = paired ? fa.njobs / 2u : fa.njobs, pair_step = paired ? nwalk : 0u;
     // the job (or pair) of tile t: first tiles at multiples of 2^walk_shift give it in one
@@ -320,8 +375,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     };
     uint32_t tile = blockIdx.x, ji = jobs.first_job_of(tile, nwalk);
     FusedJob job = jobs.first(ji), job2 = jobs.first(ji + pair_step);
-    const float* src_a = fa.kind == PRE_ROW ? fa.row : fa.a;
-    const bool int_row = SINGLE && fa.kind == PRE_ROW_I8;
+    const bool int_row = SINGLE && kind == PRE_ROW_I8;
     const bool dot_out = SINGLE && fa.dot_out;
     float* const mirror = SINGLE ? fa.mirror : nullptr;
     float xv[EPT], bv[EPT], gv[EPT];
@@ -333,17 +387,17 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     } else {
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
-            xv[i] = gload(src_a + min(elem(i), K - 1u));
+            xv[i] = gload(row_a + min(elem(i), K - 1u));
     }
-    if (fa.b) {
+    if (row_b) {
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
-            bv[i] = gload(fa.b + min(elem(i), K - 1u));
+            bv[i] = gload(row_b + min(elem(i), K - 1u));
     }
-    if (fa.kind == PRE_RMSNORM) {
+    if (kind == PRE_RMSNORM) {
 #pragma unroll
         for (int i = 0; i < EPT; ++i)
-            gv[i] = gload(fa.gain + min(elem(i), K - 1u));
+            gv[i] = gload(row_gain + min(elem(i), K - 1u));
     }
     // a ring of RING tiles' weights in flight: a workgroup that walks several tiles (the
     // lm_head's 2370 over one workgroup per CU) would otherwise wait one memory latency per tile
