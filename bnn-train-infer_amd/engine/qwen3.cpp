@@ -182,12 +182,16 @@ private:
     BNNE_Status open_device_path(bool fused, Resident** out);
     void step(uint32_t token, uint32_t pos, float* logits);
     void attend(uint32_t layer, uint32_t pos);
+    void host_cache();
 
     Qwen3Model& m_;
     const Shape& s_;
     // host step: the activation rows, attention scratch and the KV cache
     std::vector<float> x_, norm_, q_, k_, v_, y_, o_, gate_, up_, scores_, probs_;
-    std::vector<float> keys_, values_;  // [layer][position][kv_width], host step only
+    // host step only, per layer and key/value head: keys [n_ctx / 8][head_dim][8] (blocks
+    // of eight positions), values [n_ctx][head_dim]
+    std::vector<float> keys_, values_;
+    uint32_t ctx_blocks_ = 0;  // ceil(n_ctx / 8)
     std::vector<float> cos_, sin_;      // RoPE rotation of pair j at position p: [p][head_dim / 2]
     Resident* device_ = nullptr;
 };
@@ -217,11 +221,17 @@ Qwen3Context::Qwen3Context(Qwen3Model& m, const BNNE_ContextParams& p)
     const BNNE_Status st = open_device_path(true, &device_);
     if (st == BNNE_ENOTSUP) {
         forget_message();
-        keys_.resize((size_t)s_.layers * p.n_ctx * s_.kv_width);
-        values_.resize(keys_.size());
+        host_cache();
     } else if (st != BNNE_OK) {
         throw Failure{st};
     }
+}
+
+void Qwen3Context::host_cache() {
+    ctx_blocks_ = (params.n_ctx + 7u) / 8u;
+    keys_.assign((size_t)s_.layers * s_.kv_width * ctx_blocks_ * 8u, 0.0f);
+    values_.assign((size_t)s_.layers * s_.kv_width * params.n_ctx, 0.0f);
+    scores_.assign((size_t)ctx_blocks_ * 8u, 0.0f);  // the key blocks' lanes past the position too
 }
 
 BNNE_Status Qwen3Context::open_device_path(bool fused, Resident** out) {
@@ -256,8 +266,7 @@ void Qwen3Context::select_path(int path) {
     if (pos != 0)
         raise(BNNE_EINVAL, "the decode path is chosen before the first token");
     if (path == 0) {
-        keys_.resize((size_t)s_.layers * params.n_ctx * s_.kv_width);
-        values_.resize(keys_.size());
+        host_cache();
         resident_free(device_);
         device_ = nullptr;
         return;
@@ -294,45 +303,104 @@ void rotate(float* head, const float* c, const float* s, uint32_t half) {
     }
 }
 
+// Eight binary32 lanes (GCC vector extension).  The target clones below compile them to
+// AVX2 on processors that have it and to pairs of SSE2 operations elsewhere; neither
+// enables FMA.  Only lane-wise multiplies and adds are used, each rounded once, and each
+// lane carries one sum of the scalar loop in the scalar loop's order, so the results are
+// those of the scalar loops bit for bit.
+typedef float f32x8 __attribute__((vector_size(32)));
+// the same, for loads and stores at any float address
+typedef float f32x8_at __attribute__((vector_size(32), aligned(4), may_alias));
+#define LOAD8(p) (*(const f32x8_at*)(p))
+#define STORE8(p, v) (*(f32x8_at*)(p) = (v))
+
+// scores[t] = (q . key_t) * scale for t < 8 * ceil(n / 8) (qwen3.c:441-452), each dot in
+// index order.  The keys of a head come in blocks of eight positions, kb[(t / 8) * dim * 8
+// + i * 8 + t % 8] = key_t[i], so that eight positions' sums advance as the lanes of one
+// vector over contiguous memory; the lanes past n compute values that are not used.
+__attribute__((target_clones("avx2", "default"))) void
+key_scores(const float* q, const float* kb, uint32_t dim, uint32_t n, float scale, float* scores) {
+    const uint32_t blocks = (n + 7u) / 8u;
+    const size_t stride = (size_t)dim * 8u;
+    const float sc = scale;
+    uint32_t b = 0;
+    for (; b + 4u <= blocks; b += 4u) {
+        const float* k = kb + b * stride;
+        f32x8 d0 = {}, d1 = {}, d2 = {}, d3 = {};
+        for (uint32_t i = 0; i < dim; ++i) {
+            const float qi = q[i];
+            d0 += qi * LOAD8(k + i * 8u);
+            d1 += qi * LOAD8(k + stride + i * 8u);
+            d2 += qi * LOAD8(k + 2u * stride + i * 8u);
+            d3 += qi * LOAD8(k + 3u * stride + i * 8u);
+        }
+        STORE8(scores + 8u * b, d0 * sc);
+        STORE8(scores + 8u * b + 8u, d1 * sc);
+        STORE8(scores + 8u * b + 16u, d2 * sc);
+        STORE8(scores + 8u * b + 24u, d3 * sc);
+    }
+    for (; b < blocks; ++b) {
+        const float* k = kb + b * stride;
+        f32x8 d = {};
+        for (uint32_t i = 0; i < dim; ++i)
+            d += q[i] * LOAD8(k + i * 8u);
+        STORE8(scores + 8u * b, d * sc);
+    }
+}
+
+// out[i] = sum over t < n in position order of p[t] * v[t * dim + i], i < dim
+// (qwen3.c:466-478): the lanes are eight of the outputs.
+__attribute__((target_clones("avx2", "default"))) void
+weighted_rows(const float* p, const float* v, uint32_t n, uint32_t dim, float* out) {
+    uint32_t i = 0;
+    for (; i + 64u <= dim; i += 64u) {
+        f32x8 a0 = {}, a1 = {}, a2 = {}, a3 = {}, a4 = {}, a5 = {}, a6 = {}, a7 = {};
+        for (uint32_t t = 0; t < n; ++t) {
+            const float* r = v + (size_t)t * dim + i;
+            const float pt = p[t];
+            a0 += pt * LOAD8(r);
+            a1 += pt * LOAD8(r + 8);
+            a2 += pt * LOAD8(r + 16);
+            a3 += pt * LOAD8(r + 24);
+            a4 += pt * LOAD8(r + 32);
+            a5 += pt * LOAD8(r + 40);
+            a6 += pt * LOAD8(r + 48);
+            a7 += pt * LOAD8(r + 56);
+        }
+        STORE8(out + i, a0);
+        STORE8(out + i + 8, a1);
+        STORE8(out + i + 16, a2);
+        STORE8(out + i + 24, a3);
+        STORE8(out + i + 32, a4);
+        STORE8(out + i + 40, a5);
+        STORE8(out + i + 48, a6);
+        STORE8(out + i + 56, a7);
+    }
+    for (; i + 8u <= dim; i += 8u) {
+        f32x8 a = {};
+        for (uint32_t t = 0; t < n; ++t)
+            a += p[t] * LOAD8(v + (size_t)t * dim + i);
+        STORE8(out + i, a);
+    }
+    for (; i < dim; ++i) {
+        float a = 0.0f;
+        for (uint32_t t = 0; t < n; ++t)
+            a += p[t] * v[(size_t)t * dim + i];
+        out[i] = a;
+    }
+}
+
 // Every query head against cache rows 0..pos of its key/value head (qwen3.c:441-478):
 // scores q.k * (1 / sqrt(head_dim)), softmax, probability-weighted sum of the values.
 void Qwen3Context::attend(uint32_t layer, uint32_t pos) {
     const uint32_t HD = s_.head_dim, group = s_.heads / s_.kv_heads;
     const float scale = 1.0f / sqrtf((float)HD);
-    const float* keys = keys_.data() + (size_t)layer * params.n_ctx * s_.kv_width;
-    const float* values = values_.data() + (size_t)layer * params.n_ctx * s_.kv_width;
     for (uint32_t h = 0; h < s_.heads; ++h) {
         const float* q = q_.data() + (size_t)h * HD;
-        const size_t kv_head = (size_t)(h / group) * HD;
-        // q.k for four positions at a time: four independent in-order sums, so that their
-        // dependent additions overlap (each dot still adds its terms in index order)
-        uint32_t t = 0;
-        for (; t + 4u <= pos + 1u; t += 4u) {
-            const float* k0 = keys + (size_t)t * s_.kv_width + kv_head;
-            const float* k1 = k0 + s_.kv_width;
-            const float* k2 = k1 + s_.kv_width;
-            const float* k3 = k2 + s_.kv_width;
-            float d0 = 0.0f, d1 = 0.0f, d2 = 0.0f, d3 = 0.0f;
-            for (uint32_t i = 0; i < HD; ++i) {
-                d0 += q[i] * k0[i];
-                d1 += q[i] * k1[i];
-                d2 += q[i] * k2[i];
-                d3 += q[i] * k3[i];
-            }
-            scores_[t] = d0 * scale;
-            scores_[t + 1u] = d1 * scale;
-            scores_[t + 2u] = d2 * scale;
-            scores_[t + 3u] = d3 * scale;
-        }
-        for (; t <= pos; ++t) {
-            const float* key = keys + (size_t)t * s_.kv_width + kv_head;
-            float dot = 0.0f;
-            for (uint32_t i = 0; i < HD; ++i)
-                dot += q[i] * key[i];
-            scores_[t] = dot * scale;
-        }
+        const size_t kv = (size_t)layer * s_.kv_heads + h / group;
+        key_scores(q, keys_.data() + kv * HD * ctx_blocks_ * 8u, HD, pos + 1u, scale, scores_.data());
         float top = -INFINITY;
-        for (t = 0; t <= pos; ++t) {
+        for (uint32_t t = 0; t <= pos; ++t) {
             const float score = scores_[t];
             if (!std::isfinite(score))
                 raise(BNNE_ECOMPUTE, "non-finite attention score");
@@ -348,18 +416,7 @@ void Qwen3Context::attend(uint32_t layer, uint32_t pos) {
             raise(BNNE_ECOMPUTE, "softmax normaliser is zero or not finite");
         for (uint32_t t = 0; t <= pos; ++t)
             probs_[t] /= total;
-        // out[i] = sum over t in position order of probs[t] * value[t][i]: the positions in
-        // the outer loop, so that each cache row is read once and in order (every out[i]
-        // still receives its terms in the same order, one rounding each)
-        float* out = y_.data() + (size_t)h * HD;
-        for (uint32_t i = 0; i < HD; ++i)
-            out[i] = 0.0f;
-        for (uint32_t t = 0; t <= pos; ++t) {
-            const float p = probs_[t];
-            const float* value = values + (size_t)t * s_.kv_width + kv_head;
-            for (uint32_t i = 0; i < HD; ++i)
-                out[i] += p * value[i];
-        }
+        weighted_rows(probs_.data(), values_.data() + kv * params.n_ctx * HD, pos + 1u, HD, y_.data() + (size_t)h * HD);
     }
 }
 
@@ -388,9 +445,15 @@ void Qwen3Context::step(uint32_t token, uint32_t pos, float* logits) {
             rotate(q_.data() + (size_t)h * HD, c, sn, half);
         for (uint32_t h = 0; h < s_.kv_heads; ++h)
             rotate(k_.data() + (size_t)h * HD, c, sn, half);
-        const size_t row = ((size_t)l * params.n_ctx + pos) * s_.kv_width;
-        std::memcpy(keys_.data() + row, k_.data(), (size_t)s_.kv_width * sizeof(float));
-        std::memcpy(values_.data() + row, v_.data(), (size_t)s_.kv_width * sizeof(float));
+        // per key/value head: the keys in blocks of eight positions, [pos / 8][HD][pos % 8],
+        // the values by position, [pos][HD]
+        for (uint32_t kh = 0; kh < s_.kv_heads; ++kh) {
+            const size_t kv = (size_t)l * s_.kv_heads + kh;
+            float* key_lane = keys_.data() + (kv * ctx_blocks_ + pos / 8u) * HD * 8u + pos % 8u;
+            for (uint32_t i = 0; i < HD; ++i)
+                key_lane[i * 8u] = k_[(size_t)kh * HD + i];
+            std::memcpy(values_.data() + (kv * params.n_ctx + pos) * HD, v_.data() + (size_t)kh * HD, HD * sizeof(float));
+        }
         attend(l, pos);
         L.o.apply(*this, y_.data(), o_.data());
         for (uint32_t i = 0; i < C; ++i)
