@@ -153,16 +153,18 @@ def test_fused_rmsnorm(pkg, hipdev, oracle, k, ns, with_b, with_out):
         f.free()
 
 
-@pytest.mark.parametrize("ns,kind", [
-    ([8192, 8192, 8192], "rms"),          # 384 tiles: workgroups walk tiles, jobs at multiples of 128 tiles
-    ([8192, 3000, 8192, 4213], "row"),    # 394 tiles: jobs at irregular tiles (the table walk)
-    ([6144] * 4 + [4096], "rms"),         # 448 tiles
+@pytest.mark.parametrize("ns,kind,k", [
+    ([8192, 8192, 8192], "rms", 2048),          # 384 tiles: workgroups walk tiles, jobs at multiples of 128 tiles
+    ([8192, 3000, 8192, 4213], "row", 2048),    # 394 tiles: jobs at irregular tiles (the table walk)
+    ([6144] * 4 + [4096], "rms", 2048),         # 448 tiles
+    ([8192] * 18 + [4213], "rms", 2048),        # the lm_head's 2370 tiles (~9 per workgroup)
+    ([8192] * 8 + [3000, 4213], "row", 1152),   # 1137 tiles of 9 groups, irregular job starts
+    ([8192] * 36, "row", 128),                  # 4608 tiles of one group
 ])
-def test_fused_many_tiles(pkg, hipdev, oracle, ns, kind):
+def test_fused_many_tiles(pkg, hipdev, oracle, ns, kind, k):
     """Batches with more tiles than workgroups (one per CU): each workgroup walks several
     tiles with a ring of weights in flight, finding each tile's job in one step when the
     jobs start at multiples of a power of two and by walking the table otherwise."""
-    k = 2048
     rng = np.random.default_rng(len(ns))
     f = Fused(pkg, hipdev, k, ns, seed=17)
     try:
