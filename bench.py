@@ -48,6 +48,7 @@ import importlib.util
 import json
 import os
 import sys
+import threading
 import time
 from pathlib import Path
 
@@ -117,19 +118,65 @@ DECODE_CALLS = [((2048, 2048), 56), ((2048, 1024), 56), ((2048, 6144), 56), ((61
 MLP_SHAPES = [(896, 512), (512, 512), (512, 10)]  # bnn-mlp blocks, one GEMV_F32 each per sample
 
 
+def cpu_all_cores(pkg, api, cores, seconds: float = 3.0):
+    """The headline job on every allowed host core at once: one thread per core, each
+    pinned to its core with its own device handle (the backend's devices are independent)
+    and its own matrix, calling BNN_Execute for `seconds` after a common start; aggregate
+    GB/s = all calls' algorithmic bytes / the slowest thread's time.  The threads are joined
+    before this returns."""
+    results = [None] * len(cores)
+    start = threading.Barrier(len(cores))
+
+    def work(i, core):
+        os.sched_setaffinity(0, {core})  # this thread only
+        with pkg.Device(api, 0) as dev:
+            bits, scales = pkg.synth.matrix(N_OUT, K_IN, seed=3)
+            x = pkg.synth.normal_f32(1, K_IN, seed=3)
+            m = dev.matrix(bits, scales)
+            bi, bo = dev.buffer(x.nbytes), dev.buffer(4 * N_OUT)
+            bi.write(x)
+            job = pkg.Job(int(pkg.Op.GEMV_F32), m.handle.value, bi.view(pkg.Type.F32), bo.view(pkg.Type.F32), 1)
+            start.wait()
+            calls, t0 = 0, time.perf_counter()
+            while calls == 0 or time.perf_counter() - t0 < seconds:
+                if dev.execute(job) != 0:
+                    break
+                calls += 1
+            results[i] = (calls, time.perf_counter() - t0)
+            bi.free()
+            bo.free()
+            m.destroy()
+
+    threads = [threading.Thread(target=work, args=(i, c)) for i, c in enumerate(cores)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    if any(r is None for r in results):
+        return None
+    calls = sum(c for c, _ in results)
+    wall = max(w for _, w in results)
+    return {"value": round(calls * BYTES_PER_JOB / wall / 1e9, 5), "unit": "GB/s", "cores": len(cores),
+            "sample": f"{calls} GEMV_F32 {K_IN}->{N_OUT} rows=1 calls over {len(cores)} threads, one per core "
+                      f"(cores {cores[0]}..{cores[-1]}), in {wall:.1f} s"}
+
+
 def cpu_baseline(pkg, seconds: float = 6.0, per_shape: float = 0.8):
     """Bounded single-core samples on the host (checker-side code): the headline job for
     `seconds`, then every benchmark configuration -- each distinct job shape timed for
     about `per_shape` seconds (at least one call) and composed into the configuration's
-    unit (samples/s, GB/s, TOPS, tok/s)."""
+    unit (samples/s, GB/s, TOPS, tok/s); beside them the headline job on all allowed
+    cores at once (`all_cores`)."""
     ref = ROOT / "oracle" / "_ref" / "libbnn_soft_ref.so"
     port = ROOT / "oracle" / "lib" / "liboracle_cpu.so"
     path, kind = (ref, "reference") if ref.exists() else (port, "port")
     if not path.exists():
         return None
-    core = sorted(os.sched_getaffinity(0))[0]
-    os.sched_setaffinity(0, {core})
     api = pkg.Api(path)
+    allowed = sorted(os.sched_getaffinity(0))
+    all_cores = cpu_all_cores(pkg, api, allowed)
+    core = allowed[0]
+    os.sched_setaffinity(0, {core})
     t_all = time.perf_counter()
 
     def per_call(dev, op, k, n, rows, seed, budget):
@@ -206,7 +253,7 @@ def cpu_baseline(pkg, seconds: float = 6.0, per_shape: float = 0.8):
                       f"({cpu_name}, nproc {os.cpu_count()}), {head * 1e3:.1f} ms/call; per config below, each "
                       f"job shape timed for ~{per_shape} s (one call at least); {time.perf_counter() - t_all:.0f} s "
                       f"in all",
-            "library": str(path.relative_to(ROOT)), "configs": configs}
+            "library": str(path.relative_to(ROOT)), "configs": configs, "all_cores": all_cores}
 
 
 def _timed_calls(dev, job, reps):
