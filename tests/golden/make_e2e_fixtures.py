@@ -7,7 +7,7 @@ them, and stores its outputs (per decode step: greedy token and an FNV-1a-64 has
 of the logits bytes; for classification: every logit's float32 bits, hashed) as
 JSON fixtures under tests/golden/.  Run from the repository root:
 
-    python tests/golden/make_e2e_fixtures.py [tiny] [mlp] [long] [rope] [error] [full FULL_OUTPUT.txt]
+    python tests/golden/make_e2e_fixtures.py [tiny] [mlp] [long] [rope] [shapes] [error] [full FULL_OUTPUT.txt]
 
 'full' converts the output of a full-size run made beforehand (it takes ~15 min on
 one core):  oracle/_ref/engine_run_soft llm MODEL.gguf PROMPT.txt 127 1024
@@ -43,6 +43,15 @@ ROPE = {
     "yarn_default_original": dict(TINY, context=8192, rope_scaling={"type": "yarn", "factor": 2.5}),
     "linear": dict(TINY, rope_scaling={"type": "linear", "factor": 4.0}),
 }
+
+# head widths that are not multiples of 32 or of 8 (20 = 2 x 8 + 4; 72 = 64 + 8; the reference
+# requires heads x head_dim = width and kv_heads x head_dim in groups of 128, qwen3.c:179-188),
+# over a context that is not a multiple of 8
+SHAPES = {
+    "hd20": dict(layers=2, hidden=640, heads=32, kv_heads=32, head_dim=20, ffn=256, vocab=300, context=128, seed=31),
+    "hd72": dict(layers=2, hidden=1152, heads=16, kv_heads=16, head_dim=72, ffn=256, vocab=300, context=128, seed=37),
+}
+SHAPES_CTX = 61
 
 
 def package():
@@ -107,6 +116,20 @@ def rope(pkg):
     (GOLDEN / "e2e_qwen3_rope.json").write_text(json.dumps(res, indent=1) + "\n")
 
 
+def shapes(pkg):
+    res = {}
+    for name, params in SHAPES.items():
+        with tempfile.TemporaryDirectory() as d:
+            model, ids = Path(d) / "shape.gguf", Path(d) / "ids.txt"
+            pkg.gguf.qwen3_random(model, **params)
+            prompt = pkg.gguf.prompt_ids(TINY_PROMPT, params["vocab"], seed=params["seed"])
+            ids.write_text(" ".join(map(str, prompt)) + "\n")
+            out = subprocess.run([str(RUN), "llm", str(model), str(ids), str(TINY_STEPS), str(SHAPES_CTX)],
+                                 check=True, capture_output=True, text=True).stdout
+        res[name] = {"model": params, "prompt": prompt, "steps_arg": TINY_STEPS, "ctx": SHAPES_CTX, **parse_llm(out)}
+    (GOLDEN / "e2e_qwen3_shapes.json").write_text(json.dumps(res, indent=1) + "\n")
+
+
 ERROR_TOKEN = 7
 
 
@@ -167,6 +190,8 @@ if __name__ == "__main__":
         long(pkg)
     if "rope" in args:
         rope(pkg)
+    if "shapes" in args:
+        shapes(pkg)
     if "error" in args:
         error(pkg)
     if "full" in args:

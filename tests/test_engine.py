@@ -29,6 +29,7 @@ MLP = json.loads((GOLDEN / "e2e_bnn_mlp.json").read_text())
 LONG = json.loads((GOLDEN / "e2e_qwen3_long.json").read_text())
 ROPE = json.loads((GOLDEN / "e2e_qwen3_rope.json").read_text())
 ERR = json.loads((GOLDEN / "e2e_qwen3_error.json").read_text())
+SHAPES = json.loads((GOLDEN / "e2e_qwen3_shapes.json").read_text())
 FULL_FIXTURE = GOLDEN / "e2e_qwen3_1p7b.json"
 
 
@@ -67,6 +68,15 @@ def write_rope(pkg, tmp_path, name):
     """The tiny model with one of the fixtures' RoPE scalings (YaRN or linear)."""
     rec = ROPE[name]
     model, ids = tmp_path / f"rope_{name}.gguf", tmp_path / f"rope_{name}.txt"
+    pkg.gguf.qwen3_random(model, **rec["model"])
+    ids.write_text(" ".join(map(str, rec["prompt"])) + "\n")
+    return rec, model, ids
+
+
+def write_shape(pkg, tmp_path, name):
+    """One of the fixtures' models with head_dim 20 or 72 (context 61)."""
+    rec = SHAPES[name]
+    model, ids = tmp_path / f"shape_{name}.gguf", tmp_path / f"shape_{name}.txt"
     pkg.gguf.qwen3_random(model, **rec["model"])
     ids.write_text(" ".join(map(str, rec["prompt"])) + "\n")
     return rec, model, ids
@@ -254,6 +264,17 @@ def test_reference_engine_reproduces_rope_fixtures(pkg, tmp_path, name):
     assert parse_llm(out) == rec["steps"]
 
 
+@pytest.mark.skipif(not ENGINE_RUN_SOFT.exists(), reason="reference engine not built (no reference tree)")
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_reference_engine_reproduces_shape_fixtures(pkg, tmp_path, name):
+    """The head-width fixtures (head_dim 20 and 72, a context of 61 positions) are what the
+    reference engine + soft backend compute on the models written here."""
+    rec, model, ids = write_shape(pkg, tmp_path, name)
+    out = subprocess.run([str(ENGINE_RUN_SOFT), "llm", str(model), str(ids), str(rec["steps_arg"]),
+                          str(rec["ctx"])], capture_output=True, text=True, check=True).stdout
+    assert parse_llm(out) == rec["steps"]
+
+
 def test_rope_fixtures_differ_from_unscaled():
     """Each scaling changes the logits (the fixtures would otherwise pin nothing of it)."""
     plain = [row[2] for row in TINY["steps"]]
@@ -295,6 +316,20 @@ def test_engine_rope_scaling_host_step_on_cpu_oracle(pkg, tmp_path, name):
     """This engine's RoPE tables (YaRN / linear scaling) in its host step, on the CPU
     oracle backend: every step's token and logits hash equal the reference's."""
     rec, model, ids = write_rope(pkg, tmp_path, name)
+    out = subprocess.run([str(ENGINE_RUN_CPU), "llm", str(model), str(ids), str(rec["steps_arg"]), str(rec["ctx"]),
+                          "host"], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr[-2000:]
+    assert parse_llm(out.stdout) == rec["steps"]
+    assert parse_greedy(out.stdout) == [row[1] for row in rec["steps"][1:]]
+
+
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_engine_head_widths_host_step_on_cpu_oracle(pkg, tmp_path, name):
+    """The host step's attention by lanes at head widths that leave partial lane groups
+    (20 = 2 x 8 + 4, 72 = 64 + 8) over a 61-position context (a partial block of eight
+    cached keys), on the CPU oracle backend: every step's token and logits hash equal the
+    reference's."""
+    rec, model, ids = write_shape(pkg, tmp_path, name)
     out = subprocess.run([str(ENGINE_RUN_CPU), "llm", str(model), str(ids), str(rec["steps_arg"]), str(rec["ctx"]),
                           "host"], capture_output=True, text=True, timeout=300)
     assert out.returncode == 0, out.stderr[-2000:]
@@ -468,6 +503,23 @@ def test_engine_rope_scaling_bit_exact(pkg, tmp_path, name, path):
     tokens, equal the reference engine + soft backend's."""
     rec, model, ids = write_rope(pkg, tmp_path, name)
     print(f"engine qwen3 rope {name}, {path} path", flush=True)
+    out = subprocess.run([str(ENGINE_RUN_OWN), "llm", str(model), str(ids), str(rec["steps_arg"]), str(rec["ctx"]),
+                          path], capture_output=True, text=True, timeout=120, check=True).stdout
+    assert parse_path(out) == path
+    assert parse_llm(out) == rec["steps"]
+    assert parse_greedy(out) == [row[1] for row in rec["steps"][1:]]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ["prepared", "host"])
+@pytest.mark.parametrize("name", sorted(SHAPES))
+def test_engine_head_widths_bit_exact(pkg, tmp_path, name, path):
+    """head_dim 20 and 72 over 61 positions: the host step's attention by lanes, and the
+    device step's per-head kernels for head widths other than the fused step's 128 (such a
+    model runs the device step with prepared batches), against the reference engine + soft
+    backend."""
+    rec, model, ids = write_shape(pkg, tmp_path, name)
+    print(f"engine qwen3 head width {name}, {path} path", flush=True)
     out = subprocess.run([str(ENGINE_RUN_OWN), "llm", str(model), str(ids), str(rec["steps_arg"]), str(rec["ctx"]),
                           path], capture_output=True, text=True, timeout=120, check=True).stdout
     assert parse_path(out) == path
