@@ -24,6 +24,8 @@
 #include <math.h>
 #include <string>
 
+#include "host_expf.h"
+
 namespace bnne {
 namespace {
 
@@ -187,7 +189,7 @@ private:
     Qwen3Model& m_;
     const Shape& s_;
     // host step: the activation rows, attention scratch and the KV cache
-    std::vector<float> x_, norm_, q_, k_, v_, y_, o_, gate_, up_, scores_, probs_;
+    std::vector<float> x_, norm_, q_, k_, v_, y_, o_, gate_, up_, ex_, scores_, probs_;
     // host step only, per layer and key/value head: keys [n_ctx / 8][head_dim][8] (blocks
     // of eight positions), values [n_ctx][head_dim]
     std::vector<float> keys_, values_;
@@ -198,7 +200,7 @@ private:
 
 Qwen3Context::Qwen3Context(Qwen3Model& m, const BNNE_ContextParams& p)
     : bnne_context(m, p), m_(m), s_(m.shape), x_(s_.width), norm_(s_.width), q_(s_.width), k_(s_.kv_width),
-      v_(s_.kv_width), y_(s_.width), o_(s_.width), gate_(s_.ffn), up_(s_.ffn), scores_(p.n_ctx), probs_(p.n_ctx) {
+      v_(s_.kv_width), y_(s_.width), o_(s_.width), gate_(s_.ffn), up_(s_.ffn), ex_(s_.ffn), scores_(p.n_ctx), probs_(p.n_ctx) {
     // rotation tables (qwen3.c:276-299): theta = pos * base^(-2j / head_dim), scaled
     const uint32_t half = s_.head_dim / 2;
     cos_.resize((size_t)p.n_ctx * half);
@@ -390,6 +392,30 @@ weighted_rows(const float* p, const float* v, uint32_t n, uint32_t dim, float* o
     }
 }
 
+// out[i] = expf(in[i]) for i < n, bit for bit the host C library's expf (host_expf.h).
+void expf_rows(const float* in, float* out, uint32_t n) {
+    static const bool lanes = bnne_expf_lanes_usable();
+    if (lanes) {
+        bnne_expf_lanes(in, out, n);
+        return;
+    }
+    for (uint32_t i = 0; i < n; ++i)
+        out[i] = expf(in[i]);
+}
+
+// gate[i] = gate[i] / (1 + e[i]) * up[i] (SiLU(gate) * up with e = expf(-gate),
+// qwen3.c:491-495), each operation rounded once, eight lanes at a time.
+__attribute__((target_clones("avx2", "default"))) void
+silu_mul(float* gate, const float* e, const float* up, uint32_t n) {
+    uint32_t i = 0;
+    for (; i + 8u <= n; i += 8u) {
+        const f32x8 one = {1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f, 1.0f};
+        STORE8(gate + i, LOAD8(gate + i) / (one + LOAD8(e + i)) * LOAD8(up + i));
+    }
+    for (; i < n; ++i)
+        gate[i] = gate[i] / (1.0f + e[i]) * up[i];
+}
+
 // Every query head against cache rows 0..pos of its key/value head (qwen3.c:441-478):
 // scores q.k * (1 / sqrt(head_dim)), softmax, probability-weighted sum of the values.
 void Qwen3Context::attend(uint32_t layer, uint32_t pos) {
@@ -407,11 +433,12 @@ void Qwen3Context::attend(uint32_t layer, uint32_t pos) {
             if (score > top)
                 top = score;
         }
+        for (uint32_t t = 0; t <= pos; ++t)
+            probs_[t] = scores_[t] - top;
+        expf_rows(probs_.data(), probs_.data(), pos + 1u);
         float total = 0.0f;
-        for (uint32_t t = 0; t <= pos; ++t) {
-            probs_[t] = expf(scores_[t] - top);
+        for (uint32_t t = 0; t <= pos; ++t)
             total += probs_[t];
-        }
         if (!(total > 0.0f) || !std::isfinite(total))
             raise(BNNE_ECOMPUTE, "softmax normaliser is zero or not finite");
         for (uint32_t t = 0; t <= pos; ++t)
@@ -461,11 +488,10 @@ void Qwen3Context::step(uint32_t token, uint32_t pos, float* logits) {
         rmsnorm(x_.data(), C, s_.eps, L.ffn_norm.data(), norm_.data());
         L.gate.apply(*this, norm_.data(), gate_.data());
         L.up.apply(*this, norm_.data(), up_.data());
-        for (uint32_t i = 0; i < s_.ffn; ++i) {
-            const float g = gate_[i];
-            const float silu = g / (1.0f + expf(-g));
-            gate_[i] = silu * up_[i];
-        }
+        for (uint32_t i = 0; i < s_.ffn; ++i)
+            ex_[i] = -gate_[i];
+        expf_rows(ex_.data(), ex_.data(), s_.ffn);
+        silu_mul(gate_.data(), ex_.data(), up_.data(), s_.ffn);
         L.down.apply(*this, gate_.data(), o_.data());
         for (uint32_t i = 0; i < C; ++i)
             x_[i] += o_[i];

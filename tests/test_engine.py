@@ -780,9 +780,10 @@ def test_engine_greedy_decode_1p7b(pkg, hip, tmp_path):
 
 
 def test_device_expf_restatement_matches_host_libm():
-    """The device expf (csrc/libc_expf.h, shared by the backend and engine kernels) returns what the
-    host C library's expf returns: every 13th float bit pattern here (the full 2^32
-    sweep is the same program with stride 1)."""
+    """The device expf (csrc/libc_expf.h, shared by the backend and engine kernels) and the
+    host step's four-lane form of it (engine/host_expf.h, on processors with AVX2 and FMA)
+    return what the host C library's expf returns: every 13th float bit pattern here (the
+    full 2^32 sweep is the same program with stride 1)."""
     exe = ROOT / "oracle" / "lib" / "libc_expf_check"
     out = subprocess.run([str(exe), "13"], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0 and out.stdout.strip().endswith("mismatches 0"), out.stdout
