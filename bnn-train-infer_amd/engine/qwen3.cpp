@@ -285,6 +285,8 @@ void Qwen3Context::select_path(int path) {
 
 // out = x / rms * gain with rms = sqrt(sum of x_i^2 in index order / n + eps) (qwen3.c:342-353);
 // out may be x.
+void scale_rows(const float* x, float rms, const float* gain, float* out, uint32_t n);
+
 void rmsnorm(const float* x, uint32_t n, float eps, const float* gain, float* out) {
     float squares = 0.0f;
     for (uint32_t i = 0; i < n; ++i)
@@ -292,8 +294,7 @@ void rmsnorm(const float* x, uint32_t n, float eps, const float* gain, float* ou
     const float rms = sqrtf(squares / (float)n + eps);
     if (!std::isfinite(rms) || rms == 0.0f)
         raise(BNNE_ECOMPUTE, "RMSNorm divisor is zero or not finite");
-    for (uint32_t i = 0; i < n; ++i)
-        out[i] = x[i] / rms * gain[i];
+    scale_rows(x, rms, gain, out, n);
 }
 
 // Rotates the pairs (j, j + half) of one head (qwen3.c:368-376).
@@ -403,6 +404,26 @@ void expf_rows(const float* in, float* out, uint32_t n) {
         out[i] = expf(in[i]);
 }
 
+// out[i] = x[i] / rms * gain[i], each operation rounded once, eight lanes at a time
+// (out may be x).
+__attribute__((target_clones("avx2", "default"))) void
+scale_rows(const float* x, float rms, const float* gain, float* out, uint32_t n) {
+    uint32_t i = 0;
+    for (; i + 8u <= n; i += 8u)
+        STORE8(out + i, LOAD8(x + i) / rms * LOAD8(gain + i));
+    for (; i < n; ++i)
+        out[i] = x[i] / rms * gain[i];
+}
+
+// x[i] += o[i], eight lanes at a time.
+__attribute__((target_clones("avx2", "default"))) void add_rows(float* x, const float* o, uint32_t n) {
+    uint32_t i = 0;
+    for (; i + 8u <= n; i += 8u)
+        STORE8(x + i, LOAD8(x + i) + LOAD8(o + i));
+    for (; i < n; ++i)
+        x[i] += o[i];
+}
+
 // gate[i] = gate[i] / (1 + e[i]) * up[i] (SiLU(gate) * up with e = expf(-gate),
 // qwen3.c:491-495), each operation rounded once, eight lanes at a time.
 __attribute__((target_clones("avx2", "default"))) void
@@ -483,8 +504,7 @@ void Qwen3Context::step(uint32_t token, uint32_t pos, float* logits) {
         }
         attend(l, pos);
         L.o.apply(*this, y_.data(), o_.data());
-        for (uint32_t i = 0; i < C; ++i)
-            x_[i] += o_[i];
+        add_rows(x_.data(), o_.data(), C);
         rmsnorm(x_.data(), C, s_.eps, L.ffn_norm.data(), norm_.data());
         L.gate.apply(*this, norm_.data(), gate_.data());
         L.up.apply(*this, norm_.data(), up_.data());
@@ -493,8 +513,7 @@ void Qwen3Context::step(uint32_t token, uint32_t pos, float* logits) {
         expf_rows(ex_.data(), ex_.data(), s_.ffn);
         silu_mul(gate_.data(), ex_.data(), up_.data(), s_.ffn);
         L.down.apply(*this, gate_.data(), o_.data());
-        for (uint32_t i = 0; i < C; ++i)
-            x_[i] += o_[i];
+        add_rows(x_.data(), o_.data(), C);
     }
     if (logits) {
         rmsnorm(x_.data(), C, s_.eps, m_.final_norm.data(), norm_.data());
