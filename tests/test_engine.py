@@ -323,15 +323,19 @@ def test_engine_rope_scaling_host_step_on_cpu_oracle(pkg, tmp_path, name):
     assert parse_greedy(out.stdout) == [row[1] for row in rec["steps"][1:]]
 
 
+@pytest.mark.parametrize("exe", [ENGINE_RUN_CPU, ENGINE_RUN_ASAN], ids=["plain", "sanitized"])
 @pytest.mark.parametrize("name", sorted(SHAPES))
-def test_engine_head_widths_host_step_on_cpu_oracle(pkg, tmp_path, name):
+def test_engine_head_widths_host_step_on_cpu_oracle(pkg, tmp_path, name, exe):
     """The host step's attention by lanes at head widths that leave partial lane groups
     (20 = 2 x 8 + 4, 72 = 64 + 8) over a 61-position context (a partial block of eight
     cached keys), on the CPU oracle backend: every step's token and logits hash equal the
-    reference's."""
+    reference's; the sanitized build runs the same under AddressSanitizer +
+    UndefinedBehaviorSanitizer."""
+    import os
     rec, model, ids = write_shape(pkg, tmp_path, name)
-    out = subprocess.run([str(ENGINE_RUN_CPU), "llm", str(model), str(ids), str(rec["steps_arg"]), str(rec["ctx"]),
-                          "host"], capture_output=True, text=True, timeout=300)
+    env = dict(os.environ, **ASAN_ENV)
+    out = subprocess.run([str(exe), "llm", str(model), str(ids), str(rec["steps_arg"]), str(rec["ctx"]), "host"],
+                         capture_output=True, text=True, timeout=300, env=env)
     assert out.returncode == 0, out.stderr[-2000:]
     assert parse_llm(out.stdout) == rec["steps"]
     assert parse_greedy(out.stdout) == [row[1] for row in rec["steps"][1:]]
