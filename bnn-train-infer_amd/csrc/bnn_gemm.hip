@@ -1451,6 +1451,13 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
     if (job.mode != MODE_DOT_I16 && job.rows <= 64u && (job.rows <= 32u || job.groups <= 16u) &&
         blocks(16, 16) <= 3u * cus)
         return launch_wv<1, 1, 1, 1, 8>(stream, job, seq, flag);
+    // K >= 6144 with between half a round and one round of 32 x 64 tiles: eight waves
+    // splitting K per tile (6144->2048 x 256 rows 17.1 us against 19.1 us for a wave per
+    // 32 x 32 block, 8192->2048 x 256 21.6 against 23.3, 8192->1024 x 320-512 21.7-22.2
+    // against 24.2-28.4; forced-choice sweep, bit-identical outputs; it loses at K = 4096,
+    // below half a round and from a second round on)
+    if (job.mode != MODE_DOT_I16 && job.groups >= 48u && blocks(32, 64) > cus / 2u && blocks(32, 64) <= cus)
+        return launch_ks<2, 4, 8, 3>(stream, job, seq, flag);
     // a long K (>= 32 groups) with two to three 32 x 32 blocks per CU: a wave per block
     // beats the tiled kernels, whose per-group steps serialise over the long K
     if (job.mode != MODE_DOT_I16 && job.groups >= 32u && blocks(32, 32) >= 2u * cus && blocks(32, 32) <= 3u * cus)

@@ -115,6 +115,7 @@ def test_quantiser_edge_rows(pkg, hipdev, oracle, i):
     (8, 2048, 6144), (17, 640, 1000), (24, 6144, 2048),       # a wave per 16 x 16 block, operands in registers
     (32, 1408, 2050), (50, 640, 1000),
     (250, 4224, 2040), (300, 6144, 2000),                     # a wave per 32 x 32 block, long K
+    (250, 6144, 2000), (300, 8192, 1000),                     # K split over 8 waves per 32 x 64 tile, long K
     (1000, 2048, 6100), (777, 1152, 8000),                    # 128 x 192, operands per wave (9 groups: odd)
     (1000, 6272, 2000), (1024, 4096, 2048),                   # 64 x 128, operands per wave, long K
 ])
