@@ -1448,6 +1448,13 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
     // registers, while that makes at most three waves per CU (the blocks of 16 columns
     // each load their rows, and more of them outrun the loads a CU keeps in flight);
     // with 33..64 rows only for K <= 2048 (a longer K favours splitting it, below)
+    // 17..32 rows, K <= 2048, and at least three quarters of a round of 32 x 32 tiles: four
+    // waves splitting K per tile (2048->6144 x 20-32 rows 7.0-7.1 us against 7.7-8.1 us,
+    // 2048->8192 x 20-32 rows 7.0-7.2 against 9.3-9.9; forced-choice sweep, bit-identical;
+    // it loses with fewer tiles, at 16 rows and from 40 rows on)
+    if (job.mode != MODE_DOT_I16 && job.rows > 16u && job.rows <= 32u && job.groups <= 16u &&
+        blocks(32, 32) >= 3u * cus / 4u)
+        return launch_ks<2, 2, 4, 3>(stream, job, seq, flag);
     if (job.mode != MODE_DOT_I16 && job.rows <= 64u && (job.rows <= 32u || job.groups <= 16u) &&
         blocks(16, 16) <= 3u * cus)
         return launch_wv<1, 1, 1, 1, 8>(stream, job, seq, flag);

@@ -112,6 +112,7 @@ def test_quantiser_edge_rows(pkg, hipdev, oracle, i):
     (120, 1152, 5000),                                         # 32 x 64
     (80, 1408, 3500), (100, 3200, 3000),                      # K split over 8 waves: 64x32, 32x32
     (40, 2304, 1500),                                          # K split over 4 waves: 32x16
+    (24, 2048, 8100), (30, 1152, 7000),                       # K split over 4 waves: 32x32, few rows
     (8, 2048, 6144), (17, 640, 1000), (24, 6144, 2048),       # a wave per 16 x 16 block, operands in registers
     (32, 1408, 2050), (50, 640, 1000),
     (250, 4224, 2040), (300, 6144, 2000),                     # a wave per 32 x 32 block, long K
