@@ -1465,6 +1465,18 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
     // below half a round and from a second round on)
     if (job.mode != MODE_DOT_I16 && job.groups >= 48u && blocks(32, 64) > cus / 2u && blocks(32, 64) <= cus)
         return launch_ks<2, 4, 8, 3>(stream, job, seq, flag);
+    // K split over four waves per 32 x 64 tile: 17..47 groups with between half a round and
+    // one round of tiles (4096->2048 x 192 rows 14.0 us against 15.9 for 32 x 64
+    // workgroup tiles, 4096->6144 x 48-64 rows 13.9-14.2 against 15.7-15.9,
+    // 3072->8100 x 40-64 rows 12.0-12.2 against 13.3), and >= 48 groups with one to two
+    // rounds (6144->2048 x 384-512 rows 24.7-25.4 against 26.3-26.8, 6144->6144 x
+    // 96-128 rows 23.8-24.4 against 26.1-26.5; forced-choice sweeps, bit-identical
+    // outputs; at 16 groups and from a third round on the tiled kernels win)
+    if (job.mode != MODE_DOT_I16 && job.groups > 16u && job.groups < 48u && blocks(32, 64) > cus / 2u &&
+        blocks(32, 64) <= cus)
+        return launch_ks<2, 4, 4, 3>(stream, job, seq, flag);
+    if (job.mode != MODE_DOT_I16 && job.groups >= 48u && blocks(32, 64) > cus && blocks(32, 64) <= 2u * cus)
+        return launch_ks<2, 4, 4, 3>(stream, job, seq, flag);
     // a long K (>= 32 groups) with two to three 32 x 32 blocks per CU: a wave per block
     // beats the tiled kernels, whose per-group steps serialise over the long K
     if (job.mode != MODE_DOT_I16 && job.groups >= 32u && blocks(32, 32) >= 2u * cus && blocks(32, 32) <= 3u * cus)
@@ -1485,15 +1497,24 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
     if (blocks(64, 64) >= cus)
         return launch_bits<64, 64, 2, 2>(stream, job, seq, flag);
     const uint64_t enough = cus * 3u / 4u;
-    if (job.mode != MODE_DOT_I16 && blocks(32, 64) < enough) {
-        // too few tiles for the CUs: K split across the waves of a workgroup (8, or 4 for
-        // the smallest tile), with the largest tile that still gives most CUs a workgroup
-        if (blocks(64, 32) >= enough)
-            return launch_ks<4, 2, 8, 3>(stream, job, seq, flag);
+    if (job.mode != MODE_DOT_I16 && blocks(32, 64) < enough && blocks(32, 32) <= cus) {
+        // too few tiles for the CUs: K split across the waves of a workgroup, with 32 x 32
+        // tiles while those fit one round (past it, 32 x 64 workgroup tiles win: 1024->2048
+        // x 136-160 rows 6.7-6.8 us against 8.5-8.6; only <= 16 groups get here then), else
+        // 32 x 16 ones.  With up to 32 groups four waves per tile beat eight, whose share
+        // of K is then too short to hide each round's loads (1024->2048 x 96-128 rows
+        // 5.4-5.7 us against 8.2-8.3, 4096->2048 x 96-128 rows 10.0-10.3 against 11.5-11.8)
+        if (blocks(32, 32) >= enough && job.groups <= 32u)
+            return launch_ks<2, 2, 4, 3>(stream, job, seq, flag);
         if (blocks(32, 32) >= enough)
             return launch_ks<2, 2, 8, 3>(stream, job, seq, flag);
         return launch_ks<2, 1, 4, 3>(stream, job, seq, flag);
     }
+    // three quarters of a round of 64 x 64 tiles: those beat a round and more of 32 x 64
+    // ones (2048->2048 x 384 rows 11.7 us against 12.6, 2048->6144 x 96-128 rows 11.6-11.7
+    // against 12.0-12.4)
+    if (blocks(64, 64) >= enough)
+        return launch_bits<64, 64, 2, 2>(stream, job, seq, flag);
     return launch_bits<32, 64, 2, 2>(stream, job, seq, flag);
 }
 
