@@ -49,6 +49,10 @@ __device__ __forceinline__ void gstore(int16_t* p, int16_t v) {
 
 // popc(x) + acc in one VALU op.  Written as asm because the compiler otherwise
 // re-associates the chain into ADD3 trees (11 instead of 9 ops per plane).
+// Bit b of the two's complement byte of a quantised value q in [-127, 127] (plane P_b):
+// bit 7 is the sign, one signed compare where the other bits take an extract and a compare
+__device__ __forceinline__ bool plane_bit(int q, int b) { return b == 7 ? q < 0 : ((q >> b) & 1) != 0; }
+
 __device__ __forceinline__ uint32_t bcnt_acc(uint32_t x, uint32_t acc) {
     uint32_t r;
     asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));

@@ -63,7 +63,7 @@ extern "C" __device__ int __ockl_wfred_add_i32(int);
 // lane as an inline constant), and `sum` accumulates sum(q) from the same masks.
 template <int B>
 __device__ __forceinline__ void plane_words(int q, uint32_t& word, int& sum) {
-    const unsigned long long mask = __ballot((q >> B) & 1);
+    const unsigned long long mask = __ballot(plane_bit(q, B));
     const int cnt = __popcll(mask);
     sum += B == 7 ? -(cnt << 7) : (cnt << B);
     // s_nop 1: the two wait states between a VALU write of an SGPR (the ballot) and a
@@ -601,7 +601,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
     // masks: kept in scalar registers for one group per wave or, with one tile per
     // workgroup, formed group by group next to that group's dots; else in LDS), and
     // -sum(Q) per group; no exchange between waves
-    const float rcp = 1.0f / s;
+    const float rcp = quant_rcp(s);
     const bool exact = quant_exact(s);  // 1 / s may overflow
     int q[EPT];
 #pragma unroll
@@ -617,7 +617,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int b = 0; b < 8; ++b)
-                masks[h][b] = __ballot((q[h] >> b) & 1);
+                masks[h][b] = __ballot(plane_bit(q[h], b));
     } else if constexpr (RING == 1) {
         // the tile's dots form each group's masks themselves (no planes in LDS: the 16 waves'
         // plane words would queue on the CU's one scalar unit); -sum(Q) of two groups per
@@ -678,7 +678,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
                     for (int h = 0; h < 2; ++h)
 #pragma unroll
                         for (int b = 0; b < 8; ++b)
-                            m[h][b] = __ballot((q[2 * i + h] >> b) & 1);
+                            m[h][b] = __ballot(plane_bit(q[2 * i + h], b));
                     d = group_dot_s(cur.w[i], m, neg_sum[i]);
                     // one group's 32 mask registers at a time (scheduled together, the
                     // groups' masks would not fit the scalar register file)

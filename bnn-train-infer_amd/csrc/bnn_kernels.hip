@@ -149,7 +149,7 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
         s = quant_row_scale(amax);
     }
 
-    const float rcp = 1.0f / s;
+    const float rcp = quant_rcp(s);
     const bool exact = quant_exact(s);  // 1 / s may overflow
     // pass 2: quantise; in iteration i wave w owns the 64 consecutive k of half (w & 1)
     // of group kPrepGroupsPerIter*i + (w >> 1)
@@ -168,7 +168,7 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
             uint32_t word = 0;
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
-                const unsigned long long mask = __ballot((q >> b) & 1);
+                const unsigned long long mask = __ballot(plane_bit(q, b));
                 if (lane == 2u * b)
                     word = (uint32_t)mask;
                 if (lane == 2u * b + 1u)

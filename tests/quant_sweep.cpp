@@ -1,11 +1,17 @@
 // Host check of the reciprocal quantiser in bnn-train-infer_amd/csrc/bnn_quant.h (the
-// one the gfx950 kernels compile) against the reference formula
+// one the gfx950 kernels compile) against the reference formulas
 //   Q = clamp(roundf(F32(x / s)), -127, 127)      (soft-bnn-accelerator.c:197-208)
+//   s = absmax == 0 ? 1 : F32(absmax / 127), FLT_TRUE_MIN if that is 0   (:187-195)
 // Built with -O2 -fno-fast-math -ffp-contract=off (SSE binary32, IEEE division).
-//   quant_sweep full <s_bits_hex>...   every finite x (2^32 - 2^24 - 2 patterns) per s
+// quantize_rcp is checked with the reciprocal F32(1 / s) and with neighbours a few ulps
+// away, standing for the device's estimate (bnn_quant.h bounds its error by 7 * 2^-24).
+//   quant_sweep full <s_bits_hex>...   every finite x (2^32 - 2^24 - 2 patterns) per s, each
+//                                      with one of F32(1 / s) and its two neighbours in turn
 //   quant_sweep near <count> <seed>    `count` seeded scales s over all exponents, and for
 //                                      every k in [-128, 128] the 129 floats nearest to
-//                                      (k + 0.5) * s
+//                                      (k + 0.5) * s, each with F32(1 / s) and the floats up to
+//                                      two ulps either side of it
+//   quant_sweep scale                  quant_row_scale for every finite absmax >= 0
 // Prints "checked N mismatches M" and the first mismatches; exit status 1 on any.
 #include <math.h>
 #include <stdint.h>
@@ -51,6 +57,36 @@ static int planted_q(float x, float s, float rcp, bool exact) {
 #define QUANTIZE bnnhip::quantize_rcp
 #endif
 
+#ifdef PLANTED_NO_CORRECTION
+// A planted mistake for the row-scale check: the product by F32(1 / 127) alone.
+static float planted_scale(float a) {
+    if (a == 0.0f)
+        return 1.0f;
+    const float s = a * 0x1.020408p-7f;
+    return s == 0.0f ? 0x1p-149f : s;
+}
+#define ROW_SCALE planted_scale
+#else
+#define ROW_SCALE bnnhip::quant_row_scale
+#endif
+
+static float reference_scale(float a) {
+    if (a == 0.0f)
+        return 1.0f;
+    volatile float s = a / 127.0f;
+    return s == 0.0f ? 0x1p-149f : s;
+}
+
+// the float `ulps` steps from the positive finite r
+static float step_ulps(float r, int ulps) {
+    uint32_t b;
+    memcpy(&b, &r, 4);
+    b = (uint32_t)((int64_t)b + ulps);
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
 static std::atomic<uint64_t> g_checked{0}, g_bad{0};
 static std::atomic<int> g_reported{0};
 
@@ -65,8 +101,10 @@ static void check(float x, float s, float rcp, bool exact) {
 }
 
 static void full(float s, unsigned threads) {
-    const float rcp = 1.0f / s;
+    const float r = 1.0f / s;
     const bool exact = bnnhip::quant_exact(s);
+    // a subnormal s has an infinite or huge reciprocal, never used (exact)
+    const float rcps[3] = {r, exact ? r : step_ulps(r, -1), exact ? r : step_ulps(r, 1)};
     std::vector<std::thread> pool;
     for (unsigned t = 0; t < threads; ++t)
         pool.emplace_back([=] {
@@ -74,7 +112,7 @@ static void full(float s, unsigned threads) {
             for (uint64_t b = t; b <= 0xffffffffull; b += threads) {
                 if (((uint32_t)b & 0x7f800000u) == 0x7f800000u)
                     continue;  // NaN / Inf: rejected before quantisation
-                check(from_bits((uint32_t)b), s, rcp, exact);
+                check(from_bits((uint32_t)b), s, rcps[b % 3u], exact);
                 ++n;
             }
             g_checked += n;
@@ -110,7 +148,7 @@ static void near(unsigned count, uint64_t seed, unsigned threads) {
             uint64_t n = 0;
             for (unsigned i; (i = at++) < scales.size();) {
                 const float s = scales[i];
-                const float rcp = 1.0f / s;
+                const float r = 1.0f / s;
                 const bool exact = bnnhip::quant_exact(s);
                 for (int k = -128; k <= 128; ++k) {
                     const float c = (float)(((double)k + 0.5) * (double)s);
@@ -122,8 +160,9 @@ static void near(unsigned count, uint64_t seed, unsigned threads) {
                         const float x = from_bits(bits);
                         if (!isfinite(x))
                             continue;
-                        check(x, s, rcp, exact);
-                        ++n;
+                        for (int u = -2; u <= 2; ++u)
+                            check(x, s, exact ? r : step_ulps(r, u), exact);
+                        n += 5;
                     }
                 }
             }
@@ -139,13 +178,33 @@ int main(int argc, char** argv) {
         threads = (unsigned)atoi(e);
     if (threads == 0)
         threads = 1;
-    if (argc >= 3 && strcmp(argv[1], "full") == 0) {
+    if (argc == 2 && strcmp(argv[1], "scale") == 0) {
+        std::vector<std::thread> pool;
+        for (unsigned t = 0; t < threads; ++t)
+            pool.emplace_back([=] {
+                uint64_t n = 0, bad = 0;
+                for (uint64_t b = t; b < 0x7f800000ull; b += threads) {
+                    const float a = from_bits((uint32_t)b);
+                    const float want = reference_scale(a), got = ROW_SCALE(a);
+                    if (to_bits(want) != to_bits(got)) {
+                        ++bad;
+                        if (g_reported++ < 10)
+                            printf("mismatch: absmax=%a got %a want %a\n", a, got, want);
+                    }
+                    ++n;
+                }
+                g_checked += n;
+                g_bad += bad;
+            });
+        for (auto& th : pool)
+            th.join();
+    } else if (argc >= 3 && strcmp(argv[1], "full") == 0) {
         for (int i = 2; i < argc; ++i)
             full(from_bits((uint32_t)strtoul(argv[i], nullptr, 16)), threads);
     } else if (argc == 4 && strcmp(argv[1], "near") == 0) {
         near((unsigned)atoi(argv[2]), strtoull(argv[3], nullptr, 10), threads);
     } else {
-        fprintf(stderr, "usage: quant_sweep full <s_bits>... | near <count> <seed>\n");
+        fprintf(stderr, "usage: quant_sweep full <s_bits>... | near <count> <seed> | scale\n");
         return 2;
     }
     printf("checked %llu mismatches %llu\n", (unsigned long long)g_checked.load(), (unsigned long long)g_bad.load());

@@ -2,8 +2,12 @@
 reference formula clamp(roundf(F32(x / s)), -127, 127) (soft-bnn-accelerator.c:175-211),
 on the host: every finite x for a set of row scales s (normal, near FLT_MIN, subnormal,
 FLT_TRUE_MIN, FLT_MAX / 127), and the floats nearest to every half-integer multiple
-(k + 0.5) * s for thousands of seeded scales.  A planted mistake (the reciprocal product
-without the division fallback) must be found by the same checker."""
+(k + 0.5) * s for thousands of seeded scales, with the reciprocal F32(1 / s) and with
+neighbours up to two ulps away (the device multiplies by an estimate within 7 * 2^-24).
+The row scale (quant_row_scale: a corrected product instead of the division) against
+F32(absmax / 127) for every finite absmax >= 0.  Planted mistakes (the reciprocal product
+without the division fallback; the row-scale product without its correction) must be
+found by the same checker."""
 from __future__ import annotations
 
 import subprocess
@@ -24,11 +28,13 @@ def _f32_bits(v) -> str:
 @pytest.fixture(scope="module")
 def sweep(tmp_path_factory):
     d = tmp_path_factory.mktemp("quant")
-    exe, planted = d / "quant_sweep", d / "quant_planted"
+    exe, planted, planted_scale = d / "quant_sweep", d / "quant_planted", d / "quant_planted_scale"
     subprocess.run(["g++", *FLAGS, str(SRC), "-o", str(exe), "-lpthread"], check=True)
     subprocess.run(["g++", *FLAGS, "-DPLANTED_NO_DIVISION", str(SRC), "-o", str(planted), "-lpthread"],
                    check=True)
-    return exe, planted
+    subprocess.run(["g++", *FLAGS, "-DPLANTED_NO_CORRECTION", str(SRC), "-o", str(planted_scale), "-lpthread"],
+                   check=True)
+    return exe, planted, planted_scale
 
 
 def _run(exe, *args):
@@ -60,8 +66,19 @@ def test_every_finite_x(sweep, name):
 
 def test_half_integer_neighbourhoods(sweep):
     rc, checked, bad, out = _run(sweep[0], "near", "20000", "7")
-    assert checked > 600_000_000
+    assert checked > 3_000_000_000  # five reciprocals per x
     assert bad == 0 and rc == 0, out
+
+
+def test_row_scale_every_absmax(sweep):
+    rc, checked, bad, out = _run(sweep[0], "scale")
+    assert checked == 2 ** 31 - 2 ** 23, checked  # every finite absmax >= 0
+    assert bad == 0 and rc == 0, out
+
+
+def test_checker_finds_a_planted_scale_mistake(sweep):
+    rc, checked, bad, out = _run(sweep[2], "scale")
+    assert rc == 1 and bad > 0, out
 
 
 def test_checker_finds_a_planted_mistake(sweep):
