@@ -36,17 +36,17 @@ BNN_QUANT_FN float quant_row_scale(float absmax) {
 // is subnormal, where 1 / s may overflow).  For |x / s| <= 128, y = F32(x * rcp) lies
 // within 128 e + 2^-18 of x / s and F32(x / s) within 2^-18, so the two are less than
 // 2^-14 apart and round to the same integer unless y lies within 2^-14 of a
-// half-integer; those lanes (and all, when s is subnormal: `exact`) divide.  Beyond
-// |x / s| = 128 both sides saturate at +-127.
+// half-integer; those lanes (and all, when s is subnormal: `exact`) divide.  Away from
+// half-integers rounding half away from zero and half to even agree, so the other lanes
+// take rint(y) (rounding to nearest even, the required mode), and |y - rint(y)| is the
+// distance that decides.  Beyond |x / s| = 128 both sides saturate at +-127.
 BNN_QUANT_FN int quantize_rcp(float x, float s, float rcp, bool exact) {
-    float y = x * rcp;
-    float t = truncf(y), d = y - t;
-    if (exact || fabsf(fabsf(d) - 0.5f) < 0x1p-14f) {
-        y = x / s;
-        t = truncf(y);
-        d = y - t;
+    const float y = x * rcp;
+    float q = rintf(y);
+    if (exact || fabsf(fabsf(y - q) - 0.5f) < 0x1p-14f) {
+        const float z = x / s, t = truncf(z), d = z - t;
+        q = t + (fabsf(d) >= 0.5f ? copysignf(1.0f, z) : 0.0f);
     }
-    const float q = t + (fabsf(d) >= 0.5f ? copysignf(1.0f, y) : 0.0f);
     return (int)fminf(fmaxf(q, -127.0f), 127.0f);
 }
 
