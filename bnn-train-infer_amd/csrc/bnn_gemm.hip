@@ -39,6 +39,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <utility>
 #include <hip/hip_fp16.h>
 
 #include "bnn_internal.h"
@@ -120,7 +121,7 @@ __device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32
 
 template <uint32_t N>
 constexpr uint64_t lane_mask() {
-    return N >= 64 ? ~0ull : (1ull << N) - 1ull;
+    return N >= 64 ? ~0ull : (1ull << (N % 64u)) - 1ull;
 }
 
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
@@ -1097,6 +1098,460 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_wv(GemmJob j, uint32_t mt
         }
 }
 
+// k_gemm_kr<TMS, TNS, W, R>: F32-accumulating jobs with few rows, whose tiles are too
+// few to hide a chain of per-group steps.  Workgroup tile (16 TMS) x (16 TNS); the W
+// waves split K (round r of wave w: group W r + w, at most R rounds), and each wave
+// requests everything its own groups need -- the tile rows' quantised bytes, the
+// columns' sign bits and scales -- into its own part of LDS by DMA before it computes
+// anything: no registers are held while the loads are in flight, and no wave reads
+// another wave's part, so a round waits for the wave's own loads (vmcnt) and for no
+// barrier.  A round expands the bits through the byte table, runs the MFMAs and keeps
+// the exact products RN(scale * D) in registers.  After the last round: one barrier,
+// every wave's products into LDS by group, a second barrier, and each output's products
+// added in group order by one thread -- the reference's order; only the integer work
+// ran in parallel.  The K order inside a group is that of k_gemm_ks (lane chunk c:
+// weights 32c .. 32c+31, MFMA half h the 16 from 32c + 16h).
+template <int TMS, int TNS, int W, int R>
+struct KrLayout {
+    static constexpr uint32_t TM = 16u * TMS, TN = 16u * TNS, SUBS = TMS * TNS, NT = 64u * W;
+    // a round's part: rows [TM][128] (chunks swizzled as swz128), the columns' 16-byte
+    // sign-bit chunks [TN][16], their fp16 scales [TN]
+    static constexpr uint32_t A_BYTES = TM * 128u, A_INS = A_BYTES / 1024u;
+    static constexpr uint32_t BITS_BYTES = TN * 16u, SC_BYTES = TN * 2u, SC_LANES = SC_BYTES / 16u;
+    static constexpr uint32_t ROUND_BYTES = A_BYTES + BITS_BYTES + SC_BYTES;
+    static constexpr uint32_t DMA_PER_ROUND = A_INS + 2u;
+    static constexpr uint32_t OPS_BYTES = W * R * ROUND_BYTES;
+    static constexpr uint32_t PROD_BYTES = W * R * SUBS * 1024u;  // float4 [group][subtile][lane]
+    // the byte table after the operands (copies of it, one per lane group, measured no
+    // faster: the larger LDS footprint costs more than the bank conflicts); the products
+    // reuse both once every wave is done with them
+    static constexpr uint32_t OFF_LUT = OPS_BYTES;
+    static constexpr uint32_t SMEM = OPS_BYTES + 2048u > PROD_BYTES ? OPS_BYTES + 2048u : PROD_BYTES;
+    static_assert(A_BYTES % 1024u == 0, "whole 1 KiB row DMAs");
+    static_assert(TN <= 64u && 64u % TN == 0, "a tile's columns lie in one 64-feature tile of the matrix layout");
+    static_assert(SC_BYTES % 16u == 0, "whole 16-byte scale DMAs");
+    static_assert(R * DMA_PER_ROUND < 64u, "vmcnt range");
+    static_assert(SMEM <= 160u * 1024u, "LDS");
+};
+
+// One round's operands of a lane, read from LDS
+template <int TMS, int TNS>
+struct KrOps {
+    v4i a[TMS][2];
+    uint32_t bits[TNS];
+    uint32_t s[TNS];
+};
+
+// f(std::integral_constant<uint32_t, i>) for i = 0 .. N-1, each i a constant expression
+template <class F, uint32_t... I>
+__device__ __forceinline__ void static_for_seq(F&& f, std::integer_sequence<uint32_t, I...>) {
+    (f(std::integral_constant<uint32_t, I>{}), ...);
+}
+template <uint32_t N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_seq(f, std::make_integer_sequence<uint32_t, N>{});
+}
+
+// s_waitcnt vmcnt(N) alone (lgkmcnt and expcnt not waited for); the gfx9 encoding
+// splits vmcnt into bits 3:0 and 15:14
+template <uint32_t N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N < 64u, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((int)((N & 15u) | 0x0F70u | ((N >> 4) << 14)));
+}
+
+// dma16_s for the lanes of a constant mask only (exec set inside the assembly)
+template <uint64_t LANES>
+__device__ __forceinline__ void dma16_s_lanes(uint32_t voff, const void* sbase, uint32_t lds_addr) {
+    if constexpr (LANES == ~0ull) {
+        dma16_s(voff, sbase, lds_addr);
+    } else {
+        uint64_t saved;
+        asm volatile(
+            "s_mov_b64 %0, exec\n\ts_mov_b64 exec, %4\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
+            "s_mov_b64 exec, %0"
+            : "=&s"(saved)
+            : "v"(voff), "s"(sbase), "{m0}"(lds_addr), "s"(LANES)
+            : "memory");
+    }
+}
+
+template <int TMS, int TNS, int W, int R>
+__global__ __launch_bounds__(64 * W) void k_gemm_kr(GemmJob j, uint32_t mtiles, uint32_t ntiles, uint32_t band,
+                                                   uint64_t seq, const uint64_t* __restrict__ flag) {
+    typedef KrLayout<TMS, TNS, W, R> T;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
+    // the job's error flag is read now and checked before anything is stored: the DMAs
+    // below read only memory of the job, so they need not wait for it
+    const uint64_t failed_seq = *flag;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const TileRC tile = gemm_tile_of_block(blockIdx.x, gridDim.x, mtiles, ntiles, band);
+    const uint32_t m0 = tile.mt * T::TM, n0 = tile.nt * T::TN;
+    const uint32_t groups = j.groups;
+
+    // 1. every round's DMAs.  Rows: position p = 64 i + lane of the 1 KiB DMA i holds
+    // chunk (p & 7) ^ ((row >> 1) & 7) of row p >> 3, so that chunk c of row r sits at
+    // swz128(r, c); rows past the end are clamped (never stored).  Columns: the tile's
+    // TN 16-byte sign-bit chunks and TN scales are contiguous per group in the matrix
+    // layout (one 64-feature tile; the tile past the last one is clamped).  Groups past
+    // the last are clamped too, so that every path issues the same DMAs for the waits.
+    const uint32_t part = lds_offset(smem) + wave * (R * T::ROUND_BYTES);
+    uint32_t a_src[T::A_INS];
+#pragma unroll
+    for (uint32_t i = 0; i < T::A_INS; ++i) {
+        const uint32_t p = 64u * i + lane, r = p >> 3;
+        a_src[i] = min(m0 + r, j.rows - 1u) * j.k + 16u * ((p & 7u) ^ ((r >> 1) & 7u));
+    }
+    const uint32_t col0 = min(n0 >> 6, j.tiles - 1u) * groups * kTile + (n0 & 63u);
+    const uint32_t bits_off = (col0 + min(lane, T::TN - 1u)) * 16u;
+    const uint32_t sc_off = col0 * 2u + 16u * min(lane, T::SC_LANES - 1u);
+    const uint32_t chunk = lane >> 4, lrow = lane & 15u;
+#pragma unroll
+    for (uint32_t r = 0; r < (uint32_t)R; ++r) {
+        const uint32_t g = min(W * r + wave, groups - 1u);
+        const uint32_t slot = part + r * T::ROUND_BYTES;
+        const int8_t* qg = j.q + (size_t)g * kGroup;
+#pragma unroll
+        for (uint32_t i = 0; i < T::A_INS; ++i)
+            dma16_s(a_src[i], qg, slot + 1024u * i);
+        dma16_s_lanes<lane_mask<T::TN>()>(bits_off + g * (kTile * 16u), j.wbits, slot + T::A_BYTES);
+        dma16_s_lanes<lane_mask<T::SC_LANES>()>(sc_off + g * (kTile * 2u), j.wscale,
+                                                slot + T::A_BYTES + T::BITS_BYTES);
+    }
+    uint2* const lut = reinterpret_cast<uint2*>(smem + T::OFF_LUT);
+    for (uint32_t i = tid; i < 256u; i += T::NT)
+        lut[i] = make_uint2(pm1_nibble(i & 15u), pm1_nibble(i >> 4));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's table entries are written
+    barrier();                           // ... and every wave's
+
+    // 2. the rounds, software-pipelined: iteration i reads round i's operands from LDS
+    // (after waiting for this wave's DMAs of round i: at most (R - 1 - i) rounds of them
+    // still in flight), expands round i-1's sign bits through the byte table, and runs
+    // round i-2's MFMAs with the exact products RN(scale * D) kept in registers
+    const unsigned char* const mine = smem + wave * (R * T::ROUND_BYTES);
+    const v4i c_init = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+    v4f p[R][TMS][TNS];
+    KrOps<TMS, TNS> raw[3];
+    v4i b[2][TNS][2];
+    const auto read = [&](auto rc) {
+        constexpr uint32_t r = decltype(rc)::value;
+        KrOps<TMS, TNS>& o = raw[r % 3u];
+        const unsigned char* const slot = mine + r * T::ROUND_BYTES;
+        wait_vm<((uint32_t)R - 1u - r) * T::DMA_PER_ROUND>();
+#pragma unroll
+        for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi)
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h)
+                o.a[mi][h] = *reinterpret_cast<const v4i*>(slot + swz128(16u * mi + lrow, 2u * chunk + h));
+#pragma unroll
+        for (uint32_t ni = 0; ni < (uint32_t)TNS; ++ni) {
+            const uint32_t f = 16u * ni + lrow;
+            o.bits[ni] = *reinterpret_cast<const uint32_t*>(slot + T::A_BYTES + 16u * f + 4u * chunk);
+            o.s[ni] = *reinterpret_cast<const uint16_t*>(slot + T::A_BYTES + T::BITS_BYTES + 2u * f);
+        }
+    };
+    const auto expand = [&](auto rc) {
+        constexpr uint32_t r = decltype(rc)::value;
+        const KrOps<TMS, TNS>& o = raw[r % 3u];
+#pragma unroll
+        for (uint32_t ni = 0; ni < (uint32_t)TNS; ++ni)
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h) {
+                const uint2 lo = lut[(o.bits[ni] >> (16u * h)) & 0xffu];
+                const uint2 hi = lut[(o.bits[ni] >> (16u * h + 8u)) & 0xffu];
+                b[r % 2u][ni][h] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+            }
+    };
+    const auto mma = [&](auto rc) {
+        constexpr uint32_t r = decltype(rc)::value;
+        const KrOps<TMS, TNS>& o = raw[r % 3u];
+#pragma unroll
+        for (uint32_t ni = 0; ni < (uint32_t)TNS; ++ni) {
+            const float sc = __half2float(__ushort_as_half((uint16_t)o.s[ni]));
+            const float cneg = sc * -kMagicValue;  // exact
+#pragma unroll
+            for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi) {
+                v4i dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a[mi][0], b[r % 2u][ni][0], c_init, 0, 0, 0);
+                dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a[mi][1], b[r % 2u][ni][1], dd, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    p[r][mi][ni][e] = __builtin_fmaf(sc, __int_as_float(dd[e]), cneg);
+            }
+        }
+    };
+    static_for<(uint32_t)R + 2u>([&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        if constexpr (i < (uint32_t)R)
+            read(std::integral_constant<uint32_t, i>{});
+        if constexpr (i >= 1u && i - 1u < (uint32_t)R)
+            expand(std::integral_constant<uint32_t, i - 1u>{});
+        if constexpr (i >= 2u)
+            mma(std::integral_constant<uint32_t, i - 2u>{});
+    });
+
+    if (failed_seq == seq)
+        return;  // an illegal input row in this job: write nothing (the whole workgroup)
+
+    // 3. the products by group into LDS (over the operands: every wave has read its own
+    // by the barrier), then the in-order sums
+    __syncthreads();
+    v4f* const prod = reinterpret_cast<v4f*>(smem);
+#pragma unroll
+    for (uint32_t r = 0; r < (uint32_t)R; ++r) {
+        const uint32_t g = W * r + wave;
+        if (g < groups) {
+#pragma unroll
+            for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi)
+#pragma unroll
+                for (uint32_t ni = 0; ni < (uint32_t)TNS; ++ni)
+                    prod[(g * T::SUBS + mi * TNS + ni) * 64u + lane] = p[r][mi][ni];
+        }
+    }
+    __syncthreads();
+    // output elements tid, tid + NT, ... (element e of block (subtile, lane l) is
+    // 4 (64 subtile + l) + e), their sums interleaved
+    constexpr uint32_t ELEMS = T::SUBS * 256u, ITEMS = (ELEMS + T::NT - 1u) / T::NT;
+    const bool scaled = j.mode == MODE_SUM_SCALED;
+    const float* const prodf = reinterpret_cast<const float*>(smem) + tid;
+    float acc[ITEMS];
+#pragma unroll
+    for (uint32_t it = 0; it < ITEMS; ++it)
+        acc[it] = 0.0f;
+    const auto add_group = [&](uint32_t g) {
+        float v[ITEMS];
+#pragma unroll
+        for (uint32_t it = 0; it < ITEMS; ++it)
+            v[it] = ELEMS % T::NT == 0 || T::NT * it + tid < ELEMS ? prodf[g * ELEMS + T::NT * it] : 0.0f;
+#pragma unroll
+        for (uint32_t it = 0; it < ITEMS; ++it)
+            acc[it] = acc[it] + v[it];
+    };
+    uint32_t g = 0;
+    for (; g + 4u <= groups; g += 4u) {
+        add_group(g);
+        add_group(g + 1u);
+        add_group(g + 2u);
+        add_group(g + 3u);
+    }
+    for (; g < groups; ++g)
+        add_group(g);
+#pragma unroll
+    for (uint32_t it = 0; it < ITEMS; ++it) {
+        const uint32_t idx = T::NT * it + tid;
+        const uint32_t blk = idx >> 2, e = idx & 3u, sub = blk >> 6, l = blk & 63u;
+        const uint32_t mi = sub / TNS, ni = sub % TNS;
+        const uint32_t n = n0 + 16u * ni + (l & 15u), m = m0 + 16u * mi + 4u * (l >> 4) + e;
+        if (idx >= ELEMS || n >= j.n || m >= j.rows)
+            continue;
+        float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
+        __builtin_nontemporal_store(scaled ? acc[it] * j.rscale[m] : acc[it], orow + n);
+    }
+}
+
+// k_gemm_kc<TMS, TNW, WN, KS, G>: F32-accumulating jobs with few rows and at most G
+// groups, as k_gemm_kr but with contiguous K slices handing on an accumulator instead
+// of exchanging every product.  Workgroup tile (16 TMS) x (16 TNW WN); wave w = s WN + nn
+// computes the 16 TMS x 16 TNW block nn of the tile over K slice s (groups s G/KS ..
+// (s+1) G/KS - 1).  All waves first bring every group's rows, sign bits and scales into
+// LDS by DMA (wave w the groups w, w + W, ...), one barrier; then each wave computes its
+// products RN(scale * D) in registers; slice 0 adds its products in group order from +0,
+// and each later slice, after a barrier, takes the running sums through LDS and adds its
+// own in group order -- the reference's order with only KS - 1 exchanges of one value
+// per output.  The K order inside a group is that of k_gemm_ks.
+template <int TMS, int TNW, int WN, int KS, int G>
+struct KcLayout {
+    static constexpr uint32_t W = WN * KS, NT = 64u * W, GS = G / KS;
+    static constexpr uint32_t TM = 16u * TMS, TN = 16u * TNW * WN;
+    static constexpr uint32_t A_BYTES = TM * 128u, A_INS = A_BYTES / 1024u;
+    static constexpr uint32_t BITS_BYTES = TN * 16u, SC_BYTES = TN * 2u, SC_LANES = SC_BYTES / 16u;
+    static constexpr uint32_t ROUND_BYTES = A_BYTES + BITS_BYTES + SC_BYTES;
+    static constexpr uint32_t RD = (G + W - 1u) / W;  // DMA rounds per wave
+    static constexpr uint32_t OPS_BYTES = G * ROUND_BYTES;
+    static constexpr uint32_t OFF_LUT = OPS_BYTES, OFF_X = OFF_LUT + 2048u;
+    static constexpr uint32_t SMEM = OFF_X + WN * TMS * TNW * 1024u;
+    static_assert(G % KS == 0, "whole K slices");
+    static_assert(A_BYTES % 1024u == 0, "whole 1 KiB row DMAs");
+    static_assert(TN <= 64u && 64u % TN == 0, "a tile's columns lie in one 64-feature tile of the matrix layout");
+    static_assert(SC_BYTES % 16u == 0, "whole 16-byte scale DMAs");
+    static_assert(RD * (A_INS + 2u) < 64u, "vmcnt range");
+    static_assert(SMEM <= 160u * 1024u, "LDS");
+};
+
+template <int TMS, int TNW, int WN, int KS, int G>
+__global__ __launch_bounds__(64 * WN * KS) void k_gemm_kc(GemmJob j, uint32_t mtiles, uint32_t ntiles, uint32_t band,
+                                                         uint64_t seq, const uint64_t* __restrict__ flag) {
+    typedef KcLayout<TMS, TNW, WN, KS, G> T;
+    __shared__ __attribute__((aligned(1024))) unsigned char smem[T::SMEM];
+    // the job's error flag, checked before anything is stored (the DMAs read only the job's
+    // own memory, so they need not wait for it)
+    const uint64_t failed_seq = *flag;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const TileRC tile = gemm_tile_of_block(blockIdx.x, gridDim.x, mtiles, ntiles, band);
+    const uint32_t m0 = tile.mt * T::TM, n0 = tile.nt * T::TN;
+    const uint32_t groups = j.groups;
+
+    // 1. the DMAs (the layout of a group as in k_gemm_kr; group g at g * ROUND_BYTES).
+    // Groups past the last are clamped: the copies write the same bytes.
+    uint32_t a_src[T::A_INS];
+#pragma unroll
+    for (uint32_t i = 0; i < T::A_INS; ++i) {
+        const uint32_t p = 64u * i + lane, r = p >> 3;
+        a_src[i] = min(m0 + r, j.rows - 1u) * j.k + 16u * ((p & 7u) ^ ((r >> 1) & 7u));
+    }
+    const uint32_t col0 = min(n0 >> 6, j.tiles - 1u) * groups * kTile + (n0 & 63u);
+    const uint32_t bits_off = (col0 + min(lane, T::TN - 1u)) * 16u;
+    const uint32_t sc_off = col0 * 2u + 16u * min(lane, T::SC_LANES - 1u);
+    const uint32_t base = lds_offset(smem);
+#pragma unroll
+    for (uint32_t r = 0; r < T::RD; ++r) {
+        const uint32_t g = min(T::W * r + wave, groups - 1u);
+        const uint32_t slot = base + g * T::ROUND_BYTES;
+        const int8_t* qg = j.q + (size_t)g * kGroup;
+#pragma unroll
+        for (uint32_t i = 0; i < T::A_INS; ++i)
+            dma16_s(a_src[i], qg, slot + 1024u * i);
+        dma16_s_lanes<lane_mask<T::TN>()>(bits_off + g * (kTile * 16u), j.wbits, slot + T::A_BYTES);
+        dma16_s_lanes<lane_mask<T::SC_LANES>()>(sc_off + g * (kTile * 2u), j.wscale,
+                                                slot + T::A_BYTES + T::BITS_BYTES);
+    }
+    uint2* const lut = reinterpret_cast<uint2*>(smem + T::OFF_LUT);
+    for (uint32_t i = tid; i < 256u; i += T::NT)
+        lut[i] = make_uint2(pm1_nibble(i & 15u), pm1_nibble(i >> 4));
+    wait_vm<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's DMAs and table entries are done
+    barrier();                           // ... and every wave's
+
+    // 2. this wave's products over its K slice, software-pipelined as in k_gemm_kr
+    const uint32_t nn = wave % WN, s = wave / WN, g0 = s * T::GS;
+    const uint32_t chunk = lane >> 4, lrow = lane & 15u;
+    const v4i c_init = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+    v4f p[T::GS][TMS][TNW];
+    KrOps<TMS, TNW> raw[3];
+    v4i b[2][TNW][2];
+    const auto read = [&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        KrOps<TMS, TNW>& o = raw[i % 3u];
+        const unsigned char* const slot = smem + min(g0 + i, groups - 1u) * T::ROUND_BYTES;
+#pragma unroll
+        for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi)
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h)
+                o.a[mi][h] = *reinterpret_cast<const v4i*>(slot + swz128(16u * mi + lrow, 2u * chunk + h));
+#pragma unroll
+        for (uint32_t ni = 0; ni < (uint32_t)TNW; ++ni) {
+            const uint32_t f = 16u * (nn * TNW + ni) + lrow;
+            o.bits[ni] = *reinterpret_cast<const uint32_t*>(slot + T::A_BYTES + 16u * f + 4u * chunk);
+            o.s[ni] = *reinterpret_cast<const uint16_t*>(slot + T::A_BYTES + T::BITS_BYTES + 2u * f);
+        }
+    };
+    const auto expand = [&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        const KrOps<TMS, TNW>& o = raw[i % 3u];
+#pragma unroll
+        for (uint32_t ni = 0; ni < (uint32_t)TNW; ++ni)
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h) {
+                const uint2 lo = lut[(o.bits[ni] >> (16u * h)) & 0xffu];
+                const uint2 hi = lut[(o.bits[ni] >> (16u * h + 8u)) & 0xffu];
+                b[i % 2u][ni][h] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+            }
+    };
+    const auto mma = [&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        const KrOps<TMS, TNW>& o = raw[i % 3u];
+#pragma unroll
+        for (uint32_t ni = 0; ni < (uint32_t)TNW; ++ni) {
+            const float sc = __half2float(__ushort_as_half((uint16_t)o.s[ni]));
+            const float cneg = sc * -kMagicValue;  // exact
+#pragma unroll
+            for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi) {
+                v4i dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a[mi][0], b[i % 2u][ni][0], c_init, 0, 0, 0);
+                dd = __builtin_amdgcn_mfma_i32_16x16x64_i8(o.a[mi][1], b[i % 2u][ni][1], dd, 0, 0, 0);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    p[i][mi][ni][e] = __builtin_fmaf(sc, __int_as_float(dd[e]), cneg);
+            }
+        }
+    };
+    static_for<T::GS + 2u>([&](auto ic) {
+        constexpr uint32_t i = decltype(ic)::value;
+        if constexpr (i < T::GS)
+            read(std::integral_constant<uint32_t, i>{});
+        if constexpr (i >= 1u && i - 1u < T::GS)
+            expand(std::integral_constant<uint32_t, i - 1u>{});
+        if constexpr (i >= 2u)
+            mma(std::integral_constant<uint32_t, i - 2u>{});
+    });
+    if (failed_seq == seq)
+        return;  // an illegal input row in this job: write nothing (the whole workgroup)
+
+    // 3. the running sums along the slices: slice 0 from +0, slice t after barrier t
+    v4f acc[TMS][TNW];
+    v4f* const xchg = reinterpret_cast<v4f*>(smem + T::OFF_X) + nn * (TMS * TNW * 64u) + lane;
+    const auto add_slice = [&]() {
+#pragma unroll
+        for (uint32_t i = 0; i < T::GS; ++i) {
+            if (g0 + i < groups) {
+#pragma unroll
+                for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi)
+#pragma unroll
+                    for (uint32_t ni = 0; ni < (uint32_t)TNW; ++ni)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[mi][ni][e] = acc[mi][ni][e] + p[i][mi][ni][e];
+            }
+        }
+    };
+#pragma unroll
+    for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi)
+#pragma unroll
+        for (uint32_t ni = 0; ni < (uint32_t)TNW; ++ni)
+            acc[mi][ni] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if (s == 0u)
+        add_slice();
+#pragma unroll
+    for (uint32_t t = 1; t < (uint32_t)KS; ++t) {
+        if (s == t - 1u) {
+#pragma unroll
+            for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi)
+#pragma unroll
+                for (uint32_t ni = 0; ni < (uint32_t)TNW; ++ni)
+                    xchg[(mi * TNW + ni) * 64u] = acc[mi][ni];
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        barrier();
+        if (s == t) {
+#pragma unroll
+            for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi)
+#pragma unroll
+                for (uint32_t ni = 0; ni < (uint32_t)TNW; ++ni)
+                    acc[mi][ni] = xchg[(mi * TNW + ni) * 64u];
+            add_slice();
+        }
+    }
+    if (s != (uint32_t)KS - 1u)
+        return;
+    const bool scaled = j.mode == MODE_SUM_SCALED;
+#pragma unroll
+    for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi)
+#pragma unroll
+        for (uint32_t ni = 0; ni < (uint32_t)TNW; ++ni) {
+            const uint32_t n = n0 + 16u * (nn * TNW + ni) + lrow;
+            if (n >= j.n)
+                continue;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t m = m0 + 16u * mi + 4u * chunk + e;
+                if (m >= j.rows)
+                    continue;
+                float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
+                __builtin_nontemporal_store(scaled ? acc[mi][ni][e] * j.rscale[m] : acc[mi][ni][e], orow + n);
+            }
+        }
+}
+
 // k_gemm_mx<TM, TN, WGM, WGN>: GEMM / GEMM_F32 with a chip's worth of TM x TN tiles,
 // one workgroup of WGM x WGN waves per CU (two waves per SIMD for 8 waves).  Per
 // 128-weight group g:
@@ -1400,6 +1855,28 @@ hipError_t launch_ks(hipStream_t stream, const GemmJob& job, uint64_t seq, const
     return hipGetLastError();
 }
 
+template <int TMS, int TNS, int W, int R>
+hipError_t launch_kr(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
+    if (job.groups > (uint32_t)(W * R) || job.mode == MODE_DOT_I16)
+        return hipErrorInvalidValue;  // the selection below never asks for this
+    const uint32_t mtiles = (job.rows + 16u * TMS - 1u) / (16u * TMS);
+    const uint32_t ntiles = (job.n + 16u * TNS - 1u) / (16u * TNS);
+    launch_kernel((k_gemm_kr<TMS, TNS, W, R>), dim3(mtiles * ntiles), dim3(64 * W), 0, stream, job, mtiles, ntiles,
+                  gemm_band(job, mtiles), seq, flag);
+    return hipGetLastError();
+}
+
+template <int TMS, int TNW, int WN, int KS, int G>
+hipError_t launch_kc(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
+    if (job.groups > (uint32_t)G || job.mode == MODE_DOT_I16)
+        return hipErrorInvalidValue;  // the selection below never asks for this
+    const uint32_t mtiles = (job.rows + 16u * TMS - 1u) / (16u * TMS);
+    const uint32_t ntiles = (job.n + 16u * TNW * WN - 1u) / (16u * TNW * WN);
+    launch_kernel((k_gemm_kc<TMS, TNW, WN, KS, G>), dim3(mtiles * ntiles), dim3(64 * WN * KS), 0, stream, job, mtiles,
+                  ntiles, gemm_band(job, mtiles), seq, flag);
+    return hipGetLastError();
+}
+
 template <int TM, int TN, int WGM, int WGN>
 hipError_t launch_mx(hipStream_t stream, const GemmJob& job, uint64_t seq, const uint64_t* flag) {
     const uint32_t mtiles = (job.rows + TM - 1u) / TM, ntiles = (job.n + TN - 1u) / TN;
@@ -1444,17 +1921,48 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
 #ifndef BNN_GEMM_CO
 #define BNN_GEMM_CO 1  // F32-accumulating jobs with a 128 x 128 tile per CU: two workgroups per CU (k_gemm_co)
 #endif
-    // few rows: one wave per 16 x 16 output block with its operands straight in
-    // registers, while that makes at most three waves per CU (the blocks of 16 columns
-    // each load their rows, and more of them outrun the loads a CU keeps in flight);
-    // with 33..64 rows only for K <= 2048 (a longer K favours splitting it, below)
-    // 17..32 rows, K <= 2048, and at least three quarters of a round of 32 x 32 tiles: four
-    // waves splitting K per tile (2048->6144 x 20-32 rows 7.0-7.1 us against 7.7-8.1 us,
-    // 2048->8192 x 20-32 rows 7.0-7.2 against 9.3-9.9; forced-choice sweep, bit-identical;
-    // it loses with fewer tiles, at 16 rows and from 40 rows on)
-    if (job.mode != MODE_DOT_I16 && job.rows > 16u && job.rows <= 32u && job.groups <= 16u &&
-        blocks(32, 32) >= 3u * cus / 4u)
-        return launch_ks<2, 2, 4, 3>(stream, job, seq, flag);
+    // Few rows: K split over the waves of a workgroup, every wave's operands brought into
+    // LDS by DMA before anything is computed (k_gemm_kr, k_gemm_kc).  The rules follow a
+    // forced-choice sweep over K = 1024..8192, N = 1024..8192 and 8..256 rows (all outputs
+    // bit-identical); against the kernels below, e.g. 2048->6144 x 64 rows 9.6 -> 5.8 us,
+    // 6144->2048 x 64 rows 9.6 -> 6.4 us, 2048->2048 x 128 rows 7.7 -> 4.6 us, 4096->2048 x
+    // 256 rows 14.5 -> 12.2 us, 6144->2048 x 128 rows 13.3 -> 9.6 us, 8192->2048 x 32 rows
+    // 9.2 -> 7.0 us.  Up to 16 groups: 32 x 32 tiles while they fit one round of two per CU,
+    // then 32 x 64 tiles while those fit one round, then 32 x 32 tiles up to 4.5 rounds
+    // (not for 8 groups, where the tiled kernels win past one round); 17..32 groups: 16 x 32
+    // tiles in one round, then 32 x 32 up to three rounds; 33..48 groups: 16 x 32 tiles, then
+    // 16 x 64 tiles with the slices' running sums handed on (k_gemm_kc), each in one round;
+    // 49..64 groups: 16 x 16 tiles in one round.
+    if (job.mode != MODE_DOT_I16) {
+        const uint32_t g = job.groups;
+        if (g <= 16u) {
+            if (job.rows <= 16u && blocks(16, 32) <= cus)
+                return launch_kr<1, 2, 4, 4>(stream, job, seq, flag);
+            if (blocks(32, 32) <= cus)
+                return launch_kr<2, 2, 8, 2>(stream, job, seq, flag);
+            if (blocks(32, 64) <= cus)
+                return launch_kr<2, 4, 8, 2>(stream, job, seq, flag);
+            if (g > 8u && blocks(32, 32) <= 9u * cus / 2u)
+                return launch_kr<2, 2, 8, 2>(stream, job, seq, flag);
+        } else if (g <= 32u) {
+            if (blocks(16, 32) <= cus)
+                return launch_kr<1, 2, 8, 4>(stream, job, seq, flag);
+            if (blocks(32, 32) <= 3u * cus)
+                return launch_kr<2, 2, 8, 4>(stream, job, seq, flag);
+        } else if (g <= 48u) {
+            if (blocks(16, 32) <= cus)
+                return launch_kr<1, 2, 8, 6>(stream, job, seq, flag);
+            if (blocks(16, 64) <= cus)
+                return launch_kc<1, 1, 4, 2, 48>(stream, job, seq, flag);
+        } else if (g <= 64u) {
+            if (blocks(16, 16) <= cus)
+                return launch_kc<1, 1, 1, 8, 64>(stream, job, seq, flag);
+        }
+    }
+    // few rows past the rules above (more than 48 groups and more than a round of 16 x 16
+    // tiles): one wave per 16 x 16 output block with its operands straight in registers,
+    // while that makes at most three waves per CU (the blocks of 16 columns each load their
+    // rows, and more of them outrun the loads a CU keeps in flight)
     if (job.mode != MODE_DOT_I16 && job.rows <= 64u && (job.rows <= 32u || job.groups <= 16u) &&
         blocks(16, 16) <= 3u * cus)
         return launch_wv<1, 1, 1, 1, 8>(stream, job, seq, flag);
@@ -1498,14 +2006,9 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
         return launch_bits<64, 64, 2, 2>(stream, job, seq, flag);
     const uint64_t enough = cus * 3u / 4u;
     if (job.mode != MODE_DOT_I16 && blocks(32, 64) < enough && blocks(32, 32) <= cus) {
-        // too few tiles for the CUs: K split across the waves of a workgroup, with 32 x 32
-        // tiles while those fit one round (past it, 32 x 64 workgroup tiles win: 1024->2048
-        // x 136-160 rows 6.7-6.8 us against 8.5-8.6; only <= 16 groups get here then), else
-        // 32 x 16 ones.  With up to 32 groups four waves per tile beat eight, whose share
-        // of K is then too short to hide each round's loads (1024->2048 x 96-128 rows
-        // 5.4-5.7 us against 8.2-8.3, 4096->2048 x 96-128 rows 10.0-10.3 against 11.5-11.8)
-        if (blocks(32, 32) >= enough && job.groups <= 32u)
-            return launch_ks<2, 2, 4, 3>(stream, job, seq, flag);
+        // too few tiles for the CUs (jobs of more than 48 groups get here): K split across
+        // eight waves of a workgroup with 32 x 32 tiles while those fit one round, else four
+        // waves with 32 x 16 tiles
         if (blocks(32, 32) >= enough)
             return launch_ks<2, 2, 8, 3>(stream, job, seq, flag);
         return launch_ks<2, 1, 4, 3>(stream, job, seq, flag);

@@ -105,25 +105,30 @@ def test_quantiser_edge_rows(pkg, hipdev, oracle, i):
 
 @pytest.mark.parametrize("op", ["GEMM", "GEMM_F32"])
 @pytest.mark.parametrize("rows,k,n", [
-    (1000, 384, 4100), (2049, 128, 2000), (1152, 640, 8128),  # 128 x 128 workgroup tiles
+    (1000, 384, 4100), (2049, 128, 2000),                      # 128 x 128 workgroup tiles, two per CU
     (400, 640, 6100),                                          # 128 x 128, one workgroup per CU
     (1000, 640, 2000),                                         # 64 x 128
     (250, 1152, 6100),                                         # 64 x 64
-    (120, 1152, 5000),                                         # 32 x 64
-    (100, 4224, 2000), (110, 6144, 1900),                     # K split over 8 waves: 32x32, > 32 groups
-    (100, 3200, 2000), (120, 1152, 2040),                     # K split over 4 waves: 32x32, <= 32 groups
-    (80, 1408, 3500), (150, 2048, 2000),                      # 32 x 64, just over a round of 32 x 32
-    (40, 2304, 1500),                                          # K split over 4 waves: 32x16
-    (24, 2048, 8100), (30, 1152, 7000),                       # K split over 4 waves: 32x32, few rows
-    (8, 2048, 6144), (17, 640, 1000), (24, 6144, 2048),       # a wave per 16 x 16 block, operands in registers
-    (32, 1408, 2050), (50, 640, 1000),
-    (330, 4224, 2040), (300, 4480, 2000),                     # a wave per 32 x 32 block, long K
-    (250, 6144, 2000), (300, 8192, 1000),                     # K split over 8 waves per 32 x 64 tile, long K
-    (180, 4096, 2040), (60, 4480, 6100), (150, 3200, 2000),   # K split over 4 waves per 32 x 64 tile, 17..47 groups
-    (380, 6144, 2000), (120, 6272, 6100),                     # the same, >= 48 groups, one to two rounds
-    (380, 2048, 2000), (100, 1152, 6100),                     # 64 x 64, three quarters of a round
-    (1000, 2048, 6100), (777, 1152, 8000),                    # 128 x 192, operands per wave (9 groups: odd)
-    (1000, 6272, 2000), (1024, 4096, 2048),                   # 64 x 128, operands per wave, long K
+    (100, 640, 7000),                                          # 64 x 64, three quarters of a round
+    (120, 640, 5000),                                          # 32 x 64
+    (8, 2048, 6144), (13, 1152, 1000),                         # K split, operands by DMA: 16 x 32, <= 16 rows
+    (17, 640, 1000), (50, 640, 1000), (24, 2048, 8100),        # the same, 32 x 32 in one round (5..16 groups)
+    (30, 1152, 7000), (32, 1408, 2050), (120, 1152, 2040),
+    (80, 1408, 3500), (150, 2048, 2000),                       # the same, 32 x 64 in one round
+    (380, 2048, 2000), (100, 1152, 6100),                      # the same, 32 x 32 past one round
+    (40, 2304, 1500),                                          # the same, 16 x 32, 17..32 groups
+    (100, 3200, 2000), (180, 4096, 2040), (150, 3200, 2000),   # the same, 32 x 32, 17..32 groups
+    (24, 6144, 2048), (56, 4608, 1000),                        # the same, 16 x 32, 33..48 groups
+    (100, 4224, 2000), (110, 6144, 1900),                      # running sums over two K slices, 16 x 64
+    (30, 8192, 2000), (9, 6400, 700),                          # the same, eight slices, 16 x 16 (50: empty slice)
+    (20, 6272, 5000),                                          # a wave per 16 x 16 block, operands in registers
+    (20, 6272, 7000), (40, 6272, 1500),                        # K split over 8 / 4 waves in registers: 32x32, 32x16
+    (330, 4224, 2040), (300, 4480, 2000),                      # a wave per 32 x 32 block, long K
+    (250, 6144, 2000), (300, 8192, 1000),                      # K split over 8 waves per 32 x 64 tile, long K
+    (60, 4480, 6100),                                          # K split over 4 waves per 32 x 64 tile, 17..47 groups
+    (380, 6144, 2000), (120, 6272, 6100),                      # the same, >= 48 groups, one to two rounds
+    (1000, 2048, 6100), (777, 1152, 8000), (1152, 640, 8128),  # 128 x 192, operands per wave (9 groups: odd)
+    (1000, 6272, 2000), (1024, 4096, 2048),                    # 64 x 128, operands per wave, long K
 ])
 def test_gemm_tilings_ragged_edges(pkg, hipdev, oracle_fast, op, rows, k, n):
     """Shapes that select each multi-row tiling, with a partial last row tile, a last
