@@ -301,13 +301,11 @@ BNN_Status open_device(int ordinal, BNN_Device* out_device) {
         d->scratch_bytes = e == hipSuccess ? kExecuteScratchBytes : 0;
     }
     if (e == hipSuccess)
-        e = hipHostMalloc(reinterpret_cast<void**>(&d->status_host), 256, hipHostMallocCoherent);
+        e = hipHostMalloc(reinterpret_cast<void**>(&d->status_host), kStatusHostBytes, hipHostMallocCoherent);
     if (e == hipSuccess) {
-        d->status_host[0] = 0;
-        d->status_host[1] = 0;
-        d->status_host[2] = 0;
-        static const uint64_t zero[2] = {0, 0};  // the illegal-input flag and the completion counter
-        e = hipMemcpyAsync(d->flag_dev, zero, sizeof zero, hipMemcpyHostToDevice, d->stream);
+        memset(d->status_host, 0, kStatusHostBytes);
+        static const uint64_t zero = 0;  // the illegal-input flag
+        e = hipMemcpyAsync(d->flag_dev, &zero, sizeof zero, hipMemcpyHostToDevice, d->stream);
         if (e == hipSuccess)
             e = hipStreamSynchronize(d->stream);
     }
@@ -768,36 +766,35 @@ GemmJob make_gemm(const JobPlan& p, const PrepJob& pj, unsigned char* out, size_
     return j;
 }
 
-// Completion of a single-row launch that signals through the pinned word status_host[2]
-// (the last of its `grid` workgroups stores seq there once every result is visible to the
-// host): spin on it instead of waiting for the end of the kernel, which the runtime reports
+// Completion of a single-row launch whose `grid` workgroups each store seq into their own
+// pinned word (status_host from kDoneFlagWord) once their results are visible to the host:
+// spin on those instead of waiting for the end of the kernel, which the runtime reports
 // several microseconds later.  Past a bound far above any single-row kernel (or with
 // kernel timing on, whose events are resolved at a stream synchronisation) the ordinary
 // stream wait takes over; it also reports device errors.
 BNN_Status finish(BNN_Device device, hipError_t e, uint64_t seq);
 
-BNN_Status finish_signalled(BNN_Device device, hipError_t e, uint64_t seq, uint64_t target) {
+BNN_Status finish_signalled(BNN_Device device, hipError_t e, uint64_t seq, uint32_t grid) {
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return BNN_EIO;
     }
     if (!device->timing) {
+        const uint64_t* const done = device->status_host + kDoneFlagWord;
         const uint64_t t0 = __builtin_readcyclecounter();
+        uint32_t seen = 0;  // workgroups 0 .. seen-1 have signalled
         for (uint32_t i = 0;; ++i) {
-            if (__atomic_load_n(&device->status_host[2], __ATOMIC_ACQUIRE) == seq) {
-                device->done_base = target;
+            while (seen < grid && __atomic_load_n(&done[seen], __ATOMIC_ACQUIRE) == seq)
+                ++seen;
+            if (seen == grid)
                 return __atomic_load_n(&device->status_host[0], __ATOMIC_ACQUIRE) == seq ? BNN_ERANGE : BNN_OK;
-            }
             // ~2 ms at a few GHz of time-stamp counter
             if ((i & 1023u) == 1023u && __builtin_readcyclecounter() - t0 > 8000000ull)
                 break;
             __builtin_ia32_pause();
         }
     }
-    const BNN_Status st = finish(device, hipSuccess, seq);
-    if (st != BNN_EIO)
-        device->done_base = target;  // the kernel ran to its end: every workgroup counted
-    return st;
+    return finish(device, hipSuccess, seq);
 }
 
 BNN_Status finish(BNN_Device device, hipError_t e, uint64_t seq) {
@@ -862,13 +859,12 @@ BNN_Status run_single_row(BNN_Device device, const BNN_Job* job, const JobPlan& 
     const uint32_t cus = device->cu_count ? device->cu_count : 256u;
     const uint32_t grid = p.m->tiles < cus ? p.m->tiles : cus;
     const uint64_t seq = ++device->seq;
-    fa.done_count = device->flag_dev + 1;
-    fa.done_target = device->done_base + grid;
-    fa.done_host = &device->status_host[2];
+    fa.done_flags = grid <= kDoneFlagSlots ? device->status_host + kDoneFlagWord : nullptr;
     const hipError_t e = timed(device, KK_DOT, [&] {
         return launch_fused(device->stream, fa, p.m->tiles, grid, seq, device->flag_dev, device->status_host);
     });
-    const BNN_Status result = finish_signalled(device, e, seq, fa.done_target);
+    const BNN_Status result =
+        fa.done_flags ? finish_signalled(device, e, seq, grid) : finish(device, e, seq);
     if (result == BNN_OK && mirror) {
         device->mirror_buf = job->output.buffer;
         device->mirror_off = job->output.offset;

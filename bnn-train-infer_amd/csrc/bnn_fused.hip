@@ -143,6 +143,18 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// System-coherent stores (write-through to memory: sc0 sc1) for the results of a single job,
+// so that once they are complete (vmcnt) the host can read them without an L2 writeback
+__device__ __forceinline__ void store_sys(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ void store_sys(int16_t* p, uint32_t v) {
+    asm volatile("global_store_short %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_sys(int16_t* p, u32x4 v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc0 sc1" ::"v"(p), "v"(v) : "memory");
+}
+
 __device__ __forceinline__ void fused_raise(uint64_t seq, uint64_t* flag, uint64_t* host_status) {
     __hip_atomic_store(flag, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(host_status, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -707,12 +719,11 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
                             v[c] = (uint32_t)__float_as_int(prod[(g + c) * 64u + lane]) & 0xffffu;
                         const u32x4 w = {v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
                                          v[6] | (v[7] << 16)};
-                        *(__attribute__((address_space(1))) u32x4*)(o + g) = w;
+                        store_sys(o + g, w);
                     }
                 } else {
                     for (uint32_t g = 0; g < G; ++g)
-                        *(__attribute__((address_space(1))) int16_t*)(o + g) =
-                            (int16_t)__float_as_int(prod[g * 64u + lane]);
+                        store_sys(o + g, (uint32_t)__float_as_int(prod[g * 64u + lane]));
                 }
             }
         } else if (wave == 0) {
@@ -732,9 +743,13 @@ __device__ __forceinline__ void fused_body(const FusedArgs& fa, uint32_t tiles_t
                 acc = acc + prod[g * 64u + lane];
             acc = acc * s;
             if (n < job.n) {
-                gstore(lane_pick(paired && lane >= 32u, job.out, job2.out) + n, acc);
-                if (mirror)
-                    mirror[n] = acc;
+                if constexpr (SINGLE) {
+                    store_sys(job.out + n, acc);
+                    if (mirror)
+                        store_sys(mirror + n, acc);
+                } else {
+                    gstore(lane_pick(paired && lane >= 32u, job.out, job2.out) + n, acc);
+                }
             }
             if (paired) {
                 // y_p / (1 + expf(-y_p)) * y_(m+p) (qwen3.c:491-495), y_(m+p) from lane + 32
@@ -780,16 +795,16 @@ __global__ __launch_bounds__(kFusedThreads) void k_fused(FusedArgs fa, uint32_t 
     fused_body<GPW, EPT, PAIRED, SINGLE, RING>(fa, tiles_total, seq, flag, host_status);
     // Completion signal of a single job, so that the host need not wait for the end of the
     // kernel: in this form every global store (outputs, host mirror, error words) comes from
-    // wave 0, which makes them visible system-wide before its workgroup counts itself; the
-    // last workgroup to count then stores seq into the pinned host word.
-    if (SINGLE && fa.done_host != nullptr && threadIdx.x < 64u) {
-        __threadfence_system();
-        if (threadIdx.x == 0) {
-            const uint64_t prev =
-                __hip_atomic_fetch_add(fa.done_count, (uint64_t)1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            if (prev + 1u == fa.done_target)
-                __hip_atomic_store(fa.done_host, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-        }
+    // wave 0 and is system-coherent (written through to memory), so once wave 0's stores are
+    // complete (vmcnt(0)) its workgroup's results are visible to the host, and it stores seq
+    // into its workgroup's own pinned host word (the host waits for all of them).  A
+    // system-scope fence per workgroup instead (a writeback of its XCD's whole L2, 96 at
+    // once) had cost ~3 us per call, and one device-scope counter shared by the workgroups
+    // nothing measurable on top.
+    if (SINGLE && fa.done_flags != nullptr && threadIdx.x < 64u) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
+        if (threadIdx.x == 0)
+            __hip_atomic_store(fa.done_flags + blockIdx.x, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
 

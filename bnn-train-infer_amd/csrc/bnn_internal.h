@@ -152,13 +152,17 @@ struct FusedArgs {
     uint32_t walk_shift;
     float* mirror;         // single F32 job: host memory that also receives the output row (may be null)
     int32_t dot_out;       // DOT_GROUPS: out receives int16 D[n][group] instead of the sums
-    // single job: completion signal (may be null).  Every workgroup adds 1 to *done_count
-    // after its results are visible system-wide; the one that brings it to done_target
-    // stores seq into the host word *done_host.
-    uint64_t* done_count;
-    uint64_t done_target;
-    uint64_t* done_host;
+    // single job: completion signal (may be null).  Workgroup b stores seq into the pinned
+    // host word done_flags[b] once its results are visible system-wide.
+    uint64_t* done_flags;
 };
+
+// Pinned host words of a device (bnn_accel_device::status_host): [0] seq of the last
+// synchronous call that met an illegal input, [1] the same for asynchronous launches,
+// then from kDoneFlagWord one completion word per workgroup of a single-row launch.
+constexpr uint32_t kDoneFlagWord = 32;     // 256 bytes in
+constexpr uint32_t kDoneFlagSlots = 1024;  // workgroups a single-row launch may signal with
+constexpr size_t kStatusHostBytes = (kDoneFlagWord + kDoneFlagSlots) * sizeof(uint64_t);
 
 // Kernel timing: when `start` is set, the next kernel launched through launch_kernel
 // records its own start and end into these events (taken from the dispatch itself,
@@ -222,12 +226,11 @@ struct bnn_accel_device {
     uint64_t seq;              // job sequence number, never 0 for a launched job
     uint64_t async_first_seq;  // first seq launched asynchronously since the last synchronise (0: none)
     uint64_t retired;          // matrices and buffers destroyed so far
-    uint64_t* flag_dev;        // device words: [0] seq of the last job that met an illegal input,
-                               // [1] completion counter of single-row launches (done_base so far)
-    uint64_t done_base;
-    // pinned host words written by the kernels: [0] seq of the last synchronous call that
-    // met an illegal input, [1] the same for asynchronous launches (read by
-    // BNNX_DeviceSynchronize), [2] seq of the last single-row launch that completed
+    uint64_t* flag_dev;        // device word [0]: seq of the last job that met an illegal input
+    // pinned host words written by the kernels (kStatusHostBytes): [0] seq of the last
+    // synchronous call that met an illegal input, [1] the same for asynchronous launches
+    // (read by BNNX_DeviceSynchronize), from kDoneFlagWord the completion words of the
+    // workgroups of single-row launches
     uint64_t* status_host;
     unsigned char* scratch;    // grow-only device scratch
     size_t scratch_bytes;
