@@ -1928,7 +1928,8 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
     // 6144->2048 x 64 rows 9.6 -> 6.4 us, 2048->2048 x 128 rows 7.7 -> 4.6 us, 4096->2048 x
     // 256 rows 14.5 -> 12.2 us, 6144->2048 x 128 rows 13.3 -> 9.6 us, 8192->2048 x 32 rows
     // 9.2 -> 7.0 us.  Up to 16 groups: 32 x 32 tiles while they fit one round of two per CU,
-    // then 32 x 64 tiles while those fit one round, then 32 x 32 tiles up to 4.5 rounds
+    // then 32 x 64 tiles while those fit one round (16 waves of one group each above 8 groups),
+    // then 32 x 32 tiles up to 4.5 rounds
     // (not for 8 groups, where the tiled kernels win past one round); 17..32 groups: 16 x 32
     // tiles in one round, then 32 x 32 up to three rounds; 33..48 groups: 16 x 32 tiles, then
     // 16 x 64 tiles with the slices' running sums handed on (k_gemm_kc), each in one round;
@@ -1940,6 +1941,8 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
                 return launch_kr<1, 2, 4, 4>(stream, job, seq, flag);
             if (blocks(32, 32) <= cus)
                 return launch_kr<2, 2, 8, 2>(stream, job, seq, flag);
+            if (blocks(32, 64) <= cus && g > 8u)
+                return launch_kr<2, 4, 16, 1>(stream, job, seq, flag);  // 2048->6144 x 64 rows 6.2 -> 5.7 us
             if (blocks(32, 64) <= cus)
                 return launch_kr<2, 4, 8, 2>(stream, job, seq, flag);
             if (g > 8u && blocks(32, 32) <= 9u * cus / 2u)

@@ -114,7 +114,8 @@ def test_quantiser_edge_rows(pkg, hipdev, oracle, i):
     (8, 2048, 6144), (13, 1152, 1000),                         # K split, operands by DMA: 16 x 32, <= 16 rows
     (17, 640, 1000), (50, 640, 1000), (24, 2048, 8100),        # the same, 32 x 32 in one round (5..16 groups)
     (30, 1152, 7000), (32, 1408, 2050), (120, 1152, 2040),
-    (80, 1408, 3500), (150, 2048, 2000),                       # the same, 32 x 64 in one round
+    (80, 1408, 3500), (150, 2048, 2000),                       # the same, 32 x 64 in one round (16 waves)
+    (190, 1024, 2040),                                         # the same, 8 waves (<= 8 groups)
     (380, 2048, 2000), (100, 1152, 6100),                      # the same, 32 x 32 past one round
     (40, 2304, 1500),                                          # the same, 16 x 32, 17..32 groups
     (100, 3200, 2000), (180, 4096, 2040), (150, 3200, 2000),   # the same, 32 x 32, 17..32 groups
