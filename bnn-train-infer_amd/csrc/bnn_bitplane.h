@@ -53,6 +53,25 @@ __device__ __forceinline__ void gstore(int16_t* p, int16_t v) {
 // bit 7 is the sign, one signed compare where the other bits take an extract and a compare
 __device__ __forceinline__ bool plane_bit(int q, int b) { return b == 7 ? q < 0 : ((q >> b) & 1) != 0; }
 
+// Plane b's 64-bit wave mask into lanes 2b (low half) and 2b + 1 (high half) of `word`:
+// two v_writelane_b32 with the lane as an inline constant, where a per-lane select of the
+// sixteen halves costs ~47 VALU instructions.  s_nop 1: the two wait states between a VALU
+// write of an SGPR (the ballot) and a VALU read of it, which the compiler cannot insert
+// for inline assembly.
+template <int B>
+__device__ __forceinline__ void put_plane_mask(unsigned long long mask, uint32_t& word) {
+    asm("s_nop 1\n\tv_writelane_b32 %0, %1, %2" : "+v"(word) : "s"((uint32_t)mask), "n"(2 * B));
+    asm("s_nop 1\n\tv_writelane_b32 %0, %1, %2" : "+v"(word) : "s"((uint32_t)(mask >> 32)), "n"(2 * B + 1));
+}
+
+// All eight plane masks of the wave's 64 quantised values q, laid out as put_plane_mask does.
+template <int B = 0>
+__device__ __forceinline__ void plane_mask_words(int q, uint32_t& word) {
+    put_plane_mask<B>(__ballot(plane_bit(q, B)), word);
+    if constexpr (B < 7)
+        plane_mask_words<B + 1>(q, word);
+}
+
 __device__ __forceinline__ uint32_t bcnt_acc(uint32_t x, uint32_t acc) {
     uint32_t r;
     asm("v_bcnt_u32_b32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(acc));

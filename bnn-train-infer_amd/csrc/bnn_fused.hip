@@ -59,17 +59,14 @@ extern "C" __device__ double __ockl_wfred_add_f64(double);
 extern "C" __device__ int __ockl_wfred_add_i32(int);
 
 // Bit planes B..7 of the wave's 64 quantised values q: lane 2b of `word` receives
-// the low and lane 2b + 1 the high half of plane b's mask (v_writelane_b32 with the
-// lane as an inline constant), and `sum` accumulates sum(q) from the same masks.
+// the low and lane 2b + 1 the high half of plane b's mask (put_plane_mask), and `sum`
+// accumulates sum(q) from the same masks.
 template <int B>
 __device__ __forceinline__ void plane_words(int q, uint32_t& word, int& sum) {
     const unsigned long long mask = __ballot(plane_bit(q, B));
     const int cnt = __popcll(mask);
     sum += B == 7 ? -(cnt << 7) : (cnt << B);
-    // s_nop 1: the two wait states between a VALU write of an SGPR (the ballot) and a
-    // VALU read of it, which the compiler cannot insert for inline assembly
-    asm("s_nop 1\n\tv_writelane_b32 %0, %1, %2" : "+v"(word) : "s"((uint32_t)mask), "n"(2 * B));
-    asm("s_nop 1\n\tv_writelane_b32 %0, %1, %2" : "+v"(word) : "s"((uint32_t)(mask >> 32)), "n"(2 * B + 1));
+    put_plane_mask<B>(mask, word);
     if constexpr (B < 7)
         plane_words<B + 1>(q, word, sum);
 }

@@ -166,14 +166,7 @@ __device__ void prep_row_t(const PrepJob& j, uint32_t m, bool validate_only, uin
             // bit planes of these 64 values, and their sum as a wave reduction (vector
             // ops: popcounts of the masks would queue the CU's waves on its one scalar unit)
             uint32_t word = 0;
-#pragma unroll
-            for (int b = 0; b < 8; ++b) {
-                const unsigned long long mask = __ballot(plane_bit(q, b));
-                if (lane == 2u * b)
-                    word = (uint32_t)mask;
-                if (lane == 2u * b + 1u)
-                    word = (uint32_t)(mask >> 32);
-            }
+            plane_mask_words(q, word);  // lane 2b / 2b + 1: low / high half of plane b's mask
             const int part = __ockl_wfred_add_i32(q);
             const uint32_t g = (uint32_t)kPrepGroupsPerIter * i + (wave >> 1), half = wave & 1u;
             if (lane < 16u)
