@@ -146,13 +146,15 @@ class Context:
         return out
 
     def set_resident(self, mode: int) -> None:
-        """Decode path, only before the first token: 1 device with fused batches (the
-        default), 2 device with prepared batches, 0 the host call pattern (True and
-        False mean 1 and 0)."""
+        """Execution path.  qwen3, only before the first token: 1 device with fused
+        batches (the default), 2 device with prepared batches, 0 the host call pattern.
+        bnn-mlp, between any two calls: 1 or 2 the device path (the default), 0 the host
+        call pattern.  True and False mean 1 and 0."""
         self.eng.check(self.eng.BNNEX_ContextSetResident(self.handle, int(mode)), "BNNEX_ContextSetResident")
 
     def resident(self) -> int:
-        """The path in effect: 1 device (fused), 2 device (prepared batches), 0 host."""
+        """The path in effect: 1 device (fused), 2 device (prepared batches), 0 host;
+        a bnn-mlp context's device path reports 2."""
         return int(self.eng.BNNEX_ContextIsResident(self.handle))
 
     def pos(self) -> int:

@@ -16,10 +16,6 @@
 
 namespace bnne {
 
-// Qwen3 decode paths (qwen3.cpp).
-BNNE_Status qwen3_select_path(bnne_context* ctx, int path);
-int qwen3_path(const bnne_context* ctx);
-
 namespace {
 
 bool binary32_floats() { return sizeof(float) == 4 && FLT_RADIX == 2 && FLT_MANT_DIG == 24 && FLT_MAX_EXP == 128; }
@@ -53,11 +49,17 @@ private:
     uint64_t start_ = 0, staged_ = 0;
 };
 
-bool all_finite(const float* v, uint64_t n) {
-    for (uint64_t i = 0; i < n; ++i)
-        if (!std::isfinite(v[i]))
-            return false;
-    return true;
+// Branch-free over the bit patterns (an exponent of all ones is an infinity or a NaN) and
+// vectorised (this build's -O2 leaves loops scalar): a classify call's input rows, tens of
+// thousands of values, are checked on every call.
+__attribute__((optimize("tree-vectorize"))) bool all_finite(const float* v, uint64_t n) {
+    uint32_t bad = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        uint32_t u;
+        std::memcpy(&u, v + i, sizeof u);
+        bad |= (uint32_t)((u & 0x7F800000u) == 0x7F800000u);
+    }
+    return bad == 0;
 }
 
 }  // namespace
@@ -281,10 +283,10 @@ BNNE_EXPORT BNNE_Status BNNEX_ContextSetResident(BNNE_Context ctx, int path) {
     forget_message();
     if (!ctx)
         return BNNE_EINVAL;
-    return qwen3_select_path(ctx, path);
+    return guarded([&] { ctx->select_path(path); });
 }
 
-BNNE_EXPORT int BNNEX_ContextIsResident(BNNE_Context ctx) { return ctx ? qwen3_path(ctx) : 0; }
+BNNE_EXPORT int BNNEX_ContextIsResident(BNNE_Context ctx) { return ctx ? ctx->path() : 0; }
 
 BNNE_EXPORT BNNE_Status BNNEX_DecodeGreedy(BNNE_Context ctx, int32_t token, uint32_t n_steps, int32_t* out_tokens) {
     forget_message();

@@ -117,6 +117,13 @@ void bnne_context::allocate_staging() {
     bnne::require(BNN_BufferAlloc(model->device, out_bytes, &stage_out), "BNN_BufferAlloc (layer output)");
 }
 
+void bnne_context::select_path(int path) {
+    if (path < 0 || path > 2)
+        bnne::raise(BNNE_EINVAL, "path %d (0 host, 1 device with fused batches, 2 device)", path);
+    if (path != 0)
+        bnne::raise(BNNE_ENOTSUP, "only qwen3 and bnn-mlp contexts have a device path");
+}
+
 void bnne_context::classify(const float*, uint32_t, float*) {
     bnne::raise(BNNE_ENOTSUP, "this model does not classify");
 }

@@ -267,6 +267,11 @@ struct bnne_context {
     // (bnn-infer-v2.c:48-54), out[i] the argmax after step i; leaves pos as it found it
     virtual void decode_greedy(int32_t token, uint32_t n, int32_t* out);
     virtual void rewind(uint32_t pos);
+    // The execution path (BNNEX_ContextSetResident): 0 the reference's host call pattern,
+    // 1 a device path with fused batches, 2 a device path with prepared batches.  Contexts
+    // without a device path stay on 0 and refuse the others (BNNE_ENOTSUP).
+    virtual int path() const { return 0; }
+    virtual void select_path(int path);
 
     // The statistics counter `field`, or null when statistics are off.
     uint64_t* counter(uint64_t BNNE_Stats::*field) { return params.enable_stats ? &(stats.*field) : nullptr; }

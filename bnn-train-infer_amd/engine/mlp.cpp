@@ -9,7 +9,14 @@
 // width), bnn-mlp.input_std (> 0), bnn-mlp.input_pixels (at most input_features when
 // present), bnn-mlp.block.<i>.activation ("relu" or "none"; absent: ReLU on every
 // block but the last).
+//
+// A context classifies on one of two paths with the same logits: the device path
+// (mlp_device.hip: a chunk's rows stay on the device through every block, one host wait
+// per chunk; the default where the backend and the shapes allow it) or the reference's
+// call pattern below (per block one write, GEMM_F32 jobs and one read, the post-operation
+// on the host).
 #include "engine.hpp"
+#include "mlp_device.h"
 
 #include <cstdio>
 #include <string>
@@ -46,12 +53,26 @@ public:
         stage_rows = p.n_batch < kChunkRows ? (p.n_batch ? p.n_batch : 1u) : kChunkRows;
         for (std::vector<float>& r : rows_)
             r.resize((size_t)stage_rows * net.widest);
+        // the device path where the backend and the shapes allow it, else the host pattern
+        const BNNE_Status st = open_device(&device_);
+        if (st == BNNE_ENOTSUP)
+            forget_message();
+        else if (st != BNNE_OK)
+            throw Failure{st};
     }
+    ~MlpContext() override { mlp_device_free(device_); }
     void classify(const float* input, uint32_t n, float* logits) override;
+    // 0 the host call pattern, 2 the device path (prepared batches; there is no fused form,
+    // so asking for 1 selects it too).  The path may change between calls.
+    int path() const override { return device_ ? 2 : 0; }
+    void select_path(int path) override;
 
 private:
+    BNNE_Status open_device(MlpDevice** out);
+
     MlpModel& net_;
     std::vector<float> rows_[2];  // the hidden activations of a chunk alternate between these
+    MlpDevice* device_ = nullptr;
 };
 
 std::string block_key(uint32_t i, const char* what) {
@@ -109,7 +130,39 @@ void MlpModel::load() {
 
 bnne_context* MlpModel::new_context(const BNNE_ContextParams& p) { return new MlpContext(*this, p); }
 
+BNNE_Status MlpContext::open_device(MlpDevice** out) {
+    std::vector<MlpDeviceBlock> blocks;
+    for (const auto& b : net_.blocks)
+        blocks.push_back(MlpDeviceBlock{&b->weight, b->post_scale.data(), b->post_bias.data(), b->relu});
+    return mlp_device_create(this, blocks.data(), (uint32_t)blocks.size(), net_.inputs, stage_rows, out);
+}
+
+void MlpContext::select_path(int path) {
+    if (path < 0 || path > 2)
+        raise(BNNE_EINVAL, "classify path %d (0 host, 1 or 2 device)", path);
+    if ((path == 0) == (device_ == nullptr))
+        return;
+    if (path == 0) {
+        mlp_device_free(device_);
+        device_ = nullptr;
+        return;
+    }
+    const BNNE_Status st = open_device(&device_);
+    if (st != BNNE_OK)
+        throw Failure{st};
+}
+
 void MlpContext::classify(const float* input, uint32_t n, float* logits) {
+    if (device_) {
+        for (uint32_t s0 = 0; s0 < n; s0 += stage_rows) {
+            const uint32_t rows = n - s0 < stage_rows ? n - s0 : stage_rows;
+            const BNNE_Status st = mlp_device_classify(this, device_, input + (size_t)s0 * net_.inputs, rows,
+                                                       logits + (size_t)s0 * net_.classes);
+            if (st != BNNE_OK)
+                throw Failure{st};
+        }
+        return;
+    }
     const size_t count = net_.blocks.size();
     for (uint32_t s0 = 0; s0 < n; s0 += stage_rows) {
         const uint32_t rows = n - s0 < stage_rows ? n - s0 : stage_rows;

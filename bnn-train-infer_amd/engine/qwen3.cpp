@@ -177,8 +177,8 @@ public:
     void decode_greedy(int32_t token, uint32_t n, int32_t* out) override;
 
     // 0 host step, 1 device path with fused batches, 2 device path with prepared batches
-    int path() const { return device_ ? (resident_fused(device_) ? 1 : 2) : 0; }
-    void select_path(int path);
+    int path() const override { return device_ ? (resident_fused(device_) ? 1 : 2) : 0; }
+    void select_path(int path) override;
 
 private:
     BNNE_Status open_device_path(bool fused, Resident** out);
@@ -547,17 +547,5 @@ bnne_context* Qwen3Model::new_context(const BNNE_ContextParams& p) { return new 
 }  // namespace
 
 bnne_model* make_qwen3() { return new Qwen3Model; }
-
-BNNE_Status qwen3_select_path(bnne_context* ctx, int path) {
-    Qwen3Context* q = dynamic_cast<Qwen3Context*>(ctx);
-    if (!q)
-        return complain(BNNE_ENOTSUP, "only qwen3 contexts have a device path");
-    return guarded([&] { q->select_path(path); });
-}
-
-int qwen3_path(const bnne_context* ctx) {
-    const Qwen3Context* q = dynamic_cast<const Qwen3Context*>(ctx);
-    return q ? q->path() : 0;
-}
 
 }  // namespace bnne

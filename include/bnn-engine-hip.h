@@ -13,6 +13,14 @@
  * copied across for every call.  Both compute the same logits bit for bit.
  * Statistics of the device path: execute_ns is the wait for the device,
  * transfer_ns the logits copy, device_calls the linear jobs run.
+ *
+ * A bnn-mlp context classifies on the device by default as well: a call's rows
+ * are copied to the device once per chunk, every block runs there as a prepared
+ * batch of GEMM_F32 jobs followed by its post_scale / post_bias / ReLU, and only
+ * the logits come back (one host wait per chunk).  The other path is the
+ * reference's call pattern: per block one write, the GEMM_F32 jobs and one read,
+ * the post-operation on the host.  Both give the same logits bit for bit.  Its
+ * device-path statistics: transfer_ns the two copies, execute_ns the wait.
  */
 #ifndef BNN_ENGINE_HIP_H
 #define BNN_ENGINE_HIP_H
@@ -23,15 +31,17 @@
 extern "C" {
 #endif
 
-/* Selects the decode path of a qwen3 context: 0 the host call pattern, 1 the
- * device path with fused batches where the backend takes them (the default), 2
- * the device path with prepared batches only.  Only before its first token
- * (BNNE_EINVAL otherwise, and for other values); BNNE_ENOTSUP for other
- * architectures or shapes the device path does not take. */
+/* Selects the path of a context: 0 the host call pattern, 1 the device path with
+ * fused batches where the backend takes them (the default), 2 the device path with
+ * prepared batches only.  qwen3: only before its first token (BNNE_EINVAL
+ * otherwise).  bnn-mlp: between any two calls; its device path has no fused form,
+ * so 1 and 2 both select it.  BNNE_EINVAL for other values; BNNE_ENOTSUP for other
+ * architectures and for shapes the device path does not take (a bnn-mlp block
+ * split over several shards). */
 BNNE_Status BNNEX_ContextSetResident(BNNE_Context ctx, int enable);
 
 /* The path in effect: 0 host, 1 device with fused batches, 2 device with
- * prepared batches. */
+ * prepared batches (a bnn-mlp context's device path). */
 int BNNEX_ContextIsResident(BNNE_Context ctx);
 
 /* Greedy decoding: n_steps BNNE_Decode calls of one token each, the first of `token`,

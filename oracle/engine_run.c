@@ -137,7 +137,7 @@ done:
     return rc;
 }
 
-static int run_classify(BNNE_Model model, const char* input_path, uint32_t samples, uint32_t batch) {
+static int run_classify(BNNE_Model model, const char* input_path, uint32_t samples, uint32_t batch, int mode) {
     BNNE_ModelInfo info;
     BNNE_Status st = BNNE_ModelGetInfo(model, &info);
     if (st != BNNE_OK)
@@ -158,6 +158,16 @@ static int run_classify(BNNE_Model model, const char* input_path, uint32_t sampl
         rc = fail("BNNE_ContextCreate", st);
         goto done;
     }
+#ifdef OWN_ENGINE
+    if (mode >= 0 && (st = BNNEX_ContextSetResident(c, mode)) != BNNE_OK) {
+        rc = fail("BNNEX_ContextSetResident", st);
+        goto done;
+    }
+    /* the path on stderr: stdout holds only the logits */
+    fprintf(stderr, "path %s\n", BNNEX_ContextIsResident(c) ? "device" : "host");
+#else
+    (void)mode;
+#endif
     for (uint32_t s0 = 0; s0 < samples; s0 += batch) {
         const uint32_t n = samples - s0 < batch ? samples - s0 : batch;
         st = BNNE_Classify(c, x + (size_t)s0 * info.input_size, n, logits);
@@ -184,12 +194,14 @@ done:
 }
 
 int main(int argc, char** argv) {
-    int mode = 1;  /* BNNEX_ContextSetResident: 0 host, 1 device (fused), 2 prepared batches */
+    /* BNNEX_ContextSetResident: 0 host, 1 device (fused), 2 prepared batches; the
+     * context's default path when not given (-2) */
+    int mode = -2;
     if (argc == 7)
         mode = strcmp(argv[6], "host") == 0 ? 0 : strcmp(argv[6], "prepared") == 0 ? 2
                                             : strcmp(argv[6], "device") == 0 ? 1 : -1;
-    if ((argc != 6 && argc != 7) || mode < 0 || (strcmp(argv[1], "llm") != 0 && strcmp(argv[1], "classify") != 0)) {
-        fprintf(stderr, "usage: %s llm MODEL IDS STEPS CTX | classify MODEL INPUT SAMPLES BATCH\n", argv[0]);
+    if ((argc != 6 && argc != 7) || mode == -1 || (strcmp(argv[1], "llm") != 0 && strcmp(argv[1], "classify") != 0)) {
+        fprintf(stderr, "usage: %s llm MODEL IDS STEPS CTX | classify MODEL INPUT SAMPLES BATCH [host|device|prepared]\n", argv[0]);
         return 1;
     }
     BNN_Device dev = NULL;
@@ -205,7 +217,8 @@ int main(int argc, char** argv) {
         return fail("BNNE_ModelLoad", st);
     }
     const uint32_t a = (uint32_t)strtoul(argv[4], NULL, 10), b = (uint32_t)strtoul(argv[5], NULL, 10);
-    const int rc = strcmp(argv[1], "llm") == 0 ? run_llm(model, argv[3], a, b, mode) : run_classify(model, argv[3], a, b);
+    const int rc = strcmp(argv[1], "llm") == 0 ? run_llm(model, argv[3], a, b, mode < 0 ? 1 : mode)
+                                                   : run_classify(model, argv[3], a, b, mode);
     BNNE_ModelFree(model);
     BNN_DeviceClose(dev);
     return rc;

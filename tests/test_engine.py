@@ -564,16 +564,89 @@ def test_reference_cli_on_this_build(pkg, tmp_path, cli):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("runner", ["own", "refhip"])
+@pytest.mark.parametrize("runner", ["own-device", "own-host", "refhip"])
 def test_engine_bnn_mlp_bit_exact(pkg, tmp_path, runner):
-    exe = ENGINE_RUN_OWN if runner == "own" else ENGINE_RUN_REFHIP
+    """The bnn-mlp fixture (1000 samples in calls of 64, reference engine + soft backend)
+    on this engine's device path (the default), its host call pattern and the reference
+    engine on this backend."""
+    exe = ENGINE_RUN_OWN if runner.startswith("own") else ENGINE_RUN_REFHIP
     if runner == "refhip" and not exe.exists():
         pytest.skip("reference engine on HIP not built")
     model, inp = write_mlp(pkg, tmp_path)
-    print(f"engine bnn-mlp via {exe.name}", flush=True)
-    out = subprocess.run([str(exe), "classify", str(model), str(inp), str(MLP["samples"]), str(MLP["batch"])],
-                         capture_output=True, text=True, timeout=120, check=True).stdout
-    check_mlp_output(out)
+    print(f"engine bnn-mlp via {exe.name} {runner}", flush=True)
+    mode = [runner.split("-")[1]] if runner.startswith("own") else []
+    out = subprocess.run([str(exe), "classify", str(model), str(inp), str(MLP["samples"]), str(MLP["batch"])] + mode,
+                         capture_output=True, text=True, timeout=120, check=True)
+    if mode:
+        assert f"path {mode[0]}" in out.stderr
+    check_mlp_output(out.stdout)
+
+
+@pytest.mark.gpu
+def test_engine_mlp_device_path_matches_host(pkg, hip, tmp_path):
+    """bnn-mlp classify on the device path: a chunk's rows are copied to the device once,
+    every block runs as a prepared batch of GEMM_F32 jobs plus the post-operation kernel
+    (post_scale * y + post_bias, ReLU), and only the logits come back.  Bit-identical to
+    the host call pattern for call sizes 1..300 (a context of 300 stages chunks of 256 +
+    44), with more chunk sizes than the path keeps batches for (evicted and rebuilt),
+    after another context's buffers were freed (its batches stale and rebuilt), and when
+    the path changes between calls; the statistics count the same jobs and MACs."""
+    model_path, _ = write_mlp(pkg, tmp_path)
+    x = pkg.gguf.bnn_mlp_inputs(300, seed=7)
+    eng = _engine_lib(pkg)
+    sizes = [1, 7, 64, 300, 2, 3, 4, 5, 300, 64]
+    with pkg.Device(hip, 0) as dev:
+        m = pkg.engine.Model(eng, dev, model_path)
+        host = pkg.engine.Context(m, n_batch=300)
+        host.set_resident(0)
+        assert host.resident() == 0
+        device = pkg.engine.Context(m, n_batch=300)
+        assert device.resident() == 2  # the default: prepared batches on the device
+        print("engine bnn-mlp device path vs host, sizes", sizes, flush=True)
+        s0 = 0
+        for n in sizes:
+            rows = x[s0:s0 + n] if s0 + n <= len(x) else x[:n]
+            want = host.classify(rows)
+            got = device.classify(rows)
+            assert got.shape == (n, 10) and got.view(np.uint32).tolist() == want.view(np.uint32).tolist(), n
+            s0 = (s0 + n) % 200
+            if n == 4:  # another context's buffers freed: the device path's batches go stale
+                other = pkg.engine.Context(m, n_batch=8)
+                other.free()
+        hs, ds = host.stats(), device.stats()
+        for field in ("calls", "items", "device_calls", "logical_macs", "executed_macs"):
+            assert hs[field] == ds[field], field
+        # the path changes between calls, both ways
+        device.set_resident(0)
+        assert device.resident() == 0
+        assert device.classify(x[:9]).view(np.uint32).tolist() == host.classify(x[:9]).view(np.uint32).tolist()
+        device.set_resident(1)
+        assert device.resident() == 2
+        assert device.classify(x[:9]).view(np.uint32).tolist() == host.classify(x[:9]).view(np.uint32).tolist()
+        with pytest.raises(pkg.engine.EngineError) as e:
+            device.set_resident(3)
+        assert e.value.status == -1 and device.resident() == 2
+        host.free()
+        device.free()
+        m.free()
+
+
+@pytest.mark.gpu
+def test_engine_mlp_sharded_block_stays_on_host(pkg, hip, tmp_path):
+    """A block split over two accelerator shards (256 -> 8320): the device path declines
+    (BNNE_ENOTSUP), the context classifies with the host call pattern."""
+    model_path, _ = write_wide_mlp(pkg, tmp_path, 4)
+    eng = _engine_lib(pkg)
+    with pkg.Device(hip, 0) as dev:
+        m = pkg.engine.Model(eng, dev, model_path)
+        c = pkg.engine.Context(m, n_batch=4)
+        assert c.resident() == 0
+        with pytest.raises(pkg.engine.EngineError) as e:
+            c.set_resident(2)
+        assert e.value.status == -3 and c.resident() == 0
+        c.set_resident(0)
+        c.free()
+        m.free()
 
 
 @pytest.mark.gpu
