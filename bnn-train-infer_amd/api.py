@@ -136,6 +136,15 @@ class PostOp(ctypes.Structure):  # include/bnn-accelerator-hip.h (BNNX_PostOp)
     ]
 
 
+class ChainLayer(ctypes.Structure):  # include/bnn-accelerator-hip.h (BNNX_ChainLayer)
+    _fields_ = [
+        ("matrix", ctypes.c_void_p),
+        ("post_scale", ctypes.c_void_p),
+        ("post_bias", ctypes.c_void_p),
+        ("relu", ctypes.c_int32),
+    ]
+
+
 class BnnError(RuntimeError):
     def __init__(self, status: int, what: str = ""):
         self.status = Status(status) if status in Status._value2member_map_ else status
@@ -184,6 +193,7 @@ class Api:
             "BNNX_BatchCreate": (S, [V, P(Job), U32, P(V)]),
             "BNNX_BatchCreateFused": (S, [V, P(Job), U32, P(PreOp), P(V)]),
             "BNNX_BatchCreateFusedPost": (S, [V, P(Job), U32, P(PreOp), P(PostOp), P(V)]),
+            "BNNX_BatchCreateChain": (S, [V, P(ChainLayer), U32, BufferView, BufferView, U32, P(V)]),
             "BNNX_BatchLaunch": (S, [V]),
             "BNNX_BatchCheck": (S, [V]),
             "BNNX_BatchDestroy": (None, [V]),

@@ -1494,7 +1494,10 @@ EXPORT BNN_Status BNNX_BatchLaunch(BNNX_Batch batch) {
     if (device->async_first_seq == 0)
         device->async_first_seq = seq;
     const hipError_t e =
-        batch->fused ? timed(device, KK_DOT,
+        batch->chain ? timed(device, KK_DOT,
+                             [&] { return launch_chain(device->stream, batch->chain_args, seq, device->flag_dev,
+                                                       device->status_host + 1); })
+        : batch->fused ? timed(device, KK_DOT,
                              [&] {
                                  return launch_fused(device->stream, batch->fused_args, batch->fused_tiles,
                                                      batch->fused_grid, seq, device->flag_dev,
@@ -1536,6 +1539,90 @@ EXPORT BNN_Status BNNX_DeviceSynchronize(BNN_Device device) {
     }
     if (first != 0 && __atomic_load_n(&device->status_host[1], __ATOMIC_ACQUIRE) >= first)
         return BNN_ERANGE;
+    return BNN_OK;
+}
+
+namespace {
+// An F32 view of `rows` rows of `width` values for a chained batch: on the device, in
+// bounds, rows 4-byte aligned.
+BNN_Status chain_view(BNN_Device device, const BNN_BufferView& v, uint32_t width, uint32_t rows,
+                      unsigned char** base, uint64_t* stride) {
+    if (v.buffer == nullptr || v.buffer->device != device || v.type != BNN_TYPE_F32)
+        return BNN_EINVAL;
+    const size_t row = (size_t)width * 4u;
+    const size_t st = v.row_stride ? v.row_stride : row;
+    if (st < row)
+        return BNN_EINVAL;
+    if (!rows_fit(v.buffer->size, v.offset, st, row, rows))
+        return BNN_ERANGE;
+    *base = v.buffer->dev + v.offset;
+    *stride = st;
+    return (((uintptr_t)*base | st) & 3u) == 0 ? BNN_OK : BNN_ENOTSUP;
+}
+}  // namespace
+
+EXPORT BNN_Status BNNX_BatchCreateChain(BNN_Device device, const BNNX_ChainLayer* layers, uint32_t count,
+                                        BNN_BufferView input, BNN_BufferView output, uint32_t rows,
+                                        BNNX_Batch* out_batch) {
+    if (out_batch == nullptr)
+        return BNN_EINVAL;
+    *out_batch = nullptr;
+    if (device == nullptr || layers == nullptr || count == 0 || rows == 0)
+        return BNN_EINVAL;
+    if (count > kChainMaxLayers || rows > kChainMaxRows)
+        return BNN_ENOTSUP;
+    ChainLayer table[kChainMaxLayers] = {};
+    for (uint32_t i = 0; i < count; ++i) {
+        const BNN_Matrix m = layers[i].matrix;
+        if (m == nullptr || m->device != device || (layers[i].post_scale == nullptr) != (layers[i].post_bias == nullptr))
+            return BNN_EINVAL;
+        if (i > 0 && m->k != layers[i - 1].matrix->n)  // each layer reads the previous one's outputs
+            return BNN_EINVAL;
+        if (m->k > kChainMaxWidth || m->n > kChainMaxWidth)
+            return BNN_ENOTSUP;
+        table[i] = ChainLayer{m->wbits, m->wscale, layers[i].post_scale, layers[i].post_bias,
+                              m->k, m->n, m->groups, m->tiles, layers[i].relu != 0, 0u};
+    }
+    if (input.buffer != nullptr && input.buffer == output.buffer)
+        return BNN_EINVAL;
+    ChainArgs args = {};
+    unsigned char* in_base = nullptr;
+    BNN_Status st = chain_view(device, input, layers[0].matrix->k, rows, &in_base, &args.in_stride);
+    args.in = in_base;
+    if (st == BNN_OK)
+        st = chain_view(device, output, layers[count - 1].matrix->n, rows, &args.out, &args.out_stride);
+    if (st != BNN_OK)
+        return st;
+    if (fegetround() != FE_TONEAREST)
+        return BNN_ENOTSUP;
+    if (hipSetDevice(device->ordinal) != hipSuccess)
+        return BNN_EIO;
+    BNNX_Batch b = static_cast<BNNX_Batch>(calloc(1, sizeof(bnnx_batch)));
+    if (b == nullptr)
+        return BNN_ENOMEM;
+    void* mem = nullptr;
+    if (hipMalloc(&mem, sizeof(ChainLayer) * count) != hipSuccess) {
+        (void)hipGetLastError();
+        free(b);
+        return BNN_ENOMEM;
+    }
+    if (hipMemcpy(mem, table, sizeof(ChainLayer) * count, hipMemcpyHostToDevice) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(mem);
+        free(b);
+        return BNN_EIO;
+    }
+    b->mem = static_cast<unsigned char*>(mem);
+    b->device = device;
+    b->retired = device->retired;
+    b->needs_nearest = true;
+    b->chain = true;
+    args.layers = static_cast<const ChainLayer*>(mem);
+    args.count = count;
+    args.rows = rows;
+    b->chain_args = args;
+    device->live_batches++;
+    *out_batch = b;
     return BNN_OK;
 }
 

@@ -47,6 +47,21 @@ __device__ __forceinline__ void gstore(int16_t* p, int16_t v) {
     *(__attribute__((address_space(1))) int16_t*)p = v;
 }
 
+extern "C" __device__ uint32_t __ockl_wfred_max_u32(uint32_t);
+
+// Max over the wave of non-negative finite floats: their bit patterns order
+// like the values, so the DPP-based unsigned wave reduction applies.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    return __uint_as_float(__ockl_wfred_max_u32(__float_as_uint(v)));
+}
+
+// An illegal input of launch `seq`: the device flag (later kernels of the launch skip their
+// stores) and the host-visible status word (BNNX_DeviceSynchronize reports BNN_ERANGE).
+__device__ __forceinline__ void raise_flag(uint64_t seq, uint64_t* flag, uint64_t* host_status) {
+    __hip_atomic_store(flag, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(host_status, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // popc(x) + acc in one VALU op.  Written as asm because the compiler otherwise
 // re-associates the chain into ADD3 trees (11 instead of 9 ops per plane).
 // Bit b of the two's complement byte of a quantised value q in [-127, 127] (plane P_b):

@@ -210,6 +210,31 @@ hipError_t launch_gemm(hipStream_t stream, const GemmJob& job, uint32_t cu_count
 // (bnn_fused.hip).
 hipError_t launch_fused(hipStream_t stream, const FusedArgs& args, uint32_t tiles, uint32_t grid, uint64_t seq,
                         uint64_t* flag, uint64_t* host_status);
+// One layer of a chained batch (BNNX_BatchCreateChain): a GEMM_F32 matrix and the
+// optional mapping of its outputs, out = post_scale * y + post_bias, then ReLU.
+struct ChainLayer {
+    const uint4* wbits;       // matrix layout [tiles][groups][64] x 16 bytes
+    const uint16_t* wscale;   // [tiles][groups][64]
+    const float* post_scale;  // [n], or null: no affine mapping
+    const float* post_bias;   // [n] (set with post_scale)
+    uint32_t k, n, groups, tiles;
+    int32_t relu;
+    uint32_t pad_;
+};
+constexpr uint32_t kChainMaxLayers = 16;
+constexpr uint32_t kChainMaxWidth = 4096;  // widest layer input or output
+constexpr uint32_t kChainMaxRows = 4096;
+struct ChainArgs {
+    const ChainLayer* layers;  // device table of `count` layers
+    uint32_t count, rows;
+    const unsigned char* in;   // row 0 of the input view (F32, 4-byte aligned)
+    uint64_t in_stride;
+    unsigned char* out;        // row 0 of the output view (F32, 4-byte aligned)
+    uint64_t out_stride;
+};
+// One launch of a chained batch: a workgroup per row (bnn_chain.hip).
+hipError_t launch_chain(hipStream_t stream, const ChainArgs& args, uint64_t seq, uint64_t* flag,
+                        uint64_t* host_status);
 hipError_t launch_scatter(hipStream_t stream, const unsigned char* src, size_t src_stride,
                           unsigned char* dst, size_t dst_stride, size_t row_bytes, uint32_t rows,
                           uint64_t seq, const uint64_t* flag);
@@ -292,6 +317,9 @@ struct bnnx_batch {
     bool fused;
     uint32_t fused_tiles, fused_grid;
     bnnhip::FusedArgs fused_args;  // jobs points into mem
+    // chained batch (BNNX_BatchCreateChain): one launch of a workgroup per row
+    bool chain;
+    bnnhip::ChainArgs chain_args;  // layers points into mem
 };
 
 struct bnn_accel_buffer {

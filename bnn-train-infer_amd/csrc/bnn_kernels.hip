@@ -62,19 +62,6 @@ __device__ __forceinline__ float load_f32(const unsigned char* row, uint32_t k, 
     return v;
 }
 
-extern "C" __device__ uint32_t __ockl_wfred_max_u32(uint32_t);
-
-// Max over the wave of non-negative finite floats: their bit patterns order
-// like the values, so the DPP-based unsigned wave reduction applies.
-__device__ __forceinline__ float wave_max_nonneg(float v) {
-    return __uint_as_float(__ockl_wfred_max_u32(__float_as_uint(v)));
-}
-
-
-__device__ __forceinline__ void raise_flag(uint64_t seq, uint64_t* flag, uint64_t* host_status) {
-    __hip_atomic_store(flag, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(host_status, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
 
 // ---------------------------------------------------------------------------
 // prep: one workgroup (256 threads) per activation row.  Checks the logical row

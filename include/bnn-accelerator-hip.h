@@ -162,6 +162,37 @@ typedef struct {
 BNN_Status BNNX_BatchCreateFusedPost(BNN_Device device, const BNN_Job* jobs, uint32_t count, const BNNX_PreOp* pre,
                                      const BNNX_PostOp* post, BNNX_Batch* out_batch);
 
+/*
+ * Chained batches: GEMM_F32 layers applied in turn to every row of an input view.
+ * Layer i computes, for each row, exactly what a GEMM_F32 job computes (check,
+ * quantisation, group dots, FP32 accumulation in group order); when post_scale is
+ * set its outputs then become out_o = post_scale[o] * y_o, then out_o + post_bias[o]
+ * (each rounded to binary32 on its own); with relu a negative result becomes +0; and
+ * the row is layer i + 1's input.  The last layer's results go to the output view.
+ * The results equal separate GEMM_F32 jobs with the mapping done on the host (the
+ * bnn-mlp classifier's blocks, bnn-mlp.c:173-198), bit for bit, in one launch: a
+ * workgroup carries a row through every layer and the rows between layers never
+ * leave the chip.  layers[i].matrix has K_i inputs and N_i outputs with
+ * K_(i+1) = N_i (else BNN_EINVAL); at most 16 layers, K_i and N_i <= 4096 and
+ * rows <= 4096 (else BNN_ENOTSUP).  post_scale and post_bias are device addresses of
+ * N_i floats (BNNX_BufferDevicePointer or memory allocated there), both NULL or both
+ * set (else BNN_EINVAL), valid whenever the batch runs.  input is an F32 view of
+ * rows x K_0 values, output an F32 view of rows x N_last values in another buffer
+ * (BNN_EINVAL), both with 4-byte aligned rows (BNN_ENOTSUP).  A row that meets a
+ * non-finite value at a layer's input writes nothing more, and the next
+ * BNNX_DeviceSynchronize reports BNN_ERANGE.  Launch, check, destroy and synchronise as
+ * any prepared batch.
+ */
+typedef struct {
+    BNN_Matrix matrix;
+    const float* post_scale; /* [N_i] or NULL */
+    const float* post_bias;  /* [N_i] or NULL */
+    int32_t relu;
+} BNNX_ChainLayer;
+BNN_Status BNNX_BatchCreateChain(BNN_Device device, const BNNX_ChainLayer* layers, uint32_t count,
+                                 BNN_BufferView input, BNN_BufferView output, uint32_t rows,
+                                 BNNX_Batch* out_batch);
+
 /* Device address of a buffer's memory, for kernels a caller runs on the device's
  * stream between batch launches.  Valid until BNN_BufferFree. */
 BNN_Status BNNX_BufferDevicePointer(BNN_Buffer buffer, void** out_pointer);
