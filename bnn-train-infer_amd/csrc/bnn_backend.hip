@@ -1620,6 +1620,7 @@ EXPORT BNN_Status BNNX_BatchCreateChain(BNN_Device device, const BNNX_ChainLayer
     args.layers = static_cast<const ChainLayer*>(mem);
     args.count = count;
     args.rows = rows;
+    args.k0 = layers[0].matrix->k;
     b->chain_args = args;
     device->live_batches++;
     *out_batch = b;

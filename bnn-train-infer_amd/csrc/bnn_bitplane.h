@@ -55,6 +55,17 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
     return __uint_as_float(__ockl_wfred_max_u32(__float_as_uint(v)));
 }
 
+// Workgroup barrier for data exchanged through LDS: waits for this wave's LDS
+// accesses only.  __syncthreads would also wait for every outstanding global load
+// and store of the wave (its release fence), i.e. for weight prefetches and for
+// the acknowledgement of earlier output stores, none of which the other waves read.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // An illegal input of launch `seq`: the device flag (later kernels of the launch skip their
 // stores) and the host-visible status word (BNNX_DeviceSynchronize reports BNN_ERANGE).
 __device__ __forceinline__ void raise_flag(uint64_t seq, uint64_t* flag, uint64_t* host_status) {

@@ -129,16 +129,6 @@ __device__ __forceinline__ void run_chains(float (&c)[NC], const float4* const (
     }
 }
 
-// Workgroup barrier for data exchanged through LDS: waits for this wave's LDS
-// accesses only.  __syncthreads would also wait for every outstanding global load
-// and store of the wave (its release fence), i.e. for the weight prefetch and for
-// the acknowledgement of earlier output stores, none of which the other waves read.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
 
 // System-coherent stores (write-through to memory: sc0 sc1) for the results of a single job,
 // so that once they are complete (vmcnt) the host can read them without an L2 writeback

@@ -224,9 +224,13 @@ struct ChainLayer {
 constexpr uint32_t kChainMaxLayers = 16;
 constexpr uint32_t kChainMaxWidth = 4096;  // widest layer input or output
 constexpr uint32_t kChainMaxRows = 4096;
+static_assert(sizeof(ChainLayer) % 4 == 0 && kChainMaxLayers * sizeof(ChainLayer) / 4 <= 1024,
+              "the chain kernel copies the layer table with one word per thread");
 struct ChainArgs {
     const ChainLayer* layers;  // device table of `count` layers
     uint32_t count, rows;
+    uint32_t k0;               // layer 0's input width
+    uint32_t pad_;
     const unsigned char* in;   // row 0 of the input view (F32, 4-byte aligned)
     uint64_t in_stride;
     unsigned char* out;        // row 0 of the output view (F32, 4-byte aligned)

@@ -1,10 +1,12 @@
 // Device-resident bnn-mlp classification: a classify call's rows go to the device once,
-// every block runs there as one prepared batch of GEMM_F32 jobs (each row of a job is that
-// sample's GEMV_F32, as SignLinear::apply_rows computes it) followed by this engine's
-// post-operation kernel (post_scale * y + post_bias, then ReLU, each operation rounded on
-// its own as mlp.cpp's host loop does), and only the last block's outputs come back: one
-// host wait per chunk of rows instead of a write, a synchronous BNN_Execute and a read per
-// block.  The logits equal the host call pattern's bit for bit.
+// the blocks run there, and only the last block's outputs come back: one host wait per
+// chunk of rows instead of a write, a synchronous BNN_Execute and a read per block.  The
+// blocks run as one chained batch of the backend (BNNX_BatchCreateChain: each block's
+// GEMM_F32 and its post_scale * y + post_bias and ReLU, one launch for all of them), or,
+// for blocks wider than a chain takes, as one prepared batch of GEMM_F32 jobs per block
+// (each row of a job is that sample's GEMV_F32, as SignLinear::apply_rows computes it)
+// followed by this engine's post-operation kernel (each operation rounded on its own as
+// mlp.cpp's host loop does).  The logits equal the host call pattern's bit for bit.
 #ifndef BNNE_MLP_DEVICE_H
 #define BNNE_MLP_DEVICE_H
 

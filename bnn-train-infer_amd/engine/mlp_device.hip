@@ -49,8 +49,9 @@ struct MlpDevice {
     };
     struct Plan {
         uint32_t rows;
-        std::vector<BNNX_Batch> batches;  // one per block
-        uint64_t jobs;
+        std::vector<BNNX_Batch> batches;  // one chained batch, or one batch per block
+        uint64_t jobs;                    // the GEMM_F32 jobs the host call pattern would run
+        bool chain;
     };
 
     BNN_Device dev = nullptr;
@@ -98,12 +99,31 @@ struct MlpDevice {
         return st;
     }
 
-    // The batches of a chunk of n rows: per block, GEMM_F32 jobs over consecutive rows of
-    // at most the backend's max_rows each (as SignLinear::apply_rows splits them).
+    // The batches of a chunk of n rows: one chained batch (every block and its mapping in
+    // one launch) where the backend takes it, else per block GEMM_F32 jobs over consecutive
+    // rows of at most the backend's max_rows each (as SignLinear::apply_rows splits them)
+    // and this engine's post-operation kernel.
     BNNE_Status build_plan(uint32_t n, uint32_t max_rows, Plan* plan) {
         plan->rows = n;
         plan->jobs = 0;
+        plan->chain = false;
         const uint32_t job_rows = max_rows ? (max_rows < n ? max_rows : n) : 1u;
+        const uint64_t jobs_per_block = (n + job_rows - 1u) / job_rows;
+        std::vector<BNNX_ChainLayer> layers;
+        for (const Block& b : blocks)
+            layers.push_back(BNNX_ChainLayer{b.weight->shards()[0].matrix, b.scale, b.scale + b.out, b.relu ? 1 : 0});
+        BNNX_Batch chain = nullptr;
+        const BNN_Status cs = BNNX_BatchCreateChain(dev, layers.data(), (uint32_t)layers.size(),
+                                                    BNN_BufferView{b_in, BNN_TYPE_F32, 0, 0},
+                                                    BNN_BufferView{b_out, BNN_TYPE_F32, 0, 0}, n, &chain);
+        if (cs == BNN_OK) {
+            plan->batches.push_back(chain);
+            plan->jobs = jobs_per_block * blocks.size();
+            plan->chain = true;
+            return BNNE_OK;
+        }
+        if (cs != BNN_ENOTSUP)
+            return accel_status(cs, "BNNX_BatchCreateChain");
         std::vector<BNN_Job> jobs;
         for (size_t i = 0; i < blocks.size(); ++i) {
             const Block& b = blocks[i];
@@ -248,7 +268,9 @@ BNNE_Status mlp_device_classify(bnne_context* c, MlpDevice* d, const float* inpu
     e = hipMemcpyAsync(d->in, d->pinned_in, in_bytes, hipMemcpyHostToDevice, d->stream);
     BNNE_Status st = e == hipSuccess ? BNNE_OK : hip_failure(e, "input rows to the device");
     const uint64_t t_in = stats ? clock_ns() : 0;
-    for (size_t i = 0; i < d->blocks.size() && st == BNNE_OK; ++i) {
+    if (st == BNNE_OK && plan.chain)
+        st = accel_status(BNNX_BatchLaunch(plan.batches[0]), "BNNX_BatchLaunch");
+    for (size_t i = 0; i < d->blocks.size() && st == BNNE_OK && !plan.chain; ++i) {
         const MlpDevice::Block& b = d->blocks[i];
         st = accel_status(BNNX_BatchLaunch(plan.batches[i]), "BNNX_BatchLaunch");
         if (st != BNNE_OK)

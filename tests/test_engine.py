@@ -583,16 +583,24 @@ def test_engine_bnn_mlp_bit_exact(pkg, tmp_path, runner):
 
 
 @pytest.mark.gpu
-def test_engine_mlp_device_path_matches_host(pkg, hip, tmp_path):
+@pytest.mark.parametrize("form", ["chain", "per-block"])
+def test_engine_mlp_device_path_matches_host(pkg, hip, tmp_path, form):
     """bnn-mlp classify on the device path: a chunk's rows are copied to the device once,
-    every block runs as a prepared batch of GEMM_F32 jobs plus the post-operation kernel
-    (post_scale * y + post_bias, ReLU), and only the logits come back.  Bit-identical to
-    the host call pattern for call sizes 1..300 (a context of 300 stages chunks of 256 +
-    44), with more chunk sizes than the path keeps batches for (evicted and rebuilt),
-    after another context's buffers were freed (its batches stale and rebuilt), and when
-    the path changes between calls; the statistics count the same jobs and MACs."""
-    model_path, _ = write_mlp(pkg, tmp_path)
-    x = pkg.gguf.bnn_mlp_inputs(300, seed=7)
+    the blocks run there -- as one chained batch (every block and its post_scale * y +
+    post_bias and ReLU in one launch), or, with a block wider than a chain takes (4224
+    outputs), as a prepared batch of GEMM_F32 jobs per block plus the engine's
+    post-operation kernel -- and only the logits come back.  Bit-identical to the host
+    call pattern for call sizes 1..300 (a context of 300 stages chunks of 256 + 44), with
+    more chunk sizes than the path keeps batches for (evicted and rebuilt), after another
+    context's buffers were freed (its batches stale and rebuilt), and when the path
+    changes between calls; the statistics count the same jobs and MACs."""
+    if form == "chain":
+        model_path, _ = write_mlp(pkg, tmp_path)
+        x = pkg.gguf.bnn_mlp_inputs(300, seed=7)
+    else:
+        model_path = tmp_path / "wide_block.gguf"
+        pkg.gguf.bnn_mlp_random(model_path, dims=(256, 4224, 10), seed=6, input_pixels=200)
+        x = pkg.gguf.bnn_mlp_inputs(300, features=256, pixels=200, seed=7)
     eng = _engine_lib(pkg)
     sizes = [1, 7, 64, 300, 2, 3, 4, 5, 300, 64]
     with pkg.Device(hip, 0) as dev:
@@ -602,7 +610,7 @@ def test_engine_mlp_device_path_matches_host(pkg, hip, tmp_path):
         assert host.resident() == 0
         device = pkg.engine.Context(m, n_batch=300)
         assert device.resident() == 2  # the default: prepared batches on the device
-        print("engine bnn-mlp device path vs host, sizes", sizes, flush=True)
+        print(f"engine bnn-mlp device path ({form}) vs host, sizes", sizes, flush=True)
         s0 = 0
         for n in sizes:
             rows = x[s0:s0 + n] if s0 + n <= len(x) else x[:n]
