@@ -136,6 +136,12 @@ __device__ __forceinline__ void wait_dma() {
     __builtin_amdgcn_s_waitcnt(0x0070 | N);
 }
 
+// A job's row scale through the global address space (a flat load would also count on the
+// LDS counter that the kernels' LDS waits use).
+__device__ __forceinline__ float row_scale(const GemmJob& j, uint32_t m) {
+    return *(const __attribute__((address_space(1))) float*)(j.rscale + m);
+}
+
 __device__ __forceinline__ void barrier() {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");  // no LDS access moves across it
@@ -1189,6 +1195,17 @@ __global__ __launch_bounds__(64 * W) void k_gemm_kr(GemmJob j, uint32_t mtiles, 
     const TileRC tile = gemm_tile_of_block(blockIdx.x, gridDim.x, mtiles, ntiles, band);
     const uint32_t m0 = tile.mt * T::TM, n0 = tile.nt * T::TN;
     const uint32_t groups = j.groups;
+    // the row scales of this thread's outputs (F32 jobs; the prep launch wrote them),
+    // requested now: read at the store they had added a memory round trip after the sums
+    constexpr uint32_t ELEMS = T::SUBS * 256u, ITEMS = (ELEMS + T::NT - 1u) / T::NT;
+    float rs[ITEMS];
+#pragma unroll
+    for (uint32_t it = 0; it < ITEMS; ++it) {
+        const uint32_t idx = T::NT * it + tid;
+        const uint32_t blk = idx >> 2, e = idx & 3u, mi = (blk >> 6) / TNS;
+        const uint32_t m = m0 + 16u * mi + 4u * ((blk & 63u) >> 4) + e;
+        rs[it] = j.mode == MODE_SUM_SCALED && idx < ELEMS && m < j.rows ? row_scale(j, m) : 1.0f;
+    }
 
     // 1. every round's DMAs.  Rows: position p = 64 i + lane of the 1 KiB DMA i holds
     // chunk (p & 7) ^ ((row >> 1) & 7) of row p >> 3, so that chunk c of row r sits at
@@ -1311,7 +1328,6 @@ __global__ __launch_bounds__(64 * W) void k_gemm_kr(GemmJob j, uint32_t mtiles, 
     __syncthreads();
     // output elements tid, tid + NT, ... (element e of block (subtile, lane l) is
     // 4 (64 subtile + l) + e), their sums interleaved
-    constexpr uint32_t ELEMS = T::SUBS * 256u, ITEMS = (ELEMS + T::NT - 1u) / T::NT;
     const bool scaled = j.mode == MODE_SUM_SCALED;
     const float* const prodf = reinterpret_cast<const float*>(smem) + tid;
     float acc[ITEMS];
@@ -1345,7 +1361,7 @@ __global__ __launch_bounds__(64 * W) void k_gemm_kr(GemmJob j, uint32_t mtiles, 
         if (idx >= ELEMS || n >= j.n || m >= j.rows)
             continue;
         float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
-        __builtin_nontemporal_store(scaled ? acc[it] * j.rscale[m] : acc[it], orow + n);
+        __builtin_nontemporal_store(scaled ? acc[it] * rs[it] : acc[it], orow + n);
     }
 }
 
@@ -1390,6 +1406,15 @@ __global__ __launch_bounds__(64 * WN * KS) void k_gemm_kc(GemmJob j, uint32_t mt
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const TileRC tile = gemm_tile_of_block(blockIdx.x, gridDim.x, mtiles, ntiles, band);
     const uint32_t m0 = tile.mt * T::TM, n0 = tile.nt * T::TN;
+    // the row scales of this thread's outputs (F32 jobs), requested now (see k_gemm_kr)
+    float rs[TMS][4];
+#pragma unroll
+    for (uint32_t mi = 0; mi < (uint32_t)TMS; ++mi)
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            const uint32_t m = m0 + 16u * mi + 4u * (lane >> 4) + e;
+            rs[mi][e] = j.mode == MODE_SUM_SCALED && m < j.rows ? row_scale(j, m) : 1.0f;
+        }
     const uint32_t groups = j.groups;
 
     // 1. the DMAs (the layout of a group as in k_gemm_kr; group g at g * ROUND_BYTES).
@@ -1547,7 +1572,7 @@ __global__ __launch_bounds__(64 * WN * KS) void k_gemm_kc(GemmJob j, uint32_t mt
                 if (m >= j.rows)
                     continue;
                 float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
-                __builtin_nontemporal_store(scaled ? acc[mi][ni][e] * j.rscale[m] : acc[mi][ni][e], orow + n);
+                __builtin_nontemporal_store(scaled ? acc[mi][ni][e] * rs[mi][e] : acc[mi][ni][e], orow + n);
             }
         }
 }
