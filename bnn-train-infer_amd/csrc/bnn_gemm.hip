@@ -804,6 +804,15 @@ __global__ __launch_bounds__(64 * W) void k_gemm_ks(GemmJob j, uint32_t mtiles, 
     const TileRC tile = gemm_tile_of_block(blockIdx.x, gridDim.x, mtiles, ntiles, band);
     const uint32_t mt = tile.mt, nt = tile.nt;
     const uint32_t m0 = mt * TM, n0 = nt * TN;
+    // the row scales of this thread's outputs (F32 jobs), requested now (see k_gemm_kr)
+    float rs[PER_THREAD][4];
+#pragma unroll
+    for (int i = 0; i < (int)PER_THREAD; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t m = m0 + 16u * ((W * i + wave) / TNS) + 4u * (lane >> 4) + r;
+            rs[i][r] = j.mode == MODE_SUM_SCALED && W * i + wave < SUBS && m < j.rows ? row_scale(j, m) : 1.0f;
+        }
     const uint32_t groups = j.groups;
     for (uint32_t i = tid; i < 256u; i += NT)
         lut[i] = make_uint2(pm1_nibble(i & 15u), pm1_nibble(i >> 4));
@@ -939,7 +948,7 @@ __global__ __launch_bounds__(64 * W) void k_gemm_ks(GemmJob j, uint32_t mtiles, 
             if (m >= j.rows || n >= j.n)
                 continue;
             float* orow = reinterpret_cast<float*>(j.out + (size_t)m * j.out_stride);
-            __builtin_nontemporal_store(j.mode == MODE_SUM_SCALED ? acc[i][r] * j.rscale[m] : acc[i][r], orow + n);
+            __builtin_nontemporal_store(j.mode == MODE_SUM_SCALED ? acc[i][r] * rs[i][r] : acc[i][r], orow + n);
         }
     }
 }
