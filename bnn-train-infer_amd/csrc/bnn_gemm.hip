@@ -481,7 +481,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_bits(GemmJob j, uint32_
             continue;
         float4 v = *reinterpret_cast<const float4*>(so + row * T::OUT_STRIDE + col);
         if (scaled) {
-            const float s = j.rscale[m];
+            const float s = row_scale(j, m);
             v.x = v.x * s;
             v.y = v.y * s;
             v.z = v.z * s;
@@ -730,7 +730,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
             continue;
         float4 v = *reinterpret_cast<const float4*>(so + row * T::OUT_STRIDE + col);
         if (scaled) {
-            const float s = j.rscale[m];
+            const float s = row_scale(j, m);
             v.x = v.x * s;
             v.y = v.y * s;
             v.z = v.z * s;
@@ -1841,7 +1841,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void k_gemm_mx(GemmJob j, uint32_t 
             continue;
         float4 v = *reinterpret_cast<const float4*>(so + row * T::OUT_STRIDE + col);
         if (scaled) {
-            const float s = j.rscale[m];
+            const float s = row_scale(j, m);
             v.x = v.x * s;
             v.y = v.y * s;
             v.z = v.z * s;
